@@ -1,0 +1,240 @@
+/*
+ * sparda.h — C ABI of libsparda.so, the MI355X (gfx950) implementation of
+ * SparDA's forecast-guided block-sparse attention path.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers, element strides
+ * and sizes, and returns an int status:
+ *     0   success
+ *    >0   a hipError_t raised by a HIP call (message in sparda_last_error())
+ *    <0   an argument error, detected before any HIP call is made
+ * No exception crosses the boundary. All tensor pointers are device pointers
+ * owned by the caller unless stated otherwise. `stream` is a hipStream_t
+ * (NULL = the legacy default stream); every call is stream-ordered and never
+ * synchronises the device. Calls are re-entrant; the offload handle is the
+ * only stateful object.
+ *
+ * Layout vocabulary (the reference's own): B batch, S/T sequence length,
+ * Hq query heads, Hkv key/value heads (== forecast heads), D head dim,
+ * Df forecast dim (== D), bs block size, NB = ceil(S/bs) KV blocks,
+ * k top-k blocks. Query head h uses KV head h / (Hq/Hkv).
+ *
+ * Reference citations are into tyborra/local-research-Small-Language-Model.
+ */
+#ifndef SPARDA_H
+#define SPARDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPARDA_API __attribute__((visibility("default")))
+
+/* Element types of tensors crossing the boundary. */
+enum {
+    SPARDA_F32 = 0,
+    SPARDA_BF16 = 1,
+};
+
+/* Argument-error status codes (all negative). */
+enum {
+    SPARDA_ERR_NULL = -1,     /* a required pointer is NULL */
+    SPARDA_ERR_SHAPE = -2,    /* a size is out of range or inconsistent */
+    SPARDA_ERR_DTYPE = -3,    /* unsupported element type */
+    SPARDA_ERR_WORKSPACE = -4,/* workspace missing or too small */
+    SPARDA_ERR_STRIDE = -5,   /* unsupported stride (innermost must be 1) */
+    SPARDA_ERR_MODE = -6,     /* unknown mode / routing value */
+    SPARDA_ERR_HANDLE = -7,   /* invalid offload handle or layer */
+    SPARDA_ERR_CAPACITY = -8, /* cache/arena capacity exceeded */
+};
+
+/* Decode routing modes (sparda_decode). */
+enum {
+    /* Score the forecast with the causal mask taken at query row 0, as the
+     * reference's decode does (model/forecast.py:120-126 called from
+     * model/attention/sparse.py:139): only block 0 is finite, the other
+     * k-1 picks are -inf ties, resolved here by lower block index. */
+    SPARDA_ROUTE_REFERENCE = 0,
+    /* Score with the mask at the query's absolute position S-1: every block
+     * up to the current one competes (forecast routing as intended). */
+    SPARDA_ROUTE_ABSOLUTE = 1,
+};
+
+/* Fixed (forecast-free) selections (sparda_select_fixed). */
+enum {
+    SPARDA_SEL_DENSE = 0,         /* every block <= own block
+                                     (model/attention/sparse.py:113-123) */
+    SPARDA_SEL_WINDOW_DECODE = 1, /* {0} U [own-k+1, own]
+                                     (model/attention/sparse.py:142-147) */
+    SPARDA_SEL_WINDOW_PREFILL = 2,/* {0} U [own-k, own]
+                                     (model/attention/sparse.py:250-251) */
+};
+
+/* Top-k algorithm selector for sparda_topk_scores. */
+enum {
+    SPARDA_TOPK_AUTO = 0,
+    SPARDA_TOPK_ROWS = 1,   /* one lane per row, register insertion list */
+    SPARDA_TOPK_WAVE = 2,   /* one workgroup per row, wavefront arg-max rounds */
+};
+
+/* Version of this ABI (major*100 + minor). */
+SPARDA_API int sparda_version(void);
+
+/* Message describing the last non-zero status returned on this thread. */
+SPARDA_API const char* sparda_last_error(void);
+
+/*
+ * KV block compressor.
+ * Replaces KVBlockCompressor.forward (model/forecast.py:57-78).
+ *   protos[b,j,h,d] = (sum_{s = j*bs}^{min((j+1)*bs, S)-1} k[b,s,h,d]) / bs
+ * The sum runs in fp32, sequentially in increasing s, and is then divided by
+ * bs (not by the count of present tokens: the reference zero-pads the last
+ * block, model/forecast.py:68-77).
+ *   k:      [B,S,H,D] of `dtype`, strides (stride_b, stride_s, stride_h, 1)
+ *   protos: [B,NB,H,D] fp32, contiguous, NB = ceil(S/bs)
+ */
+SPARDA_API int sparda_compress(const void* k, int dtype,
+                               int64_t B, int64_t S, int64_t H, int64_t D,
+                               int64_t stride_b, int64_t stride_s, int64_t stride_h,
+                               int64_t block_size, float* protos, void* stream);
+
+/*
+ * Fused forecast score + top-k block router.
+ * Replaces ForecastBlockSelector.forward (model/forecast.py:89-130) and the
+ * selection-set construction of the sparse backend
+ * (model/attention/sparse.py:126-154 decode, 231-247 prefill).
+ *   score[b,h,t,j] = (fma-chain_d f[b,t,h,d]*protos[b,j,h,d]) * scale, fp32,
+ *                    -inf where causal && j > (score_pos0 + t) / bs
+ *   topk[b,h,t,:]  = the min(top_k, NB) blocks with the largest scores,
+ *                    ordered by score descending, ties (including -inf
+ *                    ties) by lower block index
+ *   sel[b,h,t,:]   = ({0, own} U topk) restricted to blocks <= own when
+ *                    causal, sorted ascending, no duplicates, padded with -1;
+ *                    own = min((query_pos0 + t) / bs, NB-1); n_sel = count
+ *   forecast: [B,Tq,H,Df] of f_dtype, strides (f_sb, f_st, f_sh, 1)
+ *   protos:   [B,NB,H,Df] fp32 contiguous (sparda_compress output)
+ * Any of topk / scores / sel (+n_sel) may be NULL. sel_cap >= min(top_k,NB)+2.
+ * The reference's prefill uses score_pos0 = query_pos0 = 0.
+ */
+SPARDA_API int sparda_route(const void* forecast, int f_dtype,
+                            int64_t f_sb, int64_t f_st, int64_t f_sh,
+                            const float* protos,
+                            int64_t B, int64_t Tq, int64_t H, int64_t Df, int64_t NB,
+                            int64_t block_size, int64_t top_k, int causal,
+                            int64_t score_pos0, int64_t query_pos0, float scale,
+                            int32_t* topk, float* scores,
+                            int32_t* sel, int32_t* n_sel, int64_t sel_cap,
+                            void* stream);
+
+/*
+ * Canonical top-k over given fp32 score rows (no masking applied here).
+ * The selection stage of sparda_route fed with caller-provided scores, so
+ * that index parity can be checked on identical fp32 scores
+ * (torch.topk at model/forecast.py:129 with ties broken by lower index).
+ *   scores: [rows, NB] fp32 contiguous;  topk: [rows, min(top_k, NB)] int32
+ */
+SPARDA_API int sparda_topk_scores(const float* scores, int64_t rows, int64_t NB,
+                                  int64_t top_k, int algo, int32_t* topk,
+                                  void* stream);
+
+/*
+ * Forecast-free selection lists: dense causal fallback and the static
+ * sink + sliding-window modes.
+ * Replaces model/attention/sparse.py:113-123 (decode dense fallback),
+ * 142-147 (decode window), 250-251 (prefill window).
+ *   own = min((query_pos0 + t) / bs, NB-1) for t in [0, Tq)
+ *   sel/n_sel: [B,H,Tq,sel_cap] int32 / [B,H,Tq] int32, ascending, -1 padded
+ */
+SPARDA_API int sparda_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H,
+                                   int64_t NB, int64_t block_size, int64_t top_k,
+                                   int64_t query_pos0,
+                                   int32_t* sel, int32_t* n_sel, int64_t sel_cap,
+                                   void* stream);
+
+/*
+ * Materialised block gather.
+ * Replaces gather_kv_blocks (model/attention/sparse.py:19-62).
+ *   k, v:  [B,H,S,D] of dtype, strides (sb, sh, ss, 1)
+ *   idx:   [B,H,n] int32 block indices in [0, NB)
+ *   k_out, v_out: [B,H,n*bs,D] contiguous; tokens >= S are zero (the
+ *          reference pads the sequence to NB*bs, sparse.py:41-43)
+ */
+SPARDA_API int sparda_gather_blocks(const void* k, const void* v, int dtype,
+                                    int64_t sb, int64_t sh, int64_t ss,
+                                    const int32_t* idx,
+                                    int64_t B, int64_t H, int64_t S, int64_t D,
+                                    int64_t n, int64_t block_size,
+                                    void* k_out, void* v_out, void* stream);
+
+/*
+ * Block-sparse GQA prefill attention.
+ * Replaces the mask build + masked SDPA of SparseAttention._forward_masked_sdpa
+ * (model/attention/sparse.py:226-281), including its GQA expansion
+ * (repeat_interleave, sparse.py:264-270): query head h reads KV head
+ * h / (Hq/Hkv) directly.
+ *   out[b,t,h*D+d] = sum_{s in A(b,g,t)} softmax_s(q.k_s * scale) v_s[d]
+ *   A(b,g,t) = { s < T : s/bs in sel[b,g,t,:n_sel] } and s <= t if causal.
+ * sel == NULL means dense (every block), the fallback of sparse.py:201-224.
+ *   q: [B,T,Hq,D] strides (q_sb,q_st,q_sh,1); k,v: [B,T,Hkv,D] strides
+ *   (kv_sb,kv_st,kv_sh,1); sel/n_sel from sparda_route or
+ *   sparda_select_fixed ([B,Hkv,T,sel_cap] / [B,Hkv,T]);
+ *   out: [B,T,Hq*D] of dtype, strides (out_sb, out_st, 1)
+ */
+SPARDA_API int sparda_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                              const void* k, const void* v,
+                              int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                              int dtype,
+                              const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
+                              int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                              int64_t block_size, int causal, float scale,
+                              void* out, int64_t out_sb, int64_t out_st,
+                              void* stream);
+
+/* Workspace bytes sparda_decode needs for these sizes. */
+SPARDA_API size_t sparda_decode_workspace_bytes(int64_t B, int64_t S, int64_t Hq,
+                                                int64_t Hkv, int64_t D,
+                                                int64_t block_size, int64_t top_k);
+
+/*
+ * One single-token decode step of the sparse attention layer.
+ * Replaces SparseAttention._forward_decode_gather (model/attention/sparse.py:99-183)
+ * after the projections: block compression of the whole cache (sparse.py:133-135),
+ * forecast routing (sparse.py:139-141), sink + current block (126-130),
+ * removal of future blocks (150-151), the gather (157) and masked SDPA over the
+ * gathered keys (160-181), as split-K attention over the selected blocks with
+ * a combine. Dense over all S keys when NB <= top_k+2 (sparse.py:113-123);
+ * static window {0} U [cb-k+1, cb] when forecast == NULL (sparse.py:142-147).
+ *   q:        [B,Hq,D] of dtype, strides (q_sb, q_sh, 1) (position S-1)
+ *   k_cache, v_cache: [B,Smax,Hkv,D] strides (kv_sb, kv_ss, kv_sh, 1);
+ *             tokens [0,S) are valid, S includes the new token
+ *   forecast: [B,Hkv,Df] of f_dtype, strides (f_sb, f_sh, 1), or NULL
+ *   protos_in: optional cached prototypes [B,NB,Hkv,D] fp32 (skips the
+ *             compression pass; must equal sparda_compress of the cache)
+ *   protos_out: optional, receives the prototypes computed this step
+ *   sel_out/n_sel_out: optional [B,Hkv,top_k+2] / [B,Hkv] int32
+ *   out: [B,Hq*D] of dtype, stride out_sb
+ *   workspace: >= sparda_decode_workspace_bytes(), 256-byte aligned, and
+ *             zero-filled before its first use: it holds arrival counters
+ *             that the kernels return to zero at the end of every call. Calls
+ *             sharing one workspace must be ordered on one stream.
+ */
+SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh,
+                             const void* k_cache, const void* v_cache,
+                             int64_t kv_sb, int64_t kv_ss, int64_t kv_sh,
+                             int dtype,
+                             const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                             int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                             int64_t block_size, int64_t top_k, int routing, float scale,
+                             const float* protos_in, float* protos_out,
+                             int32_t* sel_out, int32_t* n_sel_out,
+                             void* out, int64_t out_sb,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARDA_H */

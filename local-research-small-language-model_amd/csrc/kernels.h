@@ -1,0 +1,56 @@
+// Internal launcher declarations (host side). The extern "C" layer in abi.cpp
+// validates arguments and calls these; each returns 0 or a status code.
+#pragma once
+
+#include "common.h"
+
+namespace sparda {
+
+int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+                    int64_t sb, int64_t ss, int64_t sh, int64_t bs, float* protos,
+                    hipStream_t stream);
+
+int launch_route(const void* f, int fdtype, int64_t fsb, int64_t fst, int64_t fsh,
+                 const float* protos, int64_t B, int64_t Tq, int64_t H, int64_t Df, int64_t NB,
+                 int64_t bs, int ke, int causal, int64_t score_pos0, int64_t query_pos0,
+                 float scale, int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel,
+                 int cap, hipStream_t stream);
+
+int launch_topk_scores(const float* scores, int64_t rows, int64_t NB, int ke, int algo,
+                       int32_t* topk, hipStream_t stream);
+
+int launch_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H, int64_t NB, int64_t bs,
+                        int64_t k, int64_t query_pos0, int32_t* sel, int32_t* n_sel, int cap,
+                        hipStream_t stream);
+
+int launch_gather(const void* k, const void* v, int dtype, int64_t sb, int64_t sh, int64_t ss,
+                  const int32_t* idx, int64_t B, int64_t H, int64_t S, int64_t D, int64_t n,
+                  int64_t bs, void* ko, void* vo, hipStream_t stream);
+
+// Workspace carve-up of the decode step.
+struct DecodeWs {
+    int32_t* cnt_b;    // [B]        arrivals of the select kernel per sequence
+    int32_t* cnt_bg;   // [B*Hkv]    arrivals of the attend kernel per (sequence, kv head)
+    float* scores;     // [B*Hkv*NB]
+    int32_t* sel;      // [B*Hkv*cap]
+    int32_t* n_sel;    // [B*Hkv]
+    float* part;       // [B*Hq*cap*(D+2)]  (m, l, o[D]) per split
+    size_t bytes;
+};
+DecodeWs decode_ws_layout(void* base, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                          int64_t bs, int64_t k);
+
+int launch_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kc, const void* vc,
+                  int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const void* f, int fdtype,
+                  int64_t f_sb, int64_t f_sh, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                  int64_t D, int64_t bs, int64_t k, int routing, float scale, const float* protos_in,
+                  float* protos_out, int32_t* sel_out, int32_t* n_sel_out, void* out, int64_t out_sb,
+                  const DecodeWs& ws, hipStream_t stream);
+
+int launch_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                   const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
+                   const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
+                   int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int causal, float scale,
+                   void* out, int64_t out_sb, int64_t out_st, hipStream_t stream);
+
+}  // namespace sparda

@@ -1,0 +1,345 @@
+// Block compressor, forecast router (score + top-k + selection list), the
+// stand-alone top-k stage, forecast-free selections and the block gather.
+//
+// Arithmetic contract (bit-exact with the oracle):
+//   prototype = sequential fp32 sum over the block's tokens, then / bs
+//   score     = fma chain over d starting at 0, then * scale
+//   top-k     = larger score first, equal scores by lower block index
+#pragma clang fp contract(off)
+
+#include "common.h"
+#include "kernels.h"
+#include "select.h"
+
+namespace sparda {
+
+// ---------------------------------------------------------------------------
+// compressor: grid (NB, B, ceil(H/heads_per_wg)), block = heads_per_wg*D/VEC.
+// Thread (h, d-group) walks the block's tokens in order, one VEC-wide load per
+// token; a wavefront reads a contiguous run of the token row.
+// ---------------------------------------------------------------------------
+template <int DT, int VEC>
+__global__ void __launch_bounds__(1024)
+compress_kernel(const void* __restrict__ k, int64_t S, int H, int D,
+                int64_t sb, int64_t ss, int64_t sh, int bs, int heads_per_wg,
+                float* __restrict__ protos, int64_t NB) {
+    const int j = blockIdx.x;
+    const int b = blockIdx.y;
+    const int groups = D / VEC;
+    const int h = blockIdx.z * heads_per_wg + threadIdx.x / groups;
+    const int d = (threadIdx.x % groups) * VEC;
+    if (h >= H) return;
+    const int64_t base = b * sb + h * sh + d;
+    const int64_t s0 = static_cast<int64_t>(j) * bs;
+    const int64_t s1 = s0 + bs < S ? s0 + bs : S;
+    float* out = protos + ((static_cast<int64_t>(b) * NB + j) * H + h) * D + d;
+    const float inv_den = static_cast<float>(bs);
+    if constexpr (VEC == 2) {
+        float ax = 0.0f, ay = 0.0f;
+#pragma unroll 8
+        for (int64_t s = s0; s < s1; ++s) {
+            float2 v = load_pair<DT>(k, base + s * ss);
+            ax = ax + v.x;
+            ay = ay + v.y;
+        }
+        out[0] = ax / inv_den;
+        out[1] = ay / inv_den;
+    } else {
+        float a = 0.0f;
+#pragma unroll 8
+        for (int64_t s = s0; s < s1; ++s) a = a + load_elem<DT>(k, base + s * ss);
+        out[0] = a / inv_den;
+    }
+}
+
+int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+                    int64_t sb, int64_t ss, int64_t sh, int64_t bs, float* protos,
+                    hipStream_t stream) {
+    const int64_t NB = cdiv(S, bs);
+    const bool aligned = (D % 2 == 0) && (sb % 2 == 0) && (ss % 2 == 0) && (sh % 2 == 0) &&
+                         (reinterpret_cast<uintptr_t>(k) % (dtype == SPARDA_F32 ? 8 : 4) == 0);
+    const int vec = aligned ? 2 : 1;
+    const int groups = static_cast<int>(D / vec);
+    int hpw = static_cast<int>(256 / groups);
+    if (hpw < 1) hpw = 1;
+    if (hpw > H) hpw = static_cast<int>(H);
+    dim3 grid(static_cast<unsigned>(NB), static_cast<unsigned>(B), static_cast<unsigned>(cdiv(H, hpw)));
+    dim3 block(static_cast<unsigned>(groups * hpw));
+#define SPARDA_COMPRESS(DT_, V_)                                                          \
+    hipLaunchKernelGGL((compress_kernel<DT_, V_>), grid, block, 0, stream, k, S,          \
+                       static_cast<int>(H), static_cast<int>(D), sb, ss, sh,              \
+                       static_cast<int>(bs), hpw, protos, NB)
+    if (dtype == SPARDA_F32) {
+        if (vec == 2) SPARDA_COMPRESS(SPARDA_F32, 2); else SPARDA_COMPRESS(SPARDA_F32, 1);
+    } else {
+        if (vec == 2) SPARDA_COMPRESS(SPARDA_BF16, 2); else SPARDA_COMPRESS(SPARDA_BF16, 1);
+    }
+#undef SPARDA_COMPRESS
+    return check_hip(hipGetLastError(), "compress_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// router, one lane per query row. grid (ceil(Tq/ROWS), H, B), block ROWS.
+// The (b,h) prototypes are staged in LDS in chunks and read as broadcasts.
+// ---------------------------------------------------------------------------
+constexpr int kRouteRows = 64;
+
+template <int FDT, int DF, int KMAX>
+__global__ void __launch_bounds__(kRouteRows)
+route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t fsh,
+                  const float* __restrict__ protos, int64_t Tq, int H, int64_t NB, int bs,
+                  int ke, int causal, int64_t score_pos0, int64_t query_pos0, float scale,
+                  int chunk_blocks,
+                  int32_t* __restrict__ topk, float* __restrict__ scores,
+                  int32_t* __restrict__ sel, int32_t* __restrict__ n_sel, int cap) {
+    extern __shared__ float p_lds[];  // [chunk_blocks][DF]
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRouteRows;
+    const int64_t t = t0 + threadIdx.x;
+    const bool active = t < Tq;
+    const int64_t t_last = (t0 + kRouteRows < Tq ? t0 + kRouteRows : Tq) - 1;
+
+    int64_t jmax_wg = causal ? (score_pos0 + t_last) / bs : NB - 1;
+    if (jmax_wg > NB - 1) jmax_wg = NB - 1;
+    int64_t limit = causal ? (score_pos0 + (active ? t : t_last)) / bs : NB - 1;
+    if (limit > NB - 1) limit = NB - 1;
+
+    float fr[DF];
+    if (active) {
+        const int64_t base = b * fsb + t * fst + h * fsh;
+#pragma unroll
+        for (int d = 0; d < DF; ++d) fr[d] = load_elem<FDT>(f, base + d);
+    } else {
+#pragma unroll
+        for (int d = 0; d < DF; ++d) fr[d] = 0.0f;
+    }
+    const int64_t row = (static_cast<int64_t>(b) * H + h) * Tq + t;
+    float* srow = (scores != nullptr && active) ? scores + row * NB : nullptr;
+
+    LaneTopK<KMAX> best;
+    best.init(ke);
+
+    const float* pbh = protos + (static_cast<int64_t>(b) * NB * H + h) * DF;  // + j*H*DF
+    for (int64_t c0 = 0; c0 <= jmax_wg; c0 += chunk_blocks) {
+        const int64_t c1 = (c0 + chunk_blocks - 1 < jmax_wg) ? c0 + chunk_blocks - 1 : jmax_wg;
+        const int nblk = static_cast<int>(c1 - c0 + 1);
+        __syncthreads();
+        for (int i = threadIdx.x; i < nblk * DF; i += kRouteRows) {
+            const int jj = i / DF, d = i % DF;
+            p_lds[i] = pbh[(c0 + jj) * H * DF + d];
+        }
+        __syncthreads();
+        const int64_t jend = limit < c1 ? limit : c1;
+        for (int64_t j = c0; j <= jend; ++j) {
+            const float* pj = p_lds + (j - c0) * DF;
+            float acc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < DF; ++d) acc = __fmaf_rn(fr[d], pj[d], acc);
+            const float s = acc * scale;
+            if (srow) srow[j] = s;
+            best.push(rank64(s, static_cast<int32_t>(j)));
+        }
+    }
+    if (!active) return;
+    if (srow) {
+        for (int64_t j = limit + 1; j < NB; ++j) srow[j] = -__builtin_inff();
+    }
+    // slots not filled by a candidate take the masked blocks in ascending order
+    int32_t picks[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) picks[i] = (i < ke) ? (best.r[i] == 0 ? i : rank64_index(best.r[i])) : -1;
+    if (topk) {
+        int32_t* tr = topk + row * ke;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i)
+            if (i < ke) tr[i] = picks[i];
+    }
+    if (sel) {
+        int64_t own = (query_pos0 + t) / bs;
+        if (own > NB - 1) own = NB - 1;
+        int32_t c[KMAX + 2];
+        c[0] = 0;
+        c[1] = static_cast<int32_t>(own);
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) c[i + 2] = picks[i];
+        emit_selection(c, static_cast<int>(own), causal != 0, sel + row * cap, cap, n_sel + row);
+    }
+}
+
+template <int FDT, int DF>
+static int launch_route_df(const void* f, int64_t fsb, int64_t fst, int64_t fsh, const float* protos,
+                           int64_t B, int64_t Tq, int64_t H, int64_t NB, int64_t bs, int ke,
+                           int causal, int64_t score_pos0, int64_t query_pos0, float scale,
+                           int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel, int cap,
+                           hipStream_t stream) {
+    const int max_lds_floats = 16384;  // 64 KiB of prototypes per pass
+    int chunk = static_cast<int>(max_lds_floats / DF);
+    if (chunk > NB) chunk = static_cast<int>(NB);
+    dim3 grid(static_cast<unsigned>(cdiv(Tq, kRouteRows)), static_cast<unsigned>(H), static_cast<unsigned>(B));
+    const size_t lds = static_cast<size_t>(chunk) * DF * sizeof(float);
+#define SPARDA_ROUTE(KM_)                                                                    \
+    hipLaunchKernelGGL((route_rows_kernel<FDT, DF, KM_>), grid, dim3(kRouteRows), lds, stream, \
+                       f, fsb, fst, fsh, protos, Tq, static_cast<int>(H), NB,                \
+                       static_cast<int>(bs), ke, causal, score_pos0, query_pos0, scale,      \
+                       chunk, topk, scores, sel, n_sel, cap)
+    if (ke <= 8) SPARDA_ROUTE(8);
+    else if (ke <= 16) SPARDA_ROUTE(16);
+    else SPARDA_ROUTE(32);
+#undef SPARDA_ROUTE
+    return check_hip(hipGetLastError(), "route_rows_kernel");
+}
+
+int launch_route(const void* f, int fdtype, int64_t fsb, int64_t fst, int64_t fsh,
+                 const float* protos, int64_t B, int64_t Tq, int64_t H, int64_t Df, int64_t NB,
+                 int64_t bs, int ke, int causal, int64_t score_pos0, int64_t query_pos0,
+                 float scale, int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel,
+                 int cap, hipStream_t stream) {
+#define SPARDA_DF(FDT_, DF_)                                                                   \
+    return launch_route_df<FDT_, DF_>(f, fsb, fst, fsh, protos, B, Tq, H, NB, bs, ke, causal,  \
+                                      score_pos0, query_pos0, scale, topk, scores, sel, n_sel, \
+                                      cap, stream)
+    if (fdtype == SPARDA_F32) {
+        switch (Df) {
+            case 16: SPARDA_DF(SPARDA_F32, 16);
+            case 32: SPARDA_DF(SPARDA_F32, 32);
+            case 64: SPARDA_DF(SPARDA_F32, 64);
+            case 128: SPARDA_DF(SPARDA_F32, 128);
+        }
+    } else {
+        switch (Df) {
+            case 16: SPARDA_DF(SPARDA_BF16, 16);
+            case 32: SPARDA_DF(SPARDA_BF16, 32);
+            case 64: SPARDA_DF(SPARDA_BF16, 64);
+            case 128: SPARDA_DF(SPARDA_BF16, 128);
+        }
+    }
+#undef SPARDA_DF
+    return set_error(SPARDA_ERR_SHAPE, "route: forecast dim %lld not in {16,32,64,128}",
+                     static_cast<long long>(Df));
+}
+
+// one workgroup per row; ranks of the row staged in LDS
+constexpr int kWaveTopkThreads = 256;
+
+__global__ void __launch_bounds__(kWaveTopkThreads)
+topk_wave_kernel(const float* __restrict__ scores, int64_t NB, int ke, int32_t* __restrict__ topk) {
+    extern __shared__ uint64_t ranks[];
+    __shared__ uint64_t wave_best[kWaveTopkThreads / kWave];
+    __shared__ int32_t picks[64];
+    const int64_t row = blockIdx.x;
+    const float* s = scores + row * NB;
+    for (int j = threadIdx.x; j < NB; j += blockDim.x) ranks[j] = rank64(s[j], j);
+    __syncthreads();
+    wg_topk(ranks, static_cast<int>(NB), ke, picks, wave_best);
+    for (int i = threadIdx.x; i < ke; i += blockDim.x) topk[row * ke + i] = picks[i];
+}
+
+// one lane per row (scores read from global)
+template <int KMAX>
+__global__ void __launch_bounds__(64)
+topk_rows_kernel(const float* __restrict__ scores, int64_t rows, int64_t NB, int ke,
+                 int32_t* __restrict__ topk) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (row >= rows) return;
+    const float* s = scores + row * NB;
+    LaneTopK<KMAX> best;
+    best.init(ke);
+    for (int64_t j = 0; j < NB; ++j) best.push(rank64(s[j], static_cast<int32_t>(j)));
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i)
+        if (i < ke) topk[row * ke + i] = rank64_index(best.r[i]);
+}
+
+int launch_topk_scores(const float* scores, int64_t rows, int64_t NB, int ke, int algo,
+                       int32_t* topk, hipStream_t stream) {
+    if (algo == SPARDA_TOPK_AUTO) algo = (rows < 2048 && NB >= 128 && NB <= 4096) ? SPARDA_TOPK_WAVE : SPARDA_TOPK_ROWS;
+    if (algo == SPARDA_TOPK_WAVE) {
+        hipLaunchKernelGGL(topk_wave_kernel, dim3(static_cast<unsigned>(rows)), dim3(kWaveTopkThreads),
+                           static_cast<size_t>(NB) * sizeof(uint64_t), stream, scores, NB, ke, topk);
+        return check_hip(hipGetLastError(), "topk_wave_kernel");
+    }
+    dim3 grid(static_cast<unsigned>(cdiv(rows, 64)));
+    if (ke <= 8)
+        hipLaunchKernelGGL((topk_rows_kernel<8>), grid, dim3(64), 0, stream, scores, rows, NB, ke, topk);
+    else if (ke <= 16)
+        hipLaunchKernelGGL((topk_rows_kernel<16>), grid, dim3(64), 0, stream, scores, rows, NB, ke, topk);
+    else
+        hipLaunchKernelGGL((topk_rows_kernel<32>), grid, dim3(64), 0, stream, scores, rows, NB, ke, topk);
+    return check_hip(hipGetLastError(), "topk_rows_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// forecast-free selection lists, one thread per (b,h,t) row
+// ---------------------------------------------------------------------------
+__global__ void select_fixed_kernel(int mode, int64_t rows, int64_t Tq, int64_t NB, int bs, int k,
+                                    int64_t query_pos0, int32_t* __restrict__ sel,
+                                    int32_t* __restrict__ n_sel, int cap) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const int64_t t = row % Tq;
+    int64_t own = (query_pos0 + t) / bs;
+    if (own > NB - 1) own = NB - 1;
+    int32_t* out = sel + row * cap;
+    int m = 0;
+    if (mode == SPARDA_SEL_DENSE) {
+        for (int64_t j = 0; j <= own; ++j) out[m++] = static_cast<int32_t>(j);
+    } else {
+        const int64_t width = (mode == SPARDA_SEL_WINDOW_DECODE) ? k : k + 1;
+        int64_t lo = own - width + 1;
+        if (lo < 0) lo = 0;
+        if (lo > 0) out[m++] = 0;
+        for (int64_t j = lo; j <= own; ++j) out[m++] = static_cast<int32_t>(j);
+    }
+    for (int i = m; i < cap; ++i) out[i] = -1;
+    n_sel[row] = m;
+}
+
+int launch_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H, int64_t NB, int64_t bs, int64_t k,
+                        int64_t query_pos0, int32_t* sel, int32_t* n_sel, int cap, hipStream_t stream) {
+    const int64_t rows = B * H * Tq;
+    hipLaunchKernelGGL(select_fixed_kernel, dim3(static_cast<unsigned>(cdiv(rows, 256))), dim3(256), 0,
+                       stream, mode, rows, Tq, NB, static_cast<int>(bs), static_cast<int>(k), query_pos0,
+                       sel, n_sel, cap);
+    return check_hip(hipGetLastError(), "select_fixed_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// gather: grid (n, H, B); each workgroup copies one block of K and of V
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ void gather_kernel(const void* __restrict__ k, const void* __restrict__ v, int64_t sb,
+                              int64_t sh, int64_t ss, const int32_t* __restrict__ idx, int64_t S,
+                              int D, int64_t n, int bs, void* __restrict__ ko, void* __restrict__ vo) {
+    const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int H = gridDim.y;
+    const int64_t j = idx[(static_cast<int64_t>(b) * H + h) * n + i];
+    const int64_t obase = ((static_cast<int64_t>(b) * H + h) * n + i) * bs * D;
+    for (int e = threadIdx.x; e < bs * D; e += blockDim.x) {
+        const int r = e / D, d = e % D;
+        const int64_t s = j * bs + r;
+        float kv = 0.0f, vv = 0.0f;
+        if (j >= 0 && s < S) {
+            const int64_t src = b * sb + h * sh + s * ss + d;
+            kv = load_elem<DT>(k, src);
+            vv = load_elem<DT>(v, src);
+        }
+        store_elem<DT>(ko, obase + e, kv);
+        store_elem<DT>(vo, obase + e, vv);
+    }
+}
+
+int launch_gather(const void* k, const void* v, int dtype, int64_t sb, int64_t sh, int64_t ss,
+                  const int32_t* idx, int64_t B, int64_t H, int64_t S, int64_t D, int64_t n,
+                  int64_t bs, void* ko, void* vo, hipStream_t stream) {
+    dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>(H), static_cast<unsigned>(B));
+    if (dtype == SPARDA_F32)
+        hipLaunchKernelGGL((gather_kernel<SPARDA_F32>), grid, dim3(256), 0, stream, k, v, sb, sh, ss, idx,
+                           S, static_cast<int>(D), n, static_cast<int>(bs), ko, vo);
+    else
+        hipLaunchKernelGGL((gather_kernel<SPARDA_BF16>), grid, dim3(256), 0, stream, k, v, sb, sh, ss, idx,
+                           S, static_cast<int>(D), n, static_cast<int>(bs), ko, vo);
+    return check_hip(hipGetLastError(), "gather_kernel");
+}
+
+}  // namespace sparda

@@ -1,0 +1,103 @@
+// Device-side selection helpers shared by the router and the decode step:
+// per-lane top-k insertion lists, workgroup top-k, selection-list emission.
+#pragma once
+
+#include "common.h"
+
+namespace sparda {
+
+// ---------------------------------------------------------------------------
+// per-lane top-k list: ranks sorted descending in registers. Slots >= ke hold
+// UINT64_MAX so an inserted rank can never displace them; the rank falling off
+// slot ke-1 is carried out and dropped.
+// ---------------------------------------------------------------------------
+template <int KMAX>
+struct LaneTopK {
+    uint64_t r[KMAX];
+    uint64_t thr;  // rank at slot ke-1 (0 while the list is not full)
+    int ke;
+
+    __device__ __forceinline__ void init(int ke_) {
+        ke = ke_;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) r[i] = i < ke ? 0ull : ~0ull;
+        thr = 0;
+    }
+    __device__ __forceinline__ void push(uint64_t x) {
+        if (x > thr) {
+#pragma unroll
+            for (int i = 0; i < KMAX; ++i) {
+                const uint64_t cur = r[i];
+                const bool sw = x > cur;
+                r[i] = sw ? x : cur;
+                x = sw ? cur : x;
+            }
+            uint64_t t = 0;
+#pragma unroll
+            for (int i = 0; i < KMAX; ++i) t = (i == ke - 1) ? r[i] : t;
+            thr = t;
+        }
+    }
+};
+
+// Sorted, de-duplicated selection list ({0, own} U picks, restricted to <= own
+// when causal) written to sel[0..cap), count to *n_out.
+template <int N>
+__device__ __forceinline__ void emit_selection(int32_t (&c)[N], int own, bool causal,
+                                               int32_t* __restrict__ sel, int cap,
+                                               int32_t* __restrict__ n_out) {
+    constexpr int32_t kNone = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (c[i] < 0 || (causal && c[i] > own)) c[i] = kNone;
+    // odd-even transposition sort, ascending
+#pragma unroll
+    for (int pass = 0; pass < N; ++pass) {
+#pragma unroll
+        for (int i = pass & 1; i + 1 < N; i += 2) {
+            const int32_t a = c[i], bb = c[i + 1];
+            c[i] = a < bb ? a : bb;
+            c[i + 1] = a < bb ? bb : a;
+        }
+    }
+    int m = 0;
+    int32_t last = -1;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (c[i] != kNone && c[i] != last) {
+            sel[m] = c[i];
+            ++m;
+            last = c[i];
+        }
+    }
+    for (int i = m; i < cap; ++i) sel[i] = -1;
+    *n_out = m;
+}
+
+// ---------------------------------------------------------------------------
+// workgroup-level top-k over `n` ranks held in LDS (consumed: taken entries
+// are zeroed). ke rounds of workgroup arg-max built on wavefront reductions.
+// All threads of the workgroup must call it.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void wg_topk(uint64_t* ranks, int n, int ke, int32_t* out_lds, uint64_t* wave_best) {
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int nwaves = (blockDim.x + kWave - 1) / kWave;
+    for (int i = 0; i < ke; ++i) {
+        uint64_t m = 0;
+        for (int j = threadIdx.x; j < n; j += blockDim.x) m = ranks[j] > m ? ranks[j] : m;
+        m = wave_max_u64(m);
+        if (lane == 0) wave_best[wave] = m;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t w = 0;
+            for (int q = 0; q < nwaves; ++q) w = wave_best[q] > w ? wave_best[q] : w;
+            const int32_t idx = rank64_index(w);
+            out_lds[i] = idx;
+            ranks[idx] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace sparda

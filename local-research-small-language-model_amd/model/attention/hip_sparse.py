@@ -1,0 +1,106 @@
+"""HIP sparse GQA attention backend — drop-in for SparseAttention
+(model/attention/sparse.py:65-439), with the block gather of
+gather_kv_blocks (model/attention/sparse.py:19-62).
+
+Prefill: compressor -> fused router -> block-sparse prefill kernel (bf16
+MFMA for D = 64, bs = 64; general kernel otherwise). The per-token allowed
+set is the reference's masked-SDPA rule (sparse.py:226-281) at every length;
+the reference's chunked path for T > 8192 (sparse.py:284-364, different
+routing semantics) is not reproduced.
+
+Decode (T == 1 with a KVCache): one libsparda call — whole-cache
+compression, routing, split-K attention over the selected blocks, combine.
+"""
+
+from typing import Optional, Tuple
+
+import torch
+
+import sparda
+from model.attention.base import BaseAttention, KVCache
+from model.config import ModelConfig
+from model.forecast import ForecastBlockSelector, KVBlockCompressor
+from model.rope import RotaryEmbedding
+
+
+def gather_kv_blocks(k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                     block_size: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """k, v [B,Hkv,S,D], block_indices [B,Hkv,n] -> [B,Hkv,n*bs,D]; tokens past S are zero."""
+    return sparda.gather_blocks(k, v, block_indices, block_size)
+
+
+class HipSparseAttention(BaseAttention):
+    """Forecast-guided (or static window) block-sparse GQA on libsparda."""
+
+    def __init__(self, config: ModelConfig, layer_idx: int, mode: Optional[str] = None):
+        super().__init__(config, layer_idx)
+        self.block_size = config.block_size
+        self.top_k_blocks = config.top_k_blocks
+        if mode is not None:
+            self.mode = mode
+        elif config.attention_backend in ("static_sparse", "static"):
+            self.mode = "static"
+        elif getattr(config, "sparse_mode", "forecast") == "static":
+            self.mode = "static"
+        else:
+            self.mode = "forecast"
+        if self.mode not in ("forecast", "static"):
+            raise ValueError(f"unknown sparse mode {self.mode!r}")
+        self.decode_routing = getattr(config, "decode_routing", "reference")
+        # parameter-free, kept for interface parity with the reference module
+        self.compressor = KVBlockCompressor(self.block_size, self.head_dim, config.forecast_dim)
+        self.selector = ForecastBlockSelector(self.block_size, config.forecast_dim)
+        self._ws = None
+
+    # -- decode ------------------------------------------------------------
+    def _decode(self, xq: torch.Tensor, cache: KVCache, forecast_vector: Optional[torch.Tensor]):
+        B = xq.shape[0]
+        if self._ws is None or self._ws.device != xq.device:
+            self._ws = sparda.DecodeWorkspace(xq.device)
+        f = forecast_vector if (self.mode == "forecast" and forecast_vector is not None) else None
+        if f is not None:
+            f = f.reshape(B, self.n_kv_head, -1)
+        out = sparda.decode(xq[:, 0], cache.k, cache.v, cache.current_len, f, self.block_size,
+                            self.top_k_blocks, routing=self.decode_routing, workspace=self._ws)
+        return self.wo(out.view(B, 1, self.n_head * self.head_dim))
+
+    # -- prefill -----------------------------------------------------------
+    def _prefill(self, xq, xk, xv, forecast_vector, is_causal):
+        B, T = xq.shape[:2]
+        nb = (T + self.block_size - 1) // self.block_size
+        dense = nb <= 2 or (self.mode == "forecast" and (forecast_vector is None or self.layer_idx == 0))
+        if dense:
+            sel = n_sel = None
+        elif self.mode == "forecast":
+            protos = sparda.compress(xk, self.block_size)
+            _, _, sel, n_sel = sparda.route(forecast_vector, protos, self.block_size, self.top_k_blocks,
+                                            causal=is_causal, want_topk=False, want_sel=True)
+        else:
+            sel, n_sel = sparda.select_fixed(sparda.SEL_WINDOW_PREFILL, B, T, self.n_kv_head, nb,
+                                             self.block_size, self.top_k_blocks, 0, device=xq.device)
+            if not is_causal:
+                raise NotImplementedError("static sparse prefill is causal only in the HIP backend")
+        out = sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=is_causal)
+        return self.wo(out)
+
+    def forward(self, x: torch.Tensor, rotary_emb: RotaryEmbedding, kv_cache: Optional[KVCache] = None,
+                mask: Optional[torch.Tensor] = None, is_causal: bool = True,
+                forecast_vector: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
+        if mask is not None:
+            raise NotImplementedError("explicit additive masks are not supported by the HIP backend")
+        if kwargs.get("return_attn_weights", False):
+            raise NotImplementedError("return_attn_weights is not available from the HIP backend")
+        B, T, _ = x.shape
+        xq = self.wq(x).view(B, T, self.n_head, self.head_dim)
+        xk = self.wk(x).view(B, T, self.n_kv_head, self.head_dim)
+        xv = self.wv(x).view(B, T, self.n_kv_head, self.head_dim)
+        offset = kv_cache.current_len if kv_cache is not None else 0
+        xq, xk = rotary_emb(xq, xk, offset=offset)
+        if kv_cache is not None and T == 1:
+            kv_cache.update(xk, xv)
+            return self._decode(xq, kv_cache, forecast_vector)
+        if kv_cache is not None:
+            if kv_cache.current_len != 0:
+                raise NotImplementedError("prefill into a non-empty cache is not supported")
+            kv_cache.update(xk, xv)
+        return self._prefill(xq, xk, xv, forecast_vector, is_causal)

@@ -1,0 +1,101 @@
+"""ctypes binding of libsparda.so (the C ABI declared in include/sparda.h).
+
+The library must have been built (``sparda.build.build()``); loading fails
+loudly otherwise — there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsparda.so")
+
+F32 = 0
+BF16 = 1
+
+ROUTE_REFERENCE = 0
+ROUTE_ABSOLUTE = 1
+
+SEL_DENSE = 0
+SEL_WINDOW_DECODE = 1
+SEL_WINDOW_PREFILL = 2
+
+TOPK_AUTO = 0
+TOPK_ROWS = 1
+TOPK_WAVE = 2
+
+ERR_NAMES = {
+    -1: "null pointer", -2: "shape", -3: "dtype", -4: "workspace", -5: "stride",
+    -6: "mode", -7: "handle", -8: "capacity",
+}
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_p = ctypes.c_void_p
+_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/sparda.h
+SIGNATURES = {
+    "sparda_version": (_int, []),
+    "sparda_last_error": (ctypes.c_char_p, []),
+    "sparda_compress": (_int, [_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
+    "sparda_route": (_int, [_p, _int, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _int, _i64, _i64, _f32, _p, _p, _p, _p, _i64, _p]),
+    "sparda_topk_scores": (_int, [_p, _i64, _i64, _i64, _int, _p, _p]),
+    "sparda_select_fixed": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p]),
+    "sparda_gather_blocks": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64,
+                                    _i64, _p, _p, _p]),
+    "sparda_prefill": (_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _p, _i64, _i64,
+                              _i64, _i64, _i64, _i64, _i64, _int, _f32, _p, _i64, _i64, _p]),
+    "sparda_decode_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "sparda_decode": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _i64,
+                             _i64, _i64, _i64, _i64, _i64, _i64, _int, _f32, _p, _p, _p, _p, _p, _i64,
+                             _p, _size, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class SpardaError(RuntimeError):
+    """A non-zero status from libsparda."""
+
+    def __init__(self, func: str, code: int, message: str):
+        kind = ERR_NAMES.get(code, "hip error" if code > 0 else "error")
+        super().__init__(f"{func} failed ({kind}, status {code}): {message}")
+        self.code = code
+
+
+class SpardaArgumentError(SpardaError, ValueError):
+    """Argument rejected by the library before any HIP call."""
+
+
+def load() -> ctypes.CDLL:
+    """Load libsparda.so once; raise if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"libsparda.so not found at {LIB_PATH}: build it with "
+                    "`python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and turn a non-zero status into an exception."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = (lib.sparda_last_error() or b"").decode(errors="replace")
+        cls = SpardaArgumentError if rc < 0 else SpardaError
+        raise cls(name, rc, msg)

@@ -1,0 +1,291 @@
+"""Tensor-level wrappers over libsparda's C ABI.
+
+PyTorch provides device memory and the current HIP stream; every computation
+runs in libsparda's HIP kernels. Tensors must live on a GPU device: a CPU
+tensor raises instead of falling back to another implementation.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"sparda: unsupported dtype {t.dtype} (float32 or bfloat16)") from None
+
+
+def require_device(*tensors: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"sparda: expected a tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"sparda: HIP kernels need tensors on a GPU device, got a {t.device.type} tensor "
+                "(there is no CPU implementation)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"sparda: tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def _inference_only(*tensors: Optional[torch.Tensor]) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise RuntimeError("sparda: the HIP sparse attention path is inference-only; "
+                           "run it under torch.no_grad() / torch.inference_mode()")
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _rowmajor(t: torch.Tensor) -> torch.Tensor:
+    """Innermost stride 1 (other strides arbitrary)."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def default_scale(dim: int) -> float:
+    return 1.0 / math.sqrt(dim)
+
+
+# ---------------------------------------------------------------------------
+# compressor / router
+# ---------------------------------------------------------------------------
+
+def compress(k: torch.Tensor, block_size: int) -> torch.Tensor:
+    """k [B,S,H,D] (fp32/bf16) -> prototypes [B,NB,H,D] fp32 (model/forecast.py:57-78)."""
+    dev = require_device(k)
+    _inference_only(k)
+    k = _rowmajor(k)
+    B, S, H, D = k.shape
+    NB = (S + block_size - 1) // block_size
+    out = torch.empty((B, NB, H, D), dtype=torch.float32, device=dev)
+    sb, ss, sh, _ = k.stride()
+    call("sparda_compress", k.data_ptr(), _dtype_code(k), B, S, H, D, sb, ss, sh, block_size,
+         out.data_ptr(), _stream(dev))
+    return out
+
+
+def route(forecast: torch.Tensor, protos: torch.Tensor, block_size: int, top_k: int,
+          causal: bool = True, score_pos0: int = 0, query_pos0: int = 0,
+          scale: Optional[float] = None, want_topk: bool = True, want_scores: bool = False,
+          want_sel: bool = False, sel_cap: Optional[int] = None):
+    """Fused score + top-k router (model/forecast.py:89-130).
+
+    forecast [B,Tq,H,Df], protos [B,NB,H,Df] fp32.
+    Returns (topk int32 [B,H,Tq,ke] | None, scores fp32 [B,H,Tq,NB] | None,
+    sel int32 [B,H,Tq,cap] | None, n_sel int32 [B,H,Tq] | None).
+    """
+    dev = require_device(forecast, protos)
+    _inference_only(forecast)
+    forecast = _rowmajor(forecast)
+    if protos.dtype != torch.float32 or not protos.is_contiguous():
+        protos = protos.float().contiguous()
+    B, Tq, H, Df = forecast.shape
+    if protos.shape[0] != B or protos.shape[2] != H or protos.shape[3] != Df:
+        raise AssertionError(f"Mismatch: forecast {tuple(forecast.shape)} vs prototypes {tuple(protos.shape)}")
+    NB = protos.shape[1]
+    ke = min(top_k, NB)
+    if scale is None:
+        scale = default_scale(Df)
+    topk = torch.empty((B, H, Tq, ke), dtype=torch.int32, device=dev) if want_topk else None
+    scores = torch.empty((B, H, Tq, NB), dtype=torch.float32, device=dev) if want_scores else None
+    sel = n_sel = None
+    if want_sel:
+        cap = sel_cap if sel_cap is not None else ke + 2
+        sel = torch.empty((B, H, Tq, cap), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, H, Tq), dtype=torch.int32, device=dev)
+    else:
+        cap = 0
+    fsb, fst, fsh, _ = forecast.stride()
+    call("sparda_route", forecast.data_ptr(), _dtype_code(forecast), fsb, fst, fsh, protos.data_ptr(),
+         B, Tq, H, Df, NB, block_size, top_k, int(causal), score_pos0, query_pos0, float(scale),
+         topk.data_ptr() if topk is not None else None,
+         scores.data_ptr() if scores is not None else None,
+         sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap, _stream(dev))
+    return topk, scores, sel, n_sel
+
+
+def topk_scores(scores: torch.Tensor, top_k: int, algo: int = _lib.TOPK_AUTO) -> torch.Tensor:
+    """Canonical top-k (score desc, lower index on ties) over the last axis of fp32 scores."""
+    dev = require_device(scores)
+    s = scores.float().contiguous()
+    NB = s.shape[-1]
+    rows = s.numel() // NB
+    ke = min(top_k, NB)
+    out = torch.empty(s.shape[:-1] + (ke,), dtype=torch.int32, device=dev)
+    call("sparda_topk_scores", s.data_ptr(), rows, NB, top_k, algo, out.data_ptr(), _stream(dev))
+    return out
+
+
+def select_fixed(mode: int, B: int, Tq: int, H: int, NB: int, block_size: int, top_k: int,
+                 query_pos0: int = 0, device=None, sel_cap: Optional[int] = None):
+    """Forecast-free selection lists (dense / static windows)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    if dev.type != "cuda":
+        raise RuntimeError("sparda: select_fixed needs a GPU device")
+    if sel_cap is None:
+        if mode == _lib.SEL_DENSE:
+            sel_cap = min((query_pos0 + Tq - 1) // block_size, NB - 1) + 1
+        else:
+            sel_cap = top_k + 2
+    sel = torch.empty((B, H, Tq, sel_cap), dtype=torch.int32, device=dev)
+    n_sel = torch.empty((B, H, Tq), dtype=torch.int32, device=dev)
+    call("sparda_select_fixed", mode, B, Tq, H, NB, block_size, top_k, query_pos0, sel.data_ptr(),
+         n_sel.data_ptr(), sel_cap, _stream(dev))
+    return sel, n_sel
+
+
+def gather_blocks(k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                  block_size: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """k, v [B,H,S,D]; block_indices [B,H,n] -> [B,H,n*bs,D] (model/attention/sparse.py:19-62)."""
+    dev = require_device(k, v, block_indices)
+    _inference_only(k, v)
+    if k.dtype != v.dtype or k.shape != v.shape:
+        raise ValueError("sparda: k and v must share shape and dtype")
+    k = _rowmajor(k)
+    v = _rowmajor(v)
+    if k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    B, H, S, D = k.shape
+    n = block_indices.shape[-1]
+    idx = block_indices.to(torch.int32).contiguous()
+    ko = torch.empty((B, H, n * block_size, D), dtype=k.dtype, device=dev)
+    vo = torch.empty_like(ko)
+    sb, sh, ss, _ = k.stride()
+    call("sparda_gather_blocks", k.data_ptr(), v.data_ptr(), _dtype_code(k), sb, sh, ss, idx.data_ptr(),
+         B, H, S, D, n, block_size, ko.data_ptr(), vo.data_ptr(), _stream(dev))
+    return ko, vo
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[torch.Tensor],
+            n_sel: Optional[torch.Tensor], block_size: int, causal: bool = True,
+            scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-sparse GQA prefill.
+
+    q [B,T,Hq,D], k/v [B,T,Hkv,D] (same dtype), sel/n_sel from ``route`` or
+    ``select_fixed`` ([B,Hkv,T,cap] / [B,Hkv,T]) or None for dense.
+    Returns out [B,T,Hq*D] in q's dtype.
+    """
+    dev = require_device(q, k, v, sel, n_sel)
+    _inference_only(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q, k, v must share a dtype")
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    if k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty((B, T, Hq * D), dtype=q.dtype, device=dev)
+    cap = 0
+    if sel is not None:
+        sel = sel.to(torch.int32).contiguous()
+        n_sel = n_sel.to(torch.int32).contiguous()
+        cap = sel.shape[-1]
+    qsb, qst, qsh, _ = q.stride()
+    ksb, kst, ksh, _ = k.stride()
+    osb, ost, _ = out.stride()
+    call("sparda_prefill", q.data_ptr(), qsb, qst, qsh, k.data_ptr(), v.data_ptr(), ksb, kst, ksh,
+         _dtype_code(q), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap, B, T, Hq, Hkv, D, block_size,
+         int(causal), float(scale), out.data_ptr(), osb, ost, _stream(dev))
+    return out
+
+
+class DecodeWorkspace:
+    """Zero-initialised device workspace for ``decode`` (reused across steps)."""
+
+    def __init__(self, device=None):
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self.buf: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+def decode_workspace_bytes(B: int, S: int, Hq: int, Hkv: int, D: int, block_size: int, top_k: int) -> int:
+    return int(_lib.load().sparda_decode_workspace_bytes(B, S, Hq, Hkv, D, block_size, top_k))
+
+
+def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, S: int,
+           forecast: Optional[torch.Tensor], block_size: int, top_k: int, routing: str = "reference",
+           scale: Optional[float] = None, workspace: Optional[DecodeWorkspace] = None,
+           protos_in: Optional[torch.Tensor] = None, want_protos: bool = False,
+           want_sel: bool = False, out: Optional[torch.Tensor] = None):
+    """One decode step (model/attention/sparse.py:99-183 after the projections).
+
+    q [B,Hq,D] at position S-1; caches [B,Smax,Hkv,D] with tokens [0,S) valid;
+    forecast [B,Hkv,Df] or None; routing "reference" | "absolute".
+    Returns out [B,Hq*D], or (out, extras) when want_protos / want_sel.
+    """
+    dev = require_device(q, k_cache, v_cache, forecast, protos_in)
+    _inference_only(q, k_cache, v_cache)
+    if not (q.dtype == k_cache.dtype == v_cache.dtype):
+        raise TypeError("sparda: q and the caches must share a dtype")
+    q, k_cache, v_cache = _rowmajor(q), _rowmajor(k_cache), _rowmajor(v_cache)
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("sparda: k_cache and v_cache must share strides")
+    B, Hq, D = q.shape
+    Hkv = k_cache.shape[2]
+    if S > k_cache.shape[1] or S <= 0:
+        raise ValueError(f"sparda: S={S} outside the cache (capacity {k_cache.shape[1]})")
+    if routing not in ("reference", "absolute"):
+        raise ValueError(f"sparda: routing must be 'reference' or 'absolute', got {routing!r}")
+    if scale is None:
+        scale = default_scale(D)
+    NB = (S + block_size - 1) // block_size
+    if forecast is not None:
+        forecast = _rowmajor(forecast.reshape(B, Hkv, -1) if forecast.dim() != 3 else forecast)
+    if out is None:
+        out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
+    nbytes = decode_workspace_bytes(B, S, Hq, Hkv, D, block_size, top_k)
+    ws = (workspace or DecodeWorkspace(dev)).get(nbytes)
+    protos_out = torch.empty((B, NB, Hkv, D), dtype=torch.float32, device=dev) if want_protos else None
+    sel = n_sel = None
+    if want_sel:
+        sel = torch.empty((B, Hkv, top_k + 2), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, Hkv), dtype=torch.int32, device=dev)
+    if protos_in is not None:
+        protos_in = protos_in.float().contiguous()
+    qsb, qsh, _ = q.stride()
+    ksb, kss, ksh, _ = k_cache.stride()
+    fsb = fsh = 0
+    fdt = _lib.F32
+    if forecast is not None:
+        fsb, fsh, _ = forecast.stride()
+        fdt = _dtype_code(forecast)
+    call("sparda_decode", q.data_ptr(), qsb, qsh, k_cache.data_ptr(), v_cache.data_ptr(), ksb, kss, ksh,
+         _dtype_code(q), forecast.data_ptr() if forecast is not None else None, fdt, fsb, fsh,
+         B, S, Hq, Hkv, D, block_size, top_k,
+         _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE, float(scale),
+         protos_in.data_ptr() if protos_in is not None else None,
+         protos_out.data_ptr() if protos_out is not None else None,
+         sel.data_ptr() if sel is not None else None, n_sel.data_ptr() if n_sel is not None else None,
+         out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(dev))
+    if want_protos or want_sel:
+        return out, {"protos": protos_out, "sel": sel, "n_sel": n_sel}
+    return out

@@ -1,0 +1,72 @@
+"""C-ABI library checks that need no GPU: it loads, exports exactly what
+include/sparda.h declares, and rejects bad arguments before any HIP call."""
+
+import os
+import re
+
+import pytest
+
+import sparda
+from sparda import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sparda.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"SPARDA_API\s+[\w\s\*]+?\b(sparda_\w+)\s*\(", text)))
+
+
+def test_library_loads_and_reports_version():
+    lib = sparda.load()
+    assert lib.sparda_version() == 100
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = sparda.load()
+    syms = header_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in sparda.h but not exported"
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+
+
+def _expect(code, name, *args):
+    with pytest.raises(sparda.SpardaArgumentError) as ei:
+        _lib.call(name, *args)
+    assert ei.value.code == code
+    assert sparda.load().sparda_last_error()
+
+
+def test_argument_errors_are_reported_before_any_hip_call():
+    P = 4096  # any non-null value: validation fails before it is dereferenced
+    _expect(-1, "sparda_compress", None, 0, 1, 1, 1, 1, 1, 1, 1, 1, P, None)
+    _expect(-3, "sparda_compress", P, 7, 1, 1, 1, 1, 1, 1, 1, 1, P, None)
+    _expect(-2, "sparda_compress", P, 1, 1, 0, 1, 1, 1, 1, 1, 1, P, None)
+    _expect(-2, "sparda_route", P, 1, 1, 1, 1, P, 1, 1, 1, 48, 4, 8, 8, 1, 0, 0, 0.125, P, None, None, None, 0,
+            None)  # Df=48 unsupported
+    _expect(-2, "sparda_route", P, 1, 1, 1, 1, P, 1, 1, 1, 64, 4, 8, 33, 1, 0, 0, 0.125, P, None, None, None,
+            0, None)  # top_k > 32
+    _expect(-2, "sparda_route", P, 1, 1, 1, 1, P, 1, 1, 1, 64, 16, 8, 8, 1, 0, 0, 0.125, None, None, P, P, 9,
+            None)  # sel_cap < k+2
+    _expect(-6, "sparda_topk_scores", P, 1, 8, 2, 9, P, None)
+    _expect(-6, "sparda_select_fixed", 7, 1, 1, 1, 1, 1, 1, 0, P, P, 4, None)
+    _expect(-2, "sparda_prefill", P, 1, 1, 1, P, P, 1, 1, 1, 1, None, None, 0, 1, 16, 12, 5, 64, 64, 1, 0.125,
+            P, 1, 1, None)  # Hq not a multiple of Hkv
+    _expect(-4, "sparda_decode", P, 1, 1, P, P, 1, 1, 1, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
+            None, None, None, None, P, 1, None, 0, None)  # no workspace
+    _expect(-4, "sparda_decode", P, 1, 1, P, P, 1, 1, 1, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
+            None, None, None, None, P, 1, P * 2, 16, None)  # workspace too small
+    _expect(-6, "sparda_decode", P, 1, 1, P, P, 1, 1, 1, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 5, 0.125,
+            None, None, None, None, P, 1, P * 2, 1 << 20, None)  # unknown routing
+
+
+def test_decode_workspace_size_formula():
+    # counters | scores | sel | n_sel | partials, each rounded up to 256 B
+    up = lambda x: (x + 255) // 256 * 256
+    B, S, Hq, Hkv, D, bs, k = 8, 16384, 12, 4, 64, 64, 8
+    NB = S // bs
+    want = (up((B + B * Hkv) * 4) + up(B * Hkv * NB * 4) + up(B * Hkv * (k + 2) * 4) + up(B * Hkv * 4)
+            + up(B * Hq * (k + 2) * (D + 2) * 4))
+    assert sparda.decode_workspace_bytes(B, S, Hq, Hkv, D, bs, k) == want

@@ -1,0 +1,293 @@
+"""GPU parity of libsparda's kernels against the CPU oracle.
+
+Integer/index outputs (prototypes, scores, top-k, selection lists) are
+compared bit-exactly; attention outputs within max-abs 2e-2 / mean-abs 2e-3
+(bf16) or max-abs 1e-4 (fp32).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import sparda
+from sparda import synth
+from oracle import sparda_oracle as O
+from helpers import assert_close_out, np32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+# ---------------------------------------------------------------------------
+# compressor
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,S,H,D,bs,dtype", [
+    (4, 4096, 4, 64, 64, torch.bfloat16),   # prefill workload (B=4, T=4096)
+    (1, 1024, 4, 64, 64, torch.float32),    # fp32 layer at T=1024
+    (2, 50, 4, 32, 16, torch.float32),      # tests/test_forecast.py:64-68 padding case
+    (3, 1000, 2, 16, 48, torch.bfloat16),   # ragged tail, odd block size
+    (8, 16384, 4, 64, 64, torch.bfloat16),  # decode cache at 16K
+])
+def test_compress_bit_exact(B, S, H, D, bs, dtype):
+    case(f"compress B={B} S={S} H={H} D={D} bs={bs} {dtype}")
+    k = torch.randn(B, S, H, D, generator=torch.Generator().manual_seed(S)).to(dtype)
+    got = sparda.compress(k.to(DEV), bs).cpu().numpy()
+    want = O.compress(np32(k), bs)
+    assert got.shape == want.shape
+    assert np.array_equal(got, want)
+
+
+def test_compress_strided_view():
+    case("compress strided view")
+    big = torch.randn(2, 300, 6, 64, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16)
+    view = big[:, :, 1:5, :]  # stride_h = 64, stride_s = 384
+    got = sparda.compress(big.to(DEV)[:, :, 1:5, :], 64).cpu().numpy()
+    assert np.array_equal(got, O.compress(np32(view), 64))
+
+
+# ---------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,Tq,H,Df,bs,k,fdtype,causal,pos0", [
+    (1, 1024, 4, 64, 64, 8, torch.float32, True, 0),     # fp32 layer at T=1024 (NB=16)
+    (4, 4096, 4, 64, 64, 8, torch.bfloat16, True, 0),    # prefill workload (NB=64)
+    (2, 333, 2, 32, 16, 2, torch.float32, True, 0),      # reference test geometry, ragged
+    (2, 256, 4, 64, 64, 8, torch.bfloat16, False, 0),    # non-causal selector
+    (1, 3, 4, 64, 64, 8, torch.float32, True, 16383),    # decode rows at the end of a 16K cache
+    (1, 2048, 2, 128, 32, 16, torch.bfloat16, True, 0),  # k=16, Df=128
+    (1, 512, 2, 16, 8, 32, torch.float32, True, 0),      # k=32, many blocks
+])
+def test_route_bit_exact(B, Tq, H, Df, bs, k, fdtype, causal, pos0):
+    case(f"route B={B} Tq={Tq} H={H} Df={Df} bs={bs} k={k} {fdtype} causal={causal} pos0={pos0}")
+    g = torch.Generator().manual_seed(Tq + k)
+    S = max(Tq, pos0 + Tq)
+    kk = torch.randn(B, S, H, Df, generator=g)
+    f = torch.randn(B, Tq, H, Df, generator=g).to(fdtype)
+    P = O.compress(kk.numpy(), bs)
+    topk, scores, sel, n = sparda.route(f.to(DEV), torch.from_numpy(P).to(DEV), bs, k, causal=causal,
+                                        score_pos0=pos0, query_pos0=pos0, want_topk=True, want_scores=True,
+                                        want_sel=True)
+    sc_o, tk_o, sel_o, n_o = O.route(np32(f), P, bs, k, causal, pos0, pos0)
+    assert np.array_equal(scores.cpu().numpy(), sc_o)
+    assert np.array_equal(topk.cpu().numpy(), tk_o)
+    assert np.array_equal(n.cpu().numpy(), n_o)
+    assert np.array_equal(sel.cpu().numpy(), sel_o)
+
+
+def test_route_ties_and_reference_decode_row():
+    case("route ties")
+    # all-equal prototypes -> every score ties; lower index must win
+    B, Tq, H, D, bs, k = 1, 700, 2, 64, 64, 8
+    P = np.ones((B, 11, H, D), np.float32)
+    f = torch.ones(B, Tq, H, D)
+    topk, _, sel, n = sparda.route(f.to(DEV), torch.from_numpy(P).to(DEV), bs, k, want_sel=True)
+    _, tk_o, sel_o, n_o = O.route(f.numpy(), P, bs, k)
+    assert np.array_equal(topk.cpu().numpy(), tk_o)
+    assert np.array_equal(sel.cpu().numpy(), sel_o)
+    assert topk[0, 0, 699].tolist() == list(range(8))
+
+
+def test_topk_identical_scores_both_algorithms():
+    case("topk on identical scores")
+    r = np.random.default_rng(3)
+    s = r.integers(-4, 4, size=(300, 256)).astype(np.float32)
+    s[r.random(s.shape) < 0.3] = -np.inf
+    s[:, 7] = -0.0
+    want = O.topk(s, 8)
+    for algo in (sparda.TOPK_ROWS, sparda.TOPK_WAVE):
+        got = sparda.topk_scores(torch.from_numpy(s).to(DEV), 8, algo).cpu().numpy()
+        assert np.array_equal(got, want), f"algo {algo}"
+
+
+def test_topk_on_reference_path_scores():
+    """Scores produced by the op-for-op reference restatement (torch matmul +
+    masked_fill) are fed unchanged to the GPU selection stage."""
+    case("topk on reference-path scores")
+    from oracle import reference_path as R
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(2, 4096, 4, 64, generator=g)
+    f = torch.randn(2, 4096, 4, 64, generator=g)
+    sc, tk_ref = R.select_blocks(f, R.block_means(k, 64), 64, 8)
+    sc = sc.contiguous()
+    want = O.topk(sc.numpy(), 8)
+    for algo in (sparda.TOPK_ROWS, sparda.TOPK_WAVE):
+        got = sparda.topk_scores(sc.to(DEV), 8, algo).cpu().numpy()
+        assert np.array_equal(got, want)
+    # where no tie is involved (at least k finite scores), torch.topk agrees too
+    fin = np.isfinite(sc.numpy()).sum(-1) >= 8
+    assert np.array_equal(want[fin], tk_ref.numpy()[fin])
+
+
+@pytest.mark.parametrize("mode,Tq,NB,bs,k,pos0", [
+    (sparda.SEL_DENSE, 1, 9, 64, 8, 520),
+    (sparda.SEL_WINDOW_DECODE, 1, 256, 64, 8, 16383),
+    (sparda.SEL_WINDOW_DECODE, 1, 256, 64, 8, 200),
+    (sparda.SEL_WINDOW_PREFILL, 1000, 16, 64, 8, 0),
+])
+def test_select_fixed(mode, Tq, NB, bs, k, pos0):
+    case(f"select_fixed mode={mode}")
+    cap = NB if mode == sparda.SEL_DENSE else k + 2
+    sel, n = sparda.select_fixed(mode, 2, Tq, 3, NB, bs, k, pos0, device=DEV, sel_cap=cap)
+    sel_o, n_o = O.sel_fixed(mode, 2, Tq, 3, NB, bs, k, pos0, cap=cap)
+    assert np.array_equal(n.cpu().numpy(), n_o)
+    assert np.array_equal(sel.cpu().numpy(), sel_o)
+
+
+def test_gather_reference_known_answer():
+    # tests/test_sparse_attention.py:33-60
+    case("gather")
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(2, 2, 48, 32, generator=g)
+    v = torch.randn(2, 2, 48, 32, generator=g)
+    idx = torch.tensor([[[0, 2], [1, 2]], [[2, 0], [0, 1]]])
+    kg, vg = sparda.gather_blocks(k.to(DEV), v.to(DEV), idx.to(DEV), 16)
+    assert kg.shape == (2, 2, 32, 32)
+    assert torch.equal(kg[0, 0, :16].cpu(), k[0, 0, :16])
+    assert torch.equal(kg[0, 0, 16:].cpu(), k[0, 0, 32:48])
+    ko, vo = O.gather_blocks(k.numpy(), v.numpy(), idx.numpy(), 16)
+    assert np.array_equal(kg.cpu().numpy(), ko) and np.array_equal(vg.cpu().numpy(), vo)
+    kb, _ = sparda.gather_blocks(k[:, :, :40].to(DEV).to(torch.bfloat16), v[:, :, :40].to(DEV).to(torch.bfloat16),
+                                 idx.to(DEV), 16)
+    assert not kb[0, 0, 24:].float().any()
+
+
+# ---------------------------------------------------------------------------
+# prefill attention
+# ---------------------------------------------------------------------------
+
+def _prefill_case(B, T, Hq, Hkv, D, bs, k, dtype, seed, causal=True, dense=False, rows=None):
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=dtype, seed=seed)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    if dense:
+        sel = n = None
+        sel_o = n_o = None
+    else:
+        protos = sparda.compress(d["k"], bs)
+        _, _, sel, n = sparda.route(d["forecast"], protos, bs, k, causal=causal, want_topk=False, want_sel=True)
+        _, _, sel_o, n_o = O.route(np32(x["forecast"]), O.compress(np32(x["k"]), bs), bs, k, causal)
+        assert np.array_equal(sel.cpu().numpy(), sel_o)
+    out = sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs, causal=causal)
+    torch.cuda.synchronize()
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, bs, causal, rows=rows)
+    got = np32(out)
+    mask = None
+    if rows is not None:
+        mask = np.zeros(got.shape, bool)
+        for b, t in rows:
+            mask[b, t] = True
+    return assert_close_out(got, want, dtype, mask)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_prefill_layer_t1024(dtype):
+    # single layer, B=1, T=1024, 12/4 heads, D=64, bs=64 (NB=16), k=8
+    case(f"prefill T=1024 {dtype}")
+    _prefill_case(1, 1024, 12, 4, 64, 64, 8, dtype, seed=1000)
+
+
+@pytest.mark.parametrize("R", [1, 2, 3, 4])
+def test_prefill_mfma_group_sizes_ragged(R):
+    case(f"prefill mfma R={R} T=1000")
+    _prefill_case(2, 1000, 4 * R, 4, 64, 64, 8, torch.bfloat16, seed=50 + R)
+
+
+def test_prefill_mfma_dense_and_noncausal():
+    case("prefill mfma dense + noncausal")
+    _prefill_case(1, 700, 12, 4, 64, 64, 8, torch.bfloat16, seed=61, dense=True)
+    _prefill_case(1, 700, 12, 4, 64, 64, 8, torch.bfloat16, seed=62, causal=False)
+    _prefill_case(1, 300, 12, 4, 64, 64, 8, torch.bfloat16, seed=63, causal=False, dense=True)
+
+
+def test_prefill_general_kernel_shapes():
+    # reference test geometry: 8 q heads / 2 kv heads, D=32, bs=16, k=2
+    case("prefill general D=32 bs=16")
+    _prefill_case(2, 64, 8, 2, 32, 16, 2, torch.float32, seed=70)
+    _prefill_case(1, 333, 8, 2, 32, 16, 2, torch.bfloat16, seed=71)
+    _prefill_case(1, 200, 4, 1, 128, 32, 3, torch.float32, seed=72)
+
+
+def test_prefill_full_size_sampled_rows():
+    # prefill workload: B=4, T=4096, 12/4 heads, D=64, bs=64 (NB=64), k=8, bf16
+    case("prefill B=4 T=4096 sampled")
+    r = np.random.default_rng(0)
+    rows = sorted({(int(b), int(t)) for b, t in zip(r.integers(0, 4, 384), r.integers(0, 4096, 384))})
+    rows += [(b, t) for b in range(4) for t in (0, 63, 64, 4095)]
+    _prefill_case(4, 4096, 12, 4, 64, 64, 8, torch.bfloat16, seed=1001, rows=rows)
+
+
+def test_prefill_topk_covering_all_blocks_equals_dense():
+    case("prefill k>=NB == dense")
+    x = synth.prefill_inputs(1, 640, 12, 4, 64, dtype=torch.bfloat16, seed=80)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    protos = sparda.compress(d["k"], 64)
+    _, _, sel, n = sparda.route(d["forecast"], protos, 64, 10, want_topk=False, want_sel=True)
+    a = sparda.prefill(d["q"], d["k"], d["v"], sel, n, 64)
+    b = sparda.prefill(d["q"], d["k"], d["v"], None, None, 64)
+    assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# decode step
+# ---------------------------------------------------------------------------
+
+def _decode_case(B, S, Hq, Hkv, D, bs, k, dtype, routing, seed, use_forecast=True, capacity=None):
+    x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=dtype, seed=seed, capacity=capacity)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    f = d["forecast"] if use_forecast else None
+    out, ex = sparda.decode(d["q"], d["k_cache"], d["v_cache"], S, f, bs, k, routing=routing,
+                            want_protos=True, want_sel=True)
+    torch.cuda.synchronize()
+    kc = np32(x["k_cache"])
+    sel_o, n_o, _ = O.decode_selection(kc, S, np32(x["forecast"]) if use_forecast else None, bs, k, routing)
+    assert np.array_equal(ex["n_sel"].cpu().numpy(), n_o)
+    assert np.array_equal(ex["sel"].cpu().numpy(), sel_o)
+    want = O.attention_decode(np32(x["q"]), kc, np32(x["v_cache"]), S, sel_o, n_o, bs)
+    assert_close_out(np32(out), want, dtype)
+    return d, out, ex
+
+
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+def test_decode_16k_cache(routing):
+    # decode at 16K: B=8, cache [8,16384,4,64] bf16, 256 blocks, k=8 + sink + current
+    case(f"decode 16K {routing}")
+    d, out, ex = _decode_case(8, 16384, 12, 4, 64, 64, 8, torch.bfloat16, routing, seed=1002)
+    assert np.array_equal(ex["protos"].cpu().numpy(), O.compress(np32(d["k_cache"]), 64))
+    # a second call on the same workspace (arrival counters reset) is identical
+    out2 = sparda.decode(d["q"], d["k_cache"], d["v_cache"], 16384, d["forecast"], 64, 8, routing=routing)
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("S", [1, 63, 64, 65, 600, 1000, 5000])
+def test_decode_lengths_fp32(S):
+    case(f"decode fp32 S={S}")
+    _decode_case(2, S, 12, 4, 64, 64, 8, torch.float32, "absolute", seed=S, capacity=S + 7)
+
+
+def test_decode_static_window_and_dense_fallback():
+    case("decode static + dense")
+    _decode_case(3, 5000, 12, 4, 64, 64, 8, torch.bfloat16, "reference", seed=11, use_forecast=False)
+    _decode_case(3, 600, 12, 4, 64, 64, 8, torch.bfloat16, "absolute", seed=12)  # NB=10 <= k+2
+
+
+def test_decode_cached_prototypes_match():
+    case("decode cached prototypes")
+    x = synth.decode_inputs(2, 3000, 12, 4, 64, dtype=torch.bfloat16, seed=13)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    out1, ex = sparda.decode(d["q"], d["k_cache"], d["v_cache"], 3000, d["forecast"], 64, 8,
+                             routing="absolute", want_protos=True, want_sel=True)
+    out2, ex2 = sparda.decode(d["q"], d["k_cache"], d["v_cache"], 3000, d["forecast"], 64, 8,
+                              routing="absolute", protos_in=ex["protos"], want_sel=True)
+    assert torch.equal(ex["sel"], ex2["sel"]) and torch.equal(out1, out2)
+
+
+def test_decode_reference_geometry():
+    # 8 q heads / 2 kv heads, D=32, bs=16, k=2 (tests/test_sparse_attention.py:14-30)
+    case("decode D=32 bs=16 R=4")
+    _decode_case(1, 53, 8, 2, 32, 16, 2, torch.float32, "reference", seed=14, capacity=128)
+    _decode_case(1, 53, 8, 2, 32, 16, 2, torch.float32, "absolute", seed=15, capacity=128)

@@ -1,0 +1,346 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+
+Each oracle function is checked against something independent of its own
+code: closed forms, brute force, exact rational arithmetic, PyTorch library
+routines (torch.topk, scaled_dot_product_attention), the op-for-op
+restatement of the reference path, and the known-answer assertions of the
+reference's tests (tests/test_forecast.py, tests/test_sparse_attention.py).
+"""
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import reference_path as R
+from oracle import sparda_oracle as O
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------------------
+# compressor (model/forecast.py:57-78)
+# ---------------------------------------------------------------------------
+
+def test_compress_matches_padded_mean():
+    k = rng(0).standard_normal((2, 50, 3, 16)).astype(np.float32)
+    bs = 16
+    got = O.compress(k, bs)
+    pad = np.zeros((2, 64, 3, 16), np.float64)
+    pad[:, :50] = k
+    want = pad.reshape(2, 4, 16, 3, 16).mean(axis=2)
+    assert got.shape == (2, 4, 3, 16)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_compress_reference_known_answers():
+    # tests/test_forecast.py:53-68: S=64, bs=16 -> 4 blocks; S=50 -> ceil = 4 blocks
+    assert O.compress(np.zeros((2, 64, 4, 32), np.float32), 16).shape == (2, 4, 4, 32)
+    assert O.compress(np.zeros((2, 50, 4, 32), np.float32), 16).shape == (2, 4, 4, 32)
+    # partial block divided by bs, not by the present count (zero-padded mean)
+    p = O.compress(np.ones((1, 50, 1, 4), np.float32), 16)
+    assert np.all(p[0, :3] == 1.0) and np.all(p[0, 3] == np.float32(2 / 16))
+
+
+def test_compress_exact_on_integers():
+    k = rng(1).integers(-50, 50, size=(1, 256, 2, 8)).astype(np.float32)
+    got = O.compress(k, 64)
+    want = k.reshape(1, 4, 64, 2, 8).sum(axis=2) / 64  # exact: small integers, power-of-2 divisor
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_compress_sequential_order_is_pinned():
+    # ((0 + 1e8) + 1) - 1e8 + 1 = 1 sequentially; a pairwise tree gives 0
+    k = np.array([1e8, 1.0, -1e8, 1.0], np.float32).reshape(1, 4, 1, 1)
+    assert O.compress(k, 4)[0, 0, 0, 0] == np.float32(0.25)
+
+
+# ---------------------------------------------------------------------------
+# scores (model/forecast.py:108-126)
+# ---------------------------------------------------------------------------
+
+def _fp32_round(fr: Fraction) -> np.float32:
+    x = np.float32(float(fr))
+    best = x
+    for c in (np.nextafter(x, np.float32(-np.inf)), np.nextafter(x, np.float32(np.inf))):
+        dc, db = abs(Fraction(float(c)) - fr), abs(Fraction(float(best)) - fr)
+        if dc < db or (dc == db and (int(c.view(np.uint32)) & 1) == 0):
+            best = c
+    return np.float32(best)
+
+
+def test_scores_fma_chain_exact():
+    r = rng(2)
+    f = r.standard_normal((1, 3, 2, 16)).astype(np.float32)
+    P = r.standard_normal((1, 5, 2, 16)).astype(np.float32)
+    got = O.scores(f, P, bs=1, causal=False, scale=0.25)
+    for h in range(2):
+        for t in range(3):
+            for j in range(5):
+                acc = np.float32(0)
+                for d in range(16):
+                    acc = _fp32_round(Fraction(float(f[0, t, h, d])) * Fraction(float(P[0, j, h, d]))
+                                      + Fraction(float(acc)))
+                assert got[0, h, t, j] == np.float32(acc * np.float32(0.25))
+
+
+def test_scores_close_to_float64_matmul():
+    r = rng(3)
+    f = r.standard_normal((2, 40, 4, 64)).astype(np.float32)
+    P = r.standard_normal((2, 5, 4, 64)).astype(np.float32)
+    got = O.scores(f, P, bs=8, causal=True)
+    want = np.einsum("bthd,bjhd->bhtj", f.astype(np.float64), P.astype(np.float64)) / 8.0
+    fin = np.isfinite(got)
+    np.testing.assert_allclose(got[fin], want[fin], atol=1e-4)
+
+
+def test_scores_causal_pattern_reference_known_answer():
+    # tests/test_forecast.py:71-92: bs=8, Tq=32, NB=4
+    r = rng(4)
+    f = r.standard_normal((2, 32, 2, 16)).astype(np.float32)
+    P = r.standard_normal((2, 4, 2, 16)).astype(np.float32)
+    s = O.scores(f, P, bs=8, causal=True)
+    tk = O.topk(s, 2)
+    assert s.shape == (2, 2, 32, 4) and tk.shape == (2, 2, 32, 2)
+    assert np.isneginf(s[:, :, 0, 1:]).all()
+    assert np.isneginf(s[:, :, 7, 1:]).all()
+    assert np.isfinite(s[:, :, 8, :2]).all()
+    assert np.isneginf(s[:, :, 8, 2:]).all()
+
+
+def test_scores_position_offset():
+    r = rng(5)
+    f = r.standard_normal((1, 1, 1, 16)).astype(np.float32)
+    P = r.standard_normal((1, 8, 1, 16)).astype(np.float32)
+    s0 = O.scores(f, P, bs=4, causal=True, score_pos0=0)
+    s1 = O.scores(f, P, bs=4, causal=True, score_pos0=29)
+    assert np.isfinite(s0[0, 0, 0, 0]) and np.isneginf(s0[0, 0, 0, 1:]).all()
+    assert np.isfinite(s1[0, 0, 0, :8]).all()  # 29 // 4 = 7 -> all 8 blocks
+
+
+# ---------------------------------------------------------------------------
+# top-k (torch.topk at model/forecast.py:128-129, ties by lower index)
+# ---------------------------------------------------------------------------
+
+def _brute_topk(row, k):
+    key = lambda j: (-(0.0 if row[j] == 0 else float(row[j])), j)
+    return sorted(range(len(row)), key=key)[:min(k, len(row))]
+
+
+def test_topk_equals_torch_on_distinct_values():
+    s = rng(6).permutation(4096 * 64).reshape(4096, 64).astype(np.float32) / 7.0
+    got = O.topk(s, 8)
+    want = torch.topk(torch.from_numpy(s), 8, dim=-1).indices.numpy()
+    assert np.array_equal(got, want)
+
+
+def test_topk_ties_lower_index_first():
+    r = rng(7)
+    s = r.integers(-3, 3, size=(500, 40)).astype(np.float32)
+    s[r.random(s.shape) < 0.2] = -np.inf
+    s[:, 5] = -0.0
+    got = O.topk(s, 8)
+    for i in range(s.shape[0]):
+        assert list(got[i]) == _brute_topk(s[i], 8)
+
+
+def test_topk_k_larger_than_blocks():
+    s = np.array([[0.5, -np.inf, 2.0]], np.float32)
+    assert O.topk(s, 8).tolist() == [[2, 0, 1]]
+
+
+# ---------------------------------------------------------------------------
+# selection sets (model/attention/sparse.py:126-154, 231-253)
+# ---------------------------------------------------------------------------
+
+def test_selection_sets_brute_force():
+    r = rng(8)
+    B, Tq, H, NB, bs, k = 2, 96, 2, 12, 8, 4
+    f = r.standard_normal((B, Tq, H, 16)).astype(np.float32)
+    P = r.standard_normal((B, NB, H, 16)).astype(np.float32)
+    for causal in (True, False):
+        sc, tk, sel, n = O.route(f, P, bs, k, causal=causal)
+        for b in range(B):
+            for h in range(H):
+                for t in range(Tq):
+                    own = min(t // bs, NB - 1)
+                    want = {0, own} | set(int(x) for x in tk[b, h, t])
+                    if causal:
+                        want = {j for j in want if j <= own}
+                    got = sel[b, h, t, :n[b, h, t]]
+                    assert list(got) == sorted(want)
+                    assert (sel[b, h, t, n[b, h, t]:] == -1).all()
+
+
+def test_decode_reference_routing_closed_form():
+    # row-0 mask (model/forecast.py:123-126 from model/attention/sparse.py:139):
+    # only block 0 is finite, ties by index give {0..k-1}, plus the current block
+    r = rng(9)
+    S, bs, k = 1000, 16, 5
+    kc = r.standard_normal((2, S, 3, 16)).astype(np.float32)
+    f = r.standard_normal((2, 3, 16)).astype(np.float32)
+    sel, n, _ = O.decode_selection(kc, S, f, bs, k, routing="reference")
+    cb = (S - 1) // bs
+    for b in range(2):
+        for g in range(3):
+            assert list(sel[b, g, :n[b, g]]) == list(range(k)) + [cb]
+
+
+def test_fixed_selections():
+    sel, n = O.sel_fixed(O.SEL_WINDOW_DECODE, 1, 1, 1, NB=20, bs=16, k=4, query_pos0=16 * 10 + 3)
+    assert list(sel[0, 0, 0, :n[0, 0, 0]]) == [0, 7, 8, 9, 10]
+    sel, n = O.sel_fixed(O.SEL_WINDOW_PREFILL, 1, 64, 1, NB=4, bs=16, k=1)
+    assert list(sel[0, 0, 63, :n[0, 0, 63]]) == [0, 2, 3]
+    assert list(sel[0, 0, 20, :n[0, 0, 20]]) == [0, 1]
+    sel, n = O.sel_fixed(O.SEL_DENSE, 1, 40, 1, NB=3, bs=16, k=1)
+    assert list(sel[0, 0, 39, :n[0, 0, 39]]) == [0, 1, 2]
+
+
+# ---------------------------------------------------------------------------
+# gather (model/attention/sparse.py:19-62; tests/test_sparse_attention.py:33-60)
+# ---------------------------------------------------------------------------
+
+def test_gather_reference_known_answer():
+    k = rng(10).standard_normal((2, 2, 48, 32)).astype(np.float32)
+    v = rng(11).standard_normal((2, 2, 48, 32)).astype(np.float32)
+    idx = np.array([[[0, 2], [1, 2]], [[2, 0], [0, 1]]])
+    kg, vg = O.gather_blocks(k, v, idx, 16)
+    assert kg.shape == (2, 2, 32, 32)
+    assert np.array_equal(kg[0, 0, :16], k[0, 0, 0:16])
+    assert np.array_equal(kg[0, 0, 16:], k[0, 0, 32:48])
+    assert np.array_equal(vg[1, 0, :16], v[1, 0, 32:48])
+    # tail block past S is zero-padded
+    kg2, _ = O.gather_blocks(k[:, :, :40], v[:, :, :40], idx, 16)
+    assert np.array_equal(kg2[0, 0, 16:24], k[0, 0, 32:40]) and not kg2[0, 0, 24:].any()
+
+
+# ---------------------------------------------------------------------------
+# attention (model/attention/sparse.py:185-282, 99-183)
+# ---------------------------------------------------------------------------
+
+def _inputs(seed, B, T, Hq, Hkv, D):
+    r = rng(seed)
+    q = r.standard_normal((B, T, Hq, D)).astype(np.float32)
+    k = r.standard_normal((B, T, Hkv, D)).astype(np.float32)
+    v = r.standard_normal((B, T, Hkv, D)).astype(np.float32)
+    f = r.standard_normal((B, T, Hkv, D)).astype(np.float32)
+    return q, k, v, f
+
+
+def test_prefill_blockwise_equals_full_mask_textbook():
+    B, T, Hq, Hkv, D, bs, k = 2, 70, 6, 2, 16, 8, 3
+    q, kk, v, f = _inputs(12, B, T, Hq, Hkv, D)
+    sel, n = O.prefill_selection(kk, f, bs, k)
+    got = O.attention_prefill(q, kk, v, sel, n, bs)
+    # textbook: explicit [T,T] allowed mask, full-row softmax in float64
+    R_ = Hq // Hkv
+    want = np.zeros_like(got)
+    for b in range(B):
+        for h in range(Hq):
+            g = h // R_
+            allowed = np.zeros((T, T), bool)
+            for t in range(T):
+                blocks = set(sel[b, g, t, :n[b, g, t]].tolist())
+                for s in range(t + 1):
+                    allowed[t, s] = (s // bs) in blocks
+            sc = q[b, :, h].astype(np.float64) @ kk[b, :, g].astype(np.float64).T / math.sqrt(D)
+            sc[~allowed] = -np.inf
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            want[b, :, h * D:(h + 1) * D] = p @ v[b, :, g].astype(np.float64)
+    np.testing.assert_allclose(got, want, atol=1e-12)
+
+
+def test_prefill_dense_cases_equal_sdpa():
+    B, T, Hq, Hkv, D, bs = 1, 50, 4, 2, 16, 8
+    q, kk, v, f = _inputs(13, B, T, Hq, Hkv, D)
+    tq = torch.from_numpy(q).double().transpose(1, 2)
+    tk = torch.repeat_interleave(torch.from_numpy(kk).double().transpose(1, 2), 2, dim=1)
+    tv = torch.repeat_interleave(torch.from_numpy(v).double().transpose(1, 2), 2, dim=1)
+    want = F.scaled_dot_product_attention(tq, tk, tv, is_causal=True).transpose(1, 2).reshape(B, T, Hq * D)
+    # k >= NB: every causal block is selected -> dense causal attention
+    sel, n = O.prefill_selection(kk, f, bs, topk_blocks=16)
+    np.testing.assert_allclose(O.attention_prefill(q, kk, v, sel, n, bs), want.numpy(), atol=1e-12)
+    # sel=None is the dense fallback (model/attention/sparse.py:201-224)
+    np.testing.assert_allclose(O.attention_prefill(q, kk, v, None, None, bs), want.numpy(), atol=1e-12)
+
+
+def test_prefill_matches_reference_path_restatement():
+    B, T, Hq, Hkv, D, bs, k = 2, 160, 6, 2, 16, 16, 3
+    q, kk, v, f = _inputs(14, B, T, Hq, Hkv, D)
+    sel, n = O.prefill_selection(kk, f, bs, k)
+    got = O.attention_prefill(q, kk, v, sel, n, bs)
+    t = lambda a: torch.from_numpy(a).double()
+    want = R.sparse_prefill(t(q).transpose(1, 2), t(kk).transpose(1, 2), t(v).transpose(1, 2), t(f), bs, k)
+    np.testing.assert_allclose(got, want.numpy(), atol=1e-10)
+
+
+def test_prefill_causality_invariant():
+    # tests/test_sparse_attention.py:80-92 restated on outputs: future tokens never matter
+    B, T, Hq, Hkv, D, bs, k = 1, 96, 4, 2, 16, 8, 3
+    q, kk, v, f = _inputs(15, B, T, Hq, Hkv, D)
+    sel, n = O.prefill_selection(kk, f, bs, k)
+    out = O.attention_prefill(q, kk, v, sel, n, bs)
+    kk2, v2 = kk.copy(), v.copy()
+    kk2[:, 60:] += 5.0
+    v2[:, 60:] -= 3.0
+    out2 = O.attention_prefill(q, kk2, v2, sel, n, bs)
+    np.testing.assert_array_equal(out[:, :60], out2[:, :60])
+
+
+def test_decode_dense_fallback_equals_sdpa():
+    B, S, Hq, Hkv, D, bs, k = 2, 90, 6, 2, 16, 16, 4  # NB = 6 <= k+2
+    r = rng(16)
+    q = r.standard_normal((B, Hq, D)).astype(np.float32)
+    kc = r.standard_normal((B, 100, Hkv, D)).astype(np.float32)
+    vc = r.standard_normal((B, 100, Hkv, D)).astype(np.float32)
+    f = r.standard_normal((B, Hkv, D)).astype(np.float32)
+    got, sel, n = O.decode_step(q, kc, vc, S, f, bs, k)
+    assert (n == 6).all()
+    tq = torch.from_numpy(q).double()[:, :, None]
+    tk = torch.repeat_interleave(torch.from_numpy(kc[:, :S]).double().transpose(1, 2), 3, dim=1)
+    tv = torch.repeat_interleave(torch.from_numpy(vc[:, :S]).double().transpose(1, 2), 3, dim=1)
+    want = F.scaled_dot_product_attention(tq, tk, tv).reshape(B, Hq * D)
+    np.testing.assert_allclose(got, want.numpy(), atol=1e-12)
+
+
+def test_decode_absolute_equals_last_prefill_row():
+    B, T, Hq, Hkv, D, bs, k = 2, 200, 6, 2, 16, 16, 4
+    q, kk, v, f = _inputs(17, B, T, Hq, Hkv, D)
+    sel, n = O.prefill_selection(kk, f, bs, k)
+    pre = O.attention_prefill(q, kk, v, sel, n, bs, rows=[(b, T - 1) for b in range(B)])
+    dec, dsel, dn = O.decode_step(q[:, T - 1], kk, v, T, f[:, T - 1], bs, k, routing="absolute")
+    np.testing.assert_allclose(dec, pre[:, T - 1], atol=1e-12)
+    for b in range(B):
+        for g in range(Hkv):
+            assert list(dsel[b, g, :dn[b, g]]) == list(sel[b, g, T - 1, :n[b, g, T - 1]])
+
+
+def test_decode_matches_reference_restatement_on_its_selection():
+    B, S, Hq, Hkv, D, bs, k = 2, 300, 6, 2, 16, 16, 4
+    r = rng(18)
+    q = r.standard_normal((B, Hq, D)).astype(np.float32)
+    kc = r.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    vc = r.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    f = r.standard_normal((B, 1, Hkv, D)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).double()
+    out, idx, valid = R.sparse_decode(t(q)[:, :, None], t(kc).transpose(1, 2), t(vc).transpose(1, 2), S,
+                                      t(f), bs, k)
+    # same attention on the selection torch.topk made (its -inf tie order is unspecified)
+    cap = k + 2
+    sel = np.full((B, Hkv, cap), -1, np.int32)
+    n = np.zeros((B, Hkv), np.int32)
+    for b in range(B):
+        for g in range(Hkv):
+            s = sorted(int(j) for j, ok in zip(idx[b, g], valid[b, g]) if ok)
+            sel[b, g, :len(s)] = s
+            n[b, g] = len(s)
+            cb = (S - 1) // bs
+            assert 0 in s and cb in s and len(s) <= k + 2
+    got = O.attention_decode(q, kc, vc, S, sel, n, bs)
+    np.testing.assert_allclose(got, out.reshape(B, Hq * D).numpy(), atol=1e-12)
