@@ -204,7 +204,8 @@ SPARDA_API size_t sparda_decode_workspace_bytes(int64_t B, int64_t S, int64_t Hq
  * forecast routing (sparse.py:139-141), sink + current block (126-130),
  * removal of future blocks (150-151), the gather (157) and masked SDPA over the
  * gathered keys (160-181), as split-K attention over the selected blocks with
- * a combine. Dense over all S keys when NB <= top_k+2 (sparse.py:113-123);
+ * a merge (two kernel launches, no host synchronisation).
+ * Dense over all S keys when NB <= top_k+2 (sparse.py:113-123);
  * static window {0} U [cb-k+1, cb] when forecast == NULL (sparse.py:142-147).
  *   q:        [B,Hq,D] of dtype, strides (q_sb, q_sh, 1) (position S-1)
  *   k_cache, v_cache: [B,Smax,Hkv,D] strides (kv_sb, kv_ss, kv_sh, 1);
@@ -215,10 +216,9 @@ SPARDA_API size_t sparda_decode_workspace_bytes(int64_t B, int64_t S, int64_t Hq
  *   protos_out: optional, receives the prototypes computed this step
  *   sel_out/n_sel_out: optional [B,Hkv,top_k+2] / [B,Hkv] int32
  *   out: [B,Hq*D] of dtype, stride out_sb
- *   workspace: >= sparda_decode_workspace_bytes(), 256-byte aligned, and
- *             zero-filled before its first use: it holds arrival counters
- *             that the kernels return to zero at the end of every call. Calls
- *             sharing one workspace must be ordered on one stream.
+ *   workspace: >= sparda_decode_workspace_bytes(), 256-byte aligned; it
+ *             holds the block scores of the step (no state survives the call). Calls sharing one workspace
+ *             must be ordered on one stream.
  */
 SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh,
                              const void* k_cache, const void* v_cache,

@@ -74,17 +74,48 @@ __device__ __forceinline__ int32_t rank64_index(uint64_t r) {
 }
 
 // ---------------------------------------------------------------------------
-// wavefront reductions (64 lanes)
+// wavefront reductions (64 lanes), all on the VALU: DPP within rows of 16
+// lanes (quad_perm xor 1 and xor 2, row_half_mirror, row_mirror), then the
+// gfx950 row swaps across rows (permlane16_swap, permlane32_swap). Every
+// pairing step combines the same two values on both lanes, so all lanes end
+// with the identical result.
 // ---------------------------------------------------------------------------
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppMirror = 0x140;     // row_mirror
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float2 rows16_swap(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 rows32_swap(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = fmaxf(v, dpp_f32<kDppXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppMirror>(v));
+    float2 r = rows16_swap(v);
+    v = fmaxf(r.x, r.y);
+    r = rows32_swap(v);
+    return fmaxf(r.x, r.y);
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v = v + dpp_f32<kDppXor1>(v);
+    v = v + dpp_f32<kDppXor2>(v);
+    v = v + dpp_f32<kDppHalfMirror>(v);
+    v = v + dpp_f32<kDppMirror>(v);
+    float2 r = rows16_swap(v);
+    v = r.x + r.y;
+    r = rows32_swap(v);
+    return r.x + r.y;
 }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
@@ -101,6 +132,54 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 }
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// VEC consecutive elements widened to fp32 (the index must be VEC-aligned).
+template <int DT, int VEC>
+__device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&o)[VEC]) {
+    if constexpr (VEC == 1) {
+        o[0] = load_elem<DT>(p, i);
+    } else if constexpr (VEC == 2) {
+        const float2 v = load_pair<DT>(p, i);
+        o[0] = v.x;
+        o[1] = v.y;
+    } else if constexpr (DT == SPARDA_F32) {
+        const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    } else {
+        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+        o[0] = __uint_as_float(w.x << 16);
+        o[1] = __uint_as_float(w.x & 0xffff0000u);
+        o[2] = __uint_as_float(w.y << 16);
+        o[3] = __uint_as_float(w.y & 0xffff0000u);
+    }
+}
+
+// Sum of one block of key rows, sequential in s (the canonical prototype
+// order): acc[v] = ((0 + k[s0]) + k[s0+1]) + ... for VEC adjacent elements.
+// For a full block of UNROLL rows every load is issued before the additions.
+template <int DT, int VEC, int UNROLL>
+__device__ __forceinline__ void block_sum(const void* __restrict__ kc, int64_t base, int64_t s0, int64_t s1,
+                                          int64_t ss, float (&acc)[VEC]) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+    if (UNROLL > 0 && s1 - s0 == UNROLL) {
+        float buf[UNROLL > 0 ? UNROLL : 1][VEC];
+#pragma unroll
+        for (int i = 0; i < UNROLL; ++i) load_vec<DT, VEC>(kc, base + (s0 + i) * ss, buf[i]);
+#pragma unroll
+        for (int i = 0; i < UNROLL; ++i)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + buf[i][v];
+    } else {
+#pragma unroll 8
+        for (int64_t s = s0; s < s1; ++s) {
+            float x[VEC];
+            load_vec<DT, VEC>(kc, base + s * ss, x);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + x[v];
+        }
+    }
+}
 
 }  // namespace sparda
 

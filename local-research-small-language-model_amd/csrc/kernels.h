@@ -29,12 +29,7 @@ int launch_gather(const void* k, const void* v, int dtype, int64_t sb, int64_t s
 
 // Workspace carve-up of the decode step.
 struct DecodeWs {
-    int32_t* cnt_b;    // [B]        arrivals of the select kernel per sequence
-    int32_t* cnt_bg;   // [B*Hkv]    arrivals of the attend kernel per (sequence, kv head)
     float* scores;     // [B*Hkv*NB]
-    int32_t* sel;      // [B*Hkv*cap]
-    int32_t* n_sel;    // [B*Hkv]
-    float* part;       // [B*Hq*cap*(D+2)]  (m, l, o[D]) per split
     size_t bytes;
 };
 DecodeWs decode_ws_layout(void* base, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,

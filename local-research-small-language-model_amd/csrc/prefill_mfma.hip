@@ -6,17 +6,19 @@
 // (column c -> token c / R, head c % R), processed as R tiles of 16 columns.
 //
 // The workgroup walks the union of its tokens' selected KV blocks in
-// ascending order. Each block's K (row-major) and V (transposed) are staged
-// once in LDS (double-buffered) and shared by all R heads; a tile skips a
-// block none of its columns selected, and columns that did not select it are
-// masked. Per tile and block, with v_mfma_f32_16x16x32_bf16:
+// ascending order. Each block's K and V are staged once in LDS, row-major
+// (double-buffered, with a second block in flight in registers), and shared
+// by all R heads; a tile skips a block none of its columns selected, and
+// columns that did not select it contribute nothing. Per tile and block,
+// with v_mfma_f32_16x16x32_bf16:
 //     S^T[key, col] = K[key, :] . Q[col, :]           (8 MFMA)
 //     online softmax per column (fp32, log2 domain)
 //     O^T[d, col]  += V^T[d, key] . P^T[key, col]      (8 MFMA)
 // S^T leaves each lane with 4 consecutive keys of 4 key tiles for one column,
 // which is directly the B operand of the PV product when the 32-key k-axis is
 // enumerated as {32m + 4g + e, 32m + 16 + 4g + e} (g = lane / 16); the V^T A
-// operand is read from LDS with the same enumeration.
+// operand is read from the row-major V tile with the same enumeration by the
+// LDS transpose read (ds_read_b64_tr_b16).
 #include "common.h"
 #include "kernels.h"
 
@@ -25,18 +27,23 @@ namespace sparda {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMBs = 64;          // block size (keys per KV block)
 constexpr int kMD = 64;           // head dim
 constexpr int kMThreads = 256;    // 4 wavefronts
-constexpr int kKRow = kMD + 8;    // K row in LDS, bf16 elements (144 B: 16 B aligned)
-constexpr int kVRow = kMBs + 4;   // V^T row in LDS, bf16 elements (136 B)
+constexpr int kKRow = kMD + 8;    // K row in LDS, bf16 elements (144 B)
+constexpr int kVRow = kMD + 16;   // V row in LDS, bf16 elements (160 B: 4 rows cover all banks)
 constexpr int kMaxNBWords = 32;   // selection bitmask words per token (NB <= 1024)
 constexpr float kLog2eM = 1.4426950408889634f;
+// KV blocks kept in flight in registers ahead of the one being computed (1 or 2)
+#ifndef SPARDA_PREFILL_PREFETCH
+#define SPARDA_PREFILL_PREFETCH 2
+#endif
 
 struct MfmaSmem {
     uint16_t k[2][kMBs * kKRow];
-    uint16_t vt[2][kMD * kVRow];
+    uint16_t v[2][kMBs * kVRow];
     uint32_t mask[64 * kMaxNBWords];
     uint16_t list[kMaxNBWords * 32];
     int n_list;
@@ -45,10 +52,35 @@ struct MfmaSmem {
 __device__ __forceinline__ bf16x8 lds_read8(const uint16_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
-__device__ __forceinline__ bf16x8 lds_read4x2(const uint16_t* p0, const uint16_t* p1) {
-    const uint2 a = *reinterpret_cast<const uint2*>(p0);
-    const uint2 c = *reinterpret_cast<const uint2*>(p1);
-    return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, c.x, c.y));
+
+// Transposed read (ds_read_b64_tr_b16). Within each 16-lane group, output
+// lane i, element e is element i%4 of the 8-byte chunk addressed by lane
+// 4e + i/4 of the group.
+__device__ __forceinline__ i16x4 lds_read_tr(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<__attribute__((address_space(3))) i16x4*>(
+            reinterpret_cast<uintptr_t>(p)));
+}
+
+// Reductions over lane pairs (l, l^16) and (l, l^32) with the gfx950 VALU
+// row swaps: permlane16_swap(x, x) hands every lane the values of rows
+// {2r, 2r+1} at its column, permlane32_swap(x, x) those of rows {r, r+2};
+// both lanes of a pair combine the same two values in the same order.
+__device__ __forceinline__ float pair16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 template <int R>
@@ -60,11 +92,13 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                     int64_t T, int H, int64_t NBq, int causal, float scale_log2,
                     uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st) {
     __shared__ MfmaSmem sm;
+    __shared__ uint16_t qs[64 * R * kKRow];  // Q rows (token, head) of this query block
+    __shared__ uint32_t uni[kMaxNBWords];
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
     const int wave = tid / kWave;
     const int col16 = lane % 16;   // column within a tile
-    const int grp = lane / 16;     // lane group (k / row sub-block)
+    const int grp = lane / 16;     // lane group
 
     // heaviest query blocks first; consecutive ids cycle through (b, g)
     const int64_t BH = static_cast<int64_t>(gridDim.x) / NBq;
@@ -75,64 +109,62 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
     const int64_t t0 = qb * 64;
     const int64_t NB = cdiv(T, kMBs);
     const int nbw = static_cast<int>((NB + 31) / 32);
+    const int t_valid = static_cast<int>(T - t0 < 64 ? T - t0 : 64);  // tokens of this block
 
     // ---- selection bitmask per token, and the workgroup's union of blocks ----
     for (int i = tid; i < 64 * nbw; i += kMThreads) sm.mask[i] = 0u;
     __syncthreads();
-    if (tid < 64) {
+    if (tid < 64 && tid < t_valid) {
         const int64_t t = t0 + tid;
         uint32_t* row = sm.mask + tid * nbw;
-        if (t < T) {
-            if (sel != nullptr) {
-                const int64_t r = (static_cast<int64_t>(b) * H + g) * T + t;
-                const int n = min(static_cast<int64_t>(n_sel[r]), cap);
-                for (int i = 0; i < n; ++i) {
-                    const int j = sel[r * cap + i];
-                    if (j >= 0 && j < NB) row[j >> 5] |= 1u << (j & 31);
-                }
-            } else {
-                const int64_t jmax = causal ? qb : NB - 1;
-                for (int64_t j = 0; j <= jmax; ++j) row[j >> 5] |= 1u << (j & 31);
+        if (sel != nullptr) {
+            const int64_t r = (static_cast<int64_t>(b) * H + g) * T + t;
+            const int n = min(static_cast<int64_t>(n_sel[r]), cap);
+            for (int i = 0; i < n; ++i) {
+                const int j = sel[r * cap + i];
+                if (j >= 0 && j < NB) row[j >> 5] |= 1u << (j & 31);
             }
+        } else {
+            const int64_t jmax = causal ? qb : NB - 1;
+            for (int64_t j = 0; j <= jmax; ++j) row[j >> 5] |= 1u << (j & 31);
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        int n = 0;
-        for (int w = 0; w < nbw; ++w) {
-            uint32_t u = 0;
-            for (int tt = 0; tt < 64; ++tt) u |= sm.mask[tt * nbw + w];
-            while (u) {
-                const int bit = __builtin_ctz(u);
-                sm.list[n++] = static_cast<uint16_t>(w * 32 + bit);
-                u &= u - 1;
-            }
+    // union of the tokens' blocks, then its ascending list (one lane per block)
+    if (tid < nbw) {
+        uint32_t u = 0;
+        for (int tt = 0; tt < 64; ++tt) u |= sm.mask[tt * nbw + tid];
+        uni[tid] = u;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int base = 0;
+        const uint64_t below = (1ull << lane) - 1ull;
+        for (int c0 = 0; c0 < NB; c0 += kWave) {
+            const int j = c0 + lane;
+            const bool bit = j < NB && ((uni[j >> 5] >> (j & 31)) & 1u);
+            const uint64_t bal = __ballot(bit);
+            if (bit) sm.list[base + __popcll(bal & below)] = static_cast<uint16_t>(j);
+            base += __popcll(bal);
         }
-        sm.n_list = n;
+        if (lane == 0) sm.n_list = base;
+    }
+    // Q rows of the block: row (token * R + head), 128 B each
+    for (int c = tid; c < 64 * R * 8; c += kMThreads) {
+        const int row = c / 8, ch = c % 8;
+        const int tk = row / R, hh = row % R;
+        uint4 val = make_uint4(0u, 0u, 0u, 0u);
+        if (tk < t_valid)
+            val = *reinterpret_cast<const uint4*>(q + b * q_sb + (t0 + tk) * q_st +
+                                                  static_cast<int64_t>(g * R + hh) * q_sh + ch * 8);
+        *reinterpret_cast<uint4*>(&qs[row * kKRow + ch * 8]) = val;
     }
 
-    // ---- Q^T B-operands (registers for the whole kernel) ----
-    bf16x8 qb_op[R][2];
-    int tok[R];          // token index within the query block for this lane's column, per tile
-    int64_t tpos[R];     // absolute position
+    // column c of tile tt is Q row 16*wave*R + c: token 16*wave + c/R, head c%R
+    int tok[R];
 #pragma unroll
-    for (int tt = 0; tt < R; ++tt) {
-        const int c = 16 * tt + col16;
-        const int tw = c / R;
-        const int hh = c % R;
-        tok[tt] = 16 * wave + tw;
-        tpos[tt] = t0 + tok[tt];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-            if (tpos[tt] < T) {
-                const uint16_t* p = q + b * q_sb + tpos[tt] * q_st + static_cast<int64_t>(g * R + hh) * q_sh +
-                                    32 * kk + 8 * grp;
-                raw = *reinterpret_cast<const uint4*>(p);
-            }
-            qb_op[tt][kk] = __builtin_bit_cast(bf16x8, raw);
-        }
-    }
+    for (int tt = 0; tt < R; ++tt) tok[tt] = 16 * wave + (16 * tt + col16) / R;
+    const uint16_t* qrow0 = qs + (16 * wave * R + col16) * kKRow + 8 * grp;
 
     f32x4 o[R][4];
     float m_run[R], l_run[R];
@@ -144,145 +176,184 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
         for (int dt = 0; dt < 4; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // ---- staging of one KV block: thread -> (row pair, 16 B chunk) ----
-    const int st_chunk = tid % 8;        // 8 bf16 of d
-    const int st_pair = tid / 8;         // rows 2*pair, 2*pair+1 (32 pairs)
-    const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh + st_chunk * 8;
-    const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh + st_chunk * 8;
-    uint4 kreg[2], vreg[2];
-    auto fetch = [&](int64_t j) {
+    // ---- staging: thread -> 16 B chunks (row c/8, chunk c%8), c = tid, tid+256 ----
+    const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
+    const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
+    uint4 kr[2][2], vr[2][2];  // two prefetch sets
+    auto fetch = [&](int set, int64_t j) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const int64_t s = j * kMBs + 2 * st_pair + r;
+            const int c = tid + r * kMThreads;
+            const int64_t s = j * kMBs + c / 8;
+            const int64_t off = s * kv_st + (c % 8) * 8;
             if (s < T) {
-                kreg[r] = *reinterpret_cast<const uint4*>(kbase + s * kv_st);
-                vreg[r] = *reinterpret_cast<const uint4*>(vbase + s * kv_st);
+                kr[set][r] = *reinterpret_cast<const uint4*>(kbase + off);
+                vr[set][r] = *reinterpret_cast<const uint4*>(vbase + off);
             } else {
-                kreg[r] = make_uint4(0u, 0u, 0u, 0u);
-                vreg[r] = make_uint4(0u, 0u, 0u, 0u);
+                kr[set][r] = make_uint4(0u, 0u, 0u, 0u);
+                vr[set][r] = make_uint4(0u, 0u, 0u, 0u);
             }
         }
     };
-    auto stash = [&](int buf) {
+    auto stash = [&](int set, int buf) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
-            *reinterpret_cast<uint4*>(&sm.k[buf][(2 * st_pair + r) * kKRow + st_chunk * 8]) = kreg[r];
-        const uint16_t* v0 = reinterpret_cast<const uint16_t*>(&vreg[0]);
-        const uint16_t* v1 = reinterpret_cast<const uint16_t*>(&vreg[1]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t w = static_cast<uint32_t>(v0[e]) | (static_cast<uint32_t>(v1[e]) << 16);
-            *reinterpret_cast<uint32_t*>(&sm.vt[buf][(st_chunk * 8 + e) * kVRow + 2 * st_pair]) = w;
+        for (int r = 0; r < 2; ++r) {
+            const int c = tid + r * kMThreads;
+            *reinterpret_cast<uint4*>(&sm.k[buf][(c / 8) * kKRow + (c % 8) * 8]) = kr[set][r];
+            *reinterpret_cast<uint4*>(&sm.v[buf][(c / 8) * kVRow + (c % 8) * 8]) = vr[set][r];
         }
     };
 
-    __syncthreads();
-    const int n_list = sm.n_list;
-    if (n_list > 0) {
-        fetch(sm.list[0]);
-        stash(0);
-    }
-    __syncthreads();
-
-    for (int u = 0; u < n_list; ++u) {
-        const int buf = u & 1;
-        const int j = sm.list[u];
-        if (u + 1 < n_list) fetch(sm.list[u + 1]);
-
-        // which tiles of this wave need block j
+    // ---- one KV block against this wave's tiles ----
+    auto compute = [&](int buf, int j) {
         bool member[R];
         bool any = false;
 #pragma unroll
         for (int tt = 0; tt < R; ++tt) {
             member[tt] = (sm.mask[tok[tt] * nbw + (j >> 5)] >> (j & 31)) & 1u;
-            const bool tile_any = __ballot(member[tt]) != 0ull;
-            any = any || tile_any;
+            any = any || (__ballot(member[tt]) != 0ull);
         }
-        if (any) {
-            bf16x8 ka[4][2];
+        if (!any) return;
+        bf16x8 ka[4][2];
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < 4; ++n)
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk)
-                    ka[n][kk] = lds_read8(&sm.k[buf][(16 * n + col16) * kKRow + 32 * kk + 8 * grp]);
-            bf16x8 va[4][2];
+            for (int kk = 0; kk < 2; ++kk)
+                ka[n][kk] = lds_read8(&sm.k[buf][(16 * n + col16) * kKRow + 32 * kk + 8 * grp]);
+        bf16x8 va[4][2];
+        {
+            // transposed A operand of V^T: source lane (grp, col16) points at
+            // row 32m + 4grp + col16/4 (+16 for the upper half), columns 16dt + 4(col16%4)
+            const int rsub = 4 * grp + col16 / 4;
+            const int csub = 4 * (col16 % 4);
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    const uint16_t* row = &sm.vt[buf][(16 * dt + col16) * kVRow];
-                    va[dt][m] = lds_read4x2(row + 32 * m + 4 * grp, row + 32 * m + 16 + 4 * grp);
+                    const uint16_t* base = &sm.v[buf][(32 * m + rsub) * kVRow + 16 * dt + csub];
+                    const i16x4 lo = lds_read_tr(base);
+                    const i16x4 hi = lds_read_tr(base + 16 * kVRow);
+                    va[dt][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
-            const bool diag = (j == qb);
+        }
+        const bool edge = (causal && j == qb) || (!causal && (j + 1) * kMBs > T);  // wave-uniform
 #pragma unroll
-            for (int tt = 0; tt < R; ++tt) {
-                if (__ballot(member[tt]) == 0ull) continue;
-                f32x4 s[4];
+        for (int tt = 0; tt < R; ++tt) {
+            if (__ballot(member[tt]) == 0ull) continue;
+            const bf16x8 qb0 = lds_read8(qrow0 + 16 * tt * kKRow);
+            const bf16x8 qb1 = lds_read8(qrow0 + 16 * tt * kKRow + 32);
+            f32x4 s[4];
 #pragma unroll
-                for (int n = 0; n < 4; ++n) {
-                    s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][0], qb_op[tt][0], s[n], 0, 0, 0);
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][1], qb_op[tt][1], s[n], 0, 0, 0);
-                }
-                // mask: column not selecting j; causal diagonal; keys beyond T
-                float mx = -__builtin_inff();
+            for (int n = 0; n < 4; ++n) {
+                s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][0], qb0, s[n], 0, 0, 0);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][1], qb1, s[n], 0, 0, 0);
+            }
+            if (edge) {
+                // causal diagonal: key <= token; non-causal tail: key < T
+                const int lim = causal ? tok[tt] : static_cast<int>(T - static_cast<int64_t>(j) * kMBs) - 1;
 #pragma unroll
                 for (int n = 0; n < 4; ++n)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t kp = static_cast<int64_t>(j) * kMBs + 16 * n + 4 * grp + i;
-                        bool ok = member[tt];
-                        if (causal) ok = ok && (!diag || kp <= tpos[tt]);
-                        else ok = ok && kp < T;
-                        s[n][i] = ok ? s[n][i] * scale_log2 : -__builtin_inff();
-                        mx = fmaxf(mx, s[n][i]);
-                    }
-                mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-                const float m_new = fmaxf(m_run[tt], mx);
-                const bool live = m_new != -__builtin_inff();
-                const float alpha = live ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
-                float rs = 0.0f;
+                    for (int i = 0; i < 4; ++i)
+                        if (16 * n + 4 * grp + i > lim) s[n][i] = -__builtin_inff();
+            }
+            float mx = s[0][0];
 #pragma unroll
-                for (int n = 0; n < 4; ++n)
+            for (int n = 0; n < 4; ++n)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float p = live ? __builtin_amdgcn_exp2f(s[n][i] - m_new) : 0.0f;
-                        s[n][i] = p;
-                        rs += p;
-                    }
-                rs += __shfl_xor(rs, 16, kWave);
-                rs += __shfl_xor(rs, 32, kWave);
-                l_run[tt] = l_run[tt] * alpha + rs;
-                m_run[tt] = m_new;
-                bf16x8 pb[2];
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[n][i]);
+            mx = member[tt] ? mx : -__builtin_inff();
+            mx = pair32_max(pair16_max(mx));
+            const float m_new = fmaxf(m_run[tt], mx * scale_log2);
+            const bool live = m_new != -__builtin_inff();
+            const float neg = live ? -m_new : 0.0f;
+            const float alpha = live ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
+            float rs = 0.0f;
 #pragma unroll
-                for (int m = 0; m < 2; ++m)
+            for (int n = 0; n < 4; ++n)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        pb[m][i] = static_cast<__bf16>(s[2 * m][i]);
-                        pb[m][4 + i] = static_cast<__bf16>(s[2 * m + 1][i]);
-                    }
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    o[tt][dt] *= alpha;
-                    o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], pb[0], o[tt][dt], 0, 0, 0);
-                    o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], pb[1], o[tt][dt], 0, 0, 0);
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][i], scale_log2, neg));
+                    s[n][i] = p;
+                    rs += p;
                 }
+            rs = member[tt] ? rs : 0.0f;
+            rs = pair32_sum(pair16_sum(rs));
+            l_run[tt] = l_run[tt] * alpha + rs;
+            m_run[tt] = m_new;
+            uint4 pw[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                bf16x8 pb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pb[i] = static_cast<__bf16>(s[2 * m][i]);
+                    pb[4 + i] = static_cast<__bf16>(s[2 * m + 1][i]);
+                }
+                pw[m] = __builtin_bit_cast(uint4, pb);
+                if (!member[tt]) pw[m] = make_uint4(0u, 0u, 0u, 0u);
+            }
+            if (__ballot(alpha != 1.0f) != 0ull) {
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[tt][dt] *= alpha;
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[0]),
+                                                                    o[tt][dt], 0, 0, 0);
+                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]),
+                                                                    o[tt][dt], 0, 0, 0);
             }
         }
-        if (u + 1 < n_list) stash(buf ^ 1);
+    };
+
+    __syncthreads();
+    const int n_list = sm.n_list;
+#if SPARDA_PREFILL_PREFETCH == 2
+    // prologue: block 0 staged, block 1 in flight
+    fetch(0, sm.list[0]);
+    if (n_list > 1) fetch(1, sm.list[1]);
+    stash(0, 0);
+    __syncthreads();
+    // iteration u computes block u from buffer u&1, keeps block u+1 in
+    // flight in register set (u+1)&1 and issues block u+2 into set u&1
+    for (int u = 0; u < n_list; u += 2) {
+        if (u + 2 < n_list) fetch(0, sm.list[u + 2]);
+        compute(0, sm.list[u]);
+        if (u + 1 < n_list) stash(1, 1);
+        __syncthreads();
+        if (u + 1 >= n_list) break;
+        if (u + 3 < n_list) fetch(1, sm.list[u + 3]);
+        compute(1, sm.list[u + 1]);
+        if (u + 2 < n_list) stash(0, 0);
         __syncthreads();
     }
+#else
+    fetch(0, sm.list[0]);
+    stash(0, 0);
+    __syncthreads();
+    for (int u = 0; u < n_list; u += 2) {
+        if (u + 1 < n_list) fetch(0, sm.list[u + 1]);
+        compute(0, sm.list[u]);
+        if (u + 1 < n_list) stash(0, 1);
+        __syncthreads();
+        if (u + 1 >= n_list) break;
+        if (u + 2 < n_list) fetch(0, sm.list[u + 2]);
+        compute(1, sm.list[u + 1]);
+        if (u + 2 < n_list) stash(0, 0);
+        __syncthreads();
+    }
+#endif
 
     // ---- epilogue: out[b, t, h*64 + d] = O / l ----
 #pragma unroll
     for (int tt = 0; tt < R; ++tt) {
-        if (tpos[tt] >= T) continue;
+        if (tok[tt] >= t_valid) continue;
         const int c = 16 * tt + col16;
         const int hh = c % R;
         const float inv = 1.0f / l_run[tt];
-        uint16_t* orow = out + b * out_sb + tpos[tt] * out_st + static_cast<int64_t>(g * R + hh) * kMD;
+        uint16_t* orow = out + b * out_sb + (t0 + tok[tt]) * out_st + static_cast<int64_t>(g * R + hh) * kMD;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
             bf16x4 w;

@@ -18,8 +18,8 @@ namespace sparda {
 // Thread (h, d-group) walks the block's tokens in order, one VEC-wide load per
 // token; a wavefront reads a contiguous run of the token row.
 // ---------------------------------------------------------------------------
-template <int DT, int VEC>
-__global__ void __launch_bounds__(1024)
+template <int DT, int VEC, int UNROLL>
+__global__ void __launch_bounds__(256)
 compress_kernel(const void* __restrict__ k, int64_t S, int H, int D,
                 int64_t sb, int64_t ss, int64_t sh, int bs, int heads_per_wg,
                 float* __restrict__ protos, int64_t NB) {
@@ -29,27 +29,14 @@ compress_kernel(const void* __restrict__ k, int64_t S, int H, int D,
     const int h = blockIdx.z * heads_per_wg + threadIdx.x / groups;
     const int d = (threadIdx.x % groups) * VEC;
     if (h >= H) return;
-    const int64_t base = b * sb + h * sh + d;
     const int64_t s0 = static_cast<int64_t>(j) * bs;
     const int64_t s1 = s0 + bs < S ? s0 + bs : S;
+    float acc[VEC];
+    block_sum<DT, VEC, UNROLL>(k, b * sb + h * sh + d, s0, s1, ss, acc);
     float* out = protos + ((static_cast<int64_t>(b) * NB + j) * H + h) * D + d;
-    const float inv_den = static_cast<float>(bs);
-    if constexpr (VEC == 2) {
-        float ax = 0.0f, ay = 0.0f;
-#pragma unroll 8
-        for (int64_t s = s0; s < s1; ++s) {
-            float2 v = load_pair<DT>(k, base + s * ss);
-            ax = ax + v.x;
-            ay = ay + v.y;
-        }
-        out[0] = ax / inv_den;
-        out[1] = ay / inv_den;
-    } else {
-        float a = 0.0f;
-#pragma unroll 8
-        for (int64_t s = s0; s < s1; ++s) a = a + load_elem<DT>(k, base + s * ss);
-        out[0] = a / inv_den;
-    }
+    const float den = static_cast<float>(bs);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) out[v] = acc[v] / den;
 }
 
 int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
@@ -62,43 +49,56 @@ int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, i
     const int groups = static_cast<int>(D / vec);
     int hpw = static_cast<int>(256 / groups);
     if (hpw < 1) hpw = 1;
+    if (groups > 256) return set_error(SPARDA_ERR_SHAPE, "compress: D/VEC > 256");
     if (hpw > H) hpw = static_cast<int>(H);
     dim3 grid(static_cast<unsigned>(NB), static_cast<unsigned>(B), static_cast<unsigned>(cdiv(H, hpw)));
     dim3 block(static_cast<unsigned>(groups * hpw));
-#define SPARDA_COMPRESS(DT_, V_)                                                          \
-    hipLaunchKernelGGL((compress_kernel<DT_, V_>), grid, block, 0, stream, k, S,          \
+#define SPARDA_COMPRESS(DT_, V_, U_)                                                      \
+    hipLaunchKernelGGL((compress_kernel<DT_, V_, U_>), grid, block, 0, stream, k, S,      \
                        static_cast<int>(H), static_cast<int>(D), sb, ss, sh,              \
                        static_cast<int>(bs), hpw, protos, NB)
+#define SPARDA_COMPRESS_U(DT_, V_)                                                        \
+    if (bs == 64) SPARDA_COMPRESS(DT_, V_, 64);                                           \
+    else if (bs == 32) SPARDA_COMPRESS(DT_, V_, 32);                                      \
+    else SPARDA_COMPRESS(DT_, V_, 0);
     if (dtype == SPARDA_F32) {
-        if (vec == 2) SPARDA_COMPRESS(SPARDA_F32, 2); else SPARDA_COMPRESS(SPARDA_F32, 1);
+        if (vec == 2) { SPARDA_COMPRESS_U(SPARDA_F32, 2) } else { SPARDA_COMPRESS_U(SPARDA_F32, 1) }
     } else {
-        if (vec == 2) SPARDA_COMPRESS(SPARDA_BF16, 2); else SPARDA_COMPRESS(SPARDA_BF16, 1);
+        if (vec == 2) { SPARDA_COMPRESS_U(SPARDA_BF16, 2) } else { SPARDA_COMPRESS_U(SPARDA_BF16, 1) }
     }
+#undef SPARDA_COMPRESS_U
 #undef SPARDA_COMPRESS
     return check_hip(hipGetLastError(), "compress_kernel");
 }
 
 // ---------------------------------------------------------------------------
-// router, one lane per query row. grid (ceil(Tq/ROWS), H, B), block ROWS.
-// The (b,h) prototypes are staged in LDS in chunks and read as broadcasts.
+// router: LPR lanes per query row, 256 threads = 256/LPR rows of one (b, h).
+// Lane `sub` of a row scores the blocks j = sub (mod LPR), two fma chains in
+// flight, and keeps its own top-k list; the LPR lists of a row are merged by
+// a butterfly of shuffles, after which every lane of the row holds the row's
+// top-k. The (b, h) prototypes are staged in LDS in chunks (rows padded to
+// DF+4 floats) and read as broadcasts.
 // ---------------------------------------------------------------------------
-constexpr int kRouteRows = 64;
+constexpr int kRouteThreads = 256;
 
-template <int FDT, int DF, int KMAX>
-__global__ void __launch_bounds__(kRouteRows)
+template <int FDT, int DF, int KMAX, int LPR>
+__global__ void __launch_bounds__(kRouteThreads)
 route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t fsh,
                   const float* __restrict__ protos, int64_t Tq, int H, int64_t NB, int bs,
                   int ke, int causal, int64_t score_pos0, int64_t query_pos0, float scale,
                   int chunk_blocks,
                   int32_t* __restrict__ topk, float* __restrict__ scores,
                   int32_t* __restrict__ sel, int32_t* __restrict__ n_sel, int cap) {
-    extern __shared__ float p_lds[];  // [chunk_blocks][DF]
+    constexpr int PS = DF + 4;                  // padded prototype row in LDS
+    constexpr int ROWS = kRouteThreads / LPR;
+    extern __shared__ float p_lds[];            // [chunk_blocks][PS]
     const int h = blockIdx.y;
     const int b = blockIdx.z;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRouteRows;
-    const int64_t t = t0 + threadIdx.x;
+    const int sub = threadIdx.x % LPR;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * ROWS;
+    const int64_t t = t0 + threadIdx.x / LPR;
     const bool active = t < Tq;
-    const int64_t t_last = (t0 + kRouteRows < Tq ? t0 + kRouteRows : Tq) - 1;
+    const int64_t t_last = (t0 + ROWS < Tq ? t0 + ROWS : Tq) - 1;
 
     int64_t jmax_wg = causal ? (score_pos0 + t_last) / bs : NB - 1;
     if (jmax_wg > NB - 1) jmax_wg = NB - 1;
@@ -106,13 +106,10 @@ route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t 
     if (limit > NB - 1) limit = NB - 1;
 
     float fr[DF];
-    if (active) {
-        const int64_t base = b * fsb + t * fst + h * fsh;
+    {
+        const int64_t base = b * fsb + (active ? t : t_last) * fst + h * fsh;
 #pragma unroll
         for (int d = 0; d < DF; ++d) fr[d] = load_elem<FDT>(f, base + d);
-    } else {
-#pragma unroll
-        for (int d = 0; d < DF; ++d) fr[d] = 0.0f;
     }
     const int64_t row = (static_cast<int64_t>(b) * H + h) * Tq + t;
     float* srow = (scores != nullptr && active) ? scores + row * NB : nullptr;
@@ -125,26 +122,55 @@ route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t 
         const int64_t c1 = (c0 + chunk_blocks - 1 < jmax_wg) ? c0 + chunk_blocks - 1 : jmax_wg;
         const int nblk = static_cast<int>(c1 - c0 + 1);
         __syncthreads();
-        for (int i = threadIdx.x; i < nblk * DF; i += kRouteRows) {
+        for (int i = threadIdx.x; i < nblk * DF; i += kRouteThreads) {
             const int jj = i / DF, d = i % DF;
-            p_lds[i] = pbh[(c0 + jj) * H * DF + d];
+            p_lds[jj * PS + d] = pbh[(c0 + jj) * H * DF + d];
         }
         __syncthreads();
         const int64_t jend = limit < c1 ? limit : c1;
-        for (int64_t j = c0; j <= jend; ++j) {
-            const float* pj = p_lds + (j - c0) * DF;
-            float acc = 0.0f;
+        int64_t j = c0 + sub;
+        for (; j + LPR <= jend; j += 2 * LPR) {
+            const float* pa = p_lds + (j - c0) * PS;
+            const float* pb = pa + LPR * PS;
+            float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DF; ++d) acc = __fmaf_rn(fr[d], pj[d], acc);
-            const float s = acc * scale;
-            if (srow) srow[j] = s;
-            best.push(rank64(s, static_cast<int32_t>(j)));
+            for (int d = 0; d < DF; ++d) {
+                a0 = __fmaf_rn(fr[d], pa[d], a0);
+                a1 = __fmaf_rn(fr[d], pb[d], a1);
+            }
+            const float s0 = a0 * scale, s1 = a1 * scale;
+            if (srow) {
+                srow[j] = s0;
+                srow[j + LPR] = s1;
+            }
+            best.push(rank64(s0, static_cast<int32_t>(j)));
+            best.push(rank64(s1, static_cast<int32_t>(j + LPR)));
         }
+        if (j <= jend) {
+            const float* pa = p_lds + (j - c0) * PS;
+            float a0 = 0.0f;
+#pragma unroll
+            for (int d = 0; d < DF; ++d) a0 = __fmaf_rn(fr[d], pa[d], a0);
+            const float s0 = a0 * scale;
+            if (srow) srow[j] = s0;
+            best.push(rank64(s0, static_cast<int32_t>(j)));
+        }
+    }
+    // butterfly merge of the LPR lists of each row (lanes of a row are adjacent)
+#pragma unroll
+    for (int lvl = 1; lvl < LPR; lvl <<= 1) {
+        uint64_t other[KMAX];
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) other[i] = __shfl_xor(best.r[i], lvl, kWave);
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i)
+            if (i < ke && other[i] != 0ull) best.push(other[i]);
     }
     if (!active) return;
     if (srow) {
-        for (int64_t j = limit + 1; j < NB; ++j) srow[j] = -__builtin_inff();
+        for (int64_t jj = limit + 1 + sub; jj < NB; jj += LPR) srow[jj] = -__builtin_inff();
     }
+    if (sub != 0) return;
     // slots not filled by a candidate take the masked blocks in ascending order
     int32_t picks[KMAX];
 #pragma unroll
@@ -174,18 +200,27 @@ static int launch_route_df(const void* f, int64_t fsb, int64_t fst, int64_t fsh,
                            int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel, int cap,
                            hipStream_t stream) {
     const int max_lds_floats = 16384;  // 64 KiB of prototypes per pass
-    int chunk = static_cast<int>(max_lds_floats / DF);
+    int chunk = static_cast<int>(max_lds_floats / (DF + 4));
     if (chunk > NB) chunk = static_cast<int>(NB);
-    dim3 grid(static_cast<unsigned>(cdiv(Tq, kRouteRows)), static_cast<unsigned>(H), static_cast<unsigned>(B));
-    const size_t lds = static_cast<size_t>(chunk) * DF * sizeof(float);
-#define SPARDA_ROUTE(KM_)                                                                    \
-    hipLaunchKernelGGL((route_rows_kernel<FDT, DF, KM_>), grid, dim3(kRouteRows), lds, stream, \
-                       f, fsb, fst, fsh, protos, Tq, static_cast<int>(H), NB,                \
-                       static_cast<int>(bs), ke, causal, score_pos0, query_pos0, scale,      \
+    const size_t lds = static_cast<size_t>(chunk) * (DF + 4) * sizeof(float);
+    // candidate blocks per row decide the lanes per row
+    const int64_t span = causal ? (score_pos0 + Tq - 1) / bs + 1 : NB;
+    const int lpr = span >= 32 ? 4 : (span >= 8 ? 2 : 1);
+    const int rows = kRouteThreads / lpr;
+    dim3 grid(static_cast<unsigned>(cdiv(Tq, rows)), static_cast<unsigned>(H), static_cast<unsigned>(B));
+#define SPARDA_ROUTE(KM_, L_)                                                                      \
+    hipLaunchKernelGGL((route_rows_kernel<FDT, DF, KM_, L_>), grid, dim3(kRouteThreads), lds, stream, \
+                       f, fsb, fst, fsh, protos, Tq, static_cast<int>(H), NB,                      \
+                       static_cast<int>(bs), ke, causal, score_pos0, query_pos0, scale,            \
                        chunk, topk, scores, sel, n_sel, cap)
-    if (ke <= 8) SPARDA_ROUTE(8);
-    else if (ke <= 16) SPARDA_ROUTE(16);
-    else SPARDA_ROUTE(32);
+#define SPARDA_ROUTE_L(KM_)                                       \
+    if (lpr == 4) SPARDA_ROUTE(KM_, 4);                           \
+    else if (lpr == 2) SPARDA_ROUTE(KM_, 2);                      \
+    else SPARDA_ROUTE(KM_, 1);
+    if (ke <= 8) { SPARDA_ROUTE_L(8) }
+    else if (ke <= 16) { SPARDA_ROUTE_L(16) }
+    else { SPARDA_ROUTE_L(32) }
+#undef SPARDA_ROUTE_L
 #undef SPARDA_ROUTE
     return check_hip(hipGetLastError(), "route_rows_kernel");
 }

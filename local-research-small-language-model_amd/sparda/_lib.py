@@ -10,7 +10,9 @@ import ctypes
 import os
 import threading
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsparda.so")
+# SPARDA_LIBRARY overrides the path (an alternative build of the same ABI)
+LIB_PATH = os.environ.get("SPARDA_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                            "libsparda.so")
 
 F32 = 0
 BF16 = 1

@@ -215,7 +215,7 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[tor
 
 
 class DecodeWorkspace:
-    """Zero-initialised device workspace for ``decode`` (reused across steps)."""
+    """Device workspace for ``decode``, grown on demand and reused across steps."""
 
     def __init__(self, device=None):
         self.device = torch.device(device) if device is not None else torch.device("cuda")
@@ -223,7 +223,7 @@ class DecodeWorkspace:
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self.buf
 
 

@@ -63,10 +63,9 @@ def test_argument_errors_are_reported_before_any_hip_call():
 
 
 def test_decode_workspace_size_formula():
-    # counters | scores | sel | n_sel | partials, each rounded up to 256 B
+    # the block scores of every (sequence, KV head), rounded up to 256 B
     up = lambda x: (x + 255) // 256 * 256
     B, S, Hq, Hkv, D, bs, k = 8, 16384, 12, 4, 64, 64, 8
     NB = S // bs
-    want = (up((B + B * Hkv) * 4) + up(B * Hkv * NB * 4) + up(B * Hkv * (k + 2) * 4) + up(B * Hkv * 4)
-            + up(B * Hq * (k + 2) * (D + 2) * 4))
+    want = up(B * Hkv * NB * 4)
     assert sparda.decode_workspace_bytes(B, S, Hq, Hkv, D, bs, k) == want
