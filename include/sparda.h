@@ -72,6 +72,17 @@ enum {
                                      (model/attention/sparse.py:250-251) */
 };
 
+/* Transfer methods of sparda_offload_fetch. */
+enum {
+    SPARDA_FETCH_KERNEL = 0, /* gather kernel reading the arena through its device
+                                mapping; indices stay on the GPU */
+    SPARDA_FETCH_DMA = 1,    /* hipMemcpyAsync per run of consecutive blocks; the
+                                selection is copied to the host first (one wait) */
+};
+
+/* Host-resident KV cache of one layer (opaque; see sparda_offload_create). */
+typedef struct sparda_offload* sparda_offload_t;
+
 /* Top-k algorithm selector for sparda_topk_scores. */
 enum {
     SPARDA_TOPK_AUTO = 0,
@@ -232,6 +243,102 @@ SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh,
                              void* out, int64_t out_sb,
                              void* workspace, size_t workspace_bytes,
                              void* stream);
+
+/*
+ * Single-token decode attention over a given block selection.
+ * Replaces the gather + validity mask + SDPA over selected blocks of
+ * SparseAttention._forward_decode_gather (model/attention/sparse.py:154-181)
+ * and of the offload backends (model/attention/offload.py:247-278,
+ * model/attention/async_offload.py:380-489).
+ *   sel/n_sel: [B,Hkv,sel_cap] / [B,Hkv] int32 (sel_cap <= 34); blocks
+ *     outside [0, (S-1)/bs] are skipped, n_sel must be >= 1 and should include
+ *     the block of position S-1. sel == NULL: every block of [0, S) (dense,
+ *     any length).
+ *   compact == 0: k/v are the cache [B,Smax,Hkv,D] strides (kv_sb, kv_ss,
+ *     kv_sh, 1), blocks are read in place.
+ *   compact == 1: k/v are compact block buffers, slot i of (b, g) holding
+ *     block sel[b,g,i]: element (b, g, i, r, d) at
+ *     b*kv_sb + g*kv_sh + (i*bs + r)*kv_ss + d (sparda_offload_fetch output).
+ *   k_new/v_new: optional [B,Hkv,D] (strides new_sb, new_sh, 1): the key and
+ *     value of position S-1, used instead of what k/v hold there.
+ *   q: [B,Hq,D]; out: [B,Hq*D] stride out_sb. 16-byte aligned rows.
+ */
+SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
+                                      const void* k, const void* v,
+                                      int64_t kv_sb, int64_t kv_ss, int64_t kv_sh,
+                                      int dtype, int compact,
+                                      const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
+                                      const void* k_new, const void* v_new,
+                                      int64_t new_sb, int64_t new_sh,
+                                      int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t block_size, float scale,
+                                      void* out, int64_t out_sb, void* stream);
+
+/*
+ * Decode-time block selection from fp32 block sums (prototype = sum / bs).
+ * Replaces the selection step of AsyncForecastOffloadAttention.prefetch
+ * (model/attention/async_offload.py:241-260) and of
+ * ForecastOffloadAttention._forward_offload_decode (offload.py:218-240)
+ * without the full-K host-to-device copy and recompression they do.
+ *   block_sums: [B,nb_stride,Hkv,D] fp32 covering tokens [0, len)
+ *     (sparda_offload_append / sparda_offload_rebuild_sums)
+ *   pos: the query position (len for the one-token lookahead of a prefetch);
+ *     own = pos / bs. If own + 1 <= top_k + 2 every block 0..own is selected.
+ *     Otherwise blocks j < ceil(len/bs) are scored as in sparda_route (mask
+ *     j > pos/bs in SPARDA_ROUTE_ABSOLUTE, j > 0 in SPARDA_ROUTE_REFERENCE)
+ *     and sel = ascending {0, own} U top-k, ties by lower index.
+ *   forecast: [B,Hkv,D] strides (f_sb, f_sh, 1); sel/n_sel: [B,Hkv,sel_cap] / [B,Hkv]
+ */
+SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                                    const float* block_sums,
+                                    int64_t B, int64_t Hkv, int64_t D, int64_t nb_stride,
+                                    int64_t len, int64_t pos, int64_t block_size, int64_t top_k,
+                                    int routing, float scale,
+                                    int32_t* sel, int32_t* n_sel, int64_t sel_cap, void* stream);
+
+/*
+ * Host-resident KV cache of one layer: pinned host arena (hipHostMalloc,
+ * mapped) of K and V, each [B][Hkv][max_seq][D] in `dtype`, zero-filled.
+ * Replaces the pinned cpu_k / cpu_v of OffloadedKVCache
+ * (model/attention/offload.py:29-65); the library owns the memory until
+ * sparda_offload_destroy. A handle is not re-entrant: calls on one handle
+ * must come from one host thread.
+ */
+SPARDA_API int sparda_offload_create(int64_t B, int64_t max_seq, int64_t Hkv, int64_t D, int dtype,
+                                     sparda_offload_t* out);
+SPARDA_API int sparda_offload_destroy(sparda_offload_t h);
+/* Host addresses of the K and V arenas ([B][Hkv][max_seq][D] each). */
+SPARDA_API int sparda_offload_host(sparda_offload_t h, void** k_host, void** v_host);
+
+/*
+ * Append tokens [pos, pos+n) from device memory to the arena.
+ * Replaces OffloadedKVCache.update (model/attention/offload.py:67-77).
+ *   k, v: [B,n,Hkv,D] device, strides (sb, st, sh, 1)
+ *   block_sums: optional [B,ceil(max_seq/bs),Hkv,D] fp32 device array; the
+ *     blocks touched get their sums continued sequentially from the block
+ *     start (restarted at 0 when pos <= the block start).
+ */
+SPARDA_API int sparda_offload_append(sparda_offload_t h, const void* k, const void* v,
+                                     int64_t sb, int64_t st, int64_t sh, int64_t pos, int64_t n,
+                                     int64_t block_size, float* block_sums, void* stream);
+
+/* Recompute block_sums of tokens [0, len) from the arena (through its device mapping). */
+SPARDA_API int sparda_offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t block_size,
+                                           float* block_sums, void* stream);
+
+/*
+ * Copy selected blocks (token rows below len) from the arena into compact
+ * device buffers k_dst/v_dst [B][Hkv][sel_cap][bs][D] (contiguous): slot i of
+ * (b, g) receives block sel[b,g,i] for i < n_sel[b,g]; rows at or beyond len
+ * and unused slots are not written.
+ * Replaces OffloadedKVCache.transfer_selected_blocks (offload.py:83-123) and
+ * AsyncOffloadedKVCache.async_transfer_selected_blocks (async_offload.py:55-112):
+ * no host gather, no per-call pinning. method: SPARDA_FETCH_KERNEL (never
+ * waits) or SPARDA_FETCH_DMA (sel_cap <= 1024; waits once for `stream`).
+ */
+SPARDA_API int sparda_offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
+                                    int64_t sel_cap, int64_t block_size, int64_t len, int method,
+                                    void* k_dst, void* v_dst, void* stream);
 
 #ifdef __cplusplus
 }

@@ -183,6 +183,13 @@ SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh, const vo
     const int64_t NB = cdiv(S, block_size);
     SPARDA_REQUIRE(NB <= 4096, SPARDA_ERR_SHAPE, "decode: more than 4096 blocks");
     SPARDA_REQUIRE(B <= 65535, SPARDA_ERR_SHAPE, "decode: B too large");
+    {
+        const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
+        const bool al = (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
+                        (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 && kv_sb % ve == 0 &&
+                        kv_ss % ve == 0 && kv_sh % ve == 0;
+        SPARDA_REQUIRE(al, SPARDA_ERR_STRIDE, "decode: K/V cache rows must be 16-byte aligned");
+    }
     const DecodeWs ws = decode_ws_layout(workspace, B, S, Hq, Hkv, D, block_size, top_k);
     SPARDA_REQUIRE(workspace_bytes >= ws.bytes, SPARDA_ERR_WORKSPACE, "decode: workspace %zu < %zu bytes",
                    workspace_bytes, ws.bytes);
@@ -191,6 +198,129 @@ SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh, const vo
     return launch_decode(q, q_sb, q_sh, k_cache, v_cache, kv_sb, kv_ss, kv_sh, dtype, forecast, f_dtype, f_sb,
                          f_sh, B, S, Hq, Hkv, D, block_size, top_k, routing, scale, protos_in, protos_out,
                          sel_out, n_sel_out, out, out_sb, ws, static_cast<hipStream_t>(stream));
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                      int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                                      const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
+                                      const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh,
+                                      int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t block_size, float scale, void* out, int64_t out_sb,
+                                      void* stream) {
+    SPARDA_REQUIRE(q && k && v && out, SPARDA_ERR_NULL, "decode_selected: null q/k/v/out");
+    SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "decode_selected: sel and n_sel go together");
+    SPARDA_REQUIRE(!k_new == !v_new, SPARDA_ERR_NULL, "decode_selected: k_new and v_new go together");
+    SPARDA_REQUIRE(!compact || sel, SPARDA_ERR_MODE, "decode_selected: compact buffers need a selection");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "decode_selected: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(B > 0 && S > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "decode_selected: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "decode_selected: head dim %lld not in {16,32,64,128}",
+                   (long long)D);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "decode_selected: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(!sel || (sel_cap >= 1 && sel_cap <= kMaxSelCap), SPARDA_ERR_SHAPE,
+                   "decode_selected: sel_cap must be in [1, %d]", kMaxSelCap);
+    SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "decode_selected: grid too large");
+    const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
+    SPARDA_REQUIRE(aligned16(k) && aligned16(v) && kv_sb % ve == 0 && kv_ss % ve == 0 && kv_sh % ve == 0,
+                   SPARDA_ERR_STRIDE, "decode_selected: K/V rows must be 16-byte aligned");
+    SPARDA_REQUIRE(!k_new || (aligned16(k_new) && aligned16(v_new) && new_sb % ve == 0 && new_sh % ve == 0),
+                   SPARDA_ERR_STRIDE, "decode_selected: k_new/v_new rows must be 16-byte aligned");
+    return launch_decode_selected(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap,
+                                  k_new, v_new, new_sb, new_sh, B, S, Hq, Hkv, D, block_size, scale, out,
+                                  out_sb, static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                                    const float* block_sums, int64_t B, int64_t Hkv, int64_t D,
+                                    int64_t nb_stride, int64_t len, int64_t pos, int64_t block_size,
+                                    int64_t top_k, int routing, float scale, int32_t* sel, int32_t* n_sel,
+                                    int64_t sel_cap, void* stream) {
+    SPARDA_REQUIRE(forecast && block_sums && sel && n_sel, SPARDA_ERR_NULL, "select_decode: null pointer");
+    SPARDA_REQUIRE(dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "select_decode: forecast dtype %d", f_dtype);
+    SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
+                   "select_decode: unknown routing %d", routing);
+    SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D <= kMaxHeadDim && block_size > 0, SPARDA_ERR_SHAPE,
+                   "select_decode: bad sizes (D must be <= %d)", kMaxHeadDim);
+    SPARDA_REQUIRE(len >= 1 && pos >= len - 1, SPARDA_ERR_SHAPE,
+                   "select_decode: need len >= 1 and pos >= len-1 (len=%lld pos=%lld)", (long long)len,
+                   (long long)pos);
+    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "select_decode: top_k out of range");
+    SPARDA_REQUIRE(sel_cap >= top_k + 2 && sel_cap <= kMaxSelCap, SPARDA_ERR_SHAPE,
+                   "select_decode: sel_cap must be in [top_k+2, %d]", kMaxSelCap);
+    SPARDA_REQUIRE(nb_stride >= cdiv(len, block_size), SPARDA_ERR_SHAPE, "select_decode: nb_stride too small");
+    SPARDA_REQUIRE(cdiv(len, block_size) <= 4096, SPARDA_ERR_SHAPE, "select_decode: more than 4096 blocks");
+    SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "select_decode: grid too large");
+    return launch_select_decode(forecast, f_dtype, f_sb, f_sh, block_sums, B, Hkv, D, nb_stride, len, pos,
+                                block_size, top_k, routing, scale, sel, n_sel, sel_cap,
+                                static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_offload_create(int64_t B, int64_t max_seq, int64_t Hkv, int64_t D, int dtype,
+                                     sparda_offload_t* out) {
+    SPARDA_REQUIRE(out, SPARDA_ERR_NULL, "offload_create: null output handle");
+    *out = nullptr;
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "offload_create: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(B > 0 && max_seq > 0 && Hkv > 0 && head_dim_ok(D), SPARDA_ERR_SHAPE,
+                   "offload_create: bad sizes (D must be 16/32/64/128)");
+    SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535 && max_seq <= (int64_t(1) << 31), SPARDA_ERR_SHAPE,
+                   "offload_create: sizes too large");
+    return offload_create(B, max_seq, Hkv, D, dtype, out);
+}
+
+SPARDA_API int sparda_offload_destroy(sparda_offload_t h) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_destroy: null handle");
+    return offload_destroy(h);
+}
+
+SPARDA_API int sparda_offload_host(sparda_offload_t h, void** k_host, void** v_host) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_host: null handle");
+    SPARDA_REQUIRE(k_host && v_host, SPARDA_ERR_NULL, "offload_host: null output");
+    offload_host(h, k_host, v_host);
+    return 0;
+}
+
+SPARDA_API int sparda_offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb, int64_t st,
+                                     int64_t sh, int64_t pos, int64_t n, int64_t block_size, float* block_sums,
+                                     void* stream) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_append: null handle");
+    SPARDA_REQUIRE(k && v, SPARDA_ERR_NULL, "offload_append: null k/v");
+    SPARDA_REQUIRE(n >= 1 && pos >= 0, SPARDA_ERR_SHAPE, "offload_append: need n >= 1, pos >= 0");
+    SPARDA_REQUIRE(pos + n <= offload_max_seq(h), SPARDA_ERR_CAPACITY,
+                   "offload_append: tokens [%lld, %lld) exceed the capacity %lld", (long long)pos,
+                   (long long)(pos + n), (long long)offload_max_seq(h));
+    SPARDA_REQUIRE(sb >= 0 && st >= 0 && sh >= 0, SPARDA_ERR_STRIDE, "offload_append: negative stride");
+    SPARDA_REQUIRE(!block_sums || block_size > 0, SPARDA_ERR_SHAPE, "offload_append: block_size must be > 0");
+    SPARDA_REQUIRE(n <= (int64_t(1) << 24), SPARDA_ERR_SHAPE, "offload_append: too many tokens in one call");
+    return offload_append(h, k, v, sb, st, sh, pos, n, block_size, block_sums, static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t block_size,
+                                           float* block_sums, void* stream) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_rebuild_sums: null handle");
+    SPARDA_REQUIRE(block_sums, SPARDA_ERR_NULL, "offload_rebuild_sums: null block_sums");
+    SPARDA_REQUIRE(block_size > 0 && len >= 1 && len <= offload_max_seq(h), SPARDA_ERR_SHAPE,
+                   "offload_rebuild_sums: bad len/block_size");
+    return offload_rebuild_sums(h, len, block_size, block_sums, static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
+                                    int64_t sel_cap, int64_t block_size, int64_t len, int method, void* k_dst,
+                                    void* v_dst, void* stream) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_fetch: null handle");
+    SPARDA_REQUIRE(sel && n_sel && k_dst && v_dst, SPARDA_ERR_NULL, "offload_fetch: null pointer");
+    SPARDA_REQUIRE(method == SPARDA_FETCH_KERNEL || method == SPARDA_FETCH_DMA, SPARDA_ERR_MODE,
+                   "offload_fetch: unknown method %d", method);
+    SPARDA_REQUIRE(block_size > 0 && len >= 0 && len <= offload_max_seq(h), SPARDA_ERR_SHAPE,
+                   "offload_fetch: bad len/block_size");
+    SPARDA_REQUIRE(sel_cap >= 1 && sel_cap <= (method == SPARDA_FETCH_DMA ? kMaxFetchSlots : 65535),
+                   SPARDA_ERR_SHAPE, "offload_fetch: sel_cap %lld out of range", (long long)sel_cap);
+    SPARDA_REQUIRE(aligned16(k_dst) && aligned16(v_dst), SPARDA_ERR_STRIDE,
+                   "offload_fetch: destinations must be 16-byte aligned");
+    return offload_fetch(h, sel, n_sel, sel_cap, block_size, len, method, k_dst, v_dst,
+                         static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

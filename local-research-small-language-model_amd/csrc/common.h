@@ -10,6 +10,8 @@
 namespace sparda {
 
 constexpr int kWave = 64;
+constexpr int kMaxSelCap = 34;    // selection list capacity: top_k (<= 32) + sink + own block
+constexpr int kMaxHeadDim = 128;
 
 // ---------------------------------------------------------------------------
 // element loads (bf16 is widened exactly to fp32)

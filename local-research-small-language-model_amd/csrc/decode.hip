@@ -21,6 +21,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "attend.h"
+#include "select.h"
 
 namespace sparda {
 
@@ -101,53 +102,6 @@ decode_score_kernel(const void* __restrict__ kc, int64_t kv_sb, int64_t kv_ss, i
 }
 
 // ---------------------------------------------------------------------------
-// Wavefront top-k selection by ballot threshold search.
-// The wave holds keys[j] (orderable score keys, index = block) for
-// j = e*64 + lane in kreg[e]. Writes to sel_lds the ascending list
-// ({0, own} U topk) restricted to blocks <= own, returns its length.
-// topk = the k largest keys, equal keys by lower index. Called by a whole
-// wavefront; all control flow is wave-uniform.
-// ---------------------------------------------------------------------------
-template <int CH>
-__device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, int k, int own,
-                                           int32_t* sel_lds) {
-    const int lane = threadIdx.x % kWave;
-    // T = the k-th largest key: the largest T with count(key >= T) >= k
-    uint32_t T = 0;
-    for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t c = T | (1u << bit);
-        int cnt = 0;
-#pragma unroll
-        for (int e = 0; e < CH; ++e) cnt += __popcll(__ballot(e * kWave + lane < n && kreg[e] >= c));
-        if (cnt >= k) T = c;
-    }
-    int above = 0;
-#pragma unroll
-    for (int e = 0; e < CH; ++e) above += __popcll(__ballot(e * kWave + lane < n && kreg[e] > T));
-    int need_eq = k - above;  // keys equal to T, taken in index order
-    const uint64_t lanes_below = (1ull << lane) - 1ull;
-    int m = 0;
-#pragma unroll
-    for (int e = 0; e < CH; ++e) {
-        const int j = e * kWave + lane;
-        const bool in = j < n;
-        const uint64_t gt = __ballot(in && kreg[e] > T);
-        uint64_t eq = __ballot(in && kreg[e] == T);
-        uint64_t keep = 0;
-        for (; need_eq > 0 && eq != 0; --need_eq) {
-            const uint64_t low = eq & (~eq + 1ull);
-            keep |= low;
-            eq ^= low;
-        }
-        const uint64_t forced = __ballot(in && (j == 0 || j == own));
-        const uint64_t take = (gt | keep | forced) & __ballot(in && j <= own);
-        if ((take >> lane) & 1ull) sel_lds[m + __popcll(take & lanes_below)] = j;
-        m += __popcll(take);
-    }
-    return m;
-}
-
-// ---------------------------------------------------------------------------
 // launch 2: selection + attention over the selected blocks + merge, one
 // workgroup per (sequence, KV head), W wavefronts; wavefront w serves the
 // selected blocks w, w+W, ... sel_mode: 0 top-k of the launch-1 scores,
@@ -159,7 +113,7 @@ __device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, in
 // region. After a barrier the partials are merged in slot order.
 // ---------------------------------------------------------------------------
 constexpr int kMaxGroup = 16;   // query heads per KV head
-constexpr int kMaxSlots = 34;   // k + 2 with k <= 32
+constexpr int kMaxSlots = kMaxSelCap;
 constexpr int kHeadBatch = 4;
 
 template <int DT>
@@ -185,6 +139,9 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int64_t S, int Hq, int H, int bs,
                      int64_t NB, int k, int sel_mode, int cap, float scale_log2,
                      const float* __restrict__ ws_scores,
+                     const int32_t* __restrict__ sel_in, const int32_t* __restrict__ n_sel_in,
+                     int compact, const void* __restrict__ k_new, const void* __restrict__ v_new,
+                     int64_t new_sb, int64_t new_sh,
                      int32_t* __restrict__ sel_out, int32_t* __restrict__ n_sel_out,
                      void* __restrict__ out, int64_t out_sb) {
     using E = typename KvElem<DT>::T;
@@ -204,8 +161,8 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     const int nwaves = blockDim.x / kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
     const int cb = static_cast<int>((S - 1) / bs);
-    float* part_all = reinterpret_cast<float*>(dyn);                       // [cap][R][DH+2]
-    const size_t part_bytes = ((static_cast<size_t>(cap) * R * (DH + 2) * 4) + 15) & ~static_cast<size_t>(15);
+    float* part_all = reinterpret_cast<float*>(dyn);                       // [nwaves][R][DH+2]
+    const size_t part_bytes = ((static_cast<size_t>(nwaves) * R * (DH + 2) * 4) + 15) & ~static_cast<size_t>(15);
     unsigned char* wbase = dyn + part_bytes + wave * attend_wave_bytes<DT, DH>();
     float* p_lds = reinterpret_cast<float*>(wbase);                         // [4][64]
     E* v_lds = reinterpret_cast<E*>(wbase + kHeadBatch * 64 * 4);           // [64][VR]
@@ -226,8 +183,11 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             }
             m = wave_select<CH>(kreg, static_cast<int>(NB), k, cb, sel_lds);
         } else if (sel_mode == 1) {
-            for (int j = lane; j <= cb; j += kWave) sel_lds[j] = j;
-            m = cb + 1;
+            m = cb + 1;  // slot w is block w; sel_lds is not used
+        } else if (sel_mode == 3) {
+            m = n_sel_in[bg];
+            m = m < 0 ? 0 : (m > cap ? cap : m);
+            if (lane < m) sel_lds[lane] = sel_in[bg * cap + lane];
         } else {
             int lo = cb - k + 1;
             if (lo < 0) lo = 0;
@@ -240,15 +200,33 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     __syncthreads();
     const int n = n_lds;
     if (threadIdx.x < cap) {
-        if (sel_out != nullptr) sel_out[bg * cap + threadIdx.x] = threadIdx.x < n ? sel_lds[threadIdx.x] : -1;
-        if (threadIdx.x == 0 && n_sel_out != nullptr) n_sel_out[bg] = n;
+        const int i = threadIdx.x;
+        if (sel_out != nullptr) sel_out[bg * cap + i] = i < n ? (sel_mode == 1 ? i : sel_lds[i]) : -1;
+        if (i == 0 && n_sel_out != nullptr) n_sel_out[bg] = n;
     }
 
+    // this wave's running partial (m, l, o[DH]) per head, merged block by block
+    float* part = part_all + static_cast<int64_t>(wave) * R * (DH + 2);
+    for (int hh = 0; hh < R; ++hh) {
+        if (lane == 0) {
+            part[hh * (DH + 2)] = -__builtin_inff();
+            part[hh * (DH + 2) + 1] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+            const int d = lane + i * kWave;
+            if (d < DH) part[hh * (DH + 2) + 2 + d] = 0.0f;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+
     for (int w = wave; w < n; w += nwaves) {
-        const int64_t j = sel_lds[w];
+        const int64_t j = sel_mode == 1 ? w : sel_lds[w];
+        if (j < 0 || j > cb) continue;  // not a block of [0, S): nothing to attend
         const int64_t s0 = j * bs;
         const int64_t s1 = s0 + bs < S ? s0 + bs : S;
-        float* part = part_all + static_cast<int64_t>(w) * R * (DH + 2);
+        // storage row of position s0: the cache row, or slot w of a compact buffer
+        const int64_t row0 = compact ? static_cast<int64_t>(w) * bs : s0;
         for (int hb = 0; hb < R; hb += kHeadBatch) {
             const int nh = R - hb < kHeadBatch ? R - hb : kHeadBatch;
             float mrun[kHeadBatch], lrun[kHeadBatch], orun[kHeadBatch][DPL];
@@ -266,14 +244,21 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 constexpr int RC = DH / EPV;            // chunks per row
                 constexpr int NC = 64 * RC / kWave;     // chunks per lane
                 uint4 kraw[NC], vraw[NC];
-                const int64_t base = b * kv_sb + c0 * kv_ss + g * kv_sh;
+                const int64_t base = b * kv_sb + (row0 + (c0 - s0)) * kv_ss + g * kv_sh;
+                const int64_t nbase = b * new_sb + g * new_sh;
 #pragma unroll
                 for (int i = 0; i < NC; ++i) {
                     const int c = lane + i * kWave;
                     const int row = c / RC, col = (c % RC) * EPV;
                     if (row < nk) {
-                        kraw[i] = *reinterpret_cast<const uint4*>(static_cast<const E*>(kc) + base + row * kv_ss + col);
-                        vraw[i] = *reinterpret_cast<const uint4*>(static_cast<const E*>(vc) + base + row * kv_ss + col);
+                        if (k_new != nullptr && c0 + row == S - 1) {
+                            // the new token, supplied apart from the (prefetched) blocks
+                            kraw[i] = *reinterpret_cast<const uint4*>(static_cast<const E*>(k_new) + nbase + col);
+                            vraw[i] = *reinterpret_cast<const uint4*>(static_cast<const E*>(v_new) + nbase + col);
+                        } else {
+                            kraw[i] = *reinterpret_cast<const uint4*>(static_cast<const E*>(kc) + base + row * kv_ss + col);
+                            vraw[i] = *reinterpret_cast<const uint4*>(static_cast<const E*>(vc) + base + row * kv_ss + col);
+                        }
                     } else {
                         kraw[i] = make_uint4(0u, 0u, 0u, 0u);
                         vraw[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -360,29 +345,37 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 }
                 __builtin_amdgcn_wave_barrier();
             }
+            // merge this block's (m, l, o) into the wave's partial
             for (int hh = 0; hh < nh; ++hh) {
                 float* pp = part + (hb + hh) * (DH + 2);
-                if (lane == 0) {
-                    pp[0] = mrun[hh];
-                    pp[1] = lrun[hh];
-                }
+                const float pm = pp[0];
+                const float M = fmaxf(pm, mrun[hh]);
+                const float a_old = exp2f(pm - M);
+                const float a_new = exp2f(mrun[hh] - M);
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) {
                     const int d = lane + i * kWave;
-                    if (d < DH) pp[2 + d] = orun[hh][i];
+                    if (d < DH) pp[2 + d] = pp[2 + d] * a_old + orun[hh][i] * a_new;
                 }
+                __builtin_amdgcn_wave_barrier();
+                if (lane == 0) {
+                    pp[0] = M;
+                    pp[1] = pp[1] * a_old + lrun[hh] * a_new;
+                }
+                __builtin_amdgcn_wave_barrier();
             }
         }
     }
     __syncthreads();
 
-    // merge the partials in slot order
+    // merge the wave partials in wave order (waves without a block hold m = -inf, l = 0)
+    const int nw = n < nwaves ? n : nwaves;
     for (int e = threadIdx.x; e < R * DH; e += blockDim.x) {
         const int hh = e / DH, d = e % DH;
         float M = -__builtin_inff();
-        for (int w = 0; w < n; ++w) M = fmaxf(M, part_all[(w * R + hh) * (DH + 2)]);
+        for (int w = 0; w < nw; ++w) M = fmaxf(M, part_all[(w * R + hh) * (DH + 2)]);
         float num = 0.0f, den = 0.0f;
-        for (int w = 0; w < n; ++w) {
+        for (int w = 0; w < nw; ++w) {
             const float* ps = part_all + (w * R + hh) * (DH + 2);
             const float wt = exp2f(ps[0] - M);
             den = den + wt * ps[1];
@@ -394,6 +387,62 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
 }
 
 // ---------------------------------------------------------------------------
+struct AttendArgs {
+    const void* q; int64_t q_sb, q_sh;
+    const void* kc; const void* vc; int64_t kv_sb, kv_ss, kv_sh;
+    int dtype; int64_t B, S, Hq, Hkv, D, bs, k;
+    int sel_mode; int cap; float scale;
+    const float* scores;
+    const int32_t* sel_in; const int32_t* n_sel_in; int compact;
+    const void* k_new; const void* v_new; int64_t new_sb, new_sh;
+    int32_t* sel_out; int32_t* n_sel_out;
+    void* out; int64_t out_sb;
+};
+
+static int launch_attend(const AttendArgs& a, hipStream_t stream) {
+    const int64_t NB = cdiv(a.S, a.bs);
+    const float scale_log2 = a.scale * kLog2e;
+    const int Hq_i = static_cast<int>(a.Hq), Hkv_i = static_cast<int>(a.Hkv);
+    const int64_t R = a.Hq / a.Hkv;
+    // most blocks one workgroup can attend: the selection capacity, or every block when dense
+    const int64_t max_blocks = a.sel_mode == 1 ? NB : a.cap;
+    constexpr size_t kLdsBudget = 150 * 1024;
+    dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
+#define SPARDA_ATT(DT_, DH_, CH_)                                                                        \
+    do {                                                                                                 \
+        const size_t wb = attend_wave_bytes<DT_, DH_>();                                                 \
+        const size_t pb = static_cast<size_t>(R) * (DH_ + 2) * 4;                                        \
+        int waves = max_blocks < kAttendMaxWaves ? static_cast<int>(max_blocks) : kAttendMaxWaves;       \
+        while (waves > 1 && ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb > kLdsBudget) --waves; \
+        const size_t lds = ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb;                  \
+        hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_>), grid2, dim3(waves * kWave), lds, stream, \
+                           a.q, a.q_sb, a.q_sh, a.kc, a.vc, a.kv_sb, a.kv_ss, a.kv_sh, a.S, Hq_i, Hkv_i,  \
+                           static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
+                           scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
+                           a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb);                 \
+    } while (0)
+#define SPARDA_ATT_C(DT_, DH_)                            \
+    if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
+    else if (NB <= 1024) SPARDA_ATT(DT_, DH_, 16);        \
+    else SPARDA_ATT(DT_, DH_, 64);
+#define SPARDA_ATT_D(DT_)                                         \
+    switch (a.D) {                                                \
+        case 16: { SPARDA_ATT_C(DT_, 16) } break;                 \
+        case 32: { SPARDA_ATT_C(DT_, 32) } break;                 \
+        case 64: { SPARDA_ATT_C(DT_, 64) } break;                 \
+        default: { SPARDA_ATT_C(DT_, 128) } break;                \
+    }
+    if (a.dtype == SPARDA_BF16) {
+        SPARDA_ATT_D(SPARDA_BF16);
+    } else {
+        SPARDA_ATT_D(SPARDA_F32);
+    }
+#undef SPARDA_ATT_D
+#undef SPARDA_ATT_C
+#undef SPARDA_ATT
+    return check_hip(hipGetLastError(), "decode_attend_kernel");
+}
+
 int launch_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kc, const void* vc,
                   int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const void* f, int fdtype,
                   int64_t f_sb, int64_t f_sh, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
@@ -448,41 +497,22 @@ int launch_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kc, con
         int rc = check_hip(hipGetLastError(), "decode_score_kernel");
         if (rc) return rc;
     }
-    const float scale_log2 = scale * kLog2e;
-    const int Hq_i = static_cast<int>(Hq), Hkv_i = static_cast<int>(Hkv);
-    const size_t part_bytes = ((static_cast<size_t>(cap) * (Hq / Hkv) * (D + 2) * 4) + 15) & ~static_cast<size_t>(15);
-    constexpr size_t kLdsBudget = 150 * 1024;
-    dim3 grid2(static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
-#define SPARDA_ATT(DT_, DH_, CH_)                                                                        \
-    do {                                                                                                 \
-        const size_t wb = attend_wave_bytes<DT_, DH_>();                                                 \
-        int waves = cap < kAttendMaxWaves ? cap : kAttendMaxWaves;                                                                 \
-        while (waves > 1 && part_bytes + waves * wb > kLdsBudget) --waves;                              \
-        hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_>), grid2, dim3(waves * kWave),            \
-                           part_bytes + waves * wb, stream, q, q_sb, q_sh, kc, vc, kv_sb, kv_ss, kv_sh,   \
-                           S, Hq_i, Hkv_i, static_cast<int>(bs), NB, static_cast<int>(k), sel_mode, cap, \
-                           scale_log2, ws.scores, sel_out, n_sel_out, out, out_sb);                      \
-    } while (0)
-#define SPARDA_ATT_C(DT_, DH_)                            \
-    if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
-    else if (NB <= 1024) SPARDA_ATT(DT_, DH_, 16);        \
-    else SPARDA_ATT(DT_, DH_, 64);
-#define SPARDA_ATT_D(DT_)                                         \
-    switch (D) {                                                  \
-        case 16: { SPARDA_ATT_C(DT_, 16) } break;                 \
-        case 32: { SPARDA_ATT_C(DT_, 32) } break;                 \
-        case 64: { SPARDA_ATT_C(DT_, 64) } break;                 \
-        default: { SPARDA_ATT_C(DT_, 128) } break;                \
-    }
-    if (dtype == SPARDA_BF16) {
-        SPARDA_ATT_D(SPARDA_BF16);
-    } else {
-        SPARDA_ATT_D(SPARDA_F32);
-    }
-#undef SPARDA_ATT_D
-#undef SPARDA_ATT_C
-#undef SPARDA_ATT
-    return check_hip(hipGetLastError(), "decode_attend_kernel");
+    AttendArgs a{q, q_sb, q_sh, kc, vc, kv_sb, kv_ss, kv_sh, dtype, B, S, Hq, Hkv, D, bs, k,
+                 sel_mode, cap, scale, ws.scores, nullptr, nullptr, 0, nullptr, nullptr, 0, 0,
+                 sel_out, n_sel_out, out, out_sb};
+    return launch_attend(a, stream);
+}
+
+int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                           int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                           const int32_t* sel, const int32_t* n_sel, int64_t cap, const void* k_new,
+                           const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B, int64_t S,
+                           int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out,
+                           int64_t out_sb, hipStream_t stream) {
+    AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S, Hq, Hkv, D, bs, cap > 2 ? cap - 2 : 0,
+                 sel == nullptr ? 1 : 3, static_cast<int>(sel == nullptr ? 0 : cap), scale, nullptr,
+                 sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb};
+    return launch_attend(a, stream);
 }
 
 }  // namespace sparda

@@ -42,6 +42,30 @@ int launch_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kc, con
                   float* protos_out, int32_t* sel_out, int32_t* n_sel_out, void* out, int64_t out_sb,
                   const DecodeWs& ws, hipStream_t stream);
 
+int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                           int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                           const int32_t* sel, const int32_t* n_sel, int64_t cap, const void* k_new,
+                           const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B, int64_t S,
+                           int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out,
+                           int64_t out_sb, hipStream_t stream);
+
+int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
+                         int64_t H, int64_t D, int64_t nb_stride, int64_t len, int64_t pos, int64_t bs,
+                         int64_t k, int routing, float scale, int32_t* sel, int32_t* n_sel, int64_t cap,
+                         hipStream_t stream);
+
+// host-resident KV arena (offload.hip)
+constexpr int64_t kMaxFetchSlots = 1024;  // selection capacity of a DMA fetch
+int offload_create(int64_t B, int64_t Smax, int64_t H, int64_t D, int dtype, sparda_offload_t* out);
+int offload_destroy(sparda_offload_t h);
+void offload_host(sparda_offload_t h, void** k, void** v);
+int64_t offload_max_seq(sparda_offload_t h);
+int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb, int64_t st, int64_t sh,
+                   int64_t pos, int64_t n, int64_t bs, float* sums, hipStream_t stream);
+int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sums, hipStream_t stream);
+int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t bs,
+                  int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream);
+
 int launch_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
                    const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
                    const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,

@@ -100,4 +100,51 @@ __device__ __forceinline__ void wg_topk(uint64_t* ranks, int n, int ke, int32_t*
     }
 }
 
+// ---------------------------------------------------------------------------
+// Wavefront top-k selection by ballot threshold search.
+// The wave holds keys[j] (orderable score keys, index = block) for
+// j = e*64 + lane in kreg[e]. Writes to sel_lds the ascending list
+// ({0, own} U topk) restricted to blocks <= own, returns its length.
+// topk = the k largest keys, equal keys by lower index. Called by a whole
+// wavefront; all control flow is wave-uniform.
+// ---------------------------------------------------------------------------
+template <int CH>
+__device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, int k, int own,
+                                           int32_t* sel_lds) {
+    const int lane = threadIdx.x % kWave;
+    // T = the k-th largest key: the largest T with count(key >= T) >= k
+    uint32_t T = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = T | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) cnt += __popcll(__ballot(e * kWave + lane < n && kreg[e] >= c));
+        if (cnt >= k) T = c;
+    }
+    int above = 0;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) above += __popcll(__ballot(e * kWave + lane < n && kreg[e] > T));
+    int need_eq = k - above;  // keys equal to T, taken in index order
+    const uint64_t lanes_below = (1ull << lane) - 1ull;
+    int m = 0;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+        const int j = e * kWave + lane;
+        const bool in = j < n;
+        const uint64_t gt = __ballot(in && kreg[e] > T);
+        uint64_t eq = __ballot(in && kreg[e] == T);
+        uint64_t keep = 0;
+        for (; need_eq > 0 && eq != 0; --need_eq) {
+            const uint64_t low = eq & (~eq + 1ull);
+            keep |= low;
+            eq ^= low;
+        }
+        const uint64_t forced = __ballot(in && (j == 0 || j == own));
+        const uint64_t take = (gt | keep | forced) & __ballot(in && j <= own);
+        if ((take >> lane) & 1ull) sel_lds[m + __popcll(take & lanes_below)] = j;
+        m += __popcll(take);
+    }
+    return m;
+}
+
 }  // namespace sparda

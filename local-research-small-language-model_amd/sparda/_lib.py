@@ -24,6 +24,9 @@ SEL_DENSE = 0
 SEL_WINDOW_DECODE = 1
 SEL_WINDOW_PREFILL = 2
 
+FETCH_KERNEL = 0
+FETCH_DMA = 1
+
 TOPK_AUTO = 0
 TOPK_ROWS = 1
 TOPK_WAVE = 2
@@ -56,6 +59,16 @@ SIGNATURES = {
     "sparda_decode": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _i64,
                              _i64, _i64, _i64, _i64, _i64, _i64, _int, _f32, _p, _p, _p, _p, _p, _i64,
                              _p, _size, _p]),
+    "sparda_decode_selected": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _p, _p,
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
+    "sparda_select_decode": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                    _int, _f32, _p, _p, _i64, _p]),
+    "sparda_offload_create": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_p)]),
+    "sparda_offload_destroy": (_int, [_p]),
+    "sparda_offload_host": (_int, [_p, ctypes.POINTER(_p), ctypes.POINTER(_p)]),
+    "sparda_offload_append": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
+    "sparda_offload_rebuild_sums": (_int, [_p, _i64, _i64, _p, _p]),
+    "sparda_offload_fetch": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

@@ -289,3 +289,170 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, S: int
     if want_protos or want_sel:
         return out, {"protos": protos_out, "sel": sel, "n_sel": n_sel}
     return out
+
+
+def decode_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, block_size: int,
+                    sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None,
+                    compact: bool = False, k_new: Optional[torch.Tensor] = None,
+                    v_new: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode attention of q [B,Hq,D] (position S-1) over the blocks sel[b,g,:n_sel]
+    (model/attention/sparse.py:154-181; offload.py:247-278; async_offload.py:380-489).
+
+    compact=False: k/v are caches [B,Smax,Hkv,D] read in place. compact=True:
+    k/v are fetched block buffers [B,Hkv,cap,bs,D], slot i holding block
+    sel[b,g,i]. sel=None: dense over [0, S). k_new/v_new [B,Hkv,D]: the key and
+    value of position S-1 (overriding what k/v hold there).
+    """
+    dev = require_device(q, k, v, sel, n_sel, k_new, v_new)
+    _inference_only(q, k, v, k_new, v_new)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q, k and v must share a dtype")
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    if k.stride() != v.stride():
+        raise ValueError("sparda: k and v must share strides")
+    B, Hq, D = q.shape
+    if compact:
+        if sel is None:
+            raise ValueError("sparda: compact block buffers need a selection")
+        _, Hkv, cap, bs_, _ = k.shape
+        if bs_ != block_size or cap != sel.shape[-1]:
+            raise ValueError("sparda: compact buffers must be [B,Hkv,sel_cap,block_size,D]")
+        kv_sb, kv_sh, _, kv_ss, _ = k.stride()
+    else:
+        Hkv = k.shape[2]
+        if S > k.shape[1] or S <= 0:
+            raise ValueError(f"sparda: S={S} outside the cache (capacity {k.shape[1]})")
+        kv_sb, kv_ss, kv_sh, _ = k.stride()
+    cap = 0
+    if sel is not None:
+        if sel.dtype != torch.int32 or n_sel is None or n_sel.dtype != torch.int32:
+            raise TypeError("sparda: sel / n_sel must be int32 tensors")
+        sel, n_sel = sel.contiguous(), n_sel.contiguous()
+        cap = sel.shape[-1]
+    nsb = nsh = 0
+    if k_new is not None:
+        k_new = _rowmajor(k_new.reshape(B, Hkv, D))
+        v_new = _rowmajor(v_new.reshape(B, Hkv, D))
+        if k_new.stride() != v_new.stride():
+            raise ValueError("sparda: k_new and v_new must share strides")
+        nsb, nsh, _ = k_new.stride()
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
+    qsb, qsh, _ = q.stride()
+    call("sparda_decode_selected", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
+         _dtype_code(q), int(compact), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap,
+         k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
+         nsb, nsh, B, S, Hq, Hkv, D, block_size, float(scale), out.data_ptr(), out.stride(0), _stream(dev))
+    return out
+
+
+def select_decode(forecast: torch.Tensor, block_sums: torch.Tensor, length: int, pos: int, block_size: int,
+                  top_k: int, routing: str = "reference", scale: Optional[float] = None,
+                  sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None):
+    """Decode selection from block sums [B,NBmax,Hkv,D] fp32 covering tokens [0, length),
+    for the query at position `pos` (model/attention/async_offload.py:196-260).
+    Returns sel [B,Hkv,top_k+2] int32 (ascending, -1 padded) and n_sel [B,Hkv]."""
+    dev = require_device(forecast, block_sums, sel, n_sel)
+    if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
+        raise TypeError("sparda: block_sums must be contiguous float32")
+    B, nbs, Hkv, D = block_sums.shape
+    forecast = _rowmajor(forecast.reshape(B, Hkv, -1) if forecast.dim() != 3 else forecast)
+    if routing not in ("reference", "absolute"):
+        raise ValueError(f"sparda: routing must be 'reference' or 'absolute', got {routing!r}")
+    if scale is None:
+        scale = default_scale(forecast.shape[-1])
+    cap = top_k + 2
+    if sel is None:
+        sel = torch.empty((B, Hkv, cap), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, Hkv), dtype=torch.int32, device=dev)
+    fsb, fsh, _ = forecast.stride()
+    call("sparda_select_decode", forecast.data_ptr(), _dtype_code(forecast), fsb, fsh, block_sums.data_ptr(),
+         B, Hkv, D, nbs, length, pos, block_size, top_k,
+         _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE, float(scale),
+         sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], _stream(dev))
+    return sel, n_sel
+
+
+class OffloadArena:
+    """Pinned host KV arena of one layer owned by libsparda (sparda_offload_create).
+
+    Layout of each of K and V: [B][Hkv][max_seq][D]. ``k_host`` / ``v_host`` are
+    CPU tensor views of it in the reference's [B,max_seq,Hkv,D] order.
+    """
+
+    def __init__(self, B: int, max_seq: int, Hkv: int, D: int, dtype: torch.dtype, device=None):
+        import ctypes
+        self.B, self.max_seq, self.Hkv, self.D, self.dtype = B, max_seq, Hkv, D, dtype
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        with torch.cuda.device(self.device):
+            h = ctypes.c_void_p()
+            call("sparda_offload_create", B, max_seq, Hkv, D, _DT[dtype], ctypes.byref(h))
+        self._h = h
+        kp, vp = ctypes.c_void_p(), ctypes.c_void_p()
+        call("sparda_offload_host", self._h, ctypes.byref(kp), ctypes.byref(vp))
+        n = B * Hkv * max_seq * D
+        esz = torch.empty((), dtype=dtype).element_size()
+
+        def view(ptr):
+            buf = (ctypes.c_uint8 * (n * esz)).from_address(ptr.value)
+            t = torch.frombuffer(buf, dtype=torch.uint8).view(dtype).view(B, Hkv, max_seq, D)
+            return t.transpose(1, 2)
+
+        self.k_host = view(kp)
+        self.v_host = view(vp)
+
+    @property
+    def handle(self):
+        if self._h is None:
+            raise RuntimeError("sparda: offload arena already destroyed")
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            self.k_host = self.v_host = None
+            call("sparda_offload_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def append(self, k: torch.Tensor, v: torch.Tensor, pos: int, block_size: int = 0,
+               block_sums: Optional[torch.Tensor] = None) -> None:
+        """Tokens [pos, pos+n) of k, v [B,n,Hkv,D] (device) into the arena (+ block sums)."""
+        dev = require_device(k, v, block_sums)
+        k, v = _rowmajor(k), _rowmajor(v)
+        if k.dtype != self.dtype or v.dtype != self.dtype:
+            raise TypeError(f"sparda: arena holds {self.dtype}, got {k.dtype}/{v.dtype}")
+        if k.stride() != v.stride():
+            k, v = k.contiguous(), v.contiguous()
+        B, n, Hkv, D = k.shape
+        if (B, Hkv, D) != (self.B, self.Hkv, self.D):
+            raise ValueError("sparda: k/v shape does not match the arena")
+        sb, st, sh, _ = k.stride()
+        call("sparda_offload_append", self.handle, k.data_ptr(), v.data_ptr(), sb, st, sh, pos, n, block_size,
+             block_sums.data_ptr() if block_sums is not None else None, _stream(dev))
+
+    def rebuild_sums(self, length: int, block_size: int, block_sums: torch.Tensor) -> None:
+        dev = require_device(block_sums)
+        call("sparda_offload_rebuild_sums", self.handle, length, block_size, block_sums.data_ptr(), _stream(dev))
+
+    def fetch(self, sel: torch.Tensor, n_sel: torch.Tensor, block_size: int, length: int,
+              k_dst: torch.Tensor, v_dst: torch.Tensor, method: int = _lib.FETCH_KERNEL) -> None:
+        """Blocks sel[b,g,:n_sel] (rows < length) into k_dst/v_dst [B,Hkv,cap,bs,D]."""
+        dev = require_device(sel, n_sel, k_dst, v_dst)
+        if not (k_dst.is_contiguous() and v_dst.is_contiguous()):
+            raise ValueError("sparda: fetch destinations must be contiguous")
+        cap = sel.shape[-1]
+        if tuple(k_dst.shape) != (self.B, self.Hkv, cap, block_size, self.D) or k_dst.shape != v_dst.shape:
+            raise ValueError("sparda: fetch destinations must be [B,Hkv,sel_cap,block_size,D]")
+        if k_dst.dtype != self.dtype or v_dst.dtype != self.dtype:
+            raise TypeError("sparda: fetch destinations must have the arena dtype")
+        call("sparda_offload_fetch", self.handle, sel.contiguous().data_ptr(), n_sel.contiguous().data_ptr(),
+             cap, block_size, length, method, k_dst.data_ptr(), v_dst.data_ptr(), _stream(dev))

@@ -311,6 +311,31 @@ def decode_selection(kc, S: int, f, bs: int, k: int, routing: str = "reference",
     return sel[:, :, 0], n[:, :, 0], sc[:, :, 0]
 
 
+def prefetch_selection(kc, length: int, pos: int, f, bs: int, k: int, routing: str = "reference",
+                       scale: Optional[float] = None):
+    """Selection made for the query at position `pos` from the first `length`
+    cached tokens (the one-token lookahead of AsyncForecastOffloadAttention.prefetch,
+    model/attention/async_offload.py:196-260): own = pos // bs; every block
+    0..own when own + 1 <= k + 2 (the small-context branch, 203-239); otherwise
+    {0, own} U top-k of the prototypes of blocks [0, ceil(length/bs)) scored
+    with the causal mask at row 0 ("reference", forecast.py:120-126) or at pos
+    ("absolute"). Returns sel [B,Hkv,k+2], n_sel [B,Hkv]."""
+    kc = np.asarray(kc, np.float32)
+    B, _, Hkv, D = kc.shape
+    own = pos // bs
+    cap = k + 2
+    if own + 1 <= k + 2:
+        sel = np.full((B, Hkv, cap), -1, np.int32)
+        sel[:, :, :own + 1] = np.arange(own + 1, dtype=np.int32)
+        return sel, np.full((B, Hkv), own + 1, np.int32)
+    P = compress(kc[:, :length], bs)
+    f4 = np.asarray(f, np.float32).reshape(B, 1, Hkv, -1)
+    sc = scores(f4, P, bs, True, 0 if routing == "reference" else pos, scale)
+    tk = topk(sc, k)
+    sel, n = sel_from_topk(tk, np.array([own], np.int64), True, cap)
+    return sel[:, :, 0], n[:, :, 0]
+
+
 def decode_step(q, kc, vc, S: int, f, bs: int, k: int, routing: str = "reference",
                 scale: Optional[float] = None):
     """Full decode step: selection then attention. Returns (out [B,Hq*D], sel, n_sel)."""

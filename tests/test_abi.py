@@ -54,11 +54,11 @@ def test_argument_errors_are_reported_before_any_hip_call():
     _expect(-6, "sparda_select_fixed", 7, 1, 1, 1, 1, 1, 1, 0, P, P, 4, None)
     _expect(-2, "sparda_prefill", P, 1, 1, 1, P, P, 1, 1, 1, 1, None, None, 0, 1, 16, 12, 5, 64, 64, 1, 0.125,
             P, 1, 1, None)  # Hq not a multiple of Hkv
-    _expect(-4, "sparda_decode", P, 1, 1, P, P, 1, 1, 1, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
+    _expect(-4, "sparda_decode", P, 1, 1, P, P, 8, 8, 8, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
             None, None, None, None, P, 1, None, 0, None)  # no workspace
-    _expect(-4, "sparda_decode", P, 1, 1, P, P, 1, 1, 1, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
+    _expect(-4, "sparda_decode", P, 1, 1, P, P, 8, 8, 8, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
             None, None, None, None, P, 1, P * 2, 16, None)  # workspace too small
-    _expect(-6, "sparda_decode", P, 1, 1, P, P, 1, 1, 1, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 5, 0.125,
+    _expect(-6, "sparda_decode", P, 1, 1, P, P, 8, 8, 8, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 5, 0.125,
             None, None, None, None, P, 1, P * 2, 1 << 20, None)  # unknown routing
 
 
@@ -69,3 +69,29 @@ def test_decode_workspace_size_formula():
     NB = S // bs
     want = up(B * Hkv * NB * 4)
     assert sparda.decode_workspace_bytes(B, S, Hq, Hkv, D, bs, k) == want
+
+
+def test_offload_and_selected_decode_argument_errors():
+    import ctypes
+    P = 4096
+    h = ctypes.c_void_p()
+    _expect(-1, "sparda_offload_create", 1, 64, 4, 64, 1, None)
+    _expect(-2, "sparda_offload_create", 1, 64, 4, 48, 1, ctypes.byref(h))  # D=48 unsupported
+    _expect(-3, "sparda_offload_create", 1, 64, 4, 64, 5, ctypes.byref(h))
+    _expect(-7, "sparda_offload_destroy", None)
+    _expect(-7, "sparda_offload_append", None, P, P, 1, 1, 1, 0, 1, 64, None, None)
+    _expect(-7, "sparda_offload_fetch", None, P, P, 10, 64, 100, 0, P, P, None)
+    _expect(-1, "sparda_decode_selected", None, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, None, None, 0, 0,
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)
+    _expect(-6, "sparda_decode_selected", P, 1, 1, P, P, 8, 8, 8, 1, 1, None, None, 0, None, None, 0, 0,
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)  # compact without a selection
+    _expect(-2, "sparda_decode_selected", P, 1, 1, P, P, 8, 8, 8, 1, 0, P, P, 40, None, None, 0, 0,
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)  # sel_cap > 34
+    _expect(-5, "sparda_decode_selected", P, 1, 1, P + 2, P, 8, 8, 8, 1, 0, None, None, 0, None, None, 0, 0,
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)  # misaligned K
+    _expect(-2, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 50, 64, 8, 1, 0.125, P, P, 10,
+            None)  # pos < len - 1
+    _expect(-2, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 100, 64, 8, 1, 0.125, P, P, 9,
+            None)  # sel_cap < k + 2
+    _expect(-6, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 100, 64, 8, 3, 0.125, P, P, 10,
+            None)  # unknown routing

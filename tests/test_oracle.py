@@ -344,3 +344,50 @@ def test_decode_matches_reference_restatement_on_its_selection():
             assert 0 in s and cb in s and len(s) <= k + 2
     got = O.attention_decode(q, kc, vc, S, sel, n, bs)
     np.testing.assert_allclose(got, out.reshape(B, Hq * D).numpy(), atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# prefetch (lookahead) selection
+# ---------------------------------------------------------------------------
+
+def test_prefetch_selection_dense_branch():
+    # own + 1 <= k + 2: every block 0..own (model/attention/async_offload.py:198-203)
+    kc = np.random.default_rng(0).standard_normal((1, 1000, 2, 8)).astype(np.float32)
+    f = np.ones((1, 2, 8), np.float32)
+    sel, n = O.prefetch_selection(kc, 600, 600, f, 64, 8)
+    assert (n == 10).all() and (sel[0, 0, :10] == np.arange(10)).all() and (sel[0, 0, 10:] == -1).all()
+
+
+def test_prefetch_selection_reference_mode_closed_form():
+    # the row-0 mask leaves only block 0 finite: {0..k-1} U {own} under canonical ties
+    rng = np.random.default_rng(1)
+    kc = rng.standard_normal((2, 2000, 2, 8)).astype(np.float32)
+    f = rng.standard_normal((2, 2, 8)).astype(np.float32)
+    for L in (1300, 1280):  # own block partial / empty
+        sel, n = O.prefetch_selection(kc, L, L, f, 64, 4, "reference")
+        own = L // 64
+        assert (n == 5).all()
+        assert (sel[..., :5] == np.array([0, 1, 2, 3, own])).all()
+
+
+def test_prefetch_selection_absolute_equals_router_and_brute_force():
+    rng = np.random.default_rng(2)
+    B, H, D, bs, k = 2, 3, 8, 16, 3
+    kc = rng.standard_normal((B, 300, H, D)).astype(np.float32)
+    f = rng.standard_normal((B, H, D)).astype(np.float32)
+    for L in (200, 208):  # 208 = 13 full blocks: the own block (13) holds no token yet
+        sel, n = O.prefetch_selection(kc, L, L, f, bs, k, "absolute")
+        P = O.compress(kc[:, :L], bs)
+        NB = P.shape[1]
+        own = L // bs
+        for b in range(B):
+            for h in range(H):
+                s = np.array([np.float32(sum(np.float64(f[b, h, d]) * np.float64(P[b, j, h, d])
+                                             for d in range(D))) for j in range(NB)])
+                order = sorted(range(NB), key=lambda j: (-s[j], j))[:k]
+                want = sorted({0, own} | set(order))
+                assert list(sel[b, h, :n[b, h]]) == want
+        if L % bs:
+            # with a partial own block the router (own clamped to NB-1 = own) agrees
+            _, _, rsel, rn = O.route(f.reshape(B, 1, H, D), P, bs, k, True, L, L)
+            assert np.array_equal(rsel[:, :, 0], sel) and np.array_equal(rn[:, :, 0], n)
