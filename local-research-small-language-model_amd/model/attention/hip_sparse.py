@@ -1,5 +1,6 @@
 """HIP sparse GQA attention backend — drop-in for SparseAttention
-(model/attention/sparse.py:65-439), with the block gather of
+(model/attention/sparse.py:65-439) and, in mode "dense", for DenseAttention
+(model/attention/dense.py), with the block gather of
 gather_kv_blocks (model/attention/sparse.py:19-62).
 
 Prefill: compressor -> fused router -> block-sparse prefill kernel (bf16
@@ -44,7 +45,7 @@ class HipSparseAttention(BaseAttention):
             self.mode = "static"
         else:
             self.mode = "forecast"
-        if self.mode not in ("forecast", "static"):
+        if self.mode not in ("forecast", "static", "dense"):
             raise ValueError(f"unknown sparse mode {self.mode!r}")
         self.decode_routing = getattr(config, "decode_routing", "reference")
         # parameter-free, kept for interface parity with the reference module
@@ -57,6 +58,9 @@ class HipSparseAttention(BaseAttention):
         B = xq.shape[0]
         if self._ws is None or self._ws.device != xq.device:
             self._ws = sparda.DecodeWorkspace(xq.device)
+        if self.mode == "dense":
+            out = sparda.decode_selected(xq[:, 0], cache.k, cache.v, cache.current_len, self.block_size)
+            return self.wo(out.view(B, 1, self.n_head * self.head_dim))
         f = forecast_vector if (self.mode == "forecast" and forecast_vector is not None) else None
         if f is not None:
             f = f.reshape(B, self.n_kv_head, -1)
@@ -68,7 +72,10 @@ class HipSparseAttention(BaseAttention):
     def _prefill(self, xq, xk, xv, forecast_vector, is_causal):
         B, T = xq.shape[:2]
         nb = (T + self.block_size - 1) // self.block_size
-        dense = nb <= 2 or (self.mode == "forecast" and (forecast_vector is None or self.layer_idx == 0))
+        dense = self.mode == "dense" or nb <= 2 or (
+            self.mode == "forecast" and (forecast_vector is None or self.layer_idx == 0))
+        if not dense and self.mode == "static" and not is_causal:
+            raise NotImplementedError("static sparse prefill is causal only in the HIP backend")
         if dense:
             sel = n_sel = None
         elif self.mode == "forecast":
@@ -78,8 +85,6 @@ class HipSparseAttention(BaseAttention):
         else:
             sel, n_sel = sparda.select_fixed(sparda.SEL_WINDOW_PREFILL, B, T, self.n_kv_head, nb,
                                              self.block_size, self.top_k_blocks, 0, device=xq.device)
-            if not is_causal:
-                raise NotImplementedError("static sparse prefill is causal only in the HIP backend")
         out = sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=is_causal)
         return self.wo(out)
 
