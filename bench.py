@@ -43,6 +43,8 @@ PB, PT, HQ, HKV, D, BS, TOPK = 4, 4096, 12, 4, 64, 64, 8
 # decode workload
 DB, DS = 8, 16384
 N_CACHES = 4
+# offload workload
+OB_LAYERS, OB_CTX = 12, 32768
 
 
 def log(msg):
@@ -57,6 +59,9 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--offload-steps", type=int, default=32)
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload"], default="all",
+                    help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
 
 
@@ -88,24 +93,36 @@ def bench_prefill(args, torch, sparda, synth):
 
     state = {}
 
-    def step():
+    def step(ev=None):
+        # ev: 4 events bracketing the three launches (same stream as the kernels)
+        if ev is not None:
+            ev[0].record()
         protos = sparda.compress(k, BS)
+        if ev is not None:
+            ev[1].record()
         _, _, sel, n = sparda.route(f, protos, BS, TOPK, want_topk=False, want_sel=True)
+        if ev is not None:
+            ev[2].record()
         sparda.prefill(q, k, v, sel, n, BS, out=out)
+        if ev is not None:
+            ev[3].record()
         state["sel"], state["n"], state["protos"] = sel, n, protos
 
     with torch.no_grad():
         for _ in range(args.warmup):
             step()
+        # the timed steps; events around each launch give the per-kernel durations
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
         torch.cuda.synchronize()
-        ms_step = events_ms(step, args.steps, torch)
+        for ev in evs:
+            step(ev)
+        evs[-1][3].synchronize()
         torch.cuda.synchronize()
-        sel, n, protos = state["sel"], state["n"], state["protos"]
-        # per-kernel durations
-        ms_compress = events_ms(lambda: sparda.compress(k, BS), args.steps, torch)
-        ms_route = events_ms(lambda: sparda.route(f, protos, BS, TOPK, want_topk=False, want_sel=True),
-                             args.steps, torch)
-        ms_attn = events_ms(lambda: sparda.prefill(q, k, v, sel, n, BS, out=out), args.steps, torch)
+        ms_step = evs[0][0].elapsed_time(evs[-1][3]) / args.steps
+        ms_compress = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+        ms_route = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+        ms_attn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+        sel, n = state["sel"], state["n"]
         assert torch.isfinite(out.float()).all(), "non-finite prefill output"
         # useful work: for each (b, g, t) the allowed keys are full blocks
         # below the own block plus t%bs+1 keys of the own block
@@ -146,8 +163,8 @@ def bench_decode(args, torch, sparda, synth):
             one(i)
         torch.cuda.synchronize()
         eager_us = events_ms(lambda: [one(i) for i in range(args.decode_steps)], 1, torch) * 1e3 / args.decode_steps
-        # capture the timed steps in one HIP graph (no memset nodes: the
-        # kernels reset their own arrival counters)
+        # capture the timed steps in one HIP graph (the decode kernels keep no
+        # state between calls, so replays need no memset nodes)
         g = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -182,6 +199,107 @@ def bench_decode(args, torch, sparda, synth):
         "gbs": total / (graph_us * 1e-6) / 1e9,
         "k_stream_bytes": k_stream,
         "gathered_bytes": gathered,
+    }
+
+
+def bench_offload(args, torch, sparda, synth):
+    """12-layer decode at a 32K context with every layer but layer 0 holding its
+    KV in a pinned host arena: forecast-routed blocks prefetched on a side
+    stream while the previous layer's attention + FFN run. Also times the
+    synchronous offload step and the fully GPU-resident sparse step."""
+    from model.attention import AsyncOffloadedKVCache, KVCache, OffloadedKVCache
+    from model.config import ModelConfig
+    from model.model import SparDAResearchModel
+    dev = torch.device("cuda")
+    W, K = 4, args.offload_steps
+    cap = OB_CTX + 3 * (W + K) + 64
+    cfg = ModelConfig(n_layer=OB_LAYERS, context_length=cap, block_size=BS, top_k_blocks=TOPK,
+                      decode_routing="absolute", attention_backend="async_offload", norm_eps=1e-5)
+    torch.manual_seed(1004)
+    model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
+    res_cfg = ModelConfig(**{**cfg.__dict__, "attention_backend": "hip_sparse"})
+    sync_cfg = ModelConfig(**{**cfg.__dict__, "attention_backend": "offload"})
+    resident = SparDAResearchModel(res_cfg).to(dev, torch.bfloat16).eval()
+    resident.load_state_dict(model.state_dict())
+    syncm = SparDAResearchModel(sync_cfg).to(dev, torch.bfloat16).eval()
+    syncm.load_state_dict(model.state_dict())
+
+    off_caches = [KVCache(1, cap, HKV, D, dev, torch.bfloat16)] + [
+        AsyncOffloadedKVCache(1, cap, HKV, D, dev, torch.bfloat16, block_size=BS) for _ in range(OB_LAYERS - 1)]
+    res_caches = [KVCache(1, cap, HKV, D, dev, torch.bfloat16) for _ in range(OB_LAYERS)]
+    for li in range(OB_LAYERS):  # the same synthetic context in both cache sets
+        for _, k, v in synth.kv_chunks(1, OB_CTX, HKV, D, seed=2000 + li):
+            kd, vd = k.to(dev, torch.bfloat16), v.to(dev, torch.bfloat16)
+            off_caches[li].update(kd, vd)
+            res_caches[li].update(kd, vd)
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(1006)
+    ids = torch.randint(0, cfg.vocab_size, (3 * (W + K), 1, 1), generator=g).to(dev)
+    it = iter(range(ids.shape[0]))
+
+    def run(m, caches, n):
+        with torch.no_grad():
+            for _ in range(n):
+                m(ids[next(it)], kv_caches=caches)
+
+    def timed(m, caches):
+        run(m, caches, W)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run(m, caches, K)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / K
+
+    # async prefetch: device-event overlap on every prefetched layer
+    attns = [model.layers[i].attention for i in range(1, OB_LAYERS)]
+    for a in attns:
+        a.track_overlap = True
+    run(model, off_caches, W)
+    torch.cuda.synchronize()
+    for a in attns:
+        a.overlap_stats(reset=True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    run(model, off_caches, K)
+    e1.record()
+    e1.synchronize()
+    us_async = e0.elapsed_time(e1) * 1e3 / K
+    stats = [a.overlap_stats() for a in attns]
+    stale = sum(a.stale_prefetches for a in attns)
+    tr = sum(s["transfer_ms"] for s in stats) / len(stats)
+    ex = sum(s["exposed_ms"] for s in stats) / len(stats)
+    fetched = sum(a.prefetched_bytes for a in attns)
+    for a in attns:
+        a.track_overlap = False
+    # same caches, synchronous offload (select + fetch on the compute stream)
+    us_sync = timed(syncm, off_caches)
+    us_res = timed(resident, res_caches)
+    # host link: one 256 MiB pinned host -> device copy
+    hb = torch.empty(256 << 20, dtype=torch.uint8).pin_memory()
+    db = torch.empty_like(hb, device=dev)
+    db.copy_(hb, non_blocking=True)
+    torch.cuda.synchronize()
+    link_ms = events_ms(lambda: db.copy_(hb, non_blocking=True), 5, torch)
+    del hb, db
+    per_layer = fetched / len(attns)
+    return {
+        "workload": f"decode with offloaded KV: {OB_LAYERS} layers, B=1, context {OB_CTX} (512 blocks of 64), "
+                    f"bf16 KV [32768,4,64] per layer in pinned host memory for layers 1..{OB_LAYERS - 1} "
+                    "(layer 0 GPU-resident), top-8 + sink + current blocks prefetched per layer on a side "
+                    "stream; step = one token through the 12-layer model incl. LM head",
+        "us_per_step_async": round(us_async, 1),
+        "us_per_step_sync": round(us_sync, 1),
+        "us_per_step_gpu_resident": round(us_res, 1),
+        "steps": K,
+        "overlap": round(1.0 - ex / tr, 4) if tr > 0 else None,
+        "transfer_us_per_layer": round(tr * 1e3, 2),
+        "exposed_us_per_layer": round(ex * 1e3, 2),
+        "h2d_bytes_per_step": int(fetched),
+        "h2d_gbs_per_layer": round(per_layer / (tr * 1e-3) / 1e9, 2) if tr > 0 else None,
+        "host_link_gbs": round((256 << 20) / (link_ms * 1e-3) / 1e9, 2),
+        "stale_prefetches": stale,
     }
 
 
@@ -220,6 +338,11 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     sparda.load()
+    if args.only != "all":
+        fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload}[args.only]
+        r = fn(args, torch, sparda, synth)
+        print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str))}}), flush=True)
+        return
     log("prefill workload")
     pre = bench_prefill(args, torch, sparda, synth)
     log(f"prefill: {pre['ms_per_step']:.3f} ms/step, attention {pre['attn_ms']*1e3:.1f} us "
@@ -227,6 +350,11 @@ def main():
     log("decode workload")
     dec = bench_decode(args, torch, sparda, synth)
     log(f"decode: {dec['us_per_step']:.2f} us/step ({dec['gbs']:.0f} GB/s), eager {dec['us_per_step_eager']:.2f}")
+    log("offload workload")
+    off = bench_offload(args, torch, sparda, synth)
+    log(f"offload: async {off['us_per_step_async']:.1f} us/step, sync {off['us_per_step_sync']:.1f}, "
+        f"resident {off['us_per_step_gpu_resident']:.1f}; overlap {off['overlap']}, "
+        f"transfer {off['transfer_us_per_layer']} us/layer, link {off['host_link_gbs']} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -270,6 +398,7 @@ def main():
             "k_stream_bytes": dec["k_stream_bytes"],
             "gathered_bytes": dec["gathered_bytes"],
         },
+        "offload": off,
     }
     print(json.dumps(line), flush=True)
 

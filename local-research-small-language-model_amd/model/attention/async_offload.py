@@ -18,7 +18,7 @@ import torch
 
 import sparda
 from model.attention.base import BaseAttention
-from model.attention.offload import OffloadedKVCache, dense_from_arena, prefill_dense
+from model.attention.offload import OffloadedKVCache, dense_from_arena, prefill_dense, resident_dense_decode
 from model.config import ModelConfig
 from model.forecast import ForecastBlockSelector, KVBlockCompressor
 from model.rope import RotaryEmbedding
@@ -255,6 +255,8 @@ class HipAsyncOffloadAttention(BaseAttention):
         xq, xk = rotary_emb(xq, xk, offset=offset)
         if isinstance(kv_cache, OffloadedKVCache) and T == 1:
             return self._async_decode(xq[:, 0], xk, xv, kv_cache, forecast_vector)
+        if kv_cache is not None and T == 1:
+            return resident_dense_decode(self, xq, xk, xv, kv_cache)
         return prefill_dense(self, xq, xk, xv, kv_cache, is_causal)
 
 

@@ -193,7 +193,20 @@ class HipOffloadAttention(BaseAttention):
         xq, xk = rotary_emb(xq, xk, offset=offset)
         if isinstance(kv_cache, OffloadedKVCache) and T == 1:
             return self._offload_decode(xq[:, 0], xk, xv, kv_cache, forecast_vector)
+        if kv_cache is not None and T == 1:
+            return resident_dense_decode(self, xq, xk, xv, kv_cache)
         return prefill_dense(self, xq, xk, xv, kv_cache, is_causal)
+
+
+def resident_dense_decode(attn: BaseAttention, xq, xk, xv, kv_cache: KVCache) -> torch.Tensor:
+    """Decode step of an offload backend whose layer keeps a GPU-resident
+    KVCache (layer 0, which is never prefetched): dense attention over the
+    cache, the attention the reference's offload fallback computes there
+    (offload.py:180-214; async_offload.py:392-430)."""
+    B = xq.shape[0]
+    kv_cache.update(xk, xv)
+    out = sparda.decode_selected(xq[:, 0], kv_cache.k, kv_cache.v, kv_cache.current_len, attn.config.block_size)
+    return attn.wo(out.view(B, 1, attn.n_head * attn.head_dim))
 
 
 def prefill_dense(attn: BaseAttention, xq, xk, xv, kv_cache, is_causal: bool) -> torch.Tensor:
@@ -207,4 +220,5 @@ def prefill_dense(attn: BaseAttention, xq, xk, xv, kv_cache, is_causal: bool) ->
     return attn.wo(out)
 
 
-__all__ = ["OffloadedKVCache", "HipOffloadAttention", "KVCache", "dense_from_arena", "prefill_dense"]
+__all__ = ["OffloadedKVCache", "HipOffloadAttention", "KVCache", "dense_from_arena", "prefill_dense",
+           "resident_dense_decode"]

@@ -62,3 +62,14 @@ def decode_inputs(B: int, S: int, Hq: int, Hkv: int, D: int, dtype=torch.bfloat1
     vc[:, :S] = v
     out = {"q": q, "k_cache": kc, "v_cache": vc, "forecast": f}
     return {n: t.to(dtype).to(device) for n, t in out.items()}
+
+
+def kv_chunks(B: int, S: int, Hkv: int, D: int, seed: int, chunk: int = 8192):
+    """Keys (RoPE at their positions) and values ~N(0,1), fp32, in chunks of
+    tokens: yields (pos0, k [B,n,Hkv,D], v [B,n,Hkv,D]) covering [0, S)."""
+    g = torch.Generator().manual_seed(seed)
+    for p0 in range(0, S, chunk):
+        n = min(chunk, S - p0)
+        k = torch.randn(B, n, Hkv, D, generator=g)
+        v = torch.randn(B, n, Hkv, D, generator=g)
+        yield p0, _rope_fp32(k, torch.arange(p0, p0 + n)), v
