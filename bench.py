@@ -45,6 +45,8 @@ DB, DS = 8, 16384
 N_CACHES = 4
 # offload workload
 OB_LAYERS, OB_CTX = 12, 32768
+# plain copy used to calibrate the HBM byte counters
+COPY_BYTES = 256 << 20
 
 
 def log(msg):
@@ -60,7 +62,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--offload-steps", type=int, default=32)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "pmc"], default="all",
                     help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
 
@@ -303,6 +305,29 @@ def bench_offload(args, torch, sparda, synth):
     }
 
 
+def pmc_workload(args, torch, sparda, synth):
+    """Short eager run for hardware-counter passes: prefill steps, decode steps
+    and a plain device copy of COPY_BYTES (the calibration of FETCH_SIZE /
+    WRITE_SIZE). Counter values are per dispatch."""
+    x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
+    c = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002, device="cuda")
+    ws = sparda.DecodeWorkspace("cuda")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    with torch.no_grad():
+        for _ in range(3):
+            protos = sparda.compress(x["k"], BS)
+            _, _, sel, n = sparda.route(x["forecast"], protos, BS, TOPK, want_topk=False, want_sel=True)
+            sparda.prefill(x["q"], x["k"], x["v"], sel, n, BS)
+        for _ in range(3):
+            sparda.decode(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], BS, TOPK, routing="absolute",
+                          workspace=ws)
+        for _ in range(3):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes": COPY_BYTES}
+
+
 def cpu_baseline(args, torch, synth):
     """Reference path restated op for op (oracle/reference_path.py), host CPU."""
     from oracle import reference_path as R
@@ -339,7 +364,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     sparda.load()
     if args.only != "all":
-        fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload}[args.only]
+        fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload,
+              "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
         print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str))}}), flush=True)
         return
