@@ -19,6 +19,8 @@
 // enumerated as {32m + 4g + e, 32m + 16 + 4g + e} (g = lane / 16); the V^T A
 // operand is read from the row-major V tile with the same enumeration by the
 // LDS transpose read (ds_read_b64_tr_b16).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -40,6 +42,13 @@ constexpr float kLog2eM = 1.4426950408889634f;
 #ifndef SPARDA_PREFILL_PREFETCH
 #define SPARDA_PREFILL_PREFETCH 2
 #endif
+// 1: the running max is only raised when a block's max exceeds it by more than
+// 2^kLazyLog2 (probabilities stay <= 2^8, exact in fp32 accumulation), so the
+// output is rarely rescaled. 0: raised on every increase.
+#ifndef SPARDA_PF_LAZY
+#define SPARDA_PF_LAZY 1
+#endif
+constexpr float kLazyLog2 = 8.0f;
 
 struct MfmaSmem {
     uint16_t k[2][kMBs * kKRow];
@@ -83,8 +92,13 @@ __device__ __forceinline__ float pair32_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// resident workgroups per CU the register budget is sized for
+#ifndef SPARDA_PF_OCCUPANCY
+#define SPARDA_PF_OCCUPANCY 2
+#endif
+
 template <int R>
-__global__ void __launch_bounds__(kMThreads, 2)
+__global__ void __launch_bounds__(kMThreads, SPARDA_PF_OCCUPANCY)
 prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                     int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
@@ -167,11 +181,18 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
     const uint16_t* qrow0 = qs + (16 * wave * R + col16) * kKRow + 8 * grp;
 
     f32x4 o[R][4];
-    float m_run[R], l_run[R];
+    float m_run[R];
+    // Row sums of P on the matrix cores: a constant A operand whose row 0 is
+    // ones (2 MFMA per tile) replaces 16 VALU adds and the cross-lane
+    // reductions; ol[tt][0] on lane group 0 holds the sum of column col16.
+    f32x4 ol[R];
+    bf16x8 ones_a;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
 #pragma unroll
     for (int tt = 0; tt < R; ++tt) {
         m_run[tt] = -__builtin_inff();
-        l_run[tt] = 0.0f;
+        ol[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -179,41 +200,53 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
     // ---- staging: thread -> 16 B chunks (row c/8, chunk c%8), c = tid, tid+256 ----
     const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
-    uint4 kr[2][2], vr[2][2];  // two prefetch sets
-    auto fetch = [&](int set, int64_t j) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int c = tid + r * kMThreads;
-            const int64_t s = j * kMBs + c / 8;
-            const int64_t off = s * kv_st + (c % 8) * 8;
-            if (s < T) {
-                kr[set][r] = *reinterpret_cast<const uint4*>(kbase + off);
-                vr[set][r] = *reinterpret_cast<const uint4*>(vbase + off);
-            } else {
-                kr[set][r] = make_uint4(0u, 0u, 0u, 0u);
-                vr[set][r] = make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
+    // two prefetch sets of plain registers: (ka, kb, va, vb) = K and V chunks
+    // c = tid and c = tid + 256 (row c/8, 16-byte chunk c%8) of one block
+    uint4 k0a, k0b, v0a, v0b, k1a, k1b, v1a, v1b;
+    const int c_lo = tid, c_hi = tid + kMThreads;
+    const int64_t col_lo = (c_lo % 8) * 8, col_hi = (c_hi % 8) * 8;
+    const int lds_k_lo = (c_lo / 8) * kKRow + (c_lo % 8) * 8, lds_k_hi = (c_hi / 8) * kKRow + (c_hi % 8) * 8;
+    const int lds_v_lo = (c_lo / 8) * kVRow + (c_lo % 8) * 8, lds_v_hi = (c_hi / 8) * kVRow + (c_hi % 8) * 8;
+    // Rows past T (a ragged last block) load row T-1 instead: unconditional
+    // loads keep the register sets free of writes while loads are in flight,
+    // and those keys are masked (causal / tail) so only finite V values matter.
+    auto row_off = [&](int64_t j, int c, int64_t col) {
+        int64_t s = j * kMBs + c / 8;
+        s = s < T ? s : T - 1;
+        return s * kv_st + col;
     };
-    auto stash = [&](int set, int buf) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int c = tid + r * kMThreads;
-            *reinterpret_cast<uint4*>(&sm.k[buf][(c / 8) * kKRow + (c % 8) * 8]) = kr[set][r];
-            *reinterpret_cast<uint4*>(&sm.v[buf][(c / 8) * kVRow + (c % 8) * 8]) = vr[set][r];
-        }
-    };
+#define SPARDA_FETCH(KA, KB, VA, VB, J)                                                   \
+    do {                                                                                  \
+        const int64_t o_lo_ = row_off((J), c_lo, col_lo), o_hi_ = row_off((J), c_hi, col_hi); \
+        KA = *reinterpret_cast<const uint4*>(kbase + o_lo_);                              \
+        VA = *reinterpret_cast<const uint4*>(vbase + o_lo_);                              \
+        KB = *reinterpret_cast<const uint4*>(kbase + o_hi_);                              \
+        VB = *reinterpret_cast<const uint4*>(vbase + o_hi_);                              \
+    } while (0)
+#define SPARDA_STASH(KA, KB, VA, VB, BUF)                                                 \
+    do {                                                                                  \
+        *reinterpret_cast<uint4*>(&sm.k[BUF][lds_k_lo]) = KA;                             \
+        *reinterpret_cast<uint4*>(&sm.v[BUF][lds_v_lo]) = VA;                             \
+        *reinterpret_cast<uint4*>(&sm.k[BUF][lds_k_hi]) = KB;                             \
+        *reinterpret_cast<uint4*>(&sm.v[BUF][lds_v_hi]) = VB;                             \
+    } while (0)
 
     // ---- one KV block against this wave's tiles ----
+    // Per tile: S^T = K Q^T, online softmax, O^T += V^T P^T. Columns that did
+    // not select the block get an exponent offset of -inf (P = 0) instead of
+    // per-element selects; a tile none of whose columns selected the block is
+    // skipped.
     auto compute = [&](int buf, int j) {
+        // causal diagonal block / ragged non-causal tail: keys are masked (wave-uniform)
+        const bool edge = (causal && j == qb) || (!causal && (j + 1) * kMBs > T);
         bool member[R];
         bool any = false;
 #pragma unroll
         for (int tt = 0; tt < R; ++tt) {
             member[tt] = (sm.mask[tok[tt] * nbw + (j >> 5)] >> (j & 31)) & 1u;
-            any = any || (__ballot(member[tt]) != 0ull);
+            any = any || member[tt];
         }
-        if (!any) return;
+        if (__ballot(any) == 0ull) return;
         bf16x8 ka[4][2];
 #pragma unroll
         for (int n = 0; n < 4; ++n)
@@ -236,51 +269,48 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                     va[dt][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
         }
-        const bool edge = (causal && j == qb) || (!causal && (j + 1) * kMBs > T);  // wave-uniform
-#pragma unroll
-        for (int tt = 0; tt < R; ++tt) {
-            if (__ballot(member[tt]) == 0ull) continue;
+        const int lim_tail = static_cast<int>(T - static_cast<int64_t>(j) * kMBs) - 1;
+        auto qk = [&](int tt, f32x4 (&s)[4]) {
             const bf16x8 qb0 = lds_read8(qrow0 + 16 * tt * kKRow);
             const bf16x8 qb1 = lds_read8(qrow0 + 16 * tt * kKRow + 32);
-            f32x4 s[4];
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
                 s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
                 s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][0], qb0, s[n], 0, 0, 0);
                 s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][1], qb1, s[n], 0, 0, 0);
             }
+        };
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt) {
+            if (__ballot(member[tt]) == 0ull) continue;
+            f32x4 s[4];
+            qk(tt, s);
             if (edge) {
                 // causal diagonal: key <= token; non-causal tail: key < T
-                const int lim = causal ? tok[tt] : static_cast<int>(T - static_cast<int64_t>(j) * kMBs) - 1;
+                const int l = causal ? tok[tt] : lim_tail;
 #pragma unroll
                 for (int n = 0; n < 4; ++n)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        if (16 * n + 4 * grp + i > lim) s[n][i] = -__builtin_inff();
+                        if (16 * n + 4 * grp + i > l) s[n][i] = -__builtin_inff();
             }
-            float mx = s[0][0];
+            float mx = __builtin_fmaxf(__builtin_fmaxf(s[0][0], s[0][1]), __builtin_fmaxf(s[0][2], s[0][3]));
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[n][i]);
+            for (int n = 1; n < 4; ++n)
+                mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(s[n][0], s[n][1]),
+                                                         __builtin_fmaxf(s[n][2], s[n][3])));
             mx = member[tt] ? mx : -__builtin_inff();
             mx = pair32_max(pair16_max(mx));
-            const float m_new = fmaxf(m_run[tt], mx * scale_log2);
-            const bool live = m_new != -__builtin_inff();
-            const float neg = live ? -m_new : 0.0f;
-            const float alpha = live ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
-            float rs = 0.0f;
-#pragma unroll
-            for (int n = 0; n < 4; ++n)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][i], scale_log2, neg));
-                    s[n][i] = p;
-                    rs += p;
-                }
-            rs = member[tt] ? rs : 0.0f;
-            rs = pair32_sum(pair16_sum(rs));
-            l_run[tt] = l_run[tt] * alpha + rs;
+            const float cand = mx * scale_log2;  // this block's column max, log2 units
+#if SPARDA_PF_LAZY
+            // m_run = -inf takes any finite max; otherwise raise only past 2^kLazyLog2
+            const float m_new = cand > m_run[tt] + kLazyLog2 ? cand : m_run[tt];
+#else
+            const float m_new = __builtin_fmaxf(m_run[tt], cand);
+#endif
+            // non-members: offset -inf gives P = 0 and leaves the running state alone
+            const float neg = member[tt] ? -m_new : -__builtin_inff();
+            const float alpha = m_new != m_run[tt] ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
             m_run[tt] = m_new;
             uint4 pw[2];
 #pragma unroll
@@ -288,15 +318,16 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                 bf16x8 pb;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pb[i] = static_cast<__bf16>(s[2 * m][i]);
-                    pb[4 + i] = static_cast<__bf16>(s[2 * m + 1][i]);
+                    pb[i] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m][i], scale_log2, neg)));
+                    pb[4 + i] =
+                        static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m + 1][i], scale_log2, neg)));
                 }
                 pw[m] = __builtin_bit_cast(uint4, pb);
-                if (!member[tt]) pw[m] = make_uint4(0u, 0u, 0u, 0u);
             }
             if (__ballot(alpha != 1.0f) != 0ull) {
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) o[tt][dt] *= alpha;
+                ol[tt] *= alpha;
             }
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
@@ -305,6 +336,8 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                 o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]),
                                                                     o[tt][dt], 0, 0, 0);
             }
+            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[0]), ol[tt], 0, 0, 0);
+            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[1]), ol[tt], 0, 0, 0);
         }
     };
 
@@ -312,47 +345,52 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
     const int n_list = sm.n_list;
 #if SPARDA_PREFILL_PREFETCH == 2
     // prologue: block 0 staged, block 1 in flight
-    fetch(0, sm.list[0]);
-    if (n_list > 1) fetch(1, sm.list[1]);
-    stash(0, 0);
+    SPARDA_FETCH(k0a, k0b, v0a, v0b, sm.list[0]);
+    if (n_list > 1) SPARDA_FETCH(k1a, k1b, v1a, v1b, sm.list[1]);
+    SPARDA_STASH(k0a, k0b, v0a, v0b, 0);
     __syncthreads();
     // iteration u computes block u from buffer u&1, keeps block u+1 in
     // flight in register set (u+1)&1 and issues block u+2 into set u&1
     for (int u = 0; u < n_list; u += 2) {
-        if (u + 2 < n_list) fetch(0, sm.list[u + 2]);
+        if (u + 2 < n_list) SPARDA_FETCH(k0a, k0b, v0a, v0b, sm.list[u + 2]);
         compute(0, sm.list[u]);
-        if (u + 1 < n_list) stash(1, 1);
+        if (u + 1 < n_list) SPARDA_STASH(k1a, k1b, v1a, v1b, 1);
         __syncthreads();
         if (u + 1 >= n_list) break;
-        if (u + 3 < n_list) fetch(1, sm.list[u + 3]);
+        if (u + 3 < n_list) SPARDA_FETCH(k1a, k1b, v1a, v1b, sm.list[u + 3]);
         compute(1, sm.list[u + 1]);
-        if (u + 2 < n_list) stash(0, 0);
+        if (u + 2 < n_list) SPARDA_STASH(k0a, k0b, v0a, v0b, 0);
         __syncthreads();
     }
 #else
-    fetch(0, sm.list[0]);
-    stash(0, 0);
+    SPARDA_FETCH(k0a, k0b, v0a, v0b, sm.list[0]);
+    SPARDA_STASH(k0a, k0b, v0a, v0b, 0);
     __syncthreads();
     for (int u = 0; u < n_list; u += 2) {
-        if (u + 1 < n_list) fetch(0, sm.list[u + 1]);
+        if (u + 1 < n_list) SPARDA_FETCH(k0a, k0b, v0a, v0b, sm.list[u + 1]);
         compute(0, sm.list[u]);
-        if (u + 1 < n_list) stash(0, 1);
+        if (u + 1 < n_list) SPARDA_STASH(k0a, k0b, v0a, v0b, 1);
         __syncthreads();
         if (u + 1 >= n_list) break;
-        if (u + 2 < n_list) fetch(0, sm.list[u + 2]);
+        if (u + 2 < n_list) SPARDA_FETCH(k0a, k0b, v0a, v0b, sm.list[u + 2]);
         compute(1, sm.list[u + 1]);
-        if (u + 2 < n_list) stash(0, 0);
+        if (u + 2 < n_list) SPARDA_STASH(k0a, k0b, v0a, v0b, 0);
         __syncthreads();
     }
 #endif
+#undef SPARDA_FETCH
+#undef SPARDA_STASH
 
     // ---- epilogue: out[b, t, h*64 + d] = O / l ----
 #pragma unroll
     for (int tt = 0; tt < R; ++tt) {
+        // row sum of column col16 sits in lane col16 (lane group 0), element 0;
+        // read by every lane before any lane leaves
+        const float lsum = __shfl(ol[tt][0], col16, kWave);
         if (tok[tt] >= t_valid) continue;
         const int c = 16 * tt + col16;
         const int hh = c % R;
-        const float inv = 1.0f / l_run[tt];
+        const float inv = 1.0f / lsum;
         uint16_t* orow = out + b * out_sb + (t0 + tok[tt]) * out_st + static_cast<int64_t>(g * R + hh) * kMD;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
