@@ -21,6 +21,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "attend.h"
+#include "mfma.h"
 #include "select.h"
 
 namespace sparda {
@@ -132,7 +133,14 @@ __host__ __device__ constexpr size_t attend_wave_bytes() {
 
 constexpr int kAttendMaxWaves = 12;
 
-template <int DT, int DH, int CH>
+// Matrix-core block attention (bf16, D = 64, bs = 64): per block and wave,
+// S^T[key, head] = K . Q^T with v_mfma_f32_16x16x32_bf16 (the group's query
+// heads are the 16 columns; K operands are read straight from memory),
+// softmax in fp32 registers, O^T += V^T . P^T (V staged row-major in the
+// wave's LDS region, read transposed), row sums on the matrix cores.
+constexpr int kDVRow = 80;  // V row in LDS for the matrix-core path, bf16 elements
+
+template <int DT, int DH, int CH, bool MF>
 __global__ void __launch_bounds__(kAttendMaxWaves * 64)
 decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      const void* __restrict__ kc, const void* __restrict__ vc,
@@ -205,8 +213,179 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
         if (i == 0 && n_sel_out != nullptr) n_sel_out[bg] = n;
     }
 
-    // this wave's running partial (m, l, o[DH]) per head, merged block by block
     float* part = part_all + static_cast<int64_t>(wave) * R * (DH + 2);
+    if constexpr (MF) {
+        static_assert(DH == 64, "matrix-core decode path is for head dim 64");
+        const int col16 = lane % 16;
+        const int grp = lane / 16;
+        constexpr int kBs = 64;
+        constexpr float kLazy = 8.0f;
+        uint16_t* vt = reinterpret_cast<uint16_t*>(wbase);  // [64][kDVRow]
+        const uint16_t* qh = static_cast<const uint16_t*>(q);
+        const uint16_t* kh = static_cast<const uint16_t*>(kc);
+        const uint16_t* vh = static_cast<const uint16_t*>(vc);
+        const uint16_t* knh = static_cast<const uint16_t*>(k_new);
+        const uint16_t* vnh = static_cast<const uint16_t*>(v_new);
+        // B operand of S^T: column col16 = query head of the group (zero past R)
+        bf16x8 qb0, qb1;
+        {
+            uint4 a = make_uint4(0u, 0u, 0u, 0u), c = a;
+            if (col16 < R) {
+                const uint16_t* qp = qh + b * q_sb + static_cast<int64_t>(g * R + col16) * q_sh + 8 * grp;
+                a = *reinterpret_cast<const uint4*>(qp);
+                c = *reinterpret_cast<const uint4*>(qp + 32);
+            }
+            qb0 = __builtin_bit_cast(bf16x8, a);
+            qb1 = __builtin_bit_cast(bf16x8, c);
+        }
+        bf16x8 ones_a;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
+        f32x4 o[4], ol = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float m_run = -__builtin_inff();
+        const int64_t nbase = b * new_sb + g * new_sh;
+        for (int w = wave; w < n; w += nwaves) {
+            const int64_t j = sel_mode == 1 ? w : sel_lds[w];
+            if (j < 0 || j > cb) continue;  // not a block of [0, S): nothing to attend
+            const int64_t s0 = j * kBs;
+            const int nk = static_cast<int>(S - s0 < kBs ? S - s0 : kBs);
+            const int64_t row0 = compact ? static_cast<int64_t>(w) * kBs : s0;
+            const int64_t base = b * kv_sb + row0 * kv_ss + g * kv_sh;
+            // the row holding position S-1 when its K/V come from k_new/v_new (else -1)
+            const int rnew = (knh != nullptr && S - 1 - s0 < kBs) ? static_cast<int>(S - 1 - s0) : -1;
+            // V rows: 512 chunks of 16 B, lane -> chunks lane + 64 i (row c/8, chunk c%8,
+            // the same chunk column lane%8 for every i); rows past S repeat row nk-1
+            // (finite values; their P is 0)
+            const uint16_t* vrow0 = vh + base + (lane % 8) * 8;
+            uint4 vr[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                int r = (lane + 64 * i) / 8;
+                r = r < nk ? r : nk - 1;
+                vr[i] = *reinterpret_cast<const uint4*>(vrow0 + r * kv_ss);
+            }
+            // K A operands: key 16n + col16, dims 32kk + 8grp .. +7
+            const uint16_t* krow0 = kh + base + 8 * grp;
+            bf16x8 ka[4][2];
+#pragma unroll
+            for (int nn = 0; nn < 4; ++nn) {
+                int r = 16 * nn + col16;
+                r = r < nk ? r : nk - 1;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    ka[nn][kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(krow0 + r * kv_ss + 32 * kk));
+            }
+            if (rnew >= 0) {  // wave-uniform: the new token's row from k_new / v_new
+                const uint4 vn = *reinterpret_cast<const uint4*>(vnh + nbase + (lane % 8) * 8);
+                const bf16x8 kn0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(knh + nbase + 8 * grp));
+                const bf16x8 kn1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(knh + nbase + 32 + 8 * grp));
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    // compare the clamped row: rows past S were read from row nk-1
+                    int r = (lane + 64 * i) / 8;
+                    r = r < nk ? r : nk - 1;
+                    const bool hit = r == rnew;
+                    vr[i].x = hit ? vn.x : vr[i].x;
+                    vr[i].y = hit ? vn.y : vr[i].y;
+                    vr[i].z = hit ? vn.z : vr[i].z;
+                    vr[i].w = hit ? vn.w : vr[i].w;
+                }
+#pragma unroll
+                for (int nn = 0; nn < 4; ++nn) {
+                    int r = 16 * nn + col16;
+                    r = r < nk ? r : nk - 1;
+                    const bool hit = r == rnew;
+                    ka[nn][0] = hit ? kn0 : ka[nn][0];
+                    ka[nn][1] = hit ? kn1 : ka[nn][1];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = lane + 64 * i;
+                *reinterpret_cast<uint4*>(vt + (c / 8) * kDVRow + (c % 8) * 8) = vr[i];
+            }
+            __builtin_amdgcn_wave_barrier();
+            f32x4 sc[4];
+#pragma unroll
+            for (int nn = 0; nn < 4; ++nn) {
+                sc[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
+                sc[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[nn][0], qb0, sc[nn], 0, 0, 0);
+                sc[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[nn][1], qb1, sc[nn], 0, 0, 0);
+            }
+            bf16x8 va[4][2];
+            {
+                const int rsub = 4 * grp + col16 / 4;
+                const int csub = 4 * (col16 % 4);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int mm = 0; mm < 2; ++mm) {
+                        const uint16_t* vb = vt + (32 * mm + rsub) * kDVRow + 16 * dt + csub;
+                        const i16x4 lo = lds_read_tr(vb);
+                        const i16x4 hi = lds_read_tr(vb + 16 * kDVRow);
+                        va[dt][mm] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    }
+            }
+            if (nk < kBs) {
+#pragma unroll
+                for (int nn = 0; nn < 4; ++nn)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (16 * nn + 4 * grp + i >= nk) sc[nn][i] = -__builtin_inff();
+            }
+            float mx = sc[0][0];
+#pragma unroll
+            for (int nn = 0; nn < 4; ++nn)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[nn][i]);
+            mx = pair32_max(pair16_max(mx));
+            const float cand = mx * scale_log2;
+            const float m_new = cand > m_run + kLazy ? cand : m_run;
+            const float alpha = m_new != m_run ? exp2f(m_run - m_new) : 1.0f;
+            m_run = m_new;
+            uint4 pw[2];
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                bf16x8 pb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pb[i] = static_cast<__bf16>(exp2f(__builtin_fmaf(sc[2 * mm][i], scale_log2, -m_new)));
+                    pb[4 + i] = static_cast<__bf16>(exp2f(__builtin_fmaf(sc[2 * mm + 1][i], scale_log2, -m_new)));
+                }
+                pw[mm] = __builtin_bit_cast(uint4, pb);
+            }
+            if (__ballot(alpha != 1.0f) != 0ull) {
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+                ol *= alpha;
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[0]), o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]), o[dt], 0, 0, 0);
+            }
+            ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[0]), ol, 0, 0, 0);
+            ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[1]), ol, 0, 0, 0);
+            __builtin_amdgcn_wave_barrier();  // the next block overwrites vt
+        }
+        // the wave's partial of head col16: m (log2 units), l (lane group 0, element 0), o[16dt+4grp+i]
+        const float lsum = __shfl(ol[0], col16, kWave);
+        if (col16 < R) {
+            float* pp = part + col16 * (DH + 2);
+            if (grp == 0) {
+                pp[0] = m_run;
+                pp[1] = lsum;
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pp[2 + 16 * dt + 4 * grp + i] = o[dt][i];
+        }
+    } else {
+    // this wave's running partial (m, l, o[DH]) per head, merged block by block
     for (int hh = 0; hh < R; ++hh) {
         if (lane == 0) {
             part[hh * (DH + 2)] = -__builtin_inff();
@@ -366,6 +545,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             }
         }
     }
+    }  // !MF
     __syncthreads();
 
     // merge the wave partials in wave order (waves without a block hold m = -inf, l = 0)
@@ -406,16 +586,29 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     const int64_t R = a.Hq / a.Hkv;
     // most blocks one workgroup can attend: the selection capacity, or every block when dense
     const int64_t max_blocks = a.sel_mode == 1 ? NB : a.cap;
+    // matrix-core block attention: bf16, D = 64, bs = 64, 16-byte aligned q rows
+    const bool mf = a.dtype == SPARDA_BF16 && a.D == 64 && a.bs == 64 && (a.q_sb % 8) == 0 &&
+                    (a.q_sh % 8) == 0 && (reinterpret_cast<uintptr_t>(a.q) & 15u) == 0;
     constexpr size_t kLdsBudget = 150 * 1024;
     dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
 #define SPARDA_ATT(DT_, DH_, CH_)                                                                        \
+    do {                                                                                                 \
+        if constexpr (DT_ == SPARDA_BF16 && DH_ == 64) {                                                 \
+            if (mf) {                                                                                    \
+                SPARDA_ATT_K(DT_, DH_, CH_, true);                                                       \
+                break;                                                                                   \
+            }                                                                                            \
+        }                                                                                                \
+        SPARDA_ATT_K(DT_, DH_, CH_, false);                                                              \
+    } while (0)
+#define SPARDA_ATT_K(DT_, DH_, CH_, MF_)                                                                 \
     do {                                                                                                 \
         const size_t wb = attend_wave_bytes<DT_, DH_>();                                                 \
         const size_t pb = static_cast<size_t>(R) * (DH_ + 2) * 4;                                        \
         int waves = max_blocks < kAttendMaxWaves ? static_cast<int>(max_blocks) : kAttendMaxWaves;       \
         while (waves > 1 && ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb > kLdsBudget) --waves; \
         const size_t lds = ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb;                  \
-        hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_>), grid2, dim3(waves * kWave), lds, stream, \
+        hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_, MF_>), grid2, dim3(waves * kWave), lds, stream, \
                            a.q, a.q_sb, a.q_sh, a.kc, a.vc, a.kv_sb, a.kv_ss, a.kv_sh, a.S, Hq_i, Hkv_i,  \
                            static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
@@ -439,6 +632,7 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     }
 #undef SPARDA_ATT_D
 #undef SPARDA_ATT_C
+#undef SPARDA_ATT_K
 #undef SPARDA_ATT
     return check_hip(hipGetLastError(), "decode_attend_kernel");
 }
