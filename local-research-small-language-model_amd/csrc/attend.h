@@ -40,8 +40,8 @@ __device__ __forceinline__ void attend_chunk(const float* q_row, const float* k_
     const float mc = wave_max(s);
     if (mc == -__builtin_inff()) return;  // wave-uniform
     const float m_new = fmaxf(acc.m, mc);
-    const float alpha = exp2f(acc.m - m_new);
-    const float p = (s == -__builtin_inff()) ? 0.0f : exp2f(s - m_new);
+    const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
+    const float p = (s == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(s - m_new);
     acc.l = acc.l * alpha + wave_sum(p);
     acc.m = m_new;
     p_wave[lane] = p;

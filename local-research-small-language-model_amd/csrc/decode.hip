@@ -175,9 +175,11 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     float* p_lds = reinterpret_cast<float*>(wbase);                         // [4][64]
     E* v_lds = reinterpret_cast<E*>(wbase + kHeadBatch * 64 * 4);           // [64][VR]
 
-    for (int e = threadIdx.x; e < R * DH; e += blockDim.x) {
-        const int hh = e / DH, d = e % DH;
-        q_lds[e] = load_elem<DT>(q, b * q_sb + static_cast<int64_t>(g * R + hh) * q_sh + d) * scale_log2;
+    if constexpr (!MF) {  // the matrix-core path reads q into registers instead
+        for (int e = threadIdx.x; e < R * DH; e += blockDim.x) {
+            const int hh = e / DH, d = e % DH;
+            q_lds[e] = load_elem<DT>(q, b * q_sb + static_cast<int64_t>(g * R + hh) * q_sh + d) * scale_log2;
+        }
     }
     if (wave == 0) {
         int m = 0;
@@ -344,7 +346,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             mx = pair32_max(pair16_max(mx));
             const float cand = mx * scale_log2;
             const float m_new = cand > m_run + kLazy ? cand : m_run;
-            const float alpha = m_new != m_run ? exp2f(m_run - m_new) : 1.0f;
+            const float alpha = m_new != m_run ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
             m_run = m_new;
             uint4 pw[2];
 #pragma unroll
@@ -352,8 +354,8 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 bf16x8 pb;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pb[i] = static_cast<__bf16>(exp2f(__builtin_fmaf(sc[2 * mm][i], scale_log2, -m_new)));
-                    pb[4 + i] = static_cast<__bf16>(exp2f(__builtin_fmaf(sc[2 * mm + 1][i], scale_log2, -m_new)));
+                    pb[i] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[2 * mm][i], scale_log2, -m_new)));
+                    pb[4 + i] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[2 * mm + 1][i], scale_log2, -m_new)));
                 }
                 pw[mm] = __builtin_bit_cast(uint4, pb);
             }
@@ -483,8 +485,8 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                     }
                     const float mc = wave_max(sc);
                     const float m_new = fmaxf(mrun[hh], mc);
-                    const float alpha = exp2f(mrun[hh] - m_new);
-                    const float p = lane < nk ? exp2f(sc - m_new) : 0.0f;
+                    const float alpha = __builtin_amdgcn_exp2f(mrun[hh] - m_new);
+                    const float p = lane < nk ? __builtin_amdgcn_exp2f(sc - m_new) : 0.0f;
                     lrun[hh] = lrun[hh] * alpha + wave_sum(p);
                     mrun[hh] = m_new;
                     p_lds[hh * 64 + lane] = p;
@@ -529,8 +531,8 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 float* pp = part + (hb + hh) * (DH + 2);
                 const float pm = pp[0];
                 const float M = fmaxf(pm, mrun[hh]);
-                const float a_old = exp2f(pm - M);
-                const float a_new = exp2f(mrun[hh] - M);
+                const float a_old = __builtin_amdgcn_exp2f(pm - M);
+                const float a_new = __builtin_amdgcn_exp2f(mrun[hh] - M);
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) {
                     const int d = lane + i * kWave;
@@ -557,7 +559,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
         float num = 0.0f, den = 0.0f;
         for (int w = 0; w < nw; ++w) {
             const float* ps = part_all + (w * R + hh) * (DH + 2);
-            const float wt = exp2f(ps[0] - M);
+            const float wt = __builtin_amdgcn_exp2f(ps[0] - M);
             den = den + wt * ps[1];
             num = num + wt * ps[2 + d];
         }

@@ -103,27 +103,34 @@ __device__ __forceinline__ void wg_topk(uint64_t* ranks, int n, int ke, int32_t*
 // ---------------------------------------------------------------------------
 // Wavefront top-k selection by ballot threshold search.
 // The wave holds keys[j] (orderable score keys, index = block) for
-// j = e*64 + lane in kreg[e]. Writes to sel_lds the ascending list
-// ({0, own} U topk) restricted to blocks <= own, returns its length.
-// topk = the k largest keys, equal keys by lower index. Called by a whole
-// wavefront; all control flow is wave-uniform.
+// j = e*64 + lane in kreg[e]; slots j >= n must hold key 0, which no
+// threshold counts (every score, -inf included, has a key >= 0x007FFFFF).
+// Writes to sel_lds the ascending list ({0, own} U topk) restricted to blocks
+// <= own, returns its length. topk = the k largest keys, equal keys by lower
+// index; n >= k. Called by a whole wavefront; control flow is wave-uniform.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int ballot_count(bool p) {
+    return __builtin_popcountll(__builtin_amdgcn_ballot_w64(p));
+}
+
 template <int CH>
 __device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, int k, int own,
                                            int32_t* sel_lds) {
     const int lane = threadIdx.x % kWave;
-    // T = the k-th largest key: the largest T with count(key >= T) >= k
+    // T = the k-th largest key: the largest T with count(key >= T) >= k,
+    // one bit per round (a compare and a popcount per key register)
     uint32_t T = 0;
+#pragma unroll 4
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t c = T | (1u << bit);
         int cnt = 0;
 #pragma unroll
-        for (int e = 0; e < CH; ++e) cnt += __popcll(__ballot(e * kWave + lane < n && kreg[e] >= c));
-        if (cnt >= k) T = c;
+        for (int e = 0; e < CH; ++e) cnt += ballot_count(kreg[e] >= c);
+        T = cnt >= k ? c : T;
     }
     int above = 0;
 #pragma unroll
-    for (int e = 0; e < CH; ++e) above += __popcll(__ballot(e * kWave + lane < n && kreg[e] > T));
+    for (int e = 0; e < CH; ++e) above += ballot_count(kreg[e] > T);
     int need_eq = k - above;  // keys equal to T, taken in index order
     const uint64_t lanes_below = (1ull << lane) - 1ull;
     int m = 0;
@@ -131,8 +138,8 @@ __device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, in
     for (int e = 0; e < CH; ++e) {
         const int j = e * kWave + lane;
         const bool in = j < n;
-        const uint64_t gt = __ballot(in && kreg[e] > T);
-        uint64_t eq = __ballot(in && kreg[e] == T);
+        const uint64_t gt = __builtin_amdgcn_ballot_w64(kreg[e] > T);
+        uint64_t eq = __builtin_amdgcn_ballot_w64(kreg[e] == T);
         uint64_t keep = 0;
         for (; need_eq > 0 && eq != 0; --need_eq) {
             const uint64_t low = eq & (~eq + 1ull);
