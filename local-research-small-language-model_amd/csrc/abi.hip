@@ -242,8 +242,10 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
     SPARDA_REQUIRE(dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "select_decode: forecast dtype %d", f_dtype);
     SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
                    "select_decode: unknown routing %d", routing);
-    SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D <= kMaxHeadDim && block_size > 0, SPARDA_ERR_SHAPE,
-                   "select_decode: bad sizes (D must be <= %d)", kMaxHeadDim);
+    SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D <= kMaxHeadDim && D % 4 == 0 && block_size > 0,
+                   SPARDA_ERR_SHAPE, "select_decode: bad sizes (D must be a multiple of 4, <= %d)", kMaxHeadDim);
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
+                   "select_decode: block_sums must be 16-byte aligned");
     SPARDA_REQUIRE(len >= 1 && pos >= len - 1, SPARDA_ERR_SHAPE,
                    "select_decode: need len >= 1 and pos >= len-1 (len=%lld pos=%lld)", (long long)len,
                    (long long)pos);

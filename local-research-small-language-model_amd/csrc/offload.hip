@@ -214,50 +214,74 @@ int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sum
 // own = pos/bs. If own+1 <= k+2 every block 0..own is selected (the dense
 // fallback); otherwise sel = ascending {0, own} U top-k (ties by lower index).
 // ---------------------------------------------------------------------------
+constexpr int kSelThreads = 256;
+constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
+
 template <int FDT, int CH>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(kSelThreads)
 select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, const float* __restrict__ sums,
                      int64_t H, int64_t D, int64_t nb_stride, int64_t n_present, int64_t pos, int64_t score_pos,
                      int64_t bs, int k, float scale, int32_t* __restrict__ sel, int32_t* __restrict__ n_sel,
                      int cap) {
     __shared__ float f_lds[kMaxHeadDim];
+    __shared__ uint32_t key_lds[kSelMaxBlocks];
     __shared__ int32_t sel_lds[kMaxSelCap + 2];
+    __shared__ int m_lds;
     const int g = blockIdx.x;
     const int b = blockIdx.y;
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
     const int own = static_cast<int>(pos / bs);
-    for (int64_t d = lane; d < D; d += kWave) f_lds[d] = load_elem<FDT>(f, b * f_sb + g * f_sh + d);
+    for (int64_t d = tid; d < D; d += kSelThreads) f_lds[d] = load_elem<FDT>(f, b * f_sb + g * f_sh + d);
     __syncthreads();
-    int m;
-    if (own + 1 <= k + 2) {
-        m = own + 1;
-        if (lane < m) sel_lds[lane] = lane;
-    } else {
+    const bool dense = own + 1 <= k + 2;
+    if (!dense) {
+        // every thread scores blocks tid, tid + 256, ...: p = sum / bs, canonical fma chain
         const float den = static_cast<float>(bs);
         const int64_t limit = score_pos / bs;
-        uint32_t kreg[CH];
-#pragma unroll
-        for (int e = 0; e < CH; ++e) {
-            const int64_t j = static_cast<int64_t>(e) * kWave + lane;
+        for (int64_t j = tid; j < n_present; j += kSelThreads) {
             float s = -__builtin_inff();
-            if (j < n_present && j <= limit) {
+            if (j <= limit) {
                 const float* p = sums + ((b * nb_stride + j) * H + g) * D;
                 float acc = 0.0f;
-                for (int64_t d = 0; d < D; ++d) acc = __fmaf_rn(f_lds[d], p[d] / den, acc);
+                for (int64_t d = 0; d < D; d += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(p + d);
+                    acc = __fmaf_rn(f_lds[d], v.x / den, acc);
+                    acc = __fmaf_rn(f_lds[d + 1], v.y / den, acc);
+                    acc = __fmaf_rn(f_lds[d + 2], v.z / den, acc);
+                    acc = __fmaf_rn(f_lds[d + 3], v.w / den, acc);
+                }
                 s = acc * scale;
             }
-            kreg[e] = j < n_present ? order_key(s) : 0u;
-        }
-        m = wave_select<CH>(kreg, static_cast<int>(n_present), k, own, sel_lds);
-        if (own >= n_present) {  // the own block holds no token yet: it has no score but is attended
-            if (lane == 0) sel_lds[m] = own;
-            m += 1;
+            key_lds[j] = order_key(s);
         }
     }
     __syncthreads();
-    for (int i = lane; i < cap; i += kWave) sel[bg * cap + i] = i < m ? sel_lds[i] : -1;
-    if (lane == 0) n_sel[bg] = m;
+    if (tid < kWave) {
+        int m;
+        if (dense) {
+            m = own + 1;
+            if (lane < m) sel_lds[lane] = lane;
+        } else {
+            uint32_t kreg[CH];
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+                const int64_t j = static_cast<int64_t>(e) * kWave + lane;
+                kreg[e] = j < n_present ? key_lds[j] : 0u;
+            }
+            m = wave_select<CH>(kreg, static_cast<int>(n_present), k, own, sel_lds);
+            if (own >= n_present) {  // the own block holds no token yet: it has no score but is attended
+                if (lane == 0) sel_lds[m] = own;
+                m += 1;
+            }
+        }
+        if (lane == 0) m_lds = m;
+    }
+    __syncthreads();
+    const int m = m_lds;
+    for (int i = tid; i < cap; i += kSelThreads) sel[bg * cap + i] = i < m ? sel_lds[i] : -1;
+    if (tid == 0) n_sel[bg] = m;
 }
 
 int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
@@ -268,7 +292,7 @@ int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, 
     const int64_t score_pos = routing == SPARDA_ROUTE_ABSOLUTE ? pos : 0;
     dim3 grid(static_cast<unsigned>(H), static_cast<unsigned>(B));
 #define SPARDA_SEL(FDT_, CH_)                                                                            \
-    hipLaunchKernelGGL((select_decode_kernel<FDT_, CH_>), grid, dim3(kWave), 0, stream, f, f_sb, f_sh,   \
+    hipLaunchKernelGGL((select_decode_kernel<FDT_, CH_>), grid, dim3(kSelThreads), 0, stream, f, f_sb, f_sh, \
                        sums, H, D, nb_stride, n_present, pos, score_pos, bs, static_cast<int>(k), scale, \
                        sel, n_sel, static_cast<int>(cap))
 #define SPARDA_SEL_C(FDT_)                          \
