@@ -125,7 +125,7 @@ SPARDA_API int sparda_compress(const void* k, int dtype,
  *                    causal, sorted ascending, no duplicates, padded with -1;
  *                    own = min((query_pos0 + t) / bs, NB-1); n_sel = count
  *   forecast: [B,Tq,H,Df] of f_dtype, strides (f_sb, f_st, f_sh, 1)
- *   protos:   [B,NB,H,Df] fp32 contiguous (sparda_compress output)
+ *   protos:   [B,NB,H,Df] fp32 contiguous, 16-byte aligned (sparda_compress output)
  * Any of topk / scores / sel (+n_sel) may be NULL. sel_cap >= min(top_k,NB)+2.
  * The reference's prefill uses score_pos0 = query_pos0 = 0.
  */

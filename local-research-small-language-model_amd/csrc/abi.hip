@@ -77,6 +77,8 @@ SPARDA_API int sparda_route(const void* forecast, int f_dtype, int64_t f_sb, int
     SPARDA_REQUIRE(!sel || sel_cap >= ke + 2, SPARDA_ERR_SHAPE, "route: sel_cap %lld < %lld",
                    (long long)sel_cap, (long long)(ke + 2));
     SPARDA_REQUIRE(f_sb >= 0 && f_st >= 0 && f_sh >= 0, SPARDA_ERR_STRIDE, "route: negative stride");
+    SPARDA_REQUIRE(reinterpret_cast<uintptr_t>(protos) % 16 == 0, SPARDA_ERR_STRIDE,
+                   "route: prototypes must be 16-byte aligned");
     return launch_route(forecast, f_dtype, f_sb, f_st, f_sh, protos, B, Tq, H, Df, NB, block_size,
                         static_cast<int>(ke), causal != 0, score_pos0, query_pos0, scale, topk, scores,
                         sel, n_sel, static_cast<int>(sel ? sel_cap : 0), static_cast<hipStream_t>(stream));

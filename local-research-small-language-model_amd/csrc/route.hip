@@ -72,124 +72,186 @@ int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, i
 }
 
 // ---------------------------------------------------------------------------
-// router: LPR lanes per query row, 256 threads = 256/LPR rows of one (b, h).
-// Lane `sub` of a row scores the blocks j = sub (mod LPR), two fma chains in
-// flight, and keeps its own top-k list; the LPR lists of a row are merged by
-// a butterfly of shuffles, after which every lane of the row holds the row's
-// top-k. The (b, h) prototypes are staged in LDS in chunks (rows padded to
-// DF+4 floats) and read as broadcasts.
+// router: one lane per query row. A workgroup of kRouteWaves wavefronts takes
+// two sets of 64 consecutive rows of one (b, h): set p and its mirror NS-1-p,
+// so that under the causal mask every workgroup scores about the same number
+// of (row, block) pairs. Within a set the waves split the candidate blocks
+// (wave w scores the blocks j = w mod kRouteWaves), so the block index is
+// uniform across the wavefront: every 16-lane row of the wavefront loads the
+// block's prototype with one coalesced load (lane i of the row holds elements
+// E*i .. E*i+E-1, E = DF/16), one block ahead of its use, and the fma chain
+// takes element d from lane d/E of the row through a DPP row broadcast. Every
+// lane keeps a descending list of route keys; after a set the waves' lists are
+// merged through LDS by one wave (rotating with the set), which writes the
+// rows' outputs.
 // ---------------------------------------------------------------------------
-constexpr int kRouteThreads = 256;
+// N consecutive fp32 values (N in {1, 2, 4, 8}), 4*N-byte aligned
+template <int N>
+__device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&o)[N]) {
+    if constexpr (N == 1) {
+        o[0] = p[0];
+    } else if constexpr (N == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(p);
+        o[0] = v.x; o[1] = v.y;
+    } else {
+#pragma unroll
+        for (int q = 0; q < N; q += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(p + q);
+            o[q] = v.x; o[q + 1] = v.y; o[q + 2] = v.z; o[q + 3] = v.w;
+        }
+    }
+}
 
-template <int FDT, int DF, int KMAX, int LPR>
+// Two fma chains, one step: acc[c] = fma(a, element of lane I of this lane's
+// 16-lane row of p[c], acc[c]), each a v_fmac_f32 with a DPP row_newbcast
+// source (a separate DPP move does not fold into the fma, which is a VOP3 op
+// at that point). A DPP instruction needs two wait states after a VALU write
+// of any register it reads. The compiler does not track that for inline
+// assembly, so the steps carry their own: the two fmas of a step write
+// different accumulators and end with s_nop 0, so an accumulator is read two
+// wait states after its last write, and the steps that first read the
+// prototype registers (FIRST) start with s_nop 1. What the compiler places
+// between steps (spill reloads, copies) is checked on the built code by the
+// test suite.
+template <int I, bool FIRST>
+__device__ __forceinline__ void fma_row_bcast(float (&acc)[2], float a, const float (&p)[2]) {
+    if constexpr (FIRST)
+        asm("s_nop 1\n\tv_fmac_f32_dpp %0, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %1, %3, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\ts_nop 0"
+            : "+v"(acc[0]), "+v"(acc[1]) : "v"(p[0]), "v"(p[1]), "v"(a), "n"(I));
+    else
+        asm("v_fmac_f32_dpp %0, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %1, %3, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\ts_nop 0"
+            : "+v"(acc[0]), "+v"(acc[1]) : "v"(p[0]), "v"(p[1]), "v"(a), "n"(I));
+}
+// acc[c] = fma chain over d = E*I + e (I = I0..15, e = 0..E-1) with element d
+// of prototype c taken from lane I of the row (register pc[e][c])
+template <int E, int DF, int C, int I0 = 0>
+__device__ __forceinline__ void row_fma_chains(const float (&fr)[DF], const float (&pc)[E][C],
+                                               float (&acc)[C]) {
+    if constexpr (I0 < 16) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) fma_row_bcast<I0, I0 == 0>(acc, fr[E * I0 + e], pc[e]);
+        row_fma_chains<E, DF, C, I0 + 1>(fr, pc, acc);
+    }
+}
+
+constexpr int kRouteWaves = 4;
+constexpr int kRouteThreads = kRouteWaves * kWave;
+
+template <int FDT, int DF, int KMAX>
 __global__ void __launch_bounds__(kRouteThreads)
 route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t fsh,
                   const float* __restrict__ protos, int64_t Tq, int H, int64_t NB, int bs,
                   int ke, int causal, int64_t score_pos0, int64_t query_pos0, float scale,
-                  int chunk_blocks,
                   int32_t* __restrict__ topk, float* __restrict__ scores,
                   int32_t* __restrict__ sel, int32_t* __restrict__ n_sel, int cap) {
-    constexpr int PS = DF + 4;                  // padded prototype row in LDS
-    constexpr int ROWS = kRouteThreads / LPR;
-    extern __shared__ float p_lds[];            // [chunk_blocks][PS]
+    extern __shared__ double lists[];  // [kRouteWaves][KMAX][kWave]
+    const int lane = threadIdx.x % kWave;
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
     const int h = blockIdx.y;
     const int b = blockIdx.z;
-    const int sub = threadIdx.x % LPR;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * ROWS;
-    const int64_t t = t0 + threadIdx.x / LPR;
-    const bool active = t < Tq;
-    const int64_t t_last = (t0 + ROWS < Tq ? t0 + ROWS : Tq) - 1;
+    const int64_t NS = cdiv(Tq, kWave);
+    const int64_t pair = blockIdx.x;
+    const float* __restrict__ pbh = protos + (static_cast<int64_t>(b) * NB * H + h) * DF;
+    const int64_t pstride = static_cast<int64_t>(H) * DF;
 
-    int64_t jmax_wg = causal ? (score_pos0 + t_last) / bs : NB - 1;
-    if (jmax_wg > NB - 1) jmax_wg = NB - 1;
-    int64_t limit = causal ? (score_pos0 + (active ? t : t_last)) / bs : NB - 1;
-    if (limit > NB - 1) limit = NB - 1;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int64_t set = pass == 0 ? pair : NS - 1 - pair;
+        if (pass == 1 && set == pair) break;  // odd set count: the middle set has no mirror
+        const int64_t t = set * kWave + lane;
+        const bool active = t < Tq;
+        const int64_t tc = active ? t : Tq - 1;
+        const int64_t t_last = (set * kWave + kWave < Tq ? set * kWave + kWave : Tq) - 1;
+        int64_t limit = causal ? (score_pos0 + tc) / bs : NB - 1;
+        if (limit > NB - 1) limit = NB - 1;
+        int64_t jmax = causal ? (score_pos0 + t_last) / bs : NB - 1;  // uniform
+        if (jmax > NB - 1) jmax = NB - 1;
 
-    float fr[DF];
-    {
-        const int64_t base = b * fsb + (active ? t : t_last) * fst + h * fsh;
+        float fr[DF];
+        {
+            const int64_t base = b * fsb + tc * fst + h * fsh;
 #pragma unroll
-        for (int d = 0; d < DF; ++d) fr[d] = load_elem<FDT>(f, base + d);
-    }
-    const int64_t row = (static_cast<int64_t>(b) * H + h) * Tq + t;
-    float* srow = (scores != nullptr && active) ? scores + row * NB : nullptr;
-
-    LaneTopK<KMAX> best;
-    best.init(ke);
-
-    const float* pbh = protos + (static_cast<int64_t>(b) * NB * H + h) * DF;  // + j*H*DF
-    for (int64_t c0 = 0; c0 <= jmax_wg; c0 += chunk_blocks) {
-        const int64_t c1 = (c0 + chunk_blocks - 1 < jmax_wg) ? c0 + chunk_blocks - 1 : jmax_wg;
-        const int nblk = static_cast<int>(c1 - c0 + 1);
-        __syncthreads();
-        for (int i = threadIdx.x; i < nblk * DF; i += kRouteThreads) {
-            const int jj = i / DF, d = i % DF;
-            p_lds[jj * PS + d] = pbh[(c0 + jj) * H * DF + d];
+            for (int d = 0; d < DF; ++d) fr[d] = load_elem<FDT>(f, base + d);
         }
-        __syncthreads();
-        const int64_t jend = limit < c1 ? limit : c1;
-        int64_t j = c0 + sub;
-        for (; j + LPR <= jend; j += 2 * LPR) {
-            const float* pa = p_lds + (j - c0) * PS;
-            const float* pb = pa + LPR * PS;
-            float a0 = 0.0f, a1 = 0.0f;
+        const int64_t row = (static_cast<int64_t>(b) * H + h) * Tq + t;
+        float* srow = (scores != nullptr && active) ? scores + row * NB : nullptr;
+
+        KeyTopK<KMAX> best;
+        best.init();
+        constexpr int E = DF / 16;
+        constexpr int C = 2;  // blocks scored side by side
+        const float* __restrict__ prow = pbh + (lane % 16) * E;
+        float pn[C][E];
 #pragma unroll
-            for (int d = 0; d < DF; ++d) {
-                a0 = __fmaf_rn(fr[d], pa[d], a0);
-                a1 = __fmaf_rn(fr[d], pb[d], a1);
+        for (int c = 0; c < C; ++c) {
+            const int64_t jc = w + c * kRouteWaves;
+            load_f32<E>(prow + (jc < jmax ? jc : jmax) * pstride, pn[c]);
+        }
+        for (int64_t j = w; j <= jmax; j += C * kRouteWaves) {
+            float pc[E][C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) pc[e][c] = pn[c][e];
+                const int64_t jn = j + (C + c) * kRouteWaves;
+                load_f32<E>(prow + (jn < jmax ? jn : jmax) * pstride, pn[c]);
             }
-            const float s0 = a0 * scale, s1 = a1 * scale;
-            if (srow) {
-                srow[j] = s0;
-                srow[j + LPR] = s1;
+            float acc[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) acc[c] = 0.0f;
+            row_fma_chains<E, DF, C>(fr, pc, acc);
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                const int64_t jc = j + c * kRouteWaves;
+                const float sc = acc[c] * scale;
+                const bool ok = jc <= limit;  // limit <= jmax
+                if (srow && ok) srow[jc] = sc;
+                best.push(ok ? route_key(sc, static_cast<int32_t>(jc)) : 0.0);
             }
-            best.push(rank64(s0, static_cast<int32_t>(j)));
-            best.push(rank64(s1, static_cast<int32_t>(j + LPR)));
         }
-        if (j <= jend) {
-            const float* pa = p_lds + (j - c0) * PS;
-            float a0 = 0.0f;
-#pragma unroll
-            for (int d = 0; d < DF; ++d) a0 = __fmaf_rn(fr[d], pa[d], a0);
-            const float s0 = a0 * scale;
-            if (srow) srow[j] = s0;
-            best.push(rank64(s0, static_cast<int32_t>(j)));
+        if (srow) {
+            for (int64_t j = w; j < NB; j += kRouteWaves)
+                if (j > limit) srow[j] = -__builtin_inff();
         }
-    }
-    // butterfly merge of the LPR lists of each row (lanes of a row are adjacent)
+
+        // merge the waves' lists in the merging wave
+        const int m = static_cast<int>((2 * pair + pass) % kRouteWaves);
+        __syncthreads();  // the previous set's merger has read its lists
+        if (w != m) {
 #pragma unroll
-    for (int lvl = 1; lvl < LPR; lvl <<= 1) {
-        uint64_t other[KMAX];
+            for (int i = 0; i < KMAX; ++i) lists[(w * KMAX + i) * kWave + lane] = best.r[i];
+        }
+        __syncthreads();
+        if (w != m) continue;
+        for (int o = 0; o < kRouteWaves; ++o) {
+            if (o == m) continue;
+            double other[KMAX];
 #pragma unroll
-        for (int i = 0; i < KMAX; ++i) other[i] = __shfl_xor(best.r[i], lvl, kWave);
+            for (int i = 0; i < KMAX; ++i) other[i] = lists[(o * KMAX + i) * kWave + lane];
+            best.merge(other);
+        }
+        if (!active) continue;
+        // slots not filled by a candidate take the masked blocks in ascending order
+        int32_t picks[KMAX];
 #pragma unroll
-        for (int i = 0; i < KMAX; ++i)
-            if (i < ke && other[i] != 0ull) best.push(other[i]);
-    }
-    if (!active) return;
-    if (srow) {
-        for (int64_t jj = limit + 1 + sub; jj < NB; jj += LPR) srow[jj] = -__builtin_inff();
-    }
-    if (sub != 0) return;
-    // slots not filled by a candidate take the masked blocks in ascending order
-    int32_t picks[KMAX];
+        for (int i = 0; i < KMAX; ++i) picks[i] = (i < ke) ? (best.r[i] == 0.0 ? i : route_key_index(best.r[i])) : -1;
+        if (topk) {
+            int32_t* tr = topk + row * ke;
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) picks[i] = (i < ke) ? (best.r[i] == 0 ? i : rank64_index(best.r[i])) : -1;
-    if (topk) {
-        int32_t* tr = topk + row * ke;
+            for (int i = 0; i < KMAX; ++i)
+                if (i < ke) tr[i] = picks[i];
+        }
+        if (sel) {
+            int64_t own = (query_pos0 + t) / bs;
+            if (own > NB - 1) own = NB - 1;
+            int32_t c[KMAX + 2];
+            c[0] = 0;
+            c[1] = static_cast<int32_t>(own);
 #pragma unroll
-        for (int i = 0; i < KMAX; ++i)
-            if (i < ke) tr[i] = picks[i];
-    }
-    if (sel) {
-        int64_t own = (query_pos0 + t) / bs;
-        if (own > NB - 1) own = NB - 1;
-        int32_t c[KMAX + 2];
-        c[0] = 0;
-        c[1] = static_cast<int32_t>(own);
-#pragma unroll
-        for (int i = 0; i < KMAX; ++i) c[i + 2] = picks[i];
-        emit_selection(c, static_cast<int>(own), causal != 0, sel + row * cap, cap, n_sel + row);
+            for (int i = 0; i < KMAX; ++i) c[i + 2] = picks[i];
+            emit_selection(c, static_cast<int>(own), causal != 0, sel + row * cap, cap, n_sel + row);
+        }
     }
 }
 
@@ -199,28 +261,17 @@ static int launch_route_df(const void* f, int64_t fsb, int64_t fst, int64_t fsh,
                            int causal, int64_t score_pos0, int64_t query_pos0, float scale,
                            int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel, int cap,
                            hipStream_t stream) {
-    const int max_lds_floats = 16384;  // 64 KiB of prototypes per pass
-    int chunk = static_cast<int>(max_lds_floats / (DF + 4));
-    if (chunk > NB) chunk = static_cast<int>(NB);
-    const size_t lds = static_cast<size_t>(chunk) * (DF + 4) * sizeof(float);
-    // candidate blocks per row decide the lanes per row
-    const int64_t span = causal ? (score_pos0 + Tq - 1) / bs + 1 : NB;
-    const int lpr = span >= 32 ? 4 : (span >= 8 ? 2 : 1);
-    const int rows = kRouteThreads / lpr;
-    dim3 grid(static_cast<unsigned>(cdiv(Tq, rows)), static_cast<unsigned>(H), static_cast<unsigned>(B));
-#define SPARDA_ROUTE(KM_, L_)                                                                      \
-    hipLaunchKernelGGL((route_rows_kernel<FDT, DF, KM_, L_>), grid, dim3(kRouteThreads), lds, stream, \
+    const int64_t pairs = cdiv(cdiv(Tq, kWave), 2);
+    dim3 grid(static_cast<unsigned>(pairs), static_cast<unsigned>(H), static_cast<unsigned>(B));
+#define SPARDA_ROUTE(KM_)                                                                          \
+    hipLaunchKernelGGL((route_rows_kernel<FDT, DF, KM_>), grid, dim3(kRouteThreads),               \
+                       static_cast<size_t>(kRouteWaves) * KM_ * kWave * sizeof(double), stream,    \
                        f, fsb, fst, fsh, protos, Tq, static_cast<int>(H), NB,                      \
                        static_cast<int>(bs), ke, causal, score_pos0, query_pos0, scale,            \
-                       chunk, topk, scores, sel, n_sel, cap)
-#define SPARDA_ROUTE_L(KM_)                                       \
-    if (lpr == 4) SPARDA_ROUTE(KM_, 4);                           \
-    else if (lpr == 2) SPARDA_ROUTE(KM_, 2);                      \
-    else SPARDA_ROUTE(KM_, 1);
-    if (ke <= 8) { SPARDA_ROUTE_L(8) }
-    else if (ke <= 16) { SPARDA_ROUTE_L(16) }
-    else { SPARDA_ROUTE_L(32) }
-#undef SPARDA_ROUTE_L
+                       topk, scores, sel, n_sel, cap)
+    if (ke <= 8) { SPARDA_ROUTE(8); }
+    else if (ke <= 16) { SPARDA_ROUTE(16); }
+    else { SPARDA_ROUTE(32); }
 #undef SPARDA_ROUTE
     return check_hip(hipGetLastError(), "route_rows_kernel");
 }

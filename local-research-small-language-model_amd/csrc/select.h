@@ -40,6 +40,74 @@ struct LaneTopK {
     }
 };
 
+// ---------------------------------------------------------------------------
+// route keys: a (score, index) pair as a non-negative double whose bit pattern
+// holds order_key(score) in bits 62..31 and 0x7FFFFFFF - index in bits 30..0.
+// A larger key is a larger score, equal scores the lower index. Non-negative
+// doubles order exactly as their bit patterns, so a compare-exchange of two
+// keys is one max and one min. Key 0 (+0.0) marks an empty slot; every real
+// key is above it. order_key is capped at 0xFFDFFFFF so that no key is a NaN
+// (only NaN scores whose two top mantissa bits are set reach the cap).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double route_key(float s, int32_t idx) {
+    uint32_t ok = order_key(s);
+    ok = ok < 0xFFDFFFFFu ? ok : 0xFFDFFFFFu;
+    const uint32_t lo = (ok << 31) | (0x7FFFFFFFu - static_cast<uint32_t>(idx));
+    return __hiloint2double(static_cast<int>(ok >> 1), static_cast<int>(lo));
+}
+__device__ __forceinline__ int32_t route_key_index(double k) {
+    return static_cast<int32_t>(0x7FFFFFFFu - (static_cast<uint32_t>(__double2loint(k)) & 0x7FFFFFFFu));
+}
+
+// max / min of two route keys. Keys are never NaN, so the quieting of inputs
+// that IEEE-mode maxnum would add is not needed: issue the instructions as is.
+__device__ __forceinline__ double key_max(double a, double b) {
+    double r;
+    asm("v_max_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ double key_min(double a, double b) {
+    double r;
+    asm("v_min_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// per-lane list of the KMAX largest route keys, descending
+template <int KMAX>
+struct KeyTopK {
+    double r[KMAX];
+
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) r[i] = 0.0;
+    }
+    __device__ __forceinline__ void push(double x) {
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            const double lo = key_min(r[i], x);
+            asm("v_max_f64 %0, %0, %1" : "+v"(r[i]) : "v"(x));
+            x = lo;
+        }
+    }
+    // r <- the KMAX largest of r and o (both descending): bitonic merge
+    __device__ __forceinline__ void merge(const double (&o)[KMAX]) {
+        static_assert((KMAX & (KMAX - 1)) == 0, "KMAX must be a power of two");
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) r[i] = key_max(r[i], o[KMAX - 1 - i]);
+#pragma unroll
+        for (int s = KMAX / 2; s > 0; s >>= 1) {
+#pragma unroll
+            for (int i = 0; i < KMAX; ++i) {
+                if ((i & s) == 0) {
+                    const double a = r[i], c = r[i + s];
+                    r[i] = key_max(a, c);
+                    r[i + s] = key_min(a, c);
+                }
+            }
+        }
+    }
+};
+
 // Sorted, de-duplicated selection list ({0, own} U picks, restricted to <= own
 // when causal) written to sel[0..cap), count to *n_out.
 template <int N>
