@@ -45,6 +45,8 @@ DB, DS = 8, 16384
 N_CACHES = 4
 # offload workload
 OB_LAYERS, OB_CTX = 12, 32768
+# 12-layer forward workload
+MT = 16384
 # plain copy used to calibrate the HBM byte counters
 COPY_BYTES = 256 << 20
 
@@ -62,7 +64,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--offload-steps", type=int, default=32)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "pmc"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "pmc"], default="all",
                     help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
 
@@ -191,9 +193,49 @@ def bench_decode(args, torch, sparda, synth):
         ref = sparda.decode(caches[0]["q"], caches[0]["k_cache"], caches[0]["v_cache"], DS, caches[0]["forecast"],
                             BS, TOPK, routing="absolute", workspace=ws)
         assert torch.equal(ref, outs[0]), "graph replay differs from eager decode"
+        # cached prototypes: block sums kept in HBM, the step recomputes the
+        # current block's sums (64 tokens), selects from the sums and attends
+        # in place -- no whole-cache compression
+        nb = DS // BS
+        cb = (DS - 1) // BS
+        sums = [torch.zeros((DB, nb, HKV, D), dtype=torch.float32, device="cuda") for _ in range(N_CACHES)]
+        sels = [torch.empty((DB, HKV, TOPK + 2), dtype=torch.int32, device="cuda") for _ in range(N_CACHES)]
+        nsel = [torch.empty((DB, HKV), dtype=torch.int32, device="cuda") for _ in range(N_CACHES)]
+        outs_c = [torch.empty((DB, HQ * D), dtype=torch.bfloat16, device="cuda") for _ in range(N_CACHES)]
+        for i, c in enumerate(caches):
+            sparda.block_sums(c["k_cache"], 0, DS, BS, sums[i])
+
+        def one_cached(i):
+            j = i % N_CACHES
+            c = caches[j]
+            sparda.block_sums(c["k_cache"], cb * BS, DS - cb * BS, BS, sums[j])
+            sparda.select_decode(c["forecast"], sums[j], DS, DS - 1, BS, TOPK, routing="absolute",
+                                 sel=sels[j], n_sel=nsel[j])
+            sparda.decode_selected(c["q"], c["k_cache"], c["v_cache"], DS, BS, sels[j], nsel[j], out=outs_c[j])
+
+        for i in range(8):
+            one_cached(i)
+        torch.cuda.synchronize()
+        eager_c_us = events_ms(lambda: [one_cached(i) for i in range(args.decode_steps)], 1, torch) * 1e3 / args.decode_steps
+        gc = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(4):
+                one_cached(i)
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(gc):
+            for i in range(args.decode_steps):
+                one_cached(i)
+        gc.replay()
+        torch.cuda.synchronize()
+        cached_us = events_ms(gc.replay, 3, torch) * 1e3 / args.decode_steps
+        assert torch.equal(sels[0], sparda.select_decode(caches[0]["forecast"], sums[0], DS, DS - 1, BS, TOPK,
+                                                         routing="absolute")[0])
     k_stream = DB * DS * HKV * D * 2
     small = DB * HQ * D * 2 * 2 + DB * HKV * D * 2 + DB * HKV * (DS // BS) * 4 * 2
     total = k_stream + gathered + small
+    cached_total = DB * nb * HKV * D * 4 + DB * BS * HKV * D * 2 + gathered + DB * HQ * D * 2 * 2 + DB * HKV * D * 2
     return {
         "us_per_step": graph_us,
         "us_per_step_eager": eager_us,
@@ -201,6 +243,9 @@ def bench_decode(args, torch, sparda, synth):
         "gbs": total / (graph_us * 1e-6) / 1e9,
         "k_stream_bytes": k_stream,
         "gathered_bytes": gathered,
+        "us_per_step_cached_protos": cached_us,
+        "us_per_step_cached_protos_eager": eager_c_us,
+        "cached_bytes_per_step": cached_total,
     }
 
 
@@ -305,6 +350,64 @@ def bench_offload(args, torch, sparda, synth):
     }
 
 
+def bench_model(args, torch, sparda, synth):
+    """12-layer forward of the model at B=1, T=16384 (bf16 weights from the
+    model's N(0, 0.02) init, vocab 32000 tied, d 768, 12/4 heads, SwiGLU 2048;
+    layer 0 dense causal, layers 1..11 forecast-routed sparse with layer L's
+    forecast routing layer L+1), token ids uniform in [0, 32000). Reports
+    tok/s of the whole forward (embeddings to logits) and the time of each
+    layer's attention (projections + RoPE + compress + route + attention +
+    output projection), from HIP events recorded around the attention modules."""
+    from model.config import ModelConfig
+    from model.model import SparDAResearchModel
+    dev = torch.device("cuda")
+    cfg = ModelConfig(n_layer=12, context_length=MT, block_size=BS, top_k_blocks=TOPK,
+                      attention_backend="hip_sparse", norm_eps=1e-5)
+    torch.manual_seed(1003)
+    model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(1003)
+    ids = torch.randint(0, cfg.vocab_size, (1, MT), generator=g).to(dev)
+    starts, ends = [], []
+    hooks = []
+    for layer in model.layers:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        starts.append(e0)
+        ends.append(e1)
+        hooks.append(layer.attention.register_forward_pre_hook(lambda m, a, e=e0: e.record()))
+        hooks.append(layer.attention.register_forward_hook(lambda m, a, o, e=e1: e.record()))
+    runs = 3
+    with torch.no_grad():
+        model(ids)
+        torch.cuda.synchronize()
+        per_layer = [0.0] * len(model.layers)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        total = 0.0
+        for _ in range(runs):
+            t0.record()
+            model(ids)
+            t1.record()
+            t1.synchronize()
+            total += t0.elapsed_time(t1)
+            for i in range(len(per_layer)):
+                per_layer[i] += starts[i].elapsed_time(ends[i])
+    for h in hooks:
+        h.remove()
+    ms = total / runs
+    attn = [x / runs for x in per_layer]
+    del model
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"12-layer forward, B=1, T={MT}, bf16 (d 768, 12/4 heads, head dim 64, SwiGLU 2048, "
+                    "vocab 32000 tied, block 64, top-8); layer 0 dense causal, layers 1-11 forecast-routed "
+                    "sparse; embeddings to logits",
+        "ms_per_forward": round(ms, 3),
+        "tok_s": round(MT / (ms * 1e-3), 1),
+        "attention_ms_per_layer": [round(x, 3) for x in attn],
+        "attention_fraction": round(sum(attn) / ms, 4),
+        "runs": runs,
+    }
+
+
 def pmc_workload(args, torch, sparda, synth):
     """Short eager run for hardware-counter passes: prefill steps, decode steps
     and a plain device copy of COPY_BYTES (the calibration of FETCH_SIZE /
@@ -365,9 +468,9 @@ def main():
     sparda.load()
     if args.only != "all":
         fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload,
-              "pmc": pmc_workload}[args.only]
+              "model": bench_model, "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
-        print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str))}}), flush=True)
+        print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}), flush=True)
         return
     log("prefill workload")
     pre = bench_prefill(args, torch, sparda, synth)
@@ -375,12 +478,18 @@ def main():
         f"({pre['attn_tflops']:.1f} TFLOP/s useful)")
     log("decode workload")
     dec = bench_decode(args, torch, sparda, synth)
-    log(f"decode: {dec['us_per_step']:.2f} us/step ({dec['gbs']:.0f} GB/s), eager {dec['us_per_step_eager']:.2f}")
+    log(f"decode: {dec['us_per_step']:.2f} us/step ({dec['gbs']:.0f} GB/s), eager {dec['us_per_step_eager']:.2f}; "
+        f"cached prototypes {dec['us_per_step_cached_protos']:.2f} us/step")
     log("offload workload")
     off = bench_offload(args, torch, sparda, synth)
     log(f"offload: async {off['us_per_step_async']:.1f} us/step, sync {off['us_per_step_sync']:.1f}, "
         f"resident {off['us_per_step_gpu_resident']:.1f}; overlap {off['overlap']}, "
         f"transfer {off['transfer_us_per_layer']} us/layer, link {off['host_link_gbs']} GB/s")
+    log("12-layer forward workload")
+    mdl = bench_model(args, torch, sparda, synth)
+    log(f"model: {mdl['ms_per_forward']:.2f} ms per {MT}-token forward ({mdl['tok_s']:.0f} tok/s), "
+        f"attention {100 * mdl['attention_fraction']:.1f}% (layer 0 dense {mdl['attention_ms_per_layer'][0]:.2f} ms, "
+        f"sparse layers {sum(mdl['attention_ms_per_layer'][1:]) / 11:.2f} ms each)")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -423,8 +532,16 @@ def main():
             "bytes_per_step": dec["bytes_per_step"],
             "k_stream_bytes": dec["k_stream_bytes"],
             "gathered_bytes": dec["gathered_bytes"],
+            "cached_prototypes": {
+                "workload": "the same step with fp32 block sums kept in HBM: recompute the current block's "
+                            "sums, select from the sums, attend in place (no whole-cache compression)",
+                "us_per_step": round(dec["us_per_step_cached_protos"], 3),
+                "us_per_step_eager": round(dec["us_per_step_cached_protos_eager"], 3),
+                "bytes_per_step": dec["cached_bytes_per_step"],
+            },
         },
         "offload": off,
+        "model_forward": mdl,
     }
     print(json.dumps(line), flush=True)
 

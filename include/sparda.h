@@ -275,6 +275,24 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                                       void* out, int64_t out_sb, void* stream);
 
 /*
+ * fp32 block sums of a device KV cache, kept current across decode steps so
+ * that decode selection (sparda_select_decode) reads the sums instead of
+ * recompressing the whole cache every step as the reference's decode does
+ * (KVBlockCompressor over all S keys, model/attention/sparse.py:133-135 with
+ * model/forecast.py:66-78). prototype = sum / bs, so the sums give the same
+ * prototypes as sparda_compress bit for bit.
+ *   k: [B,S,Hkv,D] cache base, strides (sb, st, sh, 1); tokens pos..pos+n-1
+ *     are read.
+ *   block_sums: [B,nb_stride,Hkv,D] fp32. A block whose first token is in
+ *     [pos, pos+n) is summed from zero; a block entered mid-way continues its
+ *     stored sum. With pos = j*bs the blocks j.. are recomputed from scratch,
+ *     which makes a per-step update of the current block idempotent.
+ */
+SPARDA_API int sparda_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh,
+                                 int64_t B, int64_t Hkv, int64_t D, int64_t pos, int64_t n,
+                                 int64_t block_size, int64_t nb_stride, float* block_sums, void* stream);
+
+/*
  * Decode-time block selection from fp32 block sums (prototype = sum / bs).
  * Replaces the selection step of AsyncForecastOffloadAttention.prefetch
  * (model/attention/async_offload.py:241-260) and of
@@ -287,7 +305,8 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
  *     Otherwise blocks j < ceil(len/bs) are scored as in sparda_route (mask
  *     j > pos/bs in SPARDA_ROUTE_ABSOLUTE, j > 0 in SPARDA_ROUTE_REFERENCE)
  *     and sel = ascending {0, own} U top-k, ties by lower index.
- *   forecast: [B,Hkv,D] strides (f_sb, f_sh, 1); sel/n_sel: [B,Hkv,sel_cap] / [B,Hkv]
+ *   forecast: [B,Hkv,D] strides (f_sb, f_sh, 1), D in {16, 32, 64, 128};
+ *   sel/n_sel: [B,Hkv,sel_cap] / [B,Hkv]
  */
 SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
                                     const float* block_sums,

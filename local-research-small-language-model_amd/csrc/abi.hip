@@ -244,8 +244,8 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
     SPARDA_REQUIRE(dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "select_decode: forecast dtype %d", f_dtype);
     SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
                    "select_decode: unknown routing %d", routing);
-    SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D <= kMaxHeadDim && D % 4 == 0 && block_size > 0,
-                   SPARDA_ERR_SHAPE, "select_decode: bad sizes (D must be a multiple of 4, <= %d)", kMaxHeadDim);
+    SPARDA_REQUIRE(B > 0 && Hkv > 0 && head_dim_ok(D) && block_size > 0, SPARDA_ERR_SHAPE,
+                   "select_decode: bad sizes (D must be one of 16, 32, 64, 128)");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
                    "select_decode: block_sums must be 16-byte aligned");
     SPARDA_REQUIRE(len >= 1 && pos >= len - 1, SPARDA_ERR_SHAPE,
@@ -308,6 +308,25 @@ SPARDA_API int sparda_offload_rebuild_sums(sparda_offload_t h, int64_t len, int6
     SPARDA_REQUIRE(block_size > 0 && len >= 1 && len <= offload_max_seq(h), SPARDA_ERR_SHAPE,
                    "offload_rebuild_sums: bad len/block_size");
     return offload_rebuild_sums(h, len, block_size, block_sums, static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,
+                                 int64_t Hkv, int64_t D, int64_t pos, int64_t n, int64_t block_size,
+                                 int64_t nb_stride, float* block_sums, void* stream) {
+    SPARDA_REQUIRE(k && block_sums, SPARDA_ERR_NULL, "block_sums: null k/block_sums");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "block_sums: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && block_size > 0 && nb_stride > 0, SPARDA_ERR_SHAPE,
+                   "block_sums: sizes must be positive");
+    SPARDA_REQUIRE(pos >= 0 && n >= 1, SPARDA_ERR_SHAPE, "block_sums: need pos >= 0, n >= 1");
+    SPARDA_REQUIRE((pos + n - 1) / block_size < nb_stride, SPARDA_ERR_CAPACITY,
+                   "block_sums: block %lld beyond nb_stride %lld", (long long)((pos + n - 1) / block_size),
+                   (long long)nb_stride);
+    SPARDA_REQUIRE(sb >= 0 && st >= 0 && sh >= 0, SPARDA_ERR_STRIDE, "block_sums: negative stride");
+    SPARDA_REQUIRE(B <= 65535 && (pos + n - 1) / block_size - pos / block_size < (int64_t(1) << 31),
+                   SPARDA_ERR_SHAPE, "block_sums: too large");
+    const char* kp = static_cast<const char*>(k) + pos * st * (dtype == SPARDA_F32 ? 4 : 2);
+    return launch_block_sums(kp, dtype, sb, st, sh, pos, n, B, Hkv, D, block_size, nb_stride, block_sums,
+                             static_cast<hipStream_t>(stream));
 }
 
 SPARDA_API int sparda_offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,

@@ -63,6 +63,11 @@ int64_t offload_max_seq(sparda_offload_t h);
 int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb, int64_t st, int64_t sh,
                    int64_t pos, int64_t n, int64_t bs, float* sums, hipStream_t stream);
 int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sums, hipStream_t stream);
+
+// fp32 block sums of tokens pos..pos+n-1; k points at token pos (strides sb, st, sh)
+int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
+                      int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
+                      float* sums, hipStream_t stream);
 int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t bs,
                   int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream);
 

@@ -144,6 +144,7 @@ template <int DT>
 __global__ void __launch_bounds__(256)
 block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh, int64_t pos, int64_t n,
                   int64_t H, int64_t D, int64_t bs, int64_t nb_stride, float* __restrict__ sums) {
+    constexpr int U = 32;  // token loads in flight per thread, added in token order
     const int64_t j = pos / bs + blockIdx.x;
     const int64_t b = blockIdx.y;
     const int64_t s_lo = j * bs > pos ? j * bs : pos;
@@ -151,15 +152,24 @@ block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh
     for (int64_t e = threadIdx.x; e < H * D; e += blockDim.x) {
         const int64_t g = e / D, d = e % D;
         float* out = sums + ((b * nb_stride + j) * H + g) * D + d;
+        const int64_t base = b * sb + g * sh + d;
         float acc = s_lo == j * bs ? 0.0f : *out;
-        for (int64_t s = s_lo; s < s_hi; ++s) acc = acc + load_elem<DT>(k, b * sb + (s - pos) * st + g * sh + d);
+        int64_t s = s_lo;
+        for (; s + U <= s_hi; s += U) {
+            float x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + (s + u - pos) * st);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc = acc + x[u];
+        }
+        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(k, base + (s - pos) * st);
         *out = acc;
     }
 }
 
-static int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
-                             int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
-                             float* sums, hipStream_t stream) {
+int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
+                      int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
+                      float* sums, hipStream_t stream) {
     const int64_t nblk = (pos + n - 1) / bs - pos / bs + 1;
     dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(B));
     int threads = static_cast<int>(H * D < 256 ? H * D : 256);
@@ -217,10 +227,10 @@ int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sum
 constexpr int kSelThreads = 256;
 constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
 
-template <int FDT, int CH>
+template <int FDT, int CH, int DH, bool POW2>
 __global__ void __launch_bounds__(kSelThreads)
 select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, const float* __restrict__ sums,
-                     int64_t H, int64_t D, int64_t nb_stride, int64_t n_present, int64_t pos, int64_t score_pos,
+                     int64_t H, int64_t nb_stride, int64_t n_present, int64_t pos, int64_t score_pos,
                      int64_t bs, int k, float scale, int32_t* __restrict__ sel, int32_t* __restrict__ n_sel,
                      int cap) {
     __shared__ float f_lds[kMaxHeadDim];
@@ -233,24 +243,31 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
     const int lane = tid % kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
     const int own = static_cast<int>(pos / bs);
-    for (int64_t d = tid; d < D; d += kSelThreads) f_lds[d] = load_elem<FDT>(f, b * f_sb + g * f_sh + d);
+    for (int d = tid; d < DH; d += kSelThreads) f_lds[d] = load_elem<FDT>(f, b * f_sb + g * f_sh + d);
     __syncthreads();
     const bool dense = own + 1 <= k + 2;
     if (!dense) {
-        // every thread scores blocks tid, tid + 256, ...: p = sum / bs, canonical fma chain
+        // every thread scores blocks tid, tid + 256, ...: p = sum / bs, canonical
+        // fma chain; all DH/4 loads of a block are issued before the chain. For
+        // a power-of-two bs, sum * (1/bs) is the same correctly rounded value as
+        // sum / bs (the reciprocal is exact), at the cost of one multiply.
         const float den = static_cast<float>(bs);
+        const float inv = 1.0f / den;
         const int64_t limit = score_pos / bs;
         for (int64_t j = tid; j < n_present; j += kSelThreads) {
             float s = -__builtin_inff();
             if (j <= limit) {
-                const float* p = sums + ((b * nb_stride + j) * H + g) * D;
+                const float4* p = reinterpret_cast<const float4*>(sums + ((b * nb_stride + j) * H + g) * DH);
+                float4 v[DH / 4];
+#pragma unroll
+                for (int c = 0; c < DH / 4; ++c) v[c] = p[c];
                 float acc = 0.0f;
-                for (int64_t d = 0; d < D; d += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(p + d);
-                    acc = __fmaf_rn(f_lds[d], v.x / den, acc);
-                    acc = __fmaf_rn(f_lds[d + 1], v.y / den, acc);
-                    acc = __fmaf_rn(f_lds[d + 2], v.z / den, acc);
-                    acc = __fmaf_rn(f_lds[d + 3], v.w / den, acc);
+#pragma unroll
+                for (int c = 0; c < DH / 4; ++c) {
+                    const float x[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc = __fmaf_rn(f_lds[4 * c + e], POW2 ? x[e] * inv : x[e] / den, acc);
                 }
                 s = acc * scale;
             }
@@ -290,21 +307,34 @@ int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, 
                          hipStream_t stream) {
     const int64_t n_present = cdiv(len, bs);
     const int64_t score_pos = routing == SPARDA_ROUTE_ABSOLUTE ? pos : 0;
+    const bool pow2 = (bs & (bs - 1)) == 0;
     dim3 grid(static_cast<unsigned>(H), static_cast<unsigned>(B));
-#define SPARDA_SEL(FDT_, CH_)                                                                            \
-    hipLaunchKernelGGL((select_decode_kernel<FDT_, CH_>), grid, dim3(kSelThreads), 0, stream, f, f_sb, f_sh, \
-                       sums, H, D, nb_stride, n_present, pos, score_pos, bs, static_cast<int>(k), scale, \
-                       sel, n_sel, static_cast<int>(cap))
-#define SPARDA_SEL_C(FDT_)                          \
-    if (n_present <= 256) SPARDA_SEL(FDT_, 4);      \
-    else if (n_present <= 1024) SPARDA_SEL(FDT_, 16); \
-    else SPARDA_SEL(FDT_, 64);
+#define SPARDA_SEL(FDT_, CH_, DH_, P2_)                                                                     \
+    hipLaunchKernelGGL((select_decode_kernel<FDT_, CH_, DH_, P2_>), grid, dim3(kSelThreads), 0, stream, f,  \
+                       f_sb, f_sh, sums, H, nb_stride, n_present, pos, score_pos, bs, static_cast<int>(k),  \
+                       scale, sel, n_sel, static_cast<int>(cap))
+#define SPARDA_SEL_P(FDT_, CH_, DH_)                    \
+    if (pow2) SPARDA_SEL(FDT_, CH_, DH_, true);         \
+    else SPARDA_SEL(FDT_, CH_, DH_, false);
+#define SPARDA_SEL_D(FDT_, CH_)                         \
+    switch (D) {                                        \
+        case 16: SPARDA_SEL_P(FDT_, CH_, 16) break;     \
+        case 32: SPARDA_SEL_P(FDT_, CH_, 32) break;     \
+        case 64: SPARDA_SEL_P(FDT_, CH_, 64) break;     \
+        default: SPARDA_SEL_P(FDT_, CH_, 128) break;    \
+    }
+#define SPARDA_SEL_C(FDT_)                                  \
+    if (n_present <= 256) { SPARDA_SEL_D(FDT_, 4) }         \
+    else if (n_present <= 1024) { SPARDA_SEL_D(FDT_, 16) }  \
+    else { SPARDA_SEL_D(FDT_, 64) }
     if (fdtype == SPARDA_BF16) {
         SPARDA_SEL_C(SPARDA_BF16)
     } else {
         SPARDA_SEL_C(SPARDA_F32)
     }
 #undef SPARDA_SEL_C
+#undef SPARDA_SEL_D
+#undef SPARDA_SEL_P
 #undef SPARDA_SEL
     return check_hip(hipGetLastError(), "select_decode_kernel");
 }

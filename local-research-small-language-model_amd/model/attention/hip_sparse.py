@@ -30,6 +30,30 @@ def gather_kv_blocks(k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tens
     return sparda.gather_blocks(k, v, block_indices, block_size)
 
 
+class PrototypeKVCache(KVCache):
+    """KVCache that keeps fp32 block sums of its keys current: sums / bs are
+    the block prototypes of KVBlockCompressor (model/forecast.py:66-78), so a
+    decode step selects blocks from the sums instead of recompressing all S
+    keys (model/attention/sparse.py:133-135). Each update recomputes the
+    blocks it touches from their first token, so the sums equal a fresh
+    compression bit for bit."""
+
+    def __init__(self, max_batch_size: int, max_seq_len: int, n_kv_head: int, head_dim: int,
+                 device: torch.device, dtype: torch.dtype, block_size: int = 64):
+        super().__init__(max_batch_size, max_seq_len, n_kv_head, head_dim, device, dtype)
+        self.block_size = block_size
+        nb = (max_seq_len + block_size - 1) // block_size
+        self.block_sums = torch.zeros((max_batch_size, nb, n_kv_head, head_dim), device=device,
+                                      dtype=torch.float32)
+
+    def update(self, xk: torch.Tensor, xv: torch.Tensor):
+        pos = self.current_len
+        out = super().update(xk, xv)
+        first = (pos // self.block_size) * self.block_size
+        sparda.block_sums(self.k, first, self.current_len - first, self.block_size, self.block_sums)
+        return out
+
+
 class HipSparseAttention(BaseAttention):
     """Forecast-guided (or static window) block-sparse GQA on libsparda."""
 
@@ -64,6 +88,13 @@ class HipSparseAttention(BaseAttention):
         f = forecast_vector if (self.mode == "forecast" and forecast_vector is not None) else None
         if f is not None:
             f = f.reshape(B, self.n_kv_head, -1)
+        if f is not None and isinstance(cache, PrototypeKVCache) and cache.block_size == self.block_size:
+            # cached prototypes: select from the block sums, attend in place
+            S = cache.current_len
+            sel, n_sel = sparda.select_decode(f, cache.block_sums, S, S - 1, self.block_size,
+                                              self.top_k_blocks, routing=self.decode_routing)
+            out = sparda.decode_selected(xq[:, 0], cache.k, cache.v, S, self.block_size, sel, n_sel)
+            return self.wo(out.view(B, 1, self.n_head * self.head_dim))
         out = sparda.decode(xq[:, 0], cache.k, cache.v, cache.current_len, f, self.block_size,
                             self.top_k_blocks, routing=self.decode_routing, workspace=self._ws)
         return self.wo(out.view(B, 1, self.n_head * self.head_dim))

@@ -350,6 +350,29 @@ def decode_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, b
     return out
 
 
+def block_sums(k: torch.Tensor, pos: int, n: int, block_size: int, sums: torch.Tensor) -> torch.Tensor:
+    """Accumulate fp32 block sums of tokens [pos, pos+n) of the device cache
+    k [B,S,Hkv,D] into sums [B,NBmax,Hkv,D] (in place; returned). A block whose
+    first token is in the range restarts from zero, so pos = j*block_size
+    recomputes blocks j.. exactly: sums/bs equal compress() bit for bit
+    (prototypes of model/forecast.py:66-78 without recompressing the cache)."""
+    dev = require_device(k, sums)
+    _inference_only(k)
+    if sums.dtype != torch.float32 or not sums.is_contiguous():
+        raise TypeError("sparda: block sums must be contiguous float32")
+    if k.stride(-1) != 1:
+        raise ValueError("sparda: the cache's last dimension must be contiguous")
+    B, S, Hkv, D = k.shape
+    if tuple(sums.shape[:1]) != (B,) or tuple(sums.shape[2:]) != (Hkv, D):
+        raise AssertionError(f"Mismatch: cache {tuple(k.shape)} vs block sums {tuple(sums.shape)}")
+    if pos < 0 or n < 1 or pos + n > S:
+        raise ValueError(f"sparda: tokens [{pos}, {pos + n}) outside the cache of {S}")
+    sb, st, sh, _ = k.stride()
+    call("sparda_block_sums", k.data_ptr(), _dtype_code(k), sb, st, sh, B, Hkv, D, pos, n, block_size,
+         sums.shape[1], sums.data_ptr(), _stream(dev))
+    return sums
+
+
 def select_decode(forecast: torch.Tensor, block_sums: torch.Tensor, length: int, pos: int, block_size: int,
                   top_k: int, routing: str = "reference", scale: Optional[float] = None,
                   sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None):

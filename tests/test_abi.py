@@ -95,3 +95,9 @@ def test_offload_and_selected_decode_argument_errors():
             None)  # sel_cap < k + 2
     _expect(-6, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 100, 64, 8, 3, 0.125, P, P, 10,
             None)  # unknown routing
+    # block sums of a device cache: k, dtype, sb, st, sh, B, Hkv, D, pos, n, bs, nb_stride, sums, stream
+    _expect(-1, "sparda_block_sums", None, 1, 256, 256, 64, 1, 4, 64, 0, 64, 64, 4, P, None)
+    _expect(-3, "sparda_block_sums", P, 9, 256, 256, 64, 1, 4, 64, 0, 64, 64, 4, P, None)
+    _expect(-2, "sparda_block_sums", P, 1, 256, 256, 64, 1, 4, 64, 0, 0, 64, 4, P, None)  # n = 0
+    _expect(-8, "sparda_block_sums", P, 1, 256, 256, 64, 1, 4, 64, 200, 100, 64, 4, P, None)  # block 4 of 4
+    _expect(-5, "sparda_block_sums", P, 1, -1, 256, 64, 1, 4, 64, 0, 64, 64, 4, P, None)

@@ -1,0 +1,109 @@
+"""GPU parity of the cached-prototype decode: block sums of a device KV cache
+kept current across steps, decode selection from the sums, attention over the
+selected blocks in place.
+
+Block sums / prototypes and selections are compared exactly (against
+sparda.compress, the fused decode step and the oracle); attention outputs
+within max-abs 2e-2 / mean-abs 2e-3 (bf16) or 1e-4 (fp32).
+"""
+
+import pytest
+import torch
+
+import sparda
+from sparda import synth
+from model.attention import HipSparseAttention, KVCache, PrototypeKVCache
+from model.config import ModelConfig
+from model.rope import RotaryEmbedding
+from oracle import sparda_oracle as O
+from helpers import assert_close_out, np32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("S,bs,dtype", [(4096, 64, torch.bfloat16), (5000, 64, torch.bfloat16),
+                                        (333, 16, torch.float32)])
+def test_block_sums_equal_compress_bit_exact(S, bs, dtype):
+    case(f"block sums S={S} bs={bs} {dtype}")
+    g = torch.Generator().manual_seed(S)
+    k = torch.randn(2, S, 4, 64, generator=g).to(dtype).to(DEV)
+    nb = (S + bs - 1) // bs
+    sums = torch.full((2, nb + 3, 4, 64), float("nan"), device=DEV)
+    sparda.block_sums(k, 0, S, bs, sums)
+    protos = sparda.compress(k, bs)
+    assert torch.equal(sums[:, :nb] / bs, protos)
+    assert (sums[:, :nb] / bs).cpu().numpy().tobytes() == O.compress(np32(k), bs).tobytes()
+    assert torch.isnan(sums[:, nb:]).all()  # blocks past the range untouched
+
+
+def test_prototype_cache_incremental_updates_equal_one_shot():
+    case("PrototypeKVCache incremental updates")
+    bs = 64
+    cache = PrototypeKVCache(2, 1200, 4, 64, DEV, torch.bfloat16, block_size=bs)
+    g = torch.Generator().manual_seed(7)
+    k = torch.randn(2, 1100, 4, 64, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(2, 1100, 4, 64, generator=g).to(torch.bfloat16).to(DEV)
+    cache.update(k[:, :1000], v[:, :1000])
+    for t in range(1000, 1100):  # one token at a time, crossing blocks 15 -> 17
+        cache.update(k[:, t:t + 1], v[:, t:t + 1])
+    fresh = torch.zeros_like(cache.block_sums)
+    sparda.block_sums(cache.k, 0, 1100, bs, fresh)
+    nb = (1100 + bs - 1) // bs
+    assert torch.equal(cache.block_sums[:, :nb], fresh[:, :nb])
+    assert torch.equal(cache.block_sums[:, :nb] / bs, sparda.compress(k, bs))
+
+
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+@pytest.mark.parametrize("S", [5000, 16384])
+def test_cached_selection_and_attention_equal_fused_decode(routing, S):
+    case(f"cached-prototype decode S={S} {routing}")
+    B, Hq, Hkv, D, bs, k = 4, 12, 4, 64, 64, 8
+    x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=torch.bfloat16, seed=31)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    out_f, ex = sparda.decode(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], bs, k, routing=routing,
+                              want_sel=True)
+    nb = (d["k_cache"].shape[1] + bs - 1) // bs
+    sums = torch.zeros((B, nb, Hkv, D), device=DEV)
+    sparda.block_sums(d["k_cache"], 0, S, bs, sums)
+    sel, n = sparda.select_decode(d["forecast"], sums, S, S - 1, bs, k, routing=routing)
+    out_c = sparda.decode_selected(d["q"], d["k_cache"], d["v_cache"], S, bs, sel, n)
+    torch.cuda.synchronize()
+    assert torch.equal(n, ex["n_sel"])
+    for b in range(B):
+        for g in range(Hkv):
+            m = int(n[b, g])
+            assert torch.equal(sel[b, g, :m], ex["sel"][b, g, :m])
+    assert_close_out(np32(out_c), np32(out_f), torch.bfloat16, what="cached vs fused decode")
+    want, sel_o, n_o = O.decode_step(np32(d["q"]), np32(d["k_cache"]), np32(d["v_cache"]), S,
+                                     np32(d["forecast"]), bs, k, routing)
+    assert (n.cpu().numpy() == n_o).all()
+    assert_close_out(np32(out_c), want, torch.bfloat16, what="cached decode vs oracle")
+
+
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+def test_backend_decode_through_prototype_cache_equals_plain_cache(routing):
+    case(f"HipSparseAttention with PrototypeKVCache {routing}")
+    cfg = ModelConfig(block_size=64, top_k_blocks=8, context_length=4096, decode_routing=routing)
+    torch.manual_seed(3)
+    attn = HipSparseAttention(cfg, layer_idx=1).to(DEV).eval()
+    rot = RotaryEmbedding(cfg.head_dim, 4096).to(DEV)
+    plain = KVCache(1, 4096, cfg.n_kv_head, cfg.head_dim, DEV, torch.float32)
+    proto = PrototypeKVCache(1, 4096, cfg.n_kv_head, cfg.head_dim, DEV, torch.float32, block_size=64)
+    T = 1500
+    x = torch.randn(1, T + 70, cfg.n_embd, device=DEV)
+    f = torch.randn(1, T + 70, cfg.forecast_heads, cfg.forecast_dim, device=DEV)
+    with torch.no_grad():
+        a = attn(x[:, :T], rot, kv_cache=plain, forecast_vector=f[:, :T])
+        b = attn(x[:, :T], rot, kv_cache=proto, forecast_vector=f[:, :T])
+        assert torch.equal(a, b)
+        for t in range(T, T + 70):  # crosses a block boundary (1536)
+            a = attn(x[:, t:t + 1], rot, kv_cache=plain, forecast_vector=f[:, t:t + 1])
+            b = attn(x[:, t:t + 1], rot, kv_cache=proto, forecast_vector=f[:, t:t + 1])
+            assert_close_out(np32(b), np32(a), torch.float32, what=f"step {t}")
+    nb = (T + 70 + 63) // 64
+    assert torch.equal(proto.block_sums[:, :nb] / 64, sparda.compress(proto.k[:, :T + 70], 64))
