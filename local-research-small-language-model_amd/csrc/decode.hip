@@ -338,11 +338,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                     for (int i = 0; i < 4; ++i)
                         if (16 * nn + 4 * grp + i >= nk) sc[nn][i] = -__builtin_inff();
             }
-            float mx = sc[0][0];
-#pragma unroll
-            for (int nn = 0; nn < 4; ++nn)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[nn][i]);
+            float mx = max16_nn(sc);
             mx = pair32_max(pair16_max(mx));
             const float cand = mx * scale_log2;
             const float m_new = cand > m_run + kLazy ? cand : m_run;

@@ -175,9 +175,21 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
         s = s < T ? s : T - 1;
         return s * kv_st + col;
     };
+    // a whole block (the common case): a uniform block offset plus a fixed
+    // per-thread offset, no clamp
+    const int64_t own_lo = static_cast<int64_t>(c_lo / 8) * kv_st + col_lo;
+    const int64_t own_hi = static_cast<int64_t>(c_hi / 8) * kv_st + col_hi;
 #define SPARDA_FETCH(KA, KB, VA, VB, J)                                                   \
     do {                                                                                  \
-        const int64_t o_lo_ = row_off((J), c_lo, col_lo), o_hi_ = row_off((J), c_hi, col_hi); \
+        const int64_t jb_ = static_cast<int64_t>(J) * kMBs;                               \
+        int64_t o_lo_, o_hi_;                                                             \
+        if (jb_ + kMBs <= T) {                                                            \
+            o_lo_ = jb_ * kv_st + own_lo;                                                 \
+            o_hi_ = jb_ * kv_st + own_hi;                                                 \
+        } else {                                                                          \
+            o_lo_ = row_off((J), c_lo, col_lo);                                           \
+            o_hi_ = row_off((J), c_hi, col_hi);                                           \
+        }                                                                                 \
         KA = *reinterpret_cast<const uint4*>(kbase + o_lo_);                              \
         VA = *reinterpret_cast<const uint4*>(vbase + o_lo_);                              \
         KB = *reinterpret_cast<const uint4*>(kbase + o_hi_);                              \
@@ -254,11 +266,7 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                     for (int i = 0; i < 4; ++i)
                         if (16 * n + 4 * grp + i > l) s[n][i] = -__builtin_inff();
             }
-            float mx = __builtin_fmaxf(__builtin_fmaxf(s[0][0], s[0][1]), __builtin_fmaxf(s[0][2], s[0][3]));
-#pragma unroll
-            for (int n = 1; n < 4; ++n)
-                mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(s[n][0], s[n][1]),
-                                                         __builtin_fmaxf(s[n][2], s[n][3])));
+            float mx = max16_nn(s);
             mx = member[tt] ? mx : -__builtin_inff();
             mx = pair32_max(pair16_max(mx));
             const float cand = mx * scale_log2;  // this block's column max, log2 units

@@ -1,13 +1,14 @@
-"""Wait states around the router's hand-written DPP instructions, checked on
-the code the compiler actually emits (CPU only: hipcc cross-compiles gfx950).
+"""Wait states around hand-written cross-lane instructions, checked on the
+code the compiler actually emits (CPU only: hipcc cross-compiles gfx950).
 
-A VALU instruction with a DPP source needs two wait states after any VALU
-write of a VGPR it reads (gfx9 family rule). The compiler inserts these for
-the DPP instructions it generates itself, not for inline assembly, so the
-router's asm steps carry their own s_nop padding. What the compiler places
-between the steps (spill reloads, copies, index arithmetic) is outside their
-control; this test compiles every source that uses DPP inline assembly and
-checks each DPP instruction of every kernel against the rule.
+A VALU instruction with a DPP source, and a v_permlane16/32_swap, needs two
+wait states after any VALU write of a VGPR it reads. The compiler inserts these
+for the instructions it generates itself, but it does not count the results of
+inline assembly as VALU writes, so the asm blocks carry their own s_nop
+padding. What the compiler places between them (spill reloads, copies, index
+arithmetic) is outside their control; this test compiles every source that
+uses such inline assembly and checks each DPP / permlane-swap instruction of
+every kernel against the rule.
 """
 
 import os
@@ -73,10 +74,11 @@ def dpp_hazards(asm_lines):
         ins.append(s)
     bad = []
     for i, l in enumerate(ins):
-        if l.endswith(":") or "_dpp" not in l.split()[0]:
+        op0 = l.split()[0]
+        if l.endswith(":") or ("_dpp" not in op0 and "permlane" not in op0):
             continue
         reads = set()
-        for o in _operands(l)[:3]:          # vdst (read by fmac), src0, src1
+        for o in _operands(l)[:3]:          # vdst (read by fmac / swap), src0, src1
             reads |= _vgprs(o)
         ws = 0
         for p in reversed(ins[max(0, i - 8):i]):
@@ -118,6 +120,9 @@ def test_checker_flags_a_planted_hazard():
         "v_fmac_f32_dpp v5, v1, v2 row_newbcast:0 row_mask:0xf bank_mask:0xf",
     ]
     assert len(dpp_hazards(planted)) == 1
+    swap = ["v_max_f32_e32 v4, v4, v5", "v_permlane16_swap_b32_e32 v4, v6"]
+    assert len(dpp_hazards(swap)) == 1
+    assert dpp_hazards([swap[0], "s_nop 1", swap[1]]) == []
     padded = [planted[0], "s_nop 1", planted[1]]
     assert dpp_hazards(padded) == []
     one_short = [planted[0], "s_nop 0", planted[1]]
@@ -131,10 +136,14 @@ def test_checker_flags_a_planted_hazard():
 
 
 def _dpp_sources():
+    """Sources whose kernels use DPP or permlane-swap inline assembly (also
+    through the shared headers)."""
+    hdr = {h: open(os.path.join(B.CSRC, h)).read() for h in os.listdir(B.CSRC) if h.endswith(".h")}
+    asm_hdr = [h for h, t in hdr.items() if re.search(r"asm\s*\(.*(_dpp|permlane)", t)]
     out = []
     for src in B.sources():
         text = open(src).read()
-        if re.search(r"asm\s*\(.*_dpp", text):
+        if re.search(r"asm\s*\(.*(_dpp|permlane)", text) or any(f'"{h}"' in text for h in asm_hdr):
             out.append(src)
     return out
 
@@ -151,8 +160,8 @@ def test_emitted_dpp_wait_states(src, tmp_path):
     n_dpp = 0
     problems = []
     for name, lines in ks.items():
-        n_dpp += sum(1 for l in lines if "_dpp" in l.split(";")[0])
+        n_dpp += sum(1 for l in lines if "_dpp" in l.split(";")[0] or "permlane" in l.split(";")[0])
         for w, d in dpp_hazards(lines):
             problems.append(f"{name[:60]}: {w} -> {d}")
-    assert n_dpp > 0, "no DPP instructions found; the check would be vacuous"
+    assert n_dpp > 0, "no DPP / permlane-swap instructions found; the check would be vacuous"
     assert not problems, "\n".join(problems[:20])
