@@ -19,10 +19,11 @@ __device__ __forceinline__ bf16x8 lds_read8(const uint16_t* p) {
 // Transposed read (ds_read_b64_tr_b16). Within each 16-lane group, output
 // lane i, element e is element i%4 of the 8-byte chunk addressed by lane
 // 4e + i/4 of the group.
+// The pointer is converted with an address-space cast (not through an integer)
+// so that constant offsets from a common base fold into the instruction.
 __device__ __forceinline__ i16x4 lds_read_tr(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<__attribute__((address_space(3))) i16x4*>(
-            reinterpret_cast<uintptr_t>(p)));
+        (__attribute__((address_space(3))) i16x4*)(const_cast<uint16_t*>(p)));
 }
 
 // Reductions over lane pairs (l, l^16) and (l, l^32) with the gfx950 VALU

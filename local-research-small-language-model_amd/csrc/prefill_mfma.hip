@@ -52,6 +52,10 @@ struct MfmaSmem {
     int n_list;
 };
 
+// 1: the wave's Q operands are held in registers for the whole kernel
+#ifndef SPARDA_PF_QREG
+#define SPARDA_PF_QREG 1
+#endif
 // resident workgroups per CU the register budget is sized for
 #ifndef SPARDA_PF_OCCUPANCY
 #define SPARDA_PF_OCCUPANCY 2
@@ -203,6 +207,9 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
         *reinterpret_cast<uint4*>(&sm.v[BUF][lds_v_hi]) = VB;                             \
     } while (0)
 
+#if SPARDA_PF_QREG
+    bf16x8 qreg[R][2];  // filled once qs is complete
+#endif
     // ---- one KV block against this wave's tiles ----
     // Per tile: S^T = K Q^T, online softmax, O^T += V^T P^T. Columns that did
     // not select the block get an exponent offset of -inf (P = 0) instead of
@@ -243,8 +250,13 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
         }
         const int lim_tail = static_cast<int>(T - static_cast<int64_t>(j) * kMBs) - 1;
         auto qk = [&](int tt, f32x4 (&s)[4]) {
+#if SPARDA_PF_QREG
+            const bf16x8 qb0 = qreg[tt][0];
+            const bf16x8 qb1 = qreg[tt][1];
+#else
             const bf16x8 qb0 = lds_read8(qrow0 + 16 * tt * kKRow);
             const bf16x8 qb1 = lds_read8(qrow0 + 16 * tt * kKRow + 32);
+#endif
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
                 s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -252,6 +264,45 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                 s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][1], qb1, s[n], 0, 0, 0);
             }
         };
+            const float m_new = __builtin_fmaxf(m_run[tt], cand);
+#endif
+            const float neg = member[tt] ? -m_new : -__builtin_inff();
+            alpha[tt] = m_new != m_run[tt] ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
+            rescale = rescale || alpha[tt] != 1.0f;
+            m_run[tt] = m_new;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                bf16x8 pb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pb[i] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sb[tt][2 * m][i], scale_log2, neg)));
+                    pb[4 + i] = static_cast<__bf16>(
+                        __builtin_amdgcn_exp2f(__builtin_fmaf(sb[tt][2 * m + 1][i], scale_log2, neg)));
+                }
+                pwb[tt][m] = __builtin_bit_cast(uint4, pb);
+            }
+        }
+        if (__ballot(rescale) != 0ull) {
+#pragma unroll
+            for (int tt = 0; tt < R; ++tt) {
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[tt][dt] *= alpha[tt];
+                ol[tt] *= alpha[tt];
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pwb[tt][0]),
+                                                                    o[tt][dt], 0, 0, 0);
+                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pwb[tt][1]),
+                                                                    o[tt][dt], 0, 0, 0);
+            }
+            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pwb[tt][0]), ol[tt], 0, 0, 0);
+            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pwb[tt][1]), ol[tt], 0, 0, 0);
+        }
+#else
 #pragma unroll
         for (int tt = 0; tt < R; ++tt) {
             if (__ballot(member[tt]) == 0ull) continue;
@@ -311,6 +362,14 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
 
     __syncthreads();
     const int n_list = sm.n_list;
+#if SPARDA_PF_QREG
+    // the wave's Q operands do not change across blocks: read them once
+#pragma unroll
+    for (int tt = 0; tt < R; ++tt) {
+        qreg[tt][0] = lds_read8(qrow0 + 16 * tt * kKRow);
+        qreg[tt][1] = lds_read8(qrow0 + 16 * tt * kKRow + 32);
+    }
+#endif
 #if SPARDA_PREFILL_PREFETCH == 2
     // prologue: block 0 staged, block 1 in flight
     SPARDA_FETCH(k0a, k0b, v0a, v0b, sm.list[0]);
