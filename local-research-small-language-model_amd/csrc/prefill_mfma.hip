@@ -264,45 +264,6 @@ prefill_mfma_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, 
                 s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][1], qb1, s[n], 0, 0, 0);
             }
         };
-            const float m_new = __builtin_fmaxf(m_run[tt], cand);
-#endif
-            const float neg = member[tt] ? -m_new : -__builtin_inff();
-            alpha[tt] = m_new != m_run[tt] ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
-            rescale = rescale || alpha[tt] != 1.0f;
-            m_run[tt] = m_new;
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                bf16x8 pb;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    pb[i] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sb[tt][2 * m][i], scale_log2, neg)));
-                    pb[4 + i] = static_cast<__bf16>(
-                        __builtin_amdgcn_exp2f(__builtin_fmaf(sb[tt][2 * m + 1][i], scale_log2, neg)));
-                }
-                pwb[tt][m] = __builtin_bit_cast(uint4, pb);
-            }
-        }
-        if (__ballot(rescale) != 0ull) {
-#pragma unroll
-            for (int tt = 0; tt < R; ++tt) {
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) o[tt][dt] *= alpha[tt];
-                ol[tt] *= alpha[tt];
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < R; ++tt) {
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pwb[tt][0]),
-                                                                    o[tt][dt], 0, 0, 0);
-                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pwb[tt][1]),
-                                                                    o[tt][dt], 0, 0, 0);
-            }
-            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pwb[tt][0]), ol[tt], 0, 0, 0);
-            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pwb[tt][1]), ol[tt], 0, 0, 0);
-        }
-#else
 #pragma unroll
         for (int tt = 0; tt < R; ++tt) {
             if (__ballot(member[tt]) == 0ull) continue;
