@@ -254,12 +254,12 @@ def bench_offload(args, torch, sparda, synth):
     KV in a pinned host arena: forecast-routed blocks prefetched on a side
     stream while the previous layer's attention + FFN run. Also times the
     synchronous offload step and the fully GPU-resident sparse step."""
-    from model.attention import AsyncOffloadedKVCache, KVCache, OffloadedKVCache
+    from model.attention import AsyncOffloadedKVCache, KVCache, OffloadedKVCache, PrototypeKVCache
     from model.config import ModelConfig
     from model.model import SparDAResearchModel
     dev = torch.device("cuda")
     W, K = 4, args.offload_steps
-    cap = OB_CTX + 3 * (W + K) + 64
+    cap = OB_CTX + 4 * (W + K) + 64
     cfg = ModelConfig(n_layer=OB_LAYERS, context_length=cap, block_size=BS, top_k_blocks=TOPK,
                       decode_routing="absolute", attention_backend="async_offload", norm_eps=1e-5)
     torch.manual_seed(1004)
@@ -281,7 +281,7 @@ def bench_offload(args, torch, sparda, synth):
             res_caches[li].update(kd, vd)
     torch.cuda.synchronize()
     g = torch.Generator().manual_seed(1006)
-    ids = torch.randint(0, cfg.vocab_size, (3 * (W + K), 1, 1), generator=g).to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (4 * (W + K), 1, 1), generator=g).to(dev)
     it = iter(range(ids.shape[0]))
 
     def run(m, caches, n):
@@ -323,6 +323,46 @@ def bench_offload(args, torch, sparda, synth):
     # same caches, synchronous offload (select + fetch on the compute stream)
     us_sync = timed(syncm, off_caches)
     us_res = timed(resident, res_caches)
+
+    def graph_step_us(m, caches, reps=50):
+        """One decode step captured in a HIP graph at a fixed position (each
+        replay re-appends the same token at the same slot); the replayed logits
+        must equal an eager step at that position."""
+        x = ids[0]
+        with torch.no_grad():
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                m(x, kv_caches=caches)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            lens = [c.current_len for c in caches]
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                logits = m(x, kv_caches=caches)["logits"]
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            us = events_ms(g.replay, reps, torch) * 1e3
+            got = logits.clone()
+            for c, n in zip(caches, lens):
+                c.current_len = n
+            want = m(x, kv_caches=caches)["logits"]
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), "graph replay differs from the eager decode step"
+        del g
+        return us
+
+    # the GPU-resident step replayed from a HIP graph: whole-cache compression
+    # every step (KVCache), and cached prototypes (PrototypeKVCache)
+    us_res_graph = graph_step_us(resident, res_caches)
+    proto_caches = [PrototypeKVCache(1, cap, HKV, D, dev, torch.bfloat16, block_size=BS) for _ in range(OB_LAYERS)]
+    with torch.no_grad():
+        for pc, rc in zip(proto_caches, res_caches):
+            pc.update(rc.k[:, :rc.current_len], rc.v[:, :rc.current_len])
+    us_proto_eager = timed(resident, proto_caches)
+    us_proto_graph = graph_step_us(resident, proto_caches)
+    del proto_caches
     # host link: one 256 MiB pinned host -> device copy
     hb = torch.empty(256 << 20, dtype=torch.uint8).pin_memory()
     db = torch.empty_like(hb, device=dev)
@@ -339,6 +379,9 @@ def bench_offload(args, torch, sparda, synth):
         "us_per_step_async": round(us_async, 1),
         "us_per_step_sync": round(us_sync, 1),
         "us_per_step_gpu_resident": round(us_res, 1),
+        "us_per_step_gpu_resident_graph": round(us_res_graph, 1),
+        "us_per_step_cached_prototypes": round(us_proto_eager, 1),
+        "us_per_step_cached_prototypes_graph": round(us_proto_graph, 1),
         "steps": K,
         "overlap": round(1.0 - ex / tr, 4) if tr > 0 else None,
         "transfer_us_per_layer": round(tr * 1e3, 2),
@@ -483,7 +526,9 @@ def main():
     log("offload workload")
     off = bench_offload(args, torch, sparda, synth)
     log(f"offload: async {off['us_per_step_async']:.1f} us/step, sync {off['us_per_step_sync']:.1f}, "
-        f"resident {off['us_per_step_gpu_resident']:.1f}; overlap {off['overlap']}, "
+        f"resident {off['us_per_step_gpu_resident']:.1f} (graph {off['us_per_step_gpu_resident_graph']:.1f}; "
+        f"cached prototypes {off['us_per_step_cached_prototypes']:.1f}, graph "
+        f"{off['us_per_step_cached_prototypes_graph']:.1f}); overlap {off['overlap']}, "
         f"transfer {off['transfer_us_per_layer']} us/layer, link {off['host_link_gbs']} GB/s")
     log("12-layer forward workload")
     mdl = bench_model(args, torch, sparda, synth)
