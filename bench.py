@@ -64,7 +64,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--offload-steps", type=int, default=32)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "pmc"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "producer", "pmc"],
+                    default="all",
                     help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
 
@@ -393,7 +394,7 @@ def bench_offload(args, torch, sparda, synth):
     }
 
 
-def bench_model(args, torch, sparda, synth):
+def bench_model(args, torch, sparda, synth, fused=False):
     """12-layer forward of the model at B=1, T=16384 (bf16 weights from the
     model's N(0, 0.02) init, vocab 32000 tied, d 768, 12/4 heads, SwiGLU 2048;
     layer 0 dense causal, layers 1..11 forecast-routed sparse with layer L's
@@ -405,14 +406,16 @@ def bench_model(args, torch, sparda, synth):
     from model.model import SparDAResearchModel
     dev = torch.device("cuda")
     cfg = ModelConfig(n_layer=12, context_length=MT, block_size=BS, top_k_blocks=TOPK,
-                      attention_backend="hip_sparse", norm_eps=1e-5)
+                      attention_backend="hip_sparse", norm_eps=1e-5, fused_producer=fused)
     torch.manual_seed(1003)
     model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
     g = torch.Generator().manual_seed(1003)
     ids = torch.randint(0, cfg.vocab_size, (1, MT), generator=g).to(dev)
     starts, ends = [], []
     hooks = []
-    for layer in model.layers:
+    # per-layer attention events (the fused producer enters the attention past
+    # its forward hooks: only the whole forward is timed then)
+    for layer in ([] if fused else model.layers):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         starts.append(e0)
         ends.append(e1)
@@ -422,7 +425,7 @@ def bench_model(args, torch, sparda, synth):
     with torch.no_grad():
         model(ids)
         torch.cuda.synchronize()
-        per_layer = [0.0] * len(model.layers)
+        per_layer = [0.0] * len(starts)
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         total = 0.0
         for _ in range(runs):
@@ -439,6 +442,8 @@ def bench_model(args, torch, sparda, synth):
     attn = [x / runs for x in per_layer]
     del model
     torch.cuda.empty_cache()
+    if not fused:
+        fz = bench_model(args, torch, sparda, synth, fused=True)
     return {
         "workload": f"12-layer forward, B=1, T={MT}, bf16 (d 768, 12/4 heads, head dim 64, SwiGLU 2048, "
                     "vocab 32000 tied, block 64, top-8); layer 0 dense causal, layers 1-11 forecast-routed "
@@ -446,8 +451,59 @@ def bench_model(args, torch, sparda, synth):
         "ms_per_forward": round(ms, 3),
         "tok_s": round(MT / (ms * 1e-3), 1),
         "attention_ms_per_layer": [round(x, 3) for x in attn],
-        "attention_fraction": round(sum(attn) / ms, 4),
+        "attention_fraction": round(sum(attn) / ms, 4) if attn else None,
         "runs": runs,
+        **({} if fused else {"ms_per_forward_fused_producer": fz["ms_per_forward"],
+                             "tok_s_fused_producer": fz["tok_s"]}),
+    }
+
+
+def bench_producer(args, torch, sparda, synth):
+    """The attention inputs of one layer at the prefill workload (B=4, T=4096,
+    d 768): RMSNorm + q / k / v / forecast projections + RoPE, fused (one
+    kernel) against the unfused sequence of the reference's modules (RMSNorm,
+    four bf16 linears, rotate-half RoPE)."""
+    from model.norm import RMSNorm
+    from model.rope import apply_rope, rope_tables
+    dev = torch.device("cuda")
+    C, NQ, NKV, NF = HQ * D, HQ * D, HKV * D, HKV * D
+    g = torch.Generator().manual_seed(1005)
+    x = torch.randn(PB, PT, C, generator=g).to(dev, torch.bfloat16)
+    ws = [(0.02 * torch.randn(n, C, generator=g)).to(dev, torch.bfloat16) for n in (NQ, NKV, NKV, NF)]
+    norm = RMSNorm(C, eps=1e-5).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_((1.0 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16))
+    cos, sin = (t.to(dev) for t in rope_tables(D, PT))
+    w_fold = (torch.cat([w.float() for w in ws]) * norm.weight.float()[None, :]).to(torch.bfloat16).contiguous()
+
+    def unfused():
+        h = norm(x)
+        q = torch.nn.functional.linear(h, ws[0]).view(PB, PT, HQ, D)
+        k = torch.nn.functional.linear(h, ws[1]).view(PB, PT, HKV, D)
+        v = torch.nn.functional.linear(h, ws[2]).view(PB, PT, HKV, D)
+        f = torch.nn.functional.linear(h, ws[3]).view(PB, PT, HKV, D)
+        return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v, f
+
+    def fused():
+        return sparda.produce(x, w_fold, NQ, NKV, NF, 1e-5, cos, sin)
+
+    with torch.no_grad():
+        for _ in range(3):
+            unfused()
+            fused()
+        torch.cuda.synchronize()
+        us_unfused = events_ms(unfused, 20, torch) * 1e3
+        us_fused = events_ms(fused, 20, torch) * 1e3
+        a, b = unfused(), fused()
+        err = max(float((x1.float() - x2.float()).abs().max()) for x1, x2 in zip(a, b))
+    flop = 2.0 * PB * PT * (NQ + 2 * NKV + NF) * C
+    return {
+        "workload": f"RMSNorm + q/k/v/forecast projections + RoPE of one layer, B={PB} T={PT} d={C} "
+                    f"(N = {NQ}+{NKV}+{NKV}+{NF}), bf16",
+        "us_fused": round(us_fused, 2),
+        "us_unfused_torch": round(us_unfused, 2),
+        "fused_tflops": round(flop / (us_fused * 1e-6) / 1e12, 1),
+        "max_abs_vs_unfused": round(err, 4),
     }
 
 
@@ -511,7 +567,7 @@ def main():
     sparda.load()
     if args.only != "all":
         fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload,
-              "model": bench_model, "pmc": pmc_workload}[args.only]
+              "model": bench_model, "producer": bench_producer, "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
         print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}), flush=True)
         return
@@ -534,7 +590,12 @@ def main():
     mdl = bench_model(args, torch, sparda, synth)
     log(f"model: {mdl['ms_per_forward']:.2f} ms per {MT}-token forward ({mdl['tok_s']:.0f} tok/s), "
         f"attention {100 * mdl['attention_fraction']:.1f}% (layer 0 dense {mdl['attention_ms_per_layer'][0]:.2f} ms, "
-        f"sparse layers {sum(mdl['attention_ms_per_layer'][1:]) / 11:.2f} ms each)")
+        f"sparse layers {sum(mdl['attention_ms_per_layer'][1:]) / 11:.2f} ms each); fused producer "
+        f"{mdl['ms_per_forward_fused_producer']:.2f} ms ({mdl['tok_s_fused_producer']:.0f} tok/s)")
+    log("fused producer")
+    prod = bench_producer(args, torch, sparda, synth)
+    log(f"producer: fused {prod['us_fused']:.1f} us ({prod['fused_tflops']:.0f} TFLOP/s), "
+        f"unfused torch {prod['us_unfused_torch']:.1f} us")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -587,6 +648,7 @@ def main():
         },
         "offload": off,
         "model_forward": mdl,
+        "producer": prod,
     }
     print(json.dumps(line), flush=True)
 

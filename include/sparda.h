@@ -275,6 +275,26 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                                       void* out, int64_t out_sb, void* stream);
 
 /*
+ * Producer of one layer's attention inputs, fused: RMSNorm + the q, k, v and
+ * forecast projections + RoPE of q and k. Replaces, for the HIP model, the
+ * sequence attn_norm -> ForecastProjection -> wq / wk / wv -> RotaryEmbedding
+ * of TransformerBlock.forward (model/transformer.py:104-107, 118-125;
+ * model/norm.py:15-21; model/forecast.py:30-40; model/attention/base.py:38-52;
+ * model/rope.py:34-65). Head dim 64.
+ *   x: [M, C] bf16 rows (row stride x_stride_row), M = B * T, row b*T + t is
+ *      position pos0 + t.
+ *   w: [Nq + 2*Nk + Nf, C] bf16 = [wq; wk; wv; wf] with the RMSNorm weight
+ *      folded into the columns (w[n, c] * norm_weight[c]).
+ *   rope_cos / rope_sin: [rope_len, 32] fp32 tables (angle pos * theta^(-2i/64)).
+ *   q: [M, Nq], k, v: [M, Nk] bf16; f: [M, Nf] of f_dtype (SPARDA_BF16 / F32).
+ *   y = (x w^T) / sqrt(mean(x^2) + eps) per row; q and k rotated by position.
+ */
+SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                              int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                              const float* rope_sin, int64_t rope_len, int64_t T, int64_t pos0, void* q, void* k,
+                              void* v, void* f, int f_dtype, void* stream);
+
+/*
  * fp32 block sums of a device KV cache, kept current across decode steps so
  * that decode selection (sparda_select_decode) reads the sums instead of
  * recompressing the whole cache every step as the reference's decode does

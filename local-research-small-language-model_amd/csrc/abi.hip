@@ -310,6 +310,31 @@ SPARDA_API int sparda_offload_rebuild_sums(sparda_offload_t h, int64_t len, int6
     return offload_rebuild_sums(h, len, block_size, block_sums, static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                              int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                              const float* rope_sin, int64_t rope_len, int64_t T, int64_t pos0, void* q, void* k,
+                              void* v, void* f, int f_dtype, void* stream) {
+    SPARDA_REQUIRE(x && w && rope_cos && rope_sin && q && k && v && f, SPARDA_ERR_NULL, "produce: null pointer");
+    SPARDA_REQUIRE(f_dtype == SPARDA_F32 || f_dtype == SPARDA_BF16, SPARDA_ERR_DTYPE,
+                   "produce: forecast dtype %d unsupported", f_dtype);
+    SPARDA_REQUIRE(M >= 1 && T >= 1 && M % T == 0 && pos0 >= 0, SPARDA_ERR_SHAPE,
+                   "produce: need M >= 1 rows, a multiple of T >= 1, pos0 >= 0");
+    SPARDA_REQUIRE(C >= 32 && C % 32 == 0 && C <= 65536, SPARDA_ERR_SHAPE,
+                   "produce: model width %lld must be a positive multiple of 32", (long long)C);
+    SPARDA_REQUIRE(Nq > 0 && Nk > 0 && Nf > 0 && Nq % 64 == 0 && Nk % 64 == 0 && Nf % 64 == 0 &&
+                       (Nq + 2 * Nk + Nf) % 128 == 0,
+                   SPARDA_ERR_SHAPE, "produce: regions must be whole 64-wide heads, %lld columns in all a "
+                   "multiple of 128", (long long)(Nq + 2 * Nk + Nf));
+    SPARDA_REQUIRE(pos0 + T <= rope_len, SPARDA_ERR_SHAPE, "produce: positions up to %lld beyond the RoPE "
+                   "tables (%lld)", (long long)(pos0 + T), (long long)rope_len);
+    SPARDA_REQUIRE(x_stride_row >= C && x_stride_row % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(w) % 16 == 0,
+                   SPARDA_ERR_STRIDE, "produce: x rows and w must be 16-byte aligned");
+    SPARDA_REQUIRE(M / 128 < (int64_t(1) << 31), SPARDA_ERR_SHAPE, "produce: too many rows");
+    return launch_produce(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, T, pos0, q, k, v, f,
+                          f_dtype, static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,
                                  int64_t Hkv, int64_t D, int64_t pos, int64_t n, int64_t block_size,
                                  int64_t nb_stride, float* block_sums, void* stream) {

@@ -16,6 +16,10 @@ int launch_route(const void* f, int fdtype, int64_t fsb, int64_t fst, int64_t fs
                  float scale, int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel,
                  int cap, hipStream_t stream);
 
+int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
+                   int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
+                   void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream);
+
 int launch_topk_scores(const float* scores, int64_t rows, int64_t NB, int ke, int algo,
                        int32_t* topk, hipStream_t stream);
 

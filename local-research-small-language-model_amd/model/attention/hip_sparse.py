@@ -132,6 +132,16 @@ class HipSparseAttention(BaseAttention):
         xv = self.wv(x).view(B, T, self.n_kv_head, self.head_dim)
         offset = kv_cache.current_len if kv_cache is not None else 0
         xq, xk = rotary_emb(xq, xk, offset=offset)
+        return self.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
+                                      forecast_vector=forecast_vector)
+
+    def forward_projected(self, xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
+                          kv_cache: Optional[KVCache] = None, is_causal: bool = True,
+                          forecast_vector: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The attention after the projections and RoPE: xq [B,T,Hq,D], xk / xv
+        [B,T,Hkv,D] (already rotated at the cache's current position). Entered
+        from forward, or directly by a block whose fused producer computed them."""
+        T = xq.shape[1]
         if kv_cache is not None and T == 1:
             kv_cache.update(xk, xv)
             return self._decode(xq, kv_cache, forecast_vector)

@@ -43,6 +43,11 @@ class ModelConfig:
     # -inf ties), "absolute" masks at the query's true position.
     decode_routing: str = "reference"
 
+    # HIP model only: compute RMSNorm + the q / k / v / forecast projections +
+    # RoPE of each block in one kernel (sparda.produce) when the attention
+    # backend is the GPU-resident one and the activations are bf16.
+    fused_producer: bool = False
+
     def __post_init__(self):
         assert self.n_embd == self.n_head * self.head_dim, (
             f"n_embd ({self.n_embd}) must equal n_head ({self.n_head}) * head_dim ({self.head_dim})"

@@ -38,11 +38,16 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("cos", cos, persistent=False)
         self.register_buffer("sin", sin, persistent=False)
 
-    def forward(self, xq: torch.Tensor, xk: torch.Tensor, offset: int = 0):
-        need = offset + xq.shape[1]
+    def tables(self, need: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
+        """fp32 cos, sin [L, head_dim/2] on `device`, L >= need."""
         if need > self.max_seq_len:
             self.max_seq_len = max(need, 2 * self.max_seq_len)
             cos, sin = rope_tables(self.head_dim, self.max_seq_len, self.theta)
-            self.cos, self.sin = cos.to(xq.device), sin.to(xq.device)
-        cos, sin = self.cos.to(xq.device), self.sin.to(xq.device)
+            self.cos, self.sin = cos.to(device), sin.to(device)
+        if self.cos.device != torch.device(device):
+            self.cos, self.sin = self.cos.to(device), self.sin.to(device)
+        return self.cos, self.sin
+
+    def forward(self, xq: torch.Tensor, xk: torch.Tensor, offset: int = 0):
+        cos, sin = self.tables(offset + xq.shape[1], xq.device)
         return apply_rope(xq, cos, sin, offset), apply_rope(xk, cos, sin, offset)

@@ -22,6 +22,8 @@ from model.forecast import ForecastProjection
 from model.norm import RMSNorm
 from model.rope import RotaryEmbedding
 
+import sparda
+
 
 class SwiGLU(nn.Module):
     """(SiLU(x W_gate) * x W_up) W_down (model/transformer.py:18-31)."""
@@ -73,12 +75,53 @@ class TransformerBlock(nn.Module):
         self.forecast = ForecastProjection(config)
         self.ffn_norm = RMSNorm(config.n_embd, eps=config.norm_eps)
         self.ffn = SwiGLU(config.n_embd, config.ffn_dim)
+        self._fused_w = None
+        self._fused_key = None
+
+    def _use_fused_producer(self, x: torch.Tensor, mask) -> bool:
+        a = self.attention
+        return (getattr(self.config, "fused_producer", False) and type(a) is HipSparseAttention
+                and mask is None and x.is_cuda and x.dtype == torch.bfloat16 and a.head_dim == 64
+                and self.forecast.forecast_dim == 64 and not torch.is_grad_enabled())
+
+    def _fused_weight(self) -> torch.Tensor:
+        """[wq; wk; wv; wf] with the attention RMSNorm weight folded into the
+        columns, rebuilt when any of the parameters changed."""
+        ws = (self.attention.wq.weight, self.attention.wk.weight, self.attention.wv.weight,
+              self.forecast.wf.weight, self.attn_norm.weight)
+        key = tuple((t.data_ptr(), t._version) for t in ws)
+        if key != self._fused_key:
+            with torch.no_grad():
+                w = torch.cat([t.float() for t in ws[:4]], dim=0) * ws[4].float()[None, :]
+                self._fused_w = w.to(torch.bfloat16).contiguous()
+            self._fused_key = key
+        return self._fused_w
 
     def forward(self, x: torch.Tensor, rotary_emb: RotaryEmbedding, kv_cache: Optional[KVCache] = None,
                 mask: Optional[torch.Tensor] = None, is_causal: bool = True,
                 prev_layer_forecast: Optional[torch.Tensor] = None,
                 next_layer_block: Optional["TransformerBlock"] = None,
                 next_kv_cache=None) -> Tuple[torch.Tensor, torch.Tensor]:
+        if self._use_fused_producer(x, mask):
+            # RMSNorm + q / k / v / forecast projections + RoPE in one kernel
+            a = self.attention
+            B, T, _ = x.shape
+            offset = kv_cache.current_len if kv_cache is not None else 0
+            cos, sin = rotary_emb.tables(offset + T, x.device)
+            xq, xk, xv, f = sparda.produce(x, self._fused_weight(), a.n_head * a.head_dim,
+                                           a.n_kv_head * a.head_dim,
+                                           self.forecast.forecast_heads * self.forecast.forecast_dim,
+                                           self.attn_norm.eps, cos, sin, pos0=offset, f_dtype=x.dtype)
+            current_forecast = f.view(B, T, self.forecast.forecast_heads, self.forecast.forecast_dim)
+            if next_layer_block is not None and next_kv_cache is not None:
+                if hasattr(next_layer_block.attention, "prefetch"):
+                    next_layer_block.attention.prefetch(forecast_vector=current_forecast,
+                                                        offload_cache=next_kv_cache)
+            attn_out = a.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
+                                           forecast_vector=prev_layer_forecast)
+            x = x + attn_out
+            x = x + self.ffn(self.ffn_norm(x))
+            return x, current_forecast
         normed_x = self.attn_norm(x)
         current_forecast = self.forecast(normed_x)
         if next_layer_block is not None and next_kv_cache is not None:

@@ -350,6 +350,42 @@ def decode_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, b
     return out
 
 
+def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: int, eps: float,
+            rope_cos: torch.Tensor, rope_sin: torch.Tensor, pos0: int = 0,
+            f_dtype: torch.dtype = torch.bfloat16):
+    """RMSNorm + q / k / v / forecast projections + RoPE in one kernel
+    (model/transformer.py:104-107; model/norm.py:15-21; model/forecast.py:30-40;
+    model/attention/base.py:38-52; model/rope.py:34-65).
+
+    x [B,T,C] bf16; w_stacked [n_q + 2*n_kv + n_f, C] bf16 = [wq; wk; wv; wf]
+    with the RMSNorm weight folded into its columns; rope tables [L, 32] fp32.
+    Returns q [B,T,n_q/64,64], k, v [B,T,n_kv/64,64] (bf16, q and k rotated at
+    positions pos0..pos0+T-1) and f [B,T,n_f/64,64] of f_dtype."""
+    dev = require_device(x, w_stacked, rope_cos, rope_sin)
+    _inference_only(x, w_stacked)
+    if x.dtype != torch.bfloat16 or w_stacked.dtype != torch.bfloat16:
+        raise TypeError("sparda: produce takes bf16 activations and weights")
+    B, T, C = x.shape
+    x2 = x.reshape(B * T, C)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w_stacked = w_stacked.contiguous()
+    if tuple(w_stacked.shape) != (n_q + 2 * n_kv + n_f, C):
+        raise AssertionError(f"Mismatch: stacked weight {tuple(w_stacked.shape)} vs ({n_q + 2 * n_kv + n_f}, {C})")
+    rope_cos = rope_cos.float().contiguous()
+    rope_sin = rope_sin.float().contiguous()
+    if rope_cos.shape[-1] != 32 or rope_sin.shape != rope_cos.shape:
+        raise AssertionError("sparda: RoPE tables must be [L, 32] (head dim 64)")
+    q = torch.empty((B, T, n_q // 64, 64), dtype=torch.bfloat16, device=dev)
+    k = torch.empty((B, T, n_kv // 64, 64), dtype=torch.bfloat16, device=dev)
+    v = torch.empty_like(k)
+    f = torch.empty((B, T, n_f // 64, 64), dtype=f_dtype, device=dev)
+    call("sparda_produce", x2.data_ptr(), x2.stride(0), w_stacked.data_ptr(), B * T, C, n_q, n_kv, n_f,
+         float(eps), rope_cos.data_ptr(), rope_sin.data_ptr(), rope_cos.shape[0], T, pos0,
+         q.data_ptr(), k.data_ptr(), v.data_ptr(), f.data_ptr(), _DT[f_dtype], _stream(dev))
+    return q, k, v, f
+
+
 def block_sums(k: torch.Tensor, pos: int, n: int, block_size: int, sums: torch.Tensor) -> torch.Tensor:
     """Accumulate fp32 block sums of tokens [pos, pos+n) of the device cache
     k [B,S,Hkv,D] into sums [B,NBmax,Hkv,D] (in place; returned). A block whose

@@ -95,6 +95,13 @@ def test_offload_and_selected_decode_argument_errors():
             None)  # sel_cap < k + 2
     _expect(-6, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 100, 64, 8, 3, 0.125, P, P, 10,
             None)  # unknown routing
+    # fused producer: x, x_stride, w, M, C, Nq, Nk, Nf, eps, cos, sin, rope_len, T, pos0, q, k, v, f, f_dtype, stream
+    _expect(-1, "sparda_produce", None, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 0, P, P, P, P, 1, None)
+    _expect(-3, "sparda_produce", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 0, P, P, P, P, 7, None)
+    _expect(-2, "sparda_produce", P, 768, P, 8, 768, 768, 256, 96, 1e-5, P, P, 64, 8, 0, P, P, P, P, 1, None)
+    _expect(-2, "sparda_produce", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 60, P, P, P, P, 1, None)
+    _expect(-2, "sparda_produce", P, 768, P, 9, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 0, P, P, P, P, 1, None)
+    _expect(-5, "sparda_produce", P + 2, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 0, P, P, P, P, 1, None)
     # block sums of a device cache: k, dtype, sb, st, sh, B, Hkv, D, pos, n, bs, nb_stride, sums, stream
     _expect(-1, "sparda_block_sums", None, 1, 256, 256, 64, 1, 4, 64, 0, 64, 64, 4, P, None)
     _expect(-3, "sparda_block_sums", P, 9, 256, 256, 64, 1, 4, 64, 0, 64, 64, 4, P, None)

@@ -1,0 +1,110 @@
+"""GPU parity of the fused producer (RMSNorm + q / k / v / forecast
+projections + RoPE in one kernel) against a plain PyTorch fp32 restatement of
+model/norm.py:15-21, the projections, model/forecast.py:30-40 and
+model/rope.py:34-65; and of the model with the fused producer against the
+model without it. Tolerances: max-abs 2e-2 / mean-abs 2e-3 (bf16 outputs)."""
+
+import pytest
+import torch
+
+import sparda
+from model.attention import KVCache
+from model.config import ModelConfig
+from model.model import SparDAResearchModel
+from model.rope import rope_tables
+from helpers import assert_close_out, np32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _reference(x, w_stack, norm_w, eps, cos, sin, pos0, nq, nkv):
+    """fp32: RMSNorm, stacked projection, rotate-half RoPE of the q and k heads."""
+    xf = x.float()
+    normed = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * norm_w.float()
+    y = normed @ w_stack.float().t()
+    B, T, _ = x.shape
+    q, k, v, f = torch.split(y, [nq, nkv, nkv, y.shape[-1] - nq - 2 * nkv], dim=-1)
+    c = cos[pos0:pos0 + T][None, :, None, :]
+    s = sin[pos0:pos0 + T][None, :, None, :]
+
+    def rot(t):
+        t = t.view(B, T, -1, 64)
+        a, b = t[..., :32], t[..., 32:]
+        return torch.cat((a * c - b * s, b * c + a * s), dim=-1)
+
+    return rot(q), rot(k), v.view(B, T, -1, 64), f.view(B, T, -1, 64)
+
+
+@pytest.mark.parametrize("B,T,pos0,f_dtype", [(2, 300, 5, torch.bfloat16), (1, 1024, 0, torch.float32),
+                                               (4, 1, 4000, torch.bfloat16)])
+def test_produce_matches_fp32_reference(B, T, pos0, f_dtype):
+    case(f"produce B={B} T={T} pos0={pos0} {f_dtype}")
+    g = torch.Generator().manual_seed(11 + T)
+    C, nq, nkv, nf, eps = 768, 768, 256, 256, 1e-5
+    x = torch.randn(B, T, C, generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(nq + 2 * nkv + nf, C, generator=g)).to(torch.bfloat16)
+    norm_w = (1.0 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16)
+    cos, sin = rope_tables(64, 4096)
+    w_fold = (w.float() * norm_w.float()[None, :]).to(torch.bfloat16)
+    q, k, v, f = sparda.produce(x.to(DEV), w_fold.to(DEV), nq, nkv, nf, eps, cos.to(DEV), sin.to(DEV),
+                                pos0=pos0, f_dtype=f_dtype)
+    want = _reference(x, w, norm_w, eps, cos, sin, pos0, nq, nkv)
+    for got, ref, name in zip((q, k, v, f), want, "qkvf"):
+        assert got.shape == ref.shape, name
+        assert_close_out(np32(got), ref.numpy(), torch.bfloat16, what=f"produce {name}")
+
+
+def _pair(fused, **kw):
+    # dense attention: forecast routing is a discrete top-k of F, so the bf16
+    # rounding differences between the fused and the unfused F may flip
+    # near-tied blocks; without routing the logits differ only by rounding
+    cfg = ModelConfig(n_layer=2, context_length=2048, block_size=64, top_k_blocks=8, attention_backend="dense",
+                      norm_eps=1e-5, decode_routing="absolute", fused_producer=fused, **kw)
+    torch.manual_seed(5)
+    return SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval()
+
+
+def _no_less_accurate(fused, plain, ref, what):
+    """The fused producer rounds at other places than the unfused sequence (the
+    folded weight instead of the normalised activations, RoPE in fp32), so both
+    bf16 models are compared with the same weights run in fp32: the fused one
+    must be as accurate as the unfused one (mean and max error within 25%)."""
+    f = np32(fused).astype("float64")
+    p = np32(plain).astype("float64")
+    r = np32(ref).astype("float64")
+    ef, ep = abs(f - r), abs(p - r)
+    assert ef.mean() <= 1.25 * ep.mean() + 1e-5, f"{what}: mean error {ef.mean():.3e} vs unfused {ep.mean():.3e}"
+    assert ef.max() <= 1.25 * ep.max() + 1e-3, f"{what}: max error {ef.max():.3e} vs unfused {ep.max():.3e}"
+
+
+def test_model_with_fused_producer_matches_unfused():
+    case("model forward and decode with / without the fused producer (dense attention), vs fp32")
+    plain, fused = _pair(False), _pair(True)
+    fused.load_state_dict(plain.state_dict())
+    ref = _pair(False).float()
+    ref.load_state_dict({k: v.float() for k, v in plain.state_dict().items()})
+    probe = torch.zeros(1, 1, 768, device=DEV, dtype=torch.bfloat16)
+    assert not fused.layers[1]._use_fused_producer(probe, None)  # autograd on: unfused
+    with torch.no_grad():
+        assert fused.layers[1]._use_fused_producer(probe, None)
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, plain.config.vocab_size, (2, 700), generator=g).to(DEV)
+    with torch.no_grad():
+        _no_less_accurate(fused(ids)["logits"], plain(ids)["logits"], ref(ids)["logits"], "prefill logits")
+        caches = [[KVCache(2, 800, 4, 64, DEV, dt) for _ in range(2)]
+                  for dt in (torch.bfloat16, torch.bfloat16, torch.float32)]
+        for m, c in zip((plain, fused, ref), caches):
+            m(ids[:, :650], kv_caches=c)
+        for t in range(650, 660):
+            a, b, r = (m(ids[:, t:t + 1], kv_caches=c)["logits"] for m, c in zip((plain, fused, ref), caches))
+            _no_less_accurate(b, a, r, f"decode logits {t}")
+        # the fused weight follows parameter updates
+        for m in (plain, fused, ref):
+            m.layers[1].attn_norm.weight.mul_(1.5)
+        _no_less_accurate(fused(ids[:, :300])["logits"], plain(ids[:, :300])["logits"],
+                          ref(ids[:, :300])["logits"], "logits after a weight update")
