@@ -64,7 +64,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--offload-steps", type=int, default=32)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "producer", "pmc"],
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "producer", "teacher",
+                                       "pmc"],
                     default="all",
                     help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
@@ -507,6 +508,41 @@ def bench_producer(args, torch, sparda, synth):
     }
 
 
+def bench_teacher(args, torch, sparda, synth):
+    """Routing-quality teacher at the prefill workload (B=4, T=4096, 12/4
+    heads): per-block dense attention mass from q and k in one kernel, against
+    the reference's way of getting it (materialised bf16 softmax weights
+    [4,12,4096,4096], then TeacherBlockSelector's view / mean / pad / sum)."""
+    from model.forecast import TeacherBlockSelector
+    x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
+    q, k = x["q"], x["k"]
+    sel = TeacherBlockSelector(block_size=BS, num_queries_per_kv=HQ // HKV)
+    R = HQ // HKV
+    mask = torch.full((PT, PT), float("-inf"), device="cuda").triu(1).to(torch.bfloat16)
+
+    def materialised():
+        qh = q.transpose(1, 2)
+        kt = k.repeat_interleave(R, dim=2).permute(0, 2, 3, 1).contiguous()
+        w = torch.softmax(torch.matmul(qh, kt) * (1.0 / D ** 0.5) + mask, dim=-1)
+        return sel(w, TOPK)
+
+    with torch.no_grad():
+        mass = sparda.teacher_block_mass(q, k, BS)
+        ref = materialised()
+        torch.cuda.synchronize()
+        err = float((mass - ref[0].float()).abs().max())
+        us_kernel = events_ms(lambda: sparda.teacher_block_mass(q, k, BS), 10, torch) * 1e3
+        us_mat = events_ms(materialised, 3, torch) * 1e3
+    flop = 2 * (4.0 * D * PB * HQ * PT * (PT + 1) / 2)  # QK^T over the causal pairs, two passes
+    return {
+        "workload": f"teacher block mass, B={PB} T={PT} Hq={HQ} Hkv={HKV} D={D} block={BS}, causal, bf16",
+        "us_kernel": round(us_kernel, 1),
+        "us_materialised_torch": round(us_mat, 1),
+        "kernel_tflops": round(flop / (us_kernel * 1e-6) / 1e12, 1),
+        "max_abs_vs_materialised": round(err, 5),
+    }
+
+
 def pmc_workload(args, torch, sparda, synth):
     """Short eager run for hardware-counter passes: prefill steps, decode steps
     and a plain device copy of COPY_BYTES (the calibration of FETCH_SIZE /
@@ -567,7 +603,8 @@ def main():
     sparda.load()
     if args.only != "all":
         fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload,
-              "model": bench_model, "producer": bench_producer, "pmc": pmc_workload}[args.only]
+              "model": bench_model, "producer": bench_producer, "teacher": bench_teacher,
+              "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
         print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}), flush=True)
         return
@@ -596,6 +633,10 @@ def main():
     prod = bench_producer(args, torch, sparda, synth)
     log(f"producer: fused {prod['us_fused']:.1f} us ({prod['fused_tflops']:.0f} TFLOP/s), "
         f"unfused torch {prod['us_unfused_torch']:.1f} us")
+    log("routing-quality teacher")
+    tch = bench_teacher(args, torch, sparda, synth)
+    log(f"teacher: kernel {tch['us_kernel']:.1f} us ({tch['kernel_tflops']:.0f} TFLOP/s), materialised torch "
+        f"{tch['us_materialised_torch']:.1f} us")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -649,6 +690,7 @@ def main():
         "offload": off,
         "model_forward": mdl,
         "producer": prod,
+        "teacher": tch,
     }
     print(json.dumps(line), flush=True)
 

@@ -275,6 +275,22 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                                       void* out, int64_t out_sb, void* stream);
 
 /*
+ * Teacher block mass for routing-quality evaluation: the dense attention
+ * probability of each query row on each KV block, averaged over the Hq/Hkv
+ * query heads of a KV head (TeacherBlockSelector.forward, model/forecast.py:
+ * 141-193, steps 1-3, computed from q and k without materialising the
+ * [B,Hq,T,T] weights the reference takes as input).
+ *   q: [B,T,Hq,64], k: [B,T,Hkv,64] bf16 (post-RoPE), element strides
+ *      (sb, st, sh, 1), rows 16-byte aligned; Hq / Hkv in {1, 2, 3}.
+ *   mass: [B,Hkv,T,NB] fp32, NB = ceil(T/64); causal: keys s <= t and blocks
+ *      j > t/64 hold 0. scale = 1/sqrt(64) in the reference.
+ */
+SPARDA_API int sparda_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                                   int64_t k_sb, int64_t k_st, int64_t k_sh, int dtype, int64_t B, int64_t T,
+                                   int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, int causal, float scale,
+                                   float* mass, void* stream);
+
+/*
  * Producer of one layer's attention inputs, fused: RMSNorm + the q, k, v and
  * forecast projections + RoPE of q and k. Replaces, for the HIP model, the
  * sequence attn_norm -> ForecastProjection -> wq / wk / wv -> RotaryEmbedding

@@ -310,6 +310,24 @@ SPARDA_API int sparda_offload_rebuild_sums(sparda_offload_t h, int64_t len, int6
     return offload_rebuild_sums(h, len, block_size, block_sums, static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                                   int64_t k_sb, int64_t k_st, int64_t k_sh, int dtype, int64_t B, int64_t T,
+                                   int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, int causal, float scale,
+                                   float* mass, void* stream) {
+    SPARDA_REQUIRE(q && k && mass, SPARDA_ERR_NULL, "teacher_mass: null pointer");
+    SPARDA_REQUIRE(dtype == SPARDA_BF16, SPARDA_ERR_DTYPE, "teacher_mass: bf16 q and k only");
+    SPARDA_REQUIRE(D == 64 && block_size == 64, SPARDA_ERR_SHAPE, "teacher_mass: head dim and block size 64 only");
+    SPARDA_REQUIRE(B >= 1 && T >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 && Hq / Hkv <= 3, SPARDA_ERR_SHAPE,
+                   "teacher_mass: need Hq = R * Hkv with R in {1, 2, 3}");
+    SPARDA_REQUIRE(q_sb % 8 == 0 && q_st % 8 == 0 && q_sh % 8 == 0 && k_sb % 8 == 0 && k_st % 8 == 0 &&
+                       k_sh % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(k) % 16 == 0,
+                   SPARDA_ERR_STRIDE, "teacher_mass: q and k rows must be 16-byte aligned");
+    SPARDA_REQUIRE(B * Hkv * cdiv(T, 64) < (int64_t(1) << 31), SPARDA_ERR_SHAPE, "teacher_mass: too large");
+    return launch_teacher_mass(q, q_sb, q_st, q_sh, k, k_sb, k_st, k_sh, B, T, Hq, Hkv, causal != 0, scale, mass,
+                               static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
                               int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
                               const float* rope_sin, int64_t rope_len, int64_t T, int64_t pos0, void* q, void* k,

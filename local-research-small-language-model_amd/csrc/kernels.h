@@ -20,6 +20,10 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream);
 
+int launch_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb,
+                        int64_t k_st, int64_t k_sh, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int causal,
+                        float scale, float* mass, hipStream_t stream);
+
 int launch_topk_scores(const float* scores, int64_t rows, int64_t NB, int ke, int algo,
                        int32_t* topk, hipStream_t stream);
 

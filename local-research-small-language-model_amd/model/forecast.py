@@ -14,6 +14,7 @@ from typing import Tuple
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 import sparda
 from model.config import ModelConfig
@@ -78,3 +79,77 @@ class ForecastBlockSelector(nn.Module):
                                           score_pos0=query_pos0, query_pos0=query_pos0,
                                           want_topk=True, want_scores=True)
         return scores, topk.long()
+
+
+def _canonical_topk(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Indices of the k largest scores, larger first, equal scores by lower index."""
+    return torch.sort(scores, dim=-1, descending=True, stable=True).indices[..., :k]
+
+
+class TeacherBlockSelector(nn.Module):
+    """Ground-truth block importance from dense attention (model/forecast.py:133-193).
+
+    forward(attn_weights [B,Hq,Tq,Tk], top_k, is_causal)
+      -> (block_scores [B,Hkv,Tq,NB], topk [B,Hkv,Tq,k] int64, target_distribution)
+    restates the reference on materialised post-softmax weights. from_qk(q, k,
+    top_k, is_causal) returns the same triple from the HIP kernel
+    (sparda.teacher_block_mass) without materialising the weights (q
+    [B,T,Hq,64], k [B,T,Hkv,64] bf16, block size 64). Ties in the top-k go to
+    the lower block index (torch.topk leaves their order unspecified).
+    """
+
+    def __init__(self, block_size: int = 32, num_queries_per_kv: int = 3):
+        super().__init__()
+        self.block_size = block_size
+        self.num_queries_per_kv = num_queries_per_kv
+
+    def forward(self, attn_weights: torch.Tensor, top_k: int,
+                is_causal: bool = True) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        B, Hq, Tq, Tk = attn_weights.shape
+        R = self.num_queries_per_kv
+        bs = self.block_size
+        per_kv = attn_weights.reshape(B, Hq // R, R, Tq, Tk).mean(dim=2)
+        nb = (Tk + bs - 1) // bs
+        per_kv = F.pad(per_kv, (0, nb * bs - Tk))
+        block_scores = per_kv.reshape(B, Hq // R, Tq, nb, bs).sum(dim=-1)
+        if is_causal:
+            t = torch.arange(Tq, device=attn_weights.device)[:, None]
+            j = torch.arange(nb, device=attn_weights.device)[None, :]
+            block_scores = block_scores.masked_fill(j > t // bs, 0.0)
+        return self._finish(block_scores, top_k)
+
+    def from_qk(self, q: torch.Tensor, k: torch.Tensor, top_k: int,
+                is_causal: bool = True) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        if q.shape[2] != k.shape[2] * self.num_queries_per_kv:
+            raise AssertionError(f"Mismatch: {q.shape[2]} query heads vs {k.shape[2]} KV heads x "
+                                 f"{self.num_queries_per_kv}")
+        mass = sparda.teacher_block_mass(q, k, self.block_size, causal=is_causal)
+        return self._finish(mass, top_k)
+
+    @staticmethod
+    def _finish(block_scores: torch.Tensor, top_k: int):
+        target = block_scores / (block_scores.sum(dim=-1, keepdim=True) + 1e-8)
+        kk = min(top_k, block_scores.shape[-1])
+        return block_scores, _canonical_topk(block_scores, kk), target
+
+
+def compute_forecast_loss(pred_scores: torch.Tensor, target_distribution: torch.Tensor,
+                          loss_type: str = "kl", temperature: float = 1.0) -> torch.Tensor:
+    """Auxiliary loss between forecast scores and the teacher distribution
+    (model/forecast.py:196-238): "kl" = KL(target || softmax(pred / temperature)),
+    "bce" = BCE with logits against the multi-hot support of the target; both
+    averaged over the (row, block) entries with a finite prediction in rows
+    whose target has mass."""
+    valid = torch.isfinite(pred_scores) & (target_distribution.sum(dim=-1, keepdim=True) > 0)
+    n = valid.sum().clamp(min=1)
+    if loss_type == "kl":
+        logp = F.log_softmax(pred_scores / temperature, dim=-1)
+        logp = torch.where(torch.isfinite(logp), logp, torch.zeros_like(logp))
+        per = F.kl_div(logp, target_distribution, reduction="none")
+    elif loss_type == "bce":
+        hot = (target_distribution > 0).to(pred_scores.dtype)
+        logits = torch.where(torch.isfinite(pred_scores), pred_scores, torch.full_like(pred_scores, -100.0))
+        per = F.binary_cross_entropy_with_logits(logits, hot, reduction="none")
+    else:
+        raise ValueError(f"Unknown forecast loss type: {loss_type}")
+    return torch.where(valid, per, torch.zeros_like(per)).sum() / n

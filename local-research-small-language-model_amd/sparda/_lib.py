@@ -66,6 +66,8 @@ SIGNATURES = {
     "sparda_offload_create": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_p)]),
     "sparda_offload_destroy": (_int, [_p]),
     "sparda_offload_host": (_int, [_p, ctypes.POINTER(_p), ctypes.POINTER(_p)]),
+    "sparda_teacher_mass": (_int, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _int, _i64, _i64, _i64, _i64,
+                                   _i64, _i64, _int, _f32, _p, _p]),
     "sparda_produce": (_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64, _i64, _i64,
                               _p, _p, _p, _p, _int, _p]),
     "sparda_block_sums": (_int, [_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

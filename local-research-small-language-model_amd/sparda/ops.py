@@ -350,6 +350,30 @@ def decode_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, b
     return out
 
 
+def teacher_block_mass(q: torch.Tensor, k: torch.Tensor, block_size: int = 64, causal: bool = True,
+                       scale: Optional[float] = None) -> torch.Tensor:
+    """Dense attention probability per (query row, KV block), averaged over the
+    query heads of each KV head (model/forecast.py:141-193, steps 1-3), from
+    q [B,T,Hq,64] and k [B,T,Hkv,64] bf16 without materialising the weights.
+    Returns [B,Hkv,T,ceil(T/64)] fp32."""
+    dev = require_device(q, k)
+    _inference_only(q, k)
+    q, k = _rowmajor(q), _rowmajor(k)
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if k.shape[0] != B or k.shape[1] != T or k.shape[3] != D:
+        raise AssertionError(f"Mismatch: q {tuple(q.shape)} vs k {tuple(k.shape)}")
+    if scale is None:
+        scale = default_scale(D)
+    NB = (T + block_size - 1) // block_size
+    mass = torch.empty((B, Hkv, T, NB), dtype=torch.float32, device=dev)
+    qsb, qst, qsh, _ = q.stride()
+    ksb, kst, ksh, _ = k.stride()
+    call("sparda_teacher_mass", q.data_ptr(), qsb, qst, qsh, k.data_ptr(), ksb, kst, ksh, _dtype_code(q),
+         B, T, Hq, Hkv, D, block_size, int(causal), float(scale), mass.data_ptr(), _stream(dev))
+    return mass
+
+
 def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: int, eps: float,
             rope_cos: torch.Tensor, rope_sin: torch.Tensor, pos0: int = 0,
             f_dtype: torch.dtype = torch.bfloat16):

@@ -349,3 +349,51 @@ def prefill_selection(k, f, bs: int, topk_blocks: int, causal: bool = True,
     P = compress(k, bs)
     _, _, sel, n = route(f, P, bs, topk_blocks, causal, 0, 0, scale)
     return sel, n
+
+
+def teacher_block_scores(attn_weights, bs: int, R: int, causal: bool = True) -> np.ndarray:
+    """TeacherBlockSelector.forward steps 1-3 (model/forecast.py:160-184) in
+    float64: weights [B,Hq,Tq,Tk] -> mean over the R query heads of each KV
+    head, zero-padded to whole blocks, summed per block, future blocks 0."""
+    w = np.asarray(attn_weights, np.float64)
+    B, Hq, Tq, Tk = w.shape
+    G = Hq // R
+    kv = w.reshape(B, G, R, Tq, Tk).mean(axis=2)
+    NB = num_blocks(Tk, bs)
+    pad = np.zeros((B, G, Tq, NB * bs), np.float64)
+    pad[..., :Tk] = kv
+    out = pad.reshape(B, G, Tq, NB, bs).sum(axis=-1)
+    if causal:
+        t = np.arange(Tq)[:, None]
+        j = np.arange(NB)[None, :]
+        out[..., (j > t // bs)] = 0.0
+    return out
+
+
+def dense_weights(q, k, causal: bool = True, scale: Optional[float] = None) -> np.ndarray:
+    """Post-softmax attention weights [B,Hq,T,T] in float64 from q [B,T,Hq,D],
+    k [B,T,Hkv,D] (query head h reads KV head h // (Hq/Hkv)), as the dense
+    backend's return_attn_weights gives them."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    B, T, Hq, D = q.shape
+    R = Hq // k.shape[2]
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    w = np.empty((B, Hq, T, T), np.float64)
+    for b in range(B):
+        for h in range(Hq):
+            s = (q[b, :, h, :] @ k[b, :, h // R, :].T) * scale
+            if causal:
+                s[np.triu_indices(T, 1)] = -np.inf
+            s = s - s.max(axis=1, keepdims=True)
+            e = np.exp(s)
+            w[b, h] = e / e.sum(axis=1, keepdims=True)
+    return w
+
+
+def teacher_block_mass(q, k, bs: int, causal: bool = True, scale: Optional[float] = None) -> np.ndarray:
+    """Teacher block mass [B,Hkv,T,NB] (float64) from q and k: dense weights,
+    then teacher_block_scores."""
+    R = np.asarray(q).shape[2] // np.asarray(k).shape[2]
+    return teacher_block_scores(dense_weights(q, k, causal, scale), bs, R, causal)

@@ -95,6 +95,12 @@ def test_offload_and_selected_decode_argument_errors():
             None)  # sel_cap < k + 2
     _expect(-6, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 100, 64, 8, 3, 0.125, P, P, 10,
             None)  # unknown routing
+    # teacher mass: q, q_sb, q_st, q_sh, k, k_sb, k_st, k_sh, dtype, B, T, Hq, Hkv, D, bs, causal, scale, mass, stream
+    _expect(-1, "sparda_teacher_mass", None, 8, 8, 8, P, 8, 8, 8, 1, 1, 64, 12, 4, 64, 64, 1, 0.125, P, None)
+    _expect(-3, "sparda_teacher_mass", P, 8, 8, 8, P, 8, 8, 8, 0, 1, 64, 12, 4, 64, 64, 1, 0.125, P, None)
+    _expect(-2, "sparda_teacher_mass", P, 8, 8, 8, P, 8, 8, 8, 1, 1, 64, 12, 4, 64, 32, 1, 0.125, P, None)
+    _expect(-2, "sparda_teacher_mass", P, 8, 8, 8, P, 8, 8, 8, 1, 1, 64, 16, 4, 64, 64, 1, 0.125, P, None)
+    _expect(-5, "sparda_teacher_mass", P, 8, 4, 8, P, 8, 8, 8, 1, 1, 64, 12, 4, 64, 64, 1, 0.125, P, None)
     # fused producer: x, x_stride, w, M, C, Nq, Nk, Nf, eps, cos, sin, rope_len, T, pos0, q, k, v, f, f_dtype, stream
     _expect(-1, "sparda_produce", None, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 0, P, P, P, P, 1, None)
     _expect(-3, "sparda_produce", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 8, 0, P, P, P, P, 7, None)
