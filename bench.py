@@ -64,8 +64,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--offload-steps", type=int, default=32)
+    ap.add_argument("--generate-steps", type=int, default=128)
     ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "producer", "teacher",
-                                       "pmc"],
+                                       "generate", "pmc"],
                     default="all",
                     help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
@@ -395,6 +396,71 @@ def bench_offload(args, torch, sparda, synth):
     }
 
 
+def bench_generate(args, torch, sparda, synth):
+    """Greedy generation after a 16384-token prompt with the 12-layer model of
+    bench_model (fused producer, cached prototypes, absolute-position routing,
+    B=1): per-token time of the eager cached decode loop (host-driven, one
+    launch sequence issued per token) and of GraphDecoder (one HIP graph replay
+    per token, positions read from device memory). Both loops start from the
+    same prefill; their generated tokens must agree."""
+    from model.attention import PrototypeKVCache
+    from model.config import ModelConfig
+    from model.decode_graph import GraphDecoder
+    from model.model import SparDAResearchModel
+    dev = torch.device("cuda")
+    G, W = args.generate_steps, 8
+    cap = MT + G + W + 64
+    cfg = ModelConfig(n_layer=12, context_length=cap, block_size=BS, top_k_blocks=TOPK,
+                      attention_backend="hip_sparse", norm_eps=1e-5, fused_producer=True,
+                      decode_routing="absolute")
+    torch.manual_seed(1007)
+    model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(1007)
+    prompt = torch.randint(0, cfg.vocab_size, (1, MT), generator=g).to(dev)
+
+    def loop(first_logits, step, n):
+        toks, logits = [], first_logits
+        for _ in range(n):
+            nxt = torch.argmax(logits, dim=-1, keepdim=True)
+            toks.append(nxt)
+            logits = step(nxt)
+        return toks, logits
+
+    def timed(step, first_logits):
+        toks, logits = loop(first_logits, step, W)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        more, _ = loop(logits, step, G)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / G, torch.cat(toks + more, dim=1)
+
+    with torch.no_grad():
+        caches = [PrototypeKVCache(1, cap, cfg.n_kv_head, cfg.head_dim, dev, torch.bfloat16, block_size=BS)
+                  for _ in range(cfg.n_layer)]
+        first = model(prompt, kv_caches=caches)["logits"][:, -1]
+        us_eager, toks_eager = timed(lambda t: model(t, kv_caches=caches)["logits"][:, -1], first)
+        del caches
+        gd = GraphDecoder(model, 1, cap)
+        first = gd.prefill(prompt)
+        us_graph, toks_graph = timed(gd.step, first)
+        torch.cuda.synchronize()
+    assert torch.equal(toks_eager, toks_graph), "graph-replayed generation differs from the eager loop"
+    del gd, model
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"greedy generation of {G} tokens after a {MT}-token prompt, 12-layer model of "
+                    "model_forward (fused producer, block sums kept in HBM, top-8 + sink + current, "
+                    "absolute-position routing), B=1, bf16; step = one token through all layers incl. LM head",
+        "us_per_token_eager": round(us_eager, 1),
+        "us_per_token_graph": round(us_graph, 1),
+        "tok_s_graph": round(1e6 / us_graph, 1),
+        "tokens": G,
+        "tokens_agree": True,
+    }
+
+
 def bench_model(args, torch, sparda, synth, fused=False):
     """12-layer forward of the model at B=1, T=16384 (bf16 weights from the
     model's N(0, 0.02) init, vocab 32000 tied, d 768, 12/4 heads, SwiGLU 2048;
@@ -604,7 +670,7 @@ def main():
     if args.only != "all":
         fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload,
               "model": bench_model, "producer": bench_producer, "teacher": bench_teacher,
-              "pmc": pmc_workload}[args.only]
+              "generate": bench_generate, "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
         print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}), flush=True)
         return
@@ -629,6 +695,9 @@ def main():
         f"attention {100 * mdl['attention_fraction']:.1f}% (layer 0 dense {mdl['attention_ms_per_layer'][0]:.2f} ms, "
         f"sparse layers {sum(mdl['attention_ms_per_layer'][1:]) / 11:.2f} ms each); fused producer "
         f"{mdl['ms_per_forward_fused_producer']:.2f} ms ({mdl['tok_s_fused_producer']:.0f} tok/s)")
+    log("graph-replayed generation")
+    gen = bench_generate(args, torch, sparda, synth)
+    log(f"generate: eager {gen['us_per_token_eager']:.1f} us/token, graph {gen['us_per_token_graph']:.1f} us/token")
     log("fused producer")
     prod = bench_producer(args, torch, sparda, synth)
     log(f"producer: fused {prod['us_fused']:.1f} us ({prod['fused_tflops']:.0f} TFLOP/s), "
@@ -689,6 +758,7 @@ def main():
         },
         "offload": off,
         "model_forward": mdl,
+        "generate": gen,
         "producer": prod,
         "teacher": tch,
     }

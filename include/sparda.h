@@ -352,6 +352,48 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
                                     int32_t* sel, int32_t* n_sel, int64_t sel_cap, void* stream);
 
 /*
+ * Decode steps at a device-held position, so that one recorded sequence of
+ * launches (a HIP graph) serves every step of a generation loop. The
+ * reference's loop (SparDAResearchModel.generate, model/model.py:159-195, one
+ * forward per token through KVCache.update, model/attention/base.py:11-32, and
+ * the decode branch of SparseAttention.forward, model/attention/sparse.py:99-183)
+ * passes the cache length from the host every step; these entries read the
+ * position p of the token being decoded from *pos_dev (an int64 in device
+ * memory, 8-byte aligned) when the kernels run. The cache holds p + 1 tokens
+ * (token p appended by the caller before the attention). p is clamped into
+ * [0, max_len) (the RoPE table length for produce): a position outside it
+ * never reads out of bounds, but its results are those of the clamped one.
+ *
+ * sparda_produce_at: sparda_produce with positions *pos_dev + t.
+ * sparda_block_sums_at: recomputes, per sequence, the block holding token p
+ *   over [p - p % bs, p] (k: the cache base, token 0), as
+ *   sparda_block_sums(k, ..., pos = p - p % bs, n = p % bs + 1) does.
+ * sparda_select_decode_at: sparda_select_decode with len = p + 1, pos = p.
+ * sparda_decode_at: sparda_decode_selected with S = p + 1 over the caller's
+ *   list (sel / n_sel), or, with sel NULL and window_k > 0, the static window
+ *   {0} U [cb - window_k + 1, cb] (cb = p / bs; every block while cb + 1 <=
+ *   window_k + 2) that sparda_decode uses without a forecast, or every block
+ *   (sel NULL, window_k 0).
+ */
+SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                                 int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                                 const float* rope_sin, int64_t rope_len, int64_t T, const int64_t* pos_dev,
+                                 void* q, void* k, void* v, void* f, int f_dtype, void* stream);
+SPARDA_API int sparda_block_sums_at(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,
+                                    int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
+                                    int64_t block_size, int64_t nb_stride, float* block_sums, void* stream);
+SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                                       const float* block_sums, int64_t B, int64_t Hkv, int64_t D,
+                                       int64_t nb_stride, int64_t max_len, const int64_t* pos_dev,
+                                       int64_t block_size, int64_t top_k, int routing, float scale,
+                                       int32_t* sel, int32_t* n_sel, int64_t sel_cap, void* stream);
+SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel,
+                                const int32_t* n_sel, int64_t sel_cap, int64_t window_k, int64_t B,
+                                int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
+                                int64_t block_size, float scale, void* out, int64_t out_sb, void* stream);
+
+/*
  * Host-resident KV cache of one layer: pinned host arena (hipHostMalloc,
  * mapped) of K and V, each [B][Hkv][max_seq][D] in `dtype`, zero-filled.
  * Replaces the pinned cpu_k / cpu_v of OffloadedKVCache

@@ -262,6 +262,63 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
                                 static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                                       const float* block_sums, int64_t B, int64_t Hkv, int64_t D,
+                                       int64_t nb_stride, int64_t max_len, const int64_t* pos_dev,
+                                       int64_t block_size, int64_t top_k, int routing, float scale, int32_t* sel,
+                                       int32_t* n_sel, int64_t sel_cap, void* stream) {
+    SPARDA_REQUIRE(pos_dev, SPARDA_ERR_NULL, "select_decode_at: null pos_dev");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "select_decode_at: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(forecast && block_sums && sel && n_sel, SPARDA_ERR_NULL, "select_decode_at: null pointer");
+    SPARDA_REQUIRE(dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "select_decode_at: forecast dtype %d", f_dtype);
+    SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
+                   "select_decode_at: unknown routing %d", routing);
+    SPARDA_REQUIRE(B > 0 && Hkv > 0 && head_dim_ok(D) && block_size > 0 && max_len >= 1, SPARDA_ERR_SHAPE,
+                   "select_decode_at: bad sizes (D must be one of 16, 32, 64, 128)");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
+                   "select_decode_at: block_sums must be 16-byte aligned");
+    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "select_decode_at: top_k out of range");
+    SPARDA_REQUIRE(sel_cap >= top_k + 2 && sel_cap <= kMaxSelCap, SPARDA_ERR_SHAPE,
+                   "select_decode_at: sel_cap must be in [top_k+2, %d]", kMaxSelCap);
+    SPARDA_REQUIRE(nb_stride >= cdiv(max_len, block_size), SPARDA_ERR_SHAPE,
+                   "select_decode_at: nb_stride too small");
+    SPARDA_REQUIRE(cdiv(max_len, block_size) <= 4096, SPARDA_ERR_SHAPE, "select_decode_at: more than 4096 blocks");
+    SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "select_decode_at: grid too large");
+    return launch_select_decode(forecast, f_dtype, f_sb, f_sh, block_sums, B, Hkv, D, nb_stride, max_len,
+                                max_len - 1, block_size, top_k, routing, scale, sel, n_sel, sel_cap,
+                                static_cast<hipStream_t>(stream), pos_dev);
+}
+
+SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel,
+                                const int32_t* n_sel, int64_t sel_cap, int64_t window_k, int64_t B,
+                                int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
+                                int64_t block_size, float scale, void* out, int64_t out_sb, void* stream) {
+    SPARDA_REQUIRE(q && k && v && out && pos_dev, SPARDA_ERR_NULL, "decode_at: null q/k/v/out/pos_dev");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "decode_at: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "decode_at: sel and n_sel go together");
+    SPARDA_REQUIRE(!sel || window_k == 0, SPARDA_ERR_MODE, "decode_at: a selection list or a window, not both");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "decode_at: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(B > 0 && max_len > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "decode_at: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "decode_at: head dim %lld not in {16,32,64,128}",
+                   (long long)D);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "decode_at: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(!sel || (sel_cap >= 1 && sel_cap <= kMaxSelCap), SPARDA_ERR_SHAPE,
+                   "decode_at: sel_cap must be in [1, %d]", kMaxSelCap);
+    SPARDA_REQUIRE(window_k >= 0 && window_k <= kMaxTopK, SPARDA_ERR_SHAPE, "decode_at: window_k out of range");
+    SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "decode_at: grid too large");
+    const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
+    SPARDA_REQUIRE(aligned16(k) && aligned16(v) && kv_sb % ve == 0 && kv_ss % ve == 0 && kv_sh % ve == 0,
+                   SPARDA_ERR_STRIDE, "decode_at: K/V rows must be 16-byte aligned");
+    return launch_decode_at(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, sel, n_sel, sel_cap, window_k, B,
+                            max_len, pos_dev, Hq, Hkv, D, block_size, scale, out, out_sb,
+                            static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_offload_create(int64_t B, int64_t max_seq, int64_t Hkv, int64_t D, int dtype,
                                      sparda_offload_t* out) {
     SPARDA_REQUIRE(out, SPARDA_ERR_NULL, "offload_create: null output handle");
@@ -328,10 +385,10 @@ SPARDA_API int sparda_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, in
                                static_cast<hipStream_t>(stream));
 }
 
-SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
-                              int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
-                              const float* rope_sin, int64_t rope_len, int64_t T, int64_t pos0, void* q, void* k,
-                              void* v, void* f, int f_dtype, void* stream) {
+static int produce_impl(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C, int64_t Nq,
+                        int64_t Nk, int64_t Nf, float eps, const float* rope_cos, const float* rope_sin,
+                        int64_t rope_len, int64_t T, int64_t pos0, const int64_t* pos_dev, void* q, void* k,
+                        void* v, void* f, int f_dtype, void* stream) {
     SPARDA_REQUIRE(x && w && rope_cos && rope_sin && q && k && v && f, SPARDA_ERR_NULL, "produce: null pointer");
     SPARDA_REQUIRE(f_dtype == SPARDA_F32 || f_dtype == SPARDA_BF16, SPARDA_ERR_DTYPE,
                    "produce: forecast dtype %d unsupported", f_dtype);
@@ -345,12 +402,49 @@ SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w
                    "multiple of 128", (long long)(Nq + 2 * Nk + Nf));
     SPARDA_REQUIRE(pos0 + T <= rope_len, SPARDA_ERR_SHAPE, "produce: positions up to %lld beyond the RoPE "
                    "tables (%lld)", (long long)(pos0 + T), (long long)rope_len);
+    SPARDA_REQUIRE(!pos_dev || (reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "produce_at: pos_dev must be 8-byte aligned");
     SPARDA_REQUIRE(x_stride_row >= C && x_stride_row % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(w) % 16 == 0,
                    SPARDA_ERR_STRIDE, "produce: x rows and w must be 16-byte aligned");
     SPARDA_REQUIRE(M / 128 < (int64_t(1) << 31), SPARDA_ERR_SHAPE, "produce: too many rows");
     return launch_produce(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, T, pos0, q, k, v, f,
-                          f_dtype, static_cast<hipStream_t>(stream));
+                          f_dtype, static_cast<hipStream_t>(stream), pos_dev, rope_len);
+}
+
+SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                              int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                              const float* rope_sin, int64_t rope_len, int64_t T, int64_t pos0, void* q, void* k,
+                              void* v, void* f, int f_dtype, void* stream) {
+    return produce_impl(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, rope_len, T, pos0, nullptr,
+                        q, k, v, f, f_dtype, stream);
+}
+
+SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                                 int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                                 const float* rope_sin, int64_t rope_len, int64_t T, const int64_t* pos_dev,
+                                 void* q, void* k, void* v, void* f, int f_dtype, void* stream) {
+    SPARDA_REQUIRE(pos_dev, SPARDA_ERR_NULL, "produce_at: null pos_dev");
+    return produce_impl(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, rope_len, T, 0, pos_dev, q,
+                        k, v, f, f_dtype, stream);
+}
+
+SPARDA_API int sparda_block_sums_at(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,
+                                    int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
+                                    int64_t block_size, int64_t nb_stride, float* block_sums, void* stream) {
+    SPARDA_REQUIRE(k && block_sums && pos_dev, SPARDA_ERR_NULL, "block_sums_at: null k/block_sums/pos_dev");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "block_sums_at: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "block_sums_at: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && block_size > 0 && nb_stride > 0 && max_len >= 1, SPARDA_ERR_SHAPE,
+                   "block_sums_at: sizes must be positive");
+    SPARDA_REQUIRE((max_len - 1) / block_size < nb_stride, SPARDA_ERR_CAPACITY,
+                   "block_sums_at: max_len %lld needs more than nb_stride %lld blocks", (long long)max_len,
+                   (long long)nb_stride);
+    SPARDA_REQUIRE(sb >= 0 && st >= 0 && sh >= 0, SPARDA_ERR_STRIDE, "block_sums_at: negative stride");
+    SPARDA_REQUIRE(B <= 65535, SPARDA_ERR_SHAPE, "block_sums_at: too large");
+    return launch_block_sums(k, dtype, sb, st, sh, 0, max_len, B, Hkv, D, block_size, nb_stride, block_sums,
+                             static_cast<hipStream_t>(stream), pos_dev);
 }
 
 SPARDA_API int sparda_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,

@@ -106,7 +106,9 @@ decode_score_kernel(const void* __restrict__ kc, int64_t kv_sb, int64_t kv_ss, i
 // launch 2: selection + attention over the selected blocks + merge, one
 // workgroup per (sequence, KV head), W wavefronts; wavefront w serves the
 // selected blocks w, w+W, ... sel_mode: 0 top-k of the launch-1 scores,
-// 1 dense (all blocks), 2 window {0} U [cb-k+1, cb].
+// 1 dense (all blocks), 2 window {0} U [cb-k+1, cb] (every block while
+// cb+1 <= k+2), 3 the caller's list. With pos_dev the length comes from
+// device memory (S = *pos_dev + 1, clamped to the S argument).
 // For a block, lane i holds key row j*bs + i of K in registers and stages
 // the V row in the wave's LDS region (16-byte loads); it scores the R query
 // heads of the group (4 at a time), keeps a running (m, l, o) per head over
@@ -144,14 +146,14 @@ template <int DT, int DH, int CH, bool MF>
 __global__ void __launch_bounds__(kAttendMaxWaves * 64)
 decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      const void* __restrict__ kc, const void* __restrict__ vc,
-                     int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int64_t S, int Hq, int H, int bs,
+                     int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int64_t S_arg, int Hq, int H, int bs,
                      int64_t NB, int k, int sel_mode, int cap, float scale_log2,
                      const float* __restrict__ ws_scores,
                      const int32_t* __restrict__ sel_in, const int32_t* __restrict__ n_sel_in,
                      int compact, const void* __restrict__ k_new, const void* __restrict__ v_new,
                      int64_t new_sb, int64_t new_sh,
                      int32_t* __restrict__ sel_out, int32_t* __restrict__ n_sel_out,
-                     void* __restrict__ out, int64_t out_sb) {
+                     void* __restrict__ out, int64_t out_sb, const int64_t* __restrict__ pos_dev) {
     using E = typename KvElem<DT>::T;
     constexpr int VR = v_row_elems<DT, DH>();
     constexpr int KW = DT == SPARDA_BF16 ? DH / 2 : DH;  // K row words per lane
@@ -168,6 +170,12 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     const int wave = threadIdx.x / kWave;
     const int nwaves = blockDim.x / kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
+    // with pos_dev the query is token *pos_dev (clamped into [0, S_arg)): S = *pos_dev + 1
+    int64_t S = S_arg;
+    if (pos_dev != nullptr) {
+        const int64_t p = *pos_dev;
+        S = p < 0 ? 1 : (p >= S_arg ? S_arg : p + 1);
+    }
     const int cb = static_cast<int>((S - 1) / bs);
     float* part_all = reinterpret_cast<float*>(dyn);                       // [nwaves][R][DH+2]
     const size_t part_bytes = ((static_cast<size_t>(nwaves) * R * (DH + 2) * 4) + 15) & ~static_cast<size_t>(15);
@@ -198,6 +206,9 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             m = n_sel_in[bg];
             m = m < 0 ? 0 : (m > cap ? cap : m);
             if (lane < m) sel_lds[lane] = sel_in[bg * cap + lane];
+        } else if (cb + 1 <= k + 2) {
+            m = cb + 1;  // window mode on a short cache: every block (the host picks mode 1 for these)
+            if (lane < m) sel_lds[lane] = lane;
         } else {
             int lo = cb - k + 1;
             if (lo < 0) lo = 0;
@@ -575,6 +586,7 @@ struct AttendArgs {
     const void* k_new; const void* v_new; int64_t new_sb, new_sh;
     int32_t* sel_out; int32_t* n_sel_out;
     void* out; int64_t out_sb;
+    const int64_t* pos_dev = nullptr;  // S = *pos_dev + 1, S the bound (window / list modes)
 };
 
 static int launch_attend(const AttendArgs& a, hipStream_t stream) {
@@ -610,7 +622,7 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
                            a.q, a.q_sb, a.q_sh, a.kc, a.vc, a.kv_sb, a.kv_ss, a.kv_sh, a.S, Hq_i, Hkv_i,  \
                            static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
-                           a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb);                 \
+                           a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb, a.pos_dev);      \
     } while (0)
 #define SPARDA_ATT_C(DT_, DH_)                            \
     if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
@@ -704,6 +716,25 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
     AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S, Hq, Hkv, D, bs, cap > 2 ? cap - 2 : 0,
                  sel == nullptr ? 1 : 3, static_cast<int>(sel == nullptr ? 0 : cap), scale, nullptr,
                  sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb};
+    return launch_attend(a, stream);
+}
+
+int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
+                     int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel, const int32_t* n_sel,
+                     int64_t cap, int64_t window_k, int64_t B, int64_t S_max, const int64_t* pos_dev, int64_t Hq,
+                     int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
+                     hipStream_t stream) {
+    int mode, cap_i;
+    int64_t kk;
+    if (sel != nullptr) {
+        mode = 3, cap_i = static_cast<int>(cap), kk = cap > 2 ? cap - 2 : 0;
+    } else if (window_k > 0) {
+        mode = 2, cap_i = static_cast<int>(window_k + 2), kk = window_k;
+    } else {
+        mode = 1, cap_i = 0, kk = 0;
+    }
+    AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S_max, Hq, Hkv, D, bs, kk, mode, cap_i, scale,
+                 nullptr, sel, n_sel, 0, nullptr, nullptr, 0, 0, nullptr, nullptr, out, out_sb, pos_dev};
     return launch_attend(a, stream);
 }
 

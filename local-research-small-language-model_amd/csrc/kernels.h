@@ -18,7 +18,8 @@ int launch_route(const void* f, int fdtype, int64_t fsb, int64_t fst, int64_t fs
 
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
-                   void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream);
+                   void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
+                   const int64_t* pos_dev = nullptr, int64_t rope_len = 0);
 
 int launch_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb,
                         int64_t k_st, int64_t k_sh, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int causal,
@@ -60,7 +61,15 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
 int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
                          int64_t H, int64_t D, int64_t nb_stride, int64_t len, int64_t pos, int64_t bs,
                          int64_t k, int routing, float scale, int32_t* sel, int32_t* n_sel, int64_t cap,
-                         hipStream_t stream);
+                         hipStream_t stream, const int64_t* pos_dev = nullptr);
+
+// attention at a device-held position: S = *pos_dev + 1 (clamped to S_max);
+// the caller's list (sel), the window of window_k blocks, or every block
+int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
+                     int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel, const int32_t* n_sel,
+                     int64_t cap, int64_t window_k, int64_t B, int64_t S_max, const int64_t* pos_dev, int64_t Hq,
+                     int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
+                     hipStream_t stream);
 
 // host-resident KV arena (offload.hip)
 constexpr int64_t kMaxFetchSlots = 1024;  // selection capacity of a DMA fetch
@@ -72,10 +81,11 @@ int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb,
                    int64_t pos, int64_t n, int64_t bs, float* sums, hipStream_t stream);
 int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sums, hipStream_t stream);
 
-// fp32 block sums of tokens pos..pos+n-1; k points at token pos (strides sb, st, sh)
+// fp32 block sums of tokens pos..pos+n-1; k points at token pos (strides sb, st, sh).
+// With pos_dev: the block holding token *pos_dev (< n), k pointing at token 0.
 int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
                       int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
-                      float* sums, hipStream_t stream);
+                      float* sums, hipStream_t stream, const int64_t* pos_dev = nullptr);
 int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t bs,
                   int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream);
 

@@ -140,11 +140,23 @@ arena_store_kernel(const char* __restrict__ k, const char* __restrict__ v, int64
 // (b, block j, g, d) continue the sequential sum from the block start
 // (restart at 0 when pos is at or before the block start).
 // k: [B,n,H,D] strides (sb, st, sh) holding tokens pos..pos+n-1.
+// With pos_dev (one workgroup per sequence): the block holding token
+// p = *pos_dev (clamped into [0, n)) is recomputed over [p - p % bs, p], and k
+// points at token 0.
 template <int DT>
 __global__ void __launch_bounds__(256)
-block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh, int64_t pos, int64_t n,
-                  int64_t H, int64_t D, int64_t bs, int64_t nb_stride, float* __restrict__ sums) {
+block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh, int64_t pos_arg, int64_t n_arg,
+                  int64_t H, int64_t D, int64_t bs, int64_t nb_stride, float* __restrict__ sums,
+                  const int64_t* __restrict__ pos_dev) {
     constexpr int U = 32;  // token loads in flight per thread, added in token order
+    int64_t pos = pos_arg, n = n_arg, k_tok = pos_arg;  // k_tok: the token k points at
+    if (pos_dev != nullptr) {
+        int64_t p = *pos_dev;
+        p = p < 0 ? 0 : (p >= n_arg ? n_arg - 1 : p);
+        pos = p - p % bs;
+        n = p - pos + 1;
+        k_tok = 0;
+    }
     const int64_t j = pos / bs + blockIdx.x;
     const int64_t b = blockIdx.y;
     const int64_t s_lo = j * bs > pos ? j * bs : pos;
@@ -158,28 +170,29 @@ block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh
         for (; s + U <= s_hi; s += U) {
             float x[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + (s + u - pos) * st);
+            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + (s + u - k_tok) * st);
 #pragma unroll
             for (int u = 0; u < U; ++u) acc = acc + x[u];
         }
-        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(k, base + (s - pos) * st);
+        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(k, base + (s - k_tok) * st);
         *out = acc;
     }
 }
 
 int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
                       int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
-                      float* sums, hipStream_t stream) {
-    const int64_t nblk = (pos + n - 1) / bs - pos / bs + 1;
+                      float* sums, hipStream_t stream, const int64_t* pos_dev) {
+    // with pos_dev: one block per sequence, n bounds the device position
+    const int64_t nblk = pos_dev != nullptr ? 1 : (pos + n - 1) / bs - pos / bs + 1;
     dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(B));
     int threads = static_cast<int>(H * D < 256 ? H * D : 256);
     threads = ((threads + kWave - 1) / kWave) * kWave;
     if (dtype == SPARDA_BF16)
         hipLaunchKernelGGL(block_sums_kernel<SPARDA_BF16>, grid, dim3(threads), 0, stream, k, sb, st, sh, pos, n,
-                           H, D, bs, nb_stride, sums);
+                           H, D, bs, nb_stride, sums, pos_dev);
     else
         hipLaunchKernelGGL(block_sums_kernel<SPARDA_F32>, grid, dim3(threads), 0, stream, k, sb, st, sh, pos, n,
-                           H, D, bs, nb_stride, sums);
+                           H, D, bs, nb_stride, sums, pos_dev);
     return check_hip(hipGetLastError(), "block_sums_kernel");
 }
 
@@ -230,9 +243,9 @@ constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key ar
 template <int FDT, int CH, int DH, bool POW2>
 __global__ void __launch_bounds__(kSelThreads)
 select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, const float* __restrict__ sums,
-                     int64_t H, int64_t nb_stride, int64_t n_present, int64_t pos, int64_t score_pos,
+                     int64_t H, int64_t nb_stride, int64_t n_present_arg, int64_t pos_arg, int64_t score_pos_arg,
                      int64_t bs, int k, float scale, int32_t* __restrict__ sel, int32_t* __restrict__ n_sel,
-                     int cap) {
+                     int cap, const int64_t* __restrict__ pos_dev, int absolute) {
     __shared__ float f_lds[kMaxHeadDim];
     __shared__ uint32_t key_lds[kSelMaxBlocks];
     __shared__ int32_t sel_lds[kMaxSelCap + 2];
@@ -242,6 +255,15 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
+    // with pos_dev: a decode step at token p = *pos_dev (clamped into [0, pos_arg]),
+    // len = p + 1; otherwise the host's len / pos
+    int64_t pos = pos_arg, n_present = n_present_arg, score_pos = score_pos_arg;
+    if (pos_dev != nullptr) {
+        const int64_t p = *pos_dev;
+        pos = p < 0 ? 0 : (p > pos_arg ? pos_arg : p);
+        n_present = pos / bs + 1;
+        score_pos = absolute ? pos : 0;
+    }
     const int own = static_cast<int>(pos / bs);
     for (int d = tid; d < DH; d += kSelThreads) f_lds[d] = load_elem<FDT>(f, b * f_sb + g * f_sh + d);
     __syncthreads();
@@ -304,7 +326,8 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
 int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
                          int64_t H, int64_t D, int64_t nb_stride, int64_t len, int64_t pos, int64_t bs,
                          int64_t k, int routing, float scale, int32_t* sel, int32_t* n_sel, int64_t cap,
-                         hipStream_t stream) {
+                         hipStream_t stream, const int64_t* pos_dev) {
+    // with pos_dev, len bounds the device length (pos = len - 1 is the largest position)
     const int64_t n_present = cdiv(len, bs);
     const int64_t score_pos = routing == SPARDA_ROUTE_ABSOLUTE ? pos : 0;
     const bool pow2 = (bs & (bs - 1)) == 0;
@@ -312,7 +335,8 @@ int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, 
 #define SPARDA_SEL(FDT_, CH_, DH_, P2_)                                                                     \
     hipLaunchKernelGGL((select_decode_kernel<FDT_, CH_, DH_, P2_>), grid, dim3(kSelThreads), 0, stream, f,  \
                        f_sb, f_sh, sums, H, nb_stride, n_present, pos, score_pos, bs, static_cast<int>(k),  \
-                       scale, sel, n_sel, static_cast<int>(cap))
+                       scale, sel, n_sel, static_cast<int>(cap), pos_dev,                                   \
+                       routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0)
 #define SPARDA_SEL_P(FDT_, CH_, DH_)                    \
     if (pow2) SPARDA_SEL(FDT_, CH_, DH_, true);         \
     else SPARDA_SEL(FDT_, CH_, DH_, false);

@@ -52,7 +52,7 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
                int64_t M, int C, int Nq, int Nk, int Nf, float eps,
                const float* __restrict__ cosv, const float* __restrict__ sinv, int64_t T, int64_t pos0,
                uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v,
-               void* __restrict__ f) {
+               void* __restrict__ f, const int64_t* __restrict__ pos_dev, int64_t rope_len) {
     __shared__ ProduceSmem sm;
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
@@ -141,6 +141,9 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
     else { region = 3; head = (nh - Nq - Nk - Nv) / 64; }
     const int ld = region == 0 ? Nq : (region == 3 ? Nf : Nk);  // row stride of the output
     const int64_t t_first = m0 % T;                  // position of row m0 within its sequence
+    // a device-held offset (a decode step at token *pos_dev): positions clamped into the tables
+    const int64_t pos_base = pos0 + (pos_dev != nullptr ? *pos_dev : 0);
+    const int64_t pos_hi = pos_dev != nullptr ? rope_len - 1 : INT64_MAX;
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
 #pragma unroll
@@ -151,7 +154,8 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
             const float sc = sm.inv_rms[rloc];
             int64_t t = t_first + rloc;
             while (t >= T) t -= T;
-            const int64_t pos = pos0 + t;
+            int64_t pos = pos_base + t;
+            pos = pos < 0 ? 0 : (pos > pos_hi ? pos_hi : pos);
             float y[4];
 #pragma unroll
             for (int tn = 0; tn < 4; ++tn) y[tn] = acc[tm][tn][i] * sc;
@@ -180,7 +184,8 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
 
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
-                   void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream) {
+                   void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
+                   const int64_t* pos_dev, int64_t rope_len) {
     const int64_t N = Nq + 2 * Nk + Nf;
     dim3 grid(static_cast<unsigned>(cdiv(M, kPBM)), static_cast<unsigned>(N / kPBN));
 #define SPARDA_PRODUCE(FDT_)                                                                              \
@@ -188,7 +193,7 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                        static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w), M,        \
                        static_cast<int>(C), static_cast<int>(Nq), static_cast<int>(Nk),                   \
                        static_cast<int>(Nf), eps, cosv, sinv, T, pos0, static_cast<uint16_t*>(q),         \
-                       static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), f)
+                       static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), f, pos_dev, rope_len)
     if (f_dtype == SPARDA_F32) SPARDA_PRODUCE(SPARDA_F32);
     else SPARDA_PRODUCE(SPARDA_BF16);
 #undef SPARDA_PRODUCE

@@ -376,7 +376,7 @@ def teacher_block_mass(q: torch.Tensor, k: torch.Tensor, block_size: int = 64, c
 
 def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: int, eps: float,
             rope_cos: torch.Tensor, rope_sin: torch.Tensor, pos0: int = 0,
-            f_dtype: torch.dtype = torch.bfloat16):
+            f_dtype: torch.dtype = torch.bfloat16, pos_dev: Optional[torch.Tensor] = None):
     """RMSNorm + q / k / v / forecast projections + RoPE in one kernel
     (model/transformer.py:104-107; model/norm.py:15-21; model/forecast.py:30-40;
     model/attention/base.py:38-52; model/rope.py:34-65).
@@ -384,8 +384,12 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
     x [B,T,C] bf16; w_stacked [n_q + 2*n_kv + n_f, C] bf16 = [wq; wk; wv; wf]
     with the RMSNorm weight folded into its columns; rope tables [L, 32] fp32.
     Returns q [B,T,n_q/64,64], k, v [B,T,n_kv/64,64] (bf16, q and k rotated at
-    positions pos0..pos0+T-1) and f [B,T,n_f/64,64] of f_dtype."""
-    dev = require_device(x, w_stacked, rope_cos, rope_sin)
+    positions pos0..pos0+T-1) and f [B,T,n_f/64,64] of f_dtype.
+
+    pos_dev: a one-element int64 device tensor holding the first position,
+    read when the kernel runs (pos0 must then be 0; positions are clamped into
+    the tables), for launches recorded once and replayed every decode step."""
+    dev = require_device(x, w_stacked, rope_cos, rope_sin, pos_dev)
     _inference_only(x, w_stacked)
     if x.dtype != torch.bfloat16 or w_stacked.dtype != torch.bfloat16:
         raise TypeError("sparda: produce takes bf16 activations and weights")
@@ -404,10 +408,112 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
     k = torch.empty((B, T, n_kv // 64, 64), dtype=torch.bfloat16, device=dev)
     v = torch.empty_like(k)
     f = torch.empty((B, T, n_f // 64, 64), dtype=f_dtype, device=dev)
+    if pos_dev is not None:
+        if pos0 != 0:
+            raise ValueError("sparda: produce takes pos0 or pos_dev, not both")
+        call("sparda_produce_at", x2.data_ptr(), x2.stride(0), w_stacked.data_ptr(), B * T, C, n_q, n_kv, n_f,
+             float(eps), rope_cos.data_ptr(), rope_sin.data_ptr(), rope_cos.shape[0], T, _pos_ptr(pos_dev),
+             q.data_ptr(), k.data_ptr(), v.data_ptr(), f.data_ptr(), _DT[f_dtype], _stream(dev))
+        return q, k, v, f
     call("sparda_produce", x2.data_ptr(), x2.stride(0), w_stacked.data_ptr(), B * T, C, n_q, n_kv, n_f,
          float(eps), rope_cos.data_ptr(), rope_sin.data_ptr(), rope_cos.shape[0], T, pos0,
          q.data_ptr(), k.data_ptr(), v.data_ptr(), f.data_ptr(), _DT[f_dtype], _stream(dev))
     return q, k, v, f
+
+
+def _pos_ptr(pos_dev: torch.Tensor) -> int:
+    """Address of a device-held position: one int64 element on the GPU."""
+    if pos_dev.dtype != torch.int64 or pos_dev.numel() != 1 or not pos_dev.is_cuda:
+        raise TypeError("sparda: pos_dev must be a one-element int64 tensor on the GPU")
+    return pos_dev.data_ptr()
+
+
+def block_sums_at(k: torch.Tensor, pos_dev: torch.Tensor, block_size: int, sums: torch.Tensor) -> torch.Tensor:
+    """block_sums of the block holding token p = pos_dev (a one-element int64
+    device tensor, read when the kernel runs): tokens [p - p % bs, p] of the
+    cache k [B,S,Hkv,D], summed from zero into sums (in place; returned)."""
+    dev = require_device(k, sums, pos_dev)
+    _inference_only(k)
+    if sums.dtype != torch.float32 or not sums.is_contiguous():
+        raise TypeError("sparda: block sums must be contiguous float32")
+    if k.stride(-1) != 1:
+        raise ValueError("sparda: the cache's last dimension must be contiguous")
+    B, S, Hkv, D = k.shape
+    if tuple(sums.shape[:1]) != (B,) or tuple(sums.shape[2:]) != (Hkv, D):
+        raise AssertionError(f"Mismatch: cache {tuple(k.shape)} vs block sums {tuple(sums.shape)}")
+    max_len = min(S, sums.shape[1] * block_size)
+    sb, st, sh, _ = k.stride()
+    call("sparda_block_sums_at", k.data_ptr(), _dtype_code(k), sb, st, sh, B, Hkv, D, max_len, _pos_ptr(pos_dev),
+         block_size, sums.shape[1], sums.data_ptr(), _stream(dev))
+    return sums
+
+
+def select_decode_at(forecast: torch.Tensor, block_sums: torch.Tensor, pos_dev: torch.Tensor, max_len: int,
+                     block_size: int, top_k: int, routing: str = "reference", scale: Optional[float] = None,
+                     sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None):
+    """select_decode for the decode step at token p = pos_dev (a one-element
+    int64 device tensor, read when the kernel runs): length p + 1, query
+    position p; p is clamped below max_len."""
+    dev = require_device(forecast, block_sums, pos_dev, sel, n_sel)
+    if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
+        raise TypeError("sparda: block_sums must be contiguous float32")
+    B, nbs, Hkv, D = block_sums.shape
+    forecast = _rowmajor(forecast.reshape(B, Hkv, -1) if forecast.dim() != 3 else forecast)
+    if routing not in ("reference", "absolute"):
+        raise ValueError(f"sparda: routing must be 'reference' or 'absolute', got {routing!r}")
+    if scale is None:
+        scale = default_scale(forecast.shape[-1])
+    if sel is None:
+        sel = torch.empty((B, Hkv, top_k + 2), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, Hkv), dtype=torch.int32, device=dev)
+    fsb, fsh, _ = forecast.stride()
+    call("sparda_select_decode_at", forecast.data_ptr(), _dtype_code(forecast), fsb, fsh, block_sums.data_ptr(),
+         B, Hkv, D, nbs, max_len, _pos_ptr(pos_dev), block_size, top_k,
+         _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE, float(scale),
+         sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], _stream(dev))
+    return sel, n_sel
+
+
+def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.Tensor, block_size: int,
+              sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None, window: int = 0,
+              max_len: Optional[int] = None, scale: Optional[float] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode attention of q [B,Hq,D] at token p = pos_dev (a one-element int64
+    device tensor, read when the kernel runs) over the caches [B,Smax,Hkv,D]
+    holding p + 1 tokens: the blocks sel[b,g,:n_sel], or with sel None the
+    static window of `window` blocks (+ sink; every block while the cache has
+    at most window + 2), or every block (window 0). p is clamped below max_len
+    (default: the cache capacity)."""
+    dev = require_device(q, k, v, pos_dev, sel, n_sel)
+    _inference_only(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q, k and v must share a dtype")
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    if k.stride() != v.stride():
+        raise ValueError("sparda: k and v must share strides")
+    B, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if max_len is None:
+        max_len = k.shape[1]
+    if not 0 < max_len <= k.shape[1]:
+        raise ValueError(f"sparda: max_len={max_len} outside the cache (capacity {k.shape[1]})")
+    cap = 0
+    if sel is not None:
+        if sel.dtype != torch.int32 or n_sel is None or n_sel.dtype != torch.int32:
+            raise TypeError("sparda: sel / n_sel must be int32 tensors")
+        sel, n_sel = sel.contiguous(), n_sel.contiguous()
+        cap = sel.shape[-1]
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
+    kv_sb, kv_ss, kv_sh, _ = k.stride()
+    qsb, qsh, _ = q.stride()
+    call("sparda_decode_at", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
+         _dtype_code(q), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap, int(window), B, max_len, _pos_ptr(pos_dev),
+         Hq, Hkv, D, block_size, float(scale), out.data_ptr(), out.stride(0), _stream(dev))
+    return out
 
 
 def block_sums(k: torch.Tensor, pos: int, n: int, block_size: int, sums: torch.Tensor) -> torch.Tensor:

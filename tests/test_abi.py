@@ -114,3 +114,35 @@ def test_offload_and_selected_decode_argument_errors():
     _expect(-2, "sparda_block_sums", P, 1, 256, 256, 64, 1, 4, 64, 0, 0, 64, 4, P, None)  # n = 0
     _expect(-8, "sparda_block_sums", P, 1, 256, 256, 64, 1, 4, 64, 200, 100, 64, 4, P, None)  # block 4 of 4
     _expect(-5, "sparda_block_sums", P, 1, -1, 256, 64, 1, 4, 64, 0, 64, 64, 4, P, None)
+
+
+def test_device_position_entry_argument_errors():
+    P = 4096
+    Q = 4104  # 8-byte aligned position pointer; Q + 4 is not
+    # produce_at: x, x_stride, w, M, C, Nq, Nk, Nf, eps, cos, sin, rope_len, T, pos_dev, q, k, v, f, f_dtype, stream
+    _expect(-1, "sparda_produce_at", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 1, None, P, P, P, P, 1, None)
+    _expect(-5, "sparda_produce_at", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 1, Q + 4, P, P, P, P, 1,
+            None)
+    _expect(-2, "sparda_produce_at", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 3, Q, P, P, P, P, 1,
+            None)  # M not a multiple of T
+    # block_sums_at: k, dtype, sb, st, sh, B, Hkv, D, max_len, pos_dev, bs, nb_stride, sums, stream
+    _expect(-1, "sparda_block_sums_at", P, 1, 256, 256, 64, 1, 4, 64, 256, None, 64, 4, P, None)
+    _expect(-8, "sparda_block_sums_at", P, 1, 256, 256, 64, 1, 4, 64, 257, Q, 64, 4, P, None)  # 5 blocks > 4
+    _expect(-2, "sparda_block_sums_at", P, 1, 256, 256, 64, 1, 4, 64, 0, Q, 64, 4, P, None)   # max_len 0
+    # select_decode_at: f, f_dtype, f_sb, f_sh, sums, B, Hkv, D, nb_stride, max_len, pos_dev, bs, k, routing,
+    #                   scale, sel, n_sel, sel_cap, stream
+    _expect(-1, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, None, 64, 8, 1, 0.125, P, P, 10, None)
+    _expect(-2, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 1, 100, Q, 64, 8, 1, 0.125, P, P, 10,
+            None)  # nb_stride < ceil(max_len / bs)
+    _expect(-2, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, Q, 64, 8, 1, 0.125, P, P, 9,
+            None)  # sel_cap < k + 2
+    # decode_at: q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, sel, n_sel, sel_cap, window_k, B, max_len,
+    #            pos_dev, Hq, Hkv, D, bs, scale, out, out_sb, stream
+    _expect(-1, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, None, None, 0, 8, 1, 100, None, 12, 4, 64, 64,
+            0.125, P, 1, None)
+    _expect(-6, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, P, P, 10, 8, 1, 100, Q, 12, 4, 64, 64, 0.125, P,
+            1, None)  # a list and a window
+    _expect(-2, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, None, None, 0, 33, 1, 100, Q, 12, 4, 64, 64,
+            0.125, P, 1, None)  # window > 32
+    _expect(-5, "sparda_decode_at", P, 1, 1, P + 2, P, 8, 8, 8, 1, None, None, 0, 8, 1, 100, Q, 12, 4, 64, 64,
+            0.125, P, 1, None)  # misaligned K

@@ -1,0 +1,177 @@
+"""GPU parity of the decode steps at a device-held position and of the
+generation loop replayed from one captured HIP graph.
+
+Entries that read the position from device memory are compared bit for bit
+with their host-length counterparts (same kernels, same launch shapes); the
+window mode's every-block fallback on a short cache with the dense decode
+within max-abs 2e-2 / mean-abs 2e-3 (bf16) or 1e-4 (fp32). The replayed
+generation loop is compared with the eager cached-prototype decode of the same
+model: logits of every step bit for bit, sampled tokens identical.
+"""
+
+import pytest
+import torch
+
+import sparda
+from model.attention import PrototypeKVCache
+from model.config import ModelConfig
+from model.decode_graph import GraphDecoder
+from model.model import SparDAResearchModel
+from helpers import assert_close_out, np32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _pos(p):
+    return torch.full((1,), p, dtype=torch.int64, device=DEV)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+def test_device_position_ops_equal_host_length_ops(dtype, routing):
+    case(f"device-position ops {dtype} {routing}")
+    B, Smax, Hq, Hkv, D, bs, k = 2, 2048, 12, 4, 64, 64, 8
+    g = torch.Generator().manual_seed(11)
+    kc = torch.randn(B, Smax, Hkv, D, generator=g).to(dtype).to(DEV)
+    vc = torch.randn(B, Smax, Hkv, D, generator=g).to(dtype).to(DEV)
+    q = torch.randn(B, Hq, D, generator=g).to(dtype).to(DEV)
+    f = torch.randn(B, Hkv, 64, generator=g).to(DEV)
+    nb = Smax // bs
+    sums = torch.zeros((B, nb, Hkv, D), device=DEV)
+    sparda.block_sums(kc, 0, Smax, bs, sums)
+    for p in (0, 63, 64, 639, 640, 641, 700, 1535, 2047):
+        case(f"  position {p}")
+        pos = _pos(p)
+        j = p // bs
+        # current-block sums: [j*bs, p], the other blocks untouched
+        got = torch.full_like(sums, float("nan"))
+        sparda.block_sums_at(kc, pos, bs, got)
+        want = torch.full_like(sums, float("nan"))
+        sparda.block_sums(kc, j * bs, p - j * bs + 1, bs, want)
+        assert torch.equal(got[:, j], want[:, j])
+        assert torch.isnan(got[:, :j]).all() and torch.isnan(got[:, j + 1:]).all()
+        # selection from the sums
+        s_d, n_d = sparda.select_decode_at(f, sums, pos, Smax, bs, k, routing=routing)
+        s_h, n_h = sparda.select_decode(f, sums, p + 1, p, bs, k, routing=routing)
+        assert torch.equal(n_d, n_h) and torch.equal(s_d, s_h)
+        # attention over the selection
+        o_d = sparda.decode_at(q, kc, vc, pos, bs, s_d, n_d)
+        o_h = sparda.decode_selected(q, kc, vc, p + 1, bs, s_h, n_h)
+        assert torch.equal(o_d, o_h)
+        # static window (no forecast): the fused decode's window mode
+        o_w = sparda.decode_at(q, kc, vc, pos, bs, window=k)
+        o_r = sparda.decode(q, kc, vc, p + 1, None, bs, k)
+        if j + 1 > k + 2:
+            assert torch.equal(o_w, o_r)
+        else:  # every block: the fused decode's dense mode (its own wavefront split)
+            assert_close_out(np32(o_w), np32(o_r), dtype, what=f"window fallback p={p}")
+        # every block
+        o_a = sparda.decode_at(q, kc, vc, pos, bs, window=0)
+        o_b = sparda.decode_selected(q, kc, vc, p + 1, bs)
+        assert_close_out(np32(o_a), np32(o_b), dtype, what=f"dense p={p}")
+    torch.cuda.synchronize()
+
+
+def test_device_positions_are_clamped_into_range():
+    case("device-position clamping")
+    B, Smax, Hq, Hkv, D, bs, k = 1, 1000, 12, 4, 64, 64, 8
+    g = torch.Generator().manual_seed(12)
+    kc = torch.randn(B, Smax, Hkv, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, Smax, Hkv, D, generator=g).to(torch.bfloat16).to(DEV)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    f = torch.randn(B, Hkv, 64, generator=g).to(DEV)
+    sums = torch.zeros((B, (Smax + bs - 1) // bs, Hkv, D), device=DEV)
+    sparda.block_sums(kc, 0, Smax, bs, sums)
+    hi, lo = _pos(Smax + 500), _pos(-7)
+    last, first = _pos(Smax - 1), _pos(0)
+    for a, b in ((hi, last), (lo, first)):
+        sa, na = sparda.select_decode_at(f, sums, a, Smax, bs, k)
+        sb_, nb_ = sparda.select_decode_at(f, sums, b, Smax, bs, k)
+        assert torch.equal(sa, sb_) and torch.equal(na, nb_)
+        assert torch.equal(sparda.decode_at(q, kc, vc, a, bs, sa, na), sparda.decode_at(q, kc, vc, b, bs, sb_, nb_))
+        assert torch.equal(sparda.decode_at(q, kc, vc, a, bs, window=k), sparda.decode_at(q, kc, vc, b, bs, window=k))
+        x = torch.full_like(sums, 3.0)
+        y = torch.full_like(sums, 3.0)
+        sparda.block_sums_at(kc, a, bs, x)
+        sparda.block_sums_at(kc, b, bs, y)
+        assert torch.equal(x, y)
+
+
+def test_produce_at_device_position_equals_host_position():
+    case("produce at a device position")
+    torch.manual_seed(13)
+    B, C, nq, nkv, nf = 3, 768, 768, 256, 256
+    x = (torch.randn(B, 1, C) * 0.5).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(nq + 2 * nkv + nf, C) * 0.02).to(torch.bfloat16).to(DEV)
+    from model.rope import rope_tables
+    cos, sin = rope_tables(64, 2048, 10000.0)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    for p in (0, 1, 777, 2047):
+        want = sparda.produce(x, w, nq, nkv, nf, 1e-5, cos, sin, pos0=p)
+        got = sparda.produce(x, w, nq, nkv, nf, 1e-5, cos, sin, pos_dev=_pos(p))
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
+    # positions past the tables are clamped to the last row
+    want = sparda.produce(x, w, nq, nkv, nf, 1e-5, cos, sin, pos0=2047)
+    got = sparda.produce(x, w, nq, nkv, nf, 1e-5, cos, sin, pos_dev=_pos(5000))
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+
+
+def _model(mode, routing, n_layer=3, ctx=2048):
+    backend = {"forecast": "hip_sparse", "static": "static_sparse", "dense": "dense"}[mode]
+    cfg = ModelConfig(n_layer=n_layer, context_length=ctx, block_size=64, top_k_blocks=8, decode_routing=routing,
+                      attention_backend=backend, fused_producer=True, norm_eps=1e-5)
+    torch.manual_seed(21)
+    return SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval(), cfg
+
+
+@pytest.mark.parametrize("mode,routing", [("forecast", "reference"), ("forecast", "absolute"),
+                                          ("static", "reference")])
+def test_graph_replayed_steps_equal_eager_cached_decode(mode, routing):
+    case(f"graph-replayed decode steps, {mode} {routing}")
+    model, cfg = _model(mode, routing)
+    B, T0, n, cap = 2, 900, 100, 1100  # 15 blocks at the start, crossing 960 and 1024
+    g = torch.Generator().manual_seed(22)
+    ids = torch.randint(0, cfg.vocab_size, (B, T0 + n), generator=g).to(DEV)
+    caches = [PrototypeKVCache(B, cap, cfg.n_kv_head, cfg.head_dim, DEV, torch.bfloat16, block_size=64)
+              for _ in range(cfg.n_layer)]
+    gd = GraphDecoder(model, B, cap)
+    with torch.no_grad():
+        want = [model(ids[:, :T0], kv_caches=caches)["logits"][:, -1]]
+        for t in range(T0, T0 + n):
+            want.append(model(ids[:, t:t + 1], kv_caches=caches)["logits"][:, -1])
+        got = [gd.prefill(ids[:, :T0])]
+        for t in range(T0, T0 + n):
+            got.append(gd.step(ids[:, t:t + 1]).clone())
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), f"step {i}: max diff {(a.float() - b.float()).abs().max().item()}"
+    for c, e in zip(gd.caches, caches):
+        assert c.current_len == e.current_len == T0 + n
+        assert torch.equal(c.k[:, :T0 + n], e.k[:, :T0 + n]) and torch.equal(c.v[:, :T0 + n], e.v[:, :T0 + n])
+        assert torch.equal(c.block_sums, e.block_sums)
+
+
+def test_graph_generation_equals_eager_generation_and_replays_after_reset():
+    case("graph generation vs eager generation")
+    model, cfg = _model("forecast", "absolute")
+    B, T0, n, cap = 2, 700, 80, 1024
+    g = torch.Generator().manual_seed(23)
+    prompt = torch.randint(0, cfg.vocab_size, (B, T0), generator=g).to(DEV)
+    gd = GraphDecoder(model, B, cap)
+    for temperature in (0.0, 0.8):
+        caches = [PrototypeKVCache(B, cap, cfg.n_kv_head, cfg.head_dim, DEV, torch.bfloat16, block_size=64)
+                  for _ in range(cfg.n_layer)]
+        torch.manual_seed(5)
+        want = model.generate(prompt, max_new_tokens=n, temperature=temperature, top_k=50, kv_caches=caches)
+        torch.manual_seed(5)
+        got = gd.generate(prompt, max_new_tokens=n, temperature=temperature, top_k=50)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"temperature {temperature}"
+    assert gd.graph is not None  # the second generation replayed the step recorded by the first

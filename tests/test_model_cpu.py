@@ -45,3 +45,12 @@ def test_hip_path_refuses_cpu_tensors():
     model = SparDAResearchModel(ModelConfig(n_layer=1, context_length=64)).eval()
     with torch.no_grad(), pytest.raises(RuntimeError, match="GPU"):
         model(torch.randint(0, 32000, (1, 16)))
+
+
+def test_graph_decoder_refuses_cpu_models_and_unsupported_backends():
+    from model.decode_graph import GraphDecoder
+    cfg = ModelConfig(n_layer=2, context_length=1024)
+    with pytest.raises(TypeError):
+        GraphDecoder(SparDAResearchModel(cfg).to(torch.bfloat16), 1, 512)  # CPU weights: no fallback
+    with pytest.raises(TypeError):
+        GraphDecoder(SparDAResearchModel(cfg), 1, 512)  # fp32
