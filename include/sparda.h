@@ -365,9 +365,12 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
  * never reads out of bounds, but its results are those of the clamped one.
  *
  * sparda_produce_at: sparda_produce with positions *pos_dev + t.
- * sparda_block_sums_at: recomputes, per sequence, the block holding token p
- *   over [p - p % bs, p] (k: the cache base, token 0), as
- *   sparda_block_sums(k, ..., pos = p - p % bs, n = p % bs + 1) does.
+ * sparda_append_at: per sequence, writes k_new / v_new ([B,Hkv,D], strides
+ *   (new_sb, new_sh, 1)) as row p of the caches [B,Smax,Hkv,D] (strides
+ *   (sb, st, sh, 1); KVCache.update, model/attention/base.py:19-29) and
+ *   recomputes the fp32 sums of the block holding p over [p - p % bs, p], as
+ *   sparda_block_sums(k, ..., pos = p - p % bs, n = p % bs + 1) does. With
+ *   k_new / v_new NULL only the sums are recomputed (v_cache may be NULL).
  * sparda_select_decode_at: sparda_select_decode with len = p + 1, pos = p.
  * sparda_decode_at: sparda_decode_selected with S = p + 1 over the caller's
  *   list (sel / n_sel), or, with sel NULL and window_k > 0, the static window
@@ -379,9 +382,10 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
                                  int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
                                  const float* rope_sin, int64_t rope_len, int64_t T, const int64_t* pos_dev,
                                  void* q, void* k, void* v, void* f, int f_dtype, void* stream);
-SPARDA_API int sparda_block_sums_at(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,
-                                    int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
-                                    int64_t block_size, int64_t nb_stride, float* block_sums, void* stream);
+SPARDA_API int sparda_append_at(void* k_cache, void* v_cache, int dtype, int64_t sb, int64_t st, int64_t sh,
+                                const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
+                                int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
+                                int64_t block_size, int64_t nb_stride, float* block_sums, void* stream);
 SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
                                        const float* block_sums, int64_t B, int64_t Hkv, int64_t D,
                                        int64_t nb_stride, int64_t max_len, const int64_t* pos_dev,

@@ -429,22 +429,26 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
                         k, v, f, f_dtype, stream);
 }
 
-SPARDA_API int sparda_block_sums_at(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,
-                                    int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
-                                    int64_t block_size, int64_t nb_stride, float* block_sums, void* stream) {
-    SPARDA_REQUIRE(k && block_sums && pos_dev, SPARDA_ERR_NULL, "block_sums_at: null k/block_sums/pos_dev");
+SPARDA_API int sparda_append_at(void* k_cache, void* v_cache, int dtype, int64_t sb, int64_t st, int64_t sh,
+                                const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
+                                int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
+                                int64_t block_size, int64_t nb_stride, float* block_sums, void* stream) {
+    SPARDA_REQUIRE(k_cache && block_sums && pos_dev, SPARDA_ERR_NULL, "append_at: null k_cache/block_sums/pos_dev");
+    SPARDA_REQUIRE(!k_new == !v_new, SPARDA_ERR_NULL, "append_at: k_new and v_new go together");
+    SPARDA_REQUIRE(!k_new || v_cache, SPARDA_ERR_NULL, "append_at: appending needs v_cache");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
-                   "block_sums_at: pos_dev must be 8-byte aligned");
-    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "block_sums_at: dtype %d unsupported", dtype);
+                   "append_at: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "append_at: dtype %d unsupported", dtype);
     SPARDA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && block_size > 0 && nb_stride > 0 && max_len >= 1, SPARDA_ERR_SHAPE,
-                   "block_sums_at: sizes must be positive");
+                   "append_at: sizes must be positive");
     SPARDA_REQUIRE((max_len - 1) / block_size < nb_stride, SPARDA_ERR_CAPACITY,
-                   "block_sums_at: max_len %lld needs more than nb_stride %lld blocks", (long long)max_len,
+                   "append_at: max_len %lld needs more than nb_stride %lld blocks", (long long)max_len,
                    (long long)nb_stride);
-    SPARDA_REQUIRE(sb >= 0 && st >= 0 && sh >= 0, SPARDA_ERR_STRIDE, "block_sums_at: negative stride");
-    SPARDA_REQUIRE(B <= 65535, SPARDA_ERR_SHAPE, "block_sums_at: too large");
-    return launch_block_sums(k, dtype, sb, st, sh, 0, max_len, B, Hkv, D, block_size, nb_stride, block_sums,
-                             static_cast<hipStream_t>(stream), pos_dev);
+    SPARDA_REQUIRE(sb >= 0 && st >= 0 && sh >= 0 && new_sb >= 0 && new_sh >= 0, SPARDA_ERR_STRIDE,
+                   "append_at: negative stride");
+    SPARDA_REQUIRE(B <= 65535, SPARDA_ERR_SHAPE, "append_at: too large");
+    return launch_append_at(k_cache, v_cache, dtype, sb, st, sh, k_new, v_new, new_sb, new_sh, B, Hkv, D, block_size,
+                            max_len, nb_stride, pos_dev, block_sums, static_cast<hipStream_t>(stream));
 }
 
 SPARDA_API int sparda_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t B,

@@ -81,11 +81,15 @@ int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb,
                    int64_t pos, int64_t n, int64_t bs, float* sums, hipStream_t stream);
 int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sums, hipStream_t stream);
 
-// fp32 block sums of tokens pos..pos+n-1; k points at token pos (strides sb, st, sh).
-// With pos_dev: the block holding token *pos_dev (< n), k pointing at token 0.
+// fp32 block sums of tokens pos..pos+n-1; k points at token pos (strides sb, st, sh)
 int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
                       int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
-                      float* sums, hipStream_t stream, const int64_t* pos_dev = nullptr);
+                      float* sums, hipStream_t stream);
+// decode-step append of k_new / v_new (optional) at row *pos_dev of the caches
+// and the fp32 sums of the block holding it
+int launch_append_at(void* kc, void* vc, int dtype, int64_t sb, int64_t st, int64_t sh, const void* k_new,
+                     const void* v_new, int64_t n_sb, int64_t n_sh, int64_t B, int64_t H, int64_t D, int64_t bs,
+                     int64_t max_len, int64_t nb_stride, const int64_t* pos_dev, float* sums, hipStream_t stream);
 int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t bs,
                   int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream);
 

@@ -140,23 +140,11 @@ arena_store_kernel(const char* __restrict__ k, const char* __restrict__ v, int64
 // (b, block j, g, d) continue the sequential sum from the block start
 // (restart at 0 when pos is at or before the block start).
 // k: [B,n,H,D] strides (sb, st, sh) holding tokens pos..pos+n-1.
-// With pos_dev (one workgroup per sequence): the block holding token
-// p = *pos_dev (clamped into [0, n)) is recomputed over [p - p % bs, p], and k
-// points at token 0.
 template <int DT>
 __global__ void __launch_bounds__(256)
-block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh, int64_t pos_arg, int64_t n_arg,
-                  int64_t H, int64_t D, int64_t bs, int64_t nb_stride, float* __restrict__ sums,
-                  const int64_t* __restrict__ pos_dev) {
+block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh, int64_t pos, int64_t n,
+                  int64_t H, int64_t D, int64_t bs, int64_t nb_stride, float* __restrict__ sums) {
     constexpr int U = 32;  // token loads in flight per thread, added in token order
-    int64_t pos = pos_arg, n = n_arg, k_tok = pos_arg;  // k_tok: the token k points at
-    if (pos_dev != nullptr) {
-        int64_t p = *pos_dev;
-        p = p < 0 ? 0 : (p >= n_arg ? n_arg - 1 : p);
-        pos = p - p % bs;
-        n = p - pos + 1;
-        k_tok = 0;
-    }
     const int64_t j = pos / bs + blockIdx.x;
     const int64_t b = blockIdx.y;
     const int64_t s_lo = j * bs > pos ? j * bs : pos;
@@ -170,30 +158,88 @@ block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh
         for (; s + U <= s_hi; s += U) {
             float x[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + (s + u - k_tok) * st);
+            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + (s + u - pos) * st);
 #pragma unroll
             for (int u = 0; u < U; ++u) acc = acc + x[u];
         }
-        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(k, base + (s - k_tok) * st);
+        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(k, base + (s - pos) * st);
         *out = acc;
     }
 }
 
 int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t sh, int64_t pos,
                       int64_t n, int64_t B, int64_t H, int64_t D, int64_t bs, int64_t nb_stride,
-                      float* sums, hipStream_t stream, const int64_t* pos_dev) {
-    // with pos_dev: one block per sequence, n bounds the device position
-    const int64_t nblk = pos_dev != nullptr ? 1 : (pos + n - 1) / bs - pos / bs + 1;
+                      float* sums, hipStream_t stream) {
+    const int64_t nblk = (pos + n - 1) / bs - pos / bs + 1;
     dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(B));
     int threads = static_cast<int>(H * D < 256 ? H * D : 256);
     threads = ((threads + kWave - 1) / kWave) * kWave;
     if (dtype == SPARDA_BF16)
         hipLaunchKernelGGL(block_sums_kernel<SPARDA_BF16>, grid, dim3(threads), 0, stream, k, sb, st, sh, pos, n,
-                           H, D, bs, nb_stride, sums, pos_dev);
+                           H, D, bs, nb_stride, sums);
     else
         hipLaunchKernelGGL(block_sums_kernel<SPARDA_F32>, grid, dim3(threads), 0, stream, k, sb, st, sh, pos, n,
-                           H, D, bs, nb_stride, sums, pos_dev);
+                           H, D, bs, nb_stride, sums);
     return check_hip(hipGetLastError(), "block_sums_kernel");
+}
+
+// Decode-step append at a device-held position p = *pos_dev (clamped into
+// [0, max_len)), one workgroup per sequence: with k_new, the token's K and V
+// rows are written into the caches at row p; the fp32 sums of the block
+// holding p are recomputed over [p - p % bs, p] in token order (the sums
+// block_sums_kernel gives), row p taken from k_new, so that no thread reads a
+// row another thread writes.
+template <int DT>
+__global__ void __launch_bounds__(256)
+append_at_kernel(void* __restrict__ kc, void* __restrict__ vc, int64_t sb, int64_t st, int64_t sh,
+                 const void* __restrict__ k_new, const void* __restrict__ v_new, int64_t n_sb, int64_t n_sh,
+                 int64_t H, int64_t D, int64_t bs, int64_t max_len, int64_t nb_stride,
+                 const int64_t* __restrict__ pos_dev, float* __restrict__ sums) {
+    using E = typename std::conditional<DT == SPARDA_BF16, uint16_t, float>::type;
+    constexpr int U = 32;
+    const int64_t b = blockIdx.x;
+    int64_t p = *pos_dev;
+    p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
+    const int64_t j = p / bs;
+    const int64_t s_hi = k_new != nullptr ? p : p + 1;  // rows read from the cache
+    E* kce = static_cast<E*>(kc);
+    for (int64_t e = threadIdx.x; e < H * D; e += blockDim.x) {
+        const int64_t g = e / D, d = e % D;
+        const int64_t base = b * sb + g * sh + d;
+        float acc = 0.0f;
+        int64_t s = j * bs;
+        for (; s + U <= s_hi; s += U) {
+            float x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(kc, base + (s + u) * st);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc = acc + x[u];
+        }
+        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(kc, base + s * st);
+        if (k_new != nullptr) {
+            const int64_t ni = b * n_sb + g * n_sh + d;
+            const E kv = static_cast<const E*>(k_new)[ni];
+            kce[base + p * st] = kv;
+            static_cast<E*>(vc)[base + p * st] = static_cast<const E*>(v_new)[ni];
+            acc = acc + load_elem<DT>(k_new, ni);
+        }
+        sums[((b * nb_stride + j) * H + g) * D + d] = acc;
+    }
+}
+
+int launch_append_at(void* kc, void* vc, int dtype, int64_t sb, int64_t st, int64_t sh, const void* k_new,
+                     const void* v_new, int64_t n_sb, int64_t n_sh, int64_t B, int64_t H, int64_t D, int64_t bs,
+                     int64_t max_len, int64_t nb_stride, const int64_t* pos_dev, float* sums, hipStream_t stream) {
+    int threads = static_cast<int>(H * D < 256 ? H * D : 256);
+    threads = ((threads + kWave - 1) / kWave) * kWave;
+    dim3 grid(static_cast<unsigned>(B));
+    if (dtype == SPARDA_BF16)
+        hipLaunchKernelGGL(append_at_kernel<SPARDA_BF16>, grid, dim3(threads), 0, stream, kc, vc, sb, st, sh, k_new,
+                           v_new, n_sb, n_sh, H, D, bs, max_len, nb_stride, pos_dev, sums);
+    else
+        hipLaunchKernelGGL(append_at_kernel<SPARDA_F32>, grid, dim3(threads), 0, stream, kc, vc, sb, st, sh, k_new,
+                           v_new, n_sb, n_sh, H, D, bs, max_len, nb_stride, pos_dev, sums);
+    return check_hip(hipGetLastError(), "append_at_kernel");
 }
 
 int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb, int64_t st, int64_t sh,
@@ -239,6 +285,19 @@ int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sum
 // ---------------------------------------------------------------------------
 constexpr int kSelThreads = 256;
 constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
+
+// wave_select over the first n keys of key_lds, CH keys per lane
+template <int CH>
+__device__ __forceinline__ int select_keys(const uint32_t* key_lds, int n, int k, int own, int32_t* sel_lds,
+                                           int lane) {
+    uint32_t kreg[CH];
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+        const int j = e * kWave + lane;
+        kreg[e] = j < n ? key_lds[j] : 0u;
+    }
+    return wave_select<CH>(kreg, n, k, own, sel_lds);
+}
 
 template <int FDT, int CH, int DH, bool POW2>
 __global__ void __launch_bounds__(kSelThreads)
@@ -303,13 +362,12 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
             m = own + 1;
             if (lane < m) sel_lds[lane] = lane;
         } else {
-            uint32_t kreg[CH];
-#pragma unroll
-            for (int e = 0; e < CH; ++e) {
-                const int64_t j = static_cast<int64_t>(e) * kWave + lane;
-                kreg[e] = j < n_present ? key_lds[j] : 0u;
-            }
-            m = wave_select<CH>(kreg, static_cast<int>(n_present), k, own, sel_lds);
+            // the smallest key-register count holding n_present keys (a device-held
+            // length may be far below the bound CH was chosen for)
+            const int n = static_cast<int>(n_present);
+            if (CH >= 64 && n > 1024) m = select_keys<(CH >= 64 ? 64 : CH)>(key_lds, n, k, own, sel_lds, lane);
+            else if (CH >= 16 && n > 256) m = select_keys<(CH >= 16 ? 16 : CH)>(key_lds, n, k, own, sel_lds, lane);
+            else m = select_keys<4>(key_lds, n, k, own, sel_lds, lane);
             if (own >= n_present) {  // the own block holds no token yet: it has no score but is attended
                 if (lane == 0) sel_lds[m] = own;
                 m += 1;

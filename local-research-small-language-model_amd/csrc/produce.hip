@@ -182,11 +182,124 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode shapes (M <= kRowsMax rows, a few tokens): the tiled kernel would run
+// N/128 workgroups and stream all of W' through a dozen CUs. Here a workgroup
+// owns 16 columns of one head (8 RoPE pairs: d0+p and d0+p+32, p < 8), so
+// N/16 workgroups share the weight read; a 16-lane group per column holds the
+// column's row of W' in registers (C/128 16-byte chunks per lane) and takes
+// the dot product with every x row, reduced across the group. The same lanes
+// see all of x's row, so each group also forms sum(x^2) for 1/rms. Results go
+// through LDS to the threads that rotate and store the pairs.
+// ---------------------------------------------------------------------------
+constexpr int kRowsMax = 16;        // rows handled by the decode kernel
+constexpr int kRowsChunks = 16;     // C / 128 <= 16 (C <= 2048)
+
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __shfl_xor(v, 8, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 1, 16);
+    return v;
+}
+
+template <int FDT>
+__global__ void __launch_bounds__(kPThreads)
+produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __restrict__ w, int M, int C,
+                    int Nq, int Nk, int Nf, float eps, const float* __restrict__ cosv,
+                    const float* __restrict__ sinv, int64_t T, int64_t pos0, uint16_t* __restrict__ q,
+                    uint16_t* __restrict__ k, uint16_t* __restrict__ v, void* __restrict__ f,
+                    const int64_t* __restrict__ pos_dev, int64_t rope_len) {
+    __shared__ float ylds[kRowsMax][16];
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    const int li = lane % 16;
+    const int lc = 4 * wave + lane / 16;             // local column: pair lc/2, half lc%2
+    const int nh = (blockIdx.x / 4) * 64;            // first column of the head
+    const int d0 = (blockIdx.x % 4) * 8;
+    const int n = nh + d0 + lc / 2 + 32 * (lc % 2);  // row of W'
+    const int nch = C / 128;
+    uint4 wreg[kRowsChunks];
+    const uint16_t* wr = w + static_cast<int64_t>(n) * C + li * 8;
+#pragma unroll
+    for (int i = 0; i < kRowsChunks; ++i)
+        if (i < nch) wreg[i] = *reinterpret_cast<const uint4*>(wr + i * 128);
+    for (int m = 0; m < M; ++m) {
+        const uint16_t* xr = x + m * x_st + li * 8;
+        float acc = 0.0f, ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kRowsChunks; ++i) {
+            if (i < nch) {
+                const uint4 xv = *reinterpret_cast<const uint4*>(xr + i * 128);
+                const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                const uint32_t ww[4] = {wreg[i].x, wreg[i].y, wreg[i].z, wreg[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x0 = __builtin_bit_cast(float, xw[e] << 16);
+                    const float x1 = __builtin_bit_cast(float, xw[e] & 0xFFFF0000u);
+                    const float w0 = __builtin_bit_cast(float, ww[e] << 16);
+                    const float w1 = __builtin_bit_cast(float, ww[e] & 0xFFFF0000u);
+                    acc = __builtin_fmaf(x0, w0, acc);
+                    acc = __builtin_fmaf(x1, w1, acc);
+                    ss = __builtin_fmaf(x0, x0, ss);
+                    ss = __builtin_fmaf(x1, x1, ss);
+                }
+            }
+        }
+        acc = row16_sum(acc);
+        ss = row16_sum(ss);
+        if (li == 0) ylds[m][lc] = acc / __builtin_sqrtf(ss / static_cast<float>(C) + eps);
+    }
+    __syncthreads();
+
+    const int Nv = Nk;
+    int region, head;
+    if (nh < Nq) { region = 0; head = nh / 64; }
+    else if (nh < Nq + Nk) { region = 1; head = (nh - Nq) / 64; }
+    else if (nh < Nq + Nk + Nv) { region = 2; head = (nh - Nq - Nk) / 64; }
+    else { region = 3; head = (nh - Nq - Nk - Nv) / 64; }
+    const int ld = region == 0 ? Nq : (region == 3 ? Nf : Nk);
+    const int64_t pos_base = pos0 + (pos_dev != nullptr ? *pos_dev : 0);
+    const int64_t pos_hi = pos_dev != nullptr ? rope_len - 1 : INT64_MAX;
+    for (int t = tid; t < M * 8; t += kPThreads) {
+        const int m = t / 8, p = t % 8;
+        float y1 = ylds[m][2 * p], y2 = ylds[m][2 * p + 1];
+        const int d = d0 + p;
+        if (region <= 1) {
+            int64_t pos = pos_base + m % T;
+            pos = pos < 0 ? 0 : (pos > pos_hi ? pos_hi : pos);
+            const float c = cosv[pos * 32 + d], sn = sinv[pos * 32 + d];
+            const float r1 = y1 * c - y2 * sn;
+            const float r2 = y2 * c + y1 * sn;
+            y1 = r1;
+            y2 = r2;
+        }
+        const int64_t base = static_cast<int64_t>(m) * ld + 64 * head + d;
+        if (region == 0) { store_out<SPARDA_BF16>(q, base, y1); store_out<SPARDA_BF16>(q, base + 32, y2); }
+        else if (region == 1) { store_out<SPARDA_BF16>(k, base, y1); store_out<SPARDA_BF16>(k, base + 32, y2); }
+        else if (region == 2) { store_out<SPARDA_BF16>(v, base, y1); store_out<SPARDA_BF16>(v, base + 32, y2); }
+        else { store_out<FDT>(f, base, y1); store_out<FDT>(f, base + 32, y2); }
+    }
+}
+
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
                    const int64_t* pos_dev, int64_t rope_len) {
     const int64_t N = Nq + 2 * Nk + Nf;
+    if (M <= kRowsMax && C % 128 == 0 && C / 128 <= kRowsChunks) {
+#define SPARDA_PRODUCE_ROWS(FDT_)                                                                            \
+    hipLaunchKernelGGL((produce_rows_kernel<FDT_>), dim3(static_cast<unsigned>(N / 16)), dim3(kPThreads), 0,  \
+                       stream, static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w),        \
+                       static_cast<int>(M), static_cast<int>(C), static_cast<int>(Nq), static_cast<int>(Nk),  \
+                       static_cast<int>(Nf), eps, cosv, sinv, T, pos0, static_cast<uint16_t*>(q),             \
+                       static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), f, pos_dev, rope_len)
+        if (f_dtype == SPARDA_F32) SPARDA_PRODUCE_ROWS(SPARDA_F32);
+        else SPARDA_PRODUCE_ROWS(SPARDA_BF16);
+#undef SPARDA_PRODUCE_ROWS
+        return check_hip(hipGetLastError(), "produce_rows_kernel");
+    }
     dim3 grid(static_cast<unsigned>(cdiv(M, kPBM)), static_cast<unsigned>(N / kPBN));
 #define SPARDA_PRODUCE(FDT_)                                                                              \
     hipLaunchKernelGGL((produce_kernel<FDT_>), grid, dim3(kPThreads), 0, stream,                          \

@@ -10,8 +10,8 @@ device memory (``pos``, int64) and every position-dependent launch reads it
 when it runs:
 
   fused producer  RMSNorm + q/k/v/forecast projections + RoPE at *pos
-  cache append    k / v row *pos written with index_copy_
-  block sums      the block holding *pos recomputed from its first token
+  cache append    k / v row *pos written, and the fp32 sums of the block
+                  holding it recomputed from its first token (one launch)
   selection       layer 0 and static layers: the static window; forecast
                   layers: top-k of the previous layer's forecast against the
                   cached prototypes (block sums / bs), sink and own block
@@ -94,9 +94,7 @@ class GraphDecoder:
             q, k, v, f = sparda.produce(x, layer._fused_weight(), a.n_head * a.head_dim, a.n_kv_head * a.head_dim,
                                         fc.forecast_heads * fc.forecast_dim, layer.attn_norm.eps, self.cos,
                                         self.sin, f_dtype=x.dtype, pos_dev=self.pos)
-            cache.k.index_copy_(1, self.pos, k)
-            cache.v.index_copy_(1, self.pos, v)
-            sparda.block_sums_at(cache.k, self.pos, self.block_size, cache.block_sums)
+            sparda.append_at(cache.k, cache.v, self.pos, self.block_size, cache.block_sums, k, v)
             out = self._attend(a, q[:, 0], cache, prev_f)
             x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
             x = x + layer.ffn(layer.ffn_norm(x))

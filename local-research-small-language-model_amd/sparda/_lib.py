@@ -74,8 +74,8 @@ SIGNATURES = {
                                  _p, _p]),
     "sparda_produce_at": (_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64, _i64, _p,
                                  _p, _p, _p, _p, _int, _p]),
-    "sparda_block_sums_at": (_int, [_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64,
-                                    _p, _p]),
+    "sparda_append_at": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
+                                _i64, _i64, _p, _p]),
     "sparda_select_decode_at": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                                        _int, _f32, _p, _p, _i64, _p]),
     "sparda_decode_at": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _p, _i64, _i64, _i64,

@@ -428,24 +428,44 @@ def _pos_ptr(pos_dev: torch.Tensor) -> int:
     return pos_dev.data_ptr()
 
 
-def block_sums_at(k: torch.Tensor, pos_dev: torch.Tensor, block_size: int, sums: torch.Tensor) -> torch.Tensor:
-    """block_sums of the block holding token p = pos_dev (a one-element int64
-    device tensor, read when the kernel runs): tokens [p - p % bs, p] of the
-    cache k [B,S,Hkv,D], summed from zero into sums (in place; returned)."""
-    dev = require_device(k, sums, pos_dev)
-    _inference_only(k)
-    if sums.dtype != torch.float32 or not sums.is_contiguous():
+def append_at(k_cache: torch.Tensor, v_cache: Optional[torch.Tensor], pos_dev: torch.Tensor, block_size: int,
+              block_sums: torch.Tensor, k_new: Optional[torch.Tensor] = None,
+              v_new: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode-step cache append at token p = pos_dev (a one-element int64 device
+    tensor, read when the kernel runs): k_new / v_new ([B,1,Hkv,D] or
+    [B,Hkv,D]) written as row p of the caches [B,Smax,Hkv,D] (KVCache.update,
+    model/attention/base.py:19-29), and the fp32 sums of the block holding p
+    recomputed over [p - p % bs, p] in block_sums (in place; returned). Without
+    k_new / v_new only the sums are recomputed."""
+    dev = require_device(k_cache, v_cache, block_sums, pos_dev, k_new, v_new)
+    _inference_only(k_cache, v_cache, k_new, v_new)
+    if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
         raise TypeError("sparda: block sums must be contiguous float32")
-    if k.stride(-1) != 1:
+    if k_cache.stride(-1) != 1:
         raise ValueError("sparda: the cache's last dimension must be contiguous")
-    B, S, Hkv, D = k.shape
-    if tuple(sums.shape[:1]) != (B,) or tuple(sums.shape[2:]) != (Hkv, D):
-        raise AssertionError(f"Mismatch: cache {tuple(k.shape)} vs block sums {tuple(sums.shape)}")
-    max_len = min(S, sums.shape[1] * block_size)
-    sb, st, sh, _ = k.stride()
-    call("sparda_block_sums_at", k.data_ptr(), _dtype_code(k), sb, st, sh, B, Hkv, D, max_len, _pos_ptr(pos_dev),
-         block_size, sums.shape[1], sums.data_ptr(), _stream(dev))
-    return sums
+    B, S, Hkv, D = k_cache.shape
+    if tuple(block_sums.shape[:1]) != (B,) or tuple(block_sums.shape[2:]) != (Hkv, D):
+        raise AssertionError(f"Mismatch: cache {tuple(k_cache.shape)} vs block sums {tuple(block_sums.shape)}")
+    nsb = nsh = 0
+    if (k_new is None) != (v_new is None):
+        raise ValueError("sparda: k_new and v_new go together")
+    if k_new is not None:
+        if v_cache is None or v_cache.stride() != k_cache.stride() or v_cache.shape != k_cache.shape:
+            raise ValueError("sparda: appending needs a v_cache shaped and strided like k_cache")
+        if not (k_new.dtype == v_new.dtype == k_cache.dtype == v_cache.dtype):
+            raise TypeError("sparda: the new rows and the caches must share a dtype")
+        k_new = _rowmajor(k_new.reshape(B, Hkv, D))
+        v_new = _rowmajor(v_new.reshape(B, Hkv, D))
+        if k_new.stride() != v_new.stride():
+            raise ValueError("sparda: k_new and v_new must share strides")
+        nsb, nsh, _ = k_new.stride()
+    max_len = min(S, block_sums.shape[1] * block_size)
+    sb, st, sh, _ = k_cache.stride()
+    call("sparda_append_at", k_cache.data_ptr(), v_cache.data_ptr() if v_cache is not None else None,
+         _dtype_code(k_cache), sb, st, sh, k_new.data_ptr() if k_new is not None else None,
+         v_new.data_ptr() if v_new is not None else None, nsb, nsh, B, Hkv, D, max_len, _pos_ptr(pos_dev),
+         block_size, block_sums.shape[1], block_sums.data_ptr(), _stream(dev))
+    return block_sums
 
 
 def select_decode_at(forecast: torch.Tensor, block_sums: torch.Tensor, pos_dev: torch.Tensor, max_len: int,

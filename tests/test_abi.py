@@ -125,10 +125,15 @@ def test_device_position_entry_argument_errors():
             None)
     _expect(-2, "sparda_produce_at", P, 768, P, 8, 768, 768, 256, 256, 1e-5, P, P, 64, 3, Q, P, P, P, P, 1,
             None)  # M not a multiple of T
-    # block_sums_at: k, dtype, sb, st, sh, B, Hkv, D, max_len, pos_dev, bs, nb_stride, sums, stream
-    _expect(-1, "sparda_block_sums_at", P, 1, 256, 256, 64, 1, 4, 64, 256, None, 64, 4, P, None)
-    _expect(-8, "sparda_block_sums_at", P, 1, 256, 256, 64, 1, 4, 64, 257, Q, 64, 4, P, None)  # 5 blocks > 4
-    _expect(-2, "sparda_block_sums_at", P, 1, 256, 256, 64, 1, 4, 64, 0, Q, 64, 4, P, None)   # max_len 0
+    # append_at: kc, vc, dtype, sb, st, sh, k_new, v_new, new_sb, new_sh, B, Hkv, D, max_len, pos_dev, bs,
+    #            nb_stride, sums, stream
+    _expect(-1, "sparda_append_at", P, P, 1, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 256, None, 64, 4, P, None)
+    _expect(-1, "sparda_append_at", P, P, 1, 256, 256, 64, P, None, 256, 64, 1, 4, 64, 256, Q, 64, 4, P, None)
+    _expect(-1, "sparda_append_at", P, None, 1, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 256, Q, 64, 4, P, None)
+    _expect(-8, "sparda_append_at", P, P, 1, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 257, Q, 64, 4, P,
+            None)  # 5 blocks > nb_stride 4
+    _expect(-2, "sparda_append_at", P, P, 1, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 0, Q, 64, 4, P, None)
+    _expect(-3, "sparda_append_at", P, P, 5, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 256, Q, 64, 4, P, None)
     # select_decode_at: f, f_dtype, f_sb, f_sh, sums, B, Hkv, D, nb_stride, max_len, pos_dev, bs, k, routing,
     #                   scale, sel, n_sel, sel_cap, stream
     _expect(-1, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, None, 64, 8, 1, 0.125, P, P, 10, None)

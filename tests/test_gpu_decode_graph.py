@@ -50,11 +50,21 @@ def test_device_position_ops_equal_host_length_ops(dtype, routing):
         j = p // bs
         # current-block sums: [j*bs, p], the other blocks untouched
         got = torch.full_like(sums, float("nan"))
-        sparda.block_sums_at(kc, pos, bs, got)
+        sparda.append_at(kc, None, pos, bs, got)
         want = torch.full_like(sums, float("nan"))
         sparda.block_sums(kc, j * bs, p - j * bs + 1, bs, want)
         assert torch.equal(got[:, j], want[:, j])
         assert torch.isnan(got[:, :j]).all() and torch.isnan(got[:, j + 1:]).all()
+        # append of a new row at p: the caches gain it, the sums equal a fresh sum
+        kn = torch.randn(B, 1, Hkv, D, generator=g).to(dtype).to(DEV)
+        vn = torch.randn(B, 1, Hkv, D, generator=g).to(dtype).to(DEV)
+        k2, v2, s2 = kc.clone(), vc.clone(), torch.full_like(sums, float("nan"))
+        sparda.append_at(k2, v2, pos, bs, s2, kn, vn)
+        k3, v3 = kc.clone(), vc.clone()
+        k3[:, p:p + 1], v3[:, p:p + 1] = kn, vn
+        assert torch.equal(k2, k3) and torch.equal(v2, v3)
+        sparda.block_sums(k3, j * bs, p - j * bs + 1, bs, want)
+        assert torch.equal(s2[:, j], want[:, j])
         # selection from the sums
         s_d, n_d = sparda.select_decode_at(f, sums, pos, Smax, bs, k, routing=routing)
         s_h, n_h = sparda.select_decode(f, sums, p + 1, p, bs, k, routing=routing)
@@ -97,8 +107,8 @@ def test_device_positions_are_clamped_into_range():
         assert torch.equal(sparda.decode_at(q, kc, vc, a, bs, window=k), sparda.decode_at(q, kc, vc, b, bs, window=k))
         x = torch.full_like(sums, 3.0)
         y = torch.full_like(sums, 3.0)
-        sparda.block_sums_at(kc, a, bs, x)
-        sparda.block_sums_at(kc, b, bs, y)
+        sparda.append_at(kc, None, a, bs, x)
+        sparda.append_at(kc, None, b, bs, y)
         assert torch.equal(x, y)
 
 

@@ -41,7 +41,9 @@ def _reference(x, w_stack, norm_w, eps, cos, sin, pos0, nq, nkv):
 
 
 @pytest.mark.parametrize("B,T,pos0,f_dtype", [(2, 300, 5, torch.bfloat16), (1, 1024, 0, torch.float32),
-                                               (4, 1, 4000, torch.bfloat16)])
+                                               (4, 1, 4000, torch.bfloat16), (1, 1, 0, torch.bfloat16),
+                                               (16, 1, 77, torch.float32), (8, 2, 9, torch.bfloat16),
+                                               (17, 1, 3, torch.bfloat16)])
 def test_produce_matches_fp32_reference(B, T, pos0, f_dtype):
     case(f"produce B={B} T={T} pos0={pos0} {f_dtype}")
     g = torch.Generator().manual_seed(11 + T)
