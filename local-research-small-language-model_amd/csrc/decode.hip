@@ -161,6 +161,8 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
     __shared__ float q_lds[kMaxGroup * DH];
     __shared__ int32_t sel_lds[kMaxSlots + 6];
+    __shared__ uint32_t ck_lds[kWave];  // selection candidates (keys, block indices)
+    __shared__ int32_t ci_lds[kWave];
     __shared__ int n_lds;
 
     const int g = blockIdx.x;
@@ -199,7 +201,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 const int j = e * kWave + lane;
                 kreg[e] = j < NB ? order_key(srow[j]) : 0u;
             }
-            m = wave_select<CH>(kreg, static_cast<int>(NB), k, cb, sel_lds);
+            m = wave_select_pre<CH>(kreg, static_cast<int>(NB), k, cb, sel_lds, ck_lds, ci_lds);
         } else if (sel_mode == 1) {
             m = cb + 1;  // slot w is block w; sel_lds is not used
         } else if (sel_mode == 3) {

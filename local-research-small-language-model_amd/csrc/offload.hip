@@ -286,17 +286,17 @@ int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sum
 constexpr int kSelThreads = 256;
 constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
 
-// wave_select over the first n keys of key_lds, CH keys per lane
+// top-k selection over the first n keys of key_lds, CH keys per lane
 template <int CH>
 __device__ __forceinline__ int select_keys(const uint32_t* key_lds, int n, int k, int own, int32_t* sel_lds,
-                                           int lane) {
+                                           int lane, uint32_t* ck_lds, int32_t* ci_lds) {
     uint32_t kreg[CH];
 #pragma unroll
     for (int e = 0; e < CH; ++e) {
         const int j = e * kWave + lane;
         kreg[e] = j < n ? key_lds[j] : 0u;
     }
-    return wave_select<CH>(kreg, n, k, own, sel_lds);
+    return wave_select_pre<CH>(kreg, n, k, own, sel_lds, ck_lds, ci_lds);
 }
 
 template <int FDT, int CH, int DH, bool POW2>
@@ -308,6 +308,8 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
     __shared__ float f_lds[kMaxHeadDim];
     __shared__ uint32_t key_lds[kSelMaxBlocks];
     __shared__ int32_t sel_lds[kMaxSelCap + 2];
+    __shared__ uint32_t ck_lds[kWave];
+    __shared__ int32_t ci_lds[kWave];
     __shared__ int m_lds;
     const int g = blockIdx.x;
     const int b = blockIdx.y;
@@ -365,9 +367,12 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
             // the smallest key-register count holding n_present keys (a device-held
             // length may be far below the bound CH was chosen for)
             const int n = static_cast<int>(n_present);
-            if (CH >= 64 && n > 1024) m = select_keys<(CH >= 64 ? 64 : CH)>(key_lds, n, k, own, sel_lds, lane);
-            else if (CH >= 16 && n > 256) m = select_keys<(CH >= 16 ? 16 : CH)>(key_lds, n, k, own, sel_lds, lane);
-            else m = select_keys<4>(key_lds, n, k, own, sel_lds, lane);
+            if (CH >= 64 && n > 1024)
+                m = select_keys<(CH >= 64 ? 64 : CH)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+            else if (CH >= 16 && n > 256)
+                m = select_keys<(CH >= 16 ? 16 : CH)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+            else
+                m = select_keys<4>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
             if (own >= n_present) {  // the own block holds no token yet: it has no score but is attended
                 if (lane == 0) sel_lds[m] = own;
                 m += 1;

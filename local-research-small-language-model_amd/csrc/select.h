@@ -222,4 +222,80 @@ __device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, in
     return m;
 }
 
+// The k-th largest of one key per lane (keys of empty lanes 0).
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
+    uint32_t T = 0;
+#pragma unroll 4
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = T | (1u << bit);
+        T = ballot_count(v >= c) >= k ? c : T;
+    }
+    return T;
+}
+
+// wave_select with a candidate pre-filter. T0 = the k-th largest of the 64
+// lane maxima bounds the k-th largest key from below (the k lanes whose
+// maximum is >= T0 hold k keys >= T0; the keys fill lanes 0.. first, so at
+// least min(n, 64) >= k lanes hold one), hence the top-k lies among the keys
+// >= T0. When those fit in one register per lane they are compacted in index
+// order through ck_lds / ci_lds (64 entries each) and the 32-round threshold
+// search runs on that one register instead of CH: the ballot search costs
+// ~40 cycles per key register per round. Otherwise wave_select runs as is.
+// Same result as wave_select; called by a whole wavefront (wave-uniform flow).
+template <int CH>
+__device__ __forceinline__ int wave_select_pre(const uint32_t (&kreg)[CH], int n, int k, int own,
+                                               int32_t* sel_lds, uint32_t* ck_lds, int32_t* ci_lds) {
+    const int lane = threadIdx.x % kWave;
+    uint32_t lm = kreg[0];
+#pragma unroll
+    for (int e = 1; e < CH; ++e) lm = kreg[e] > lm ? kreg[e] : lm;
+    const uint32_t T0 = wave_kth_largest(lm, k);
+    int C = 0;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) C += ballot_count(kreg[e] >= T0);
+    if (C > kWave) return wave_select<CH>(kreg, n, k, own, sel_lds);
+    const uint64_t lanes_below = (1ull << lane) - 1ull;
+    int base = 0;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+        const uint64_t msk = __builtin_amdgcn_ballot_w64(kreg[e] >= T0);
+        if ((msk >> lane) & 1ull) {
+            const int slot = base + __popcll(msk & lanes_below);
+            ck_lds[slot] = kreg[e];
+            ci_lds[slot] = e * kWave + lane;
+        }
+        base += __popcll(msk);
+    }
+    __builtin_amdgcn_wave_barrier();  // LDS operations of one wavefront complete in order
+    const uint32_t ck = lane < C ? ck_lds[lane] : 0u;
+    const int ci = lane < C ? ci_lds[lane] : 0x7fffffff;
+    const uint32_t T = wave_kth_largest(ck, k);
+    int need_eq = k - ballot_count(ck > T);
+    uint64_t eq = __builtin_amdgcn_ballot_w64(ck == T);
+    uint64_t keep = 0;
+    for (; need_eq > 0 && eq != 0; --need_eq) {
+        const uint64_t low = eq & (~eq + 1ull);
+        keep |= low;
+        eq ^= low;
+    }
+    // candidates are in ascending index order, all <= own when taken: the
+    // sink block 0 goes first and the own block last unless already taken
+    const uint64_t take = (__builtin_amdgcn_ballot_w64(ck > T) | keep) & __builtin_amdgcn_ballot_w64(ci <= own);
+    const bool mine = (take >> lane) & 1ull;
+    const bool has0 = __builtin_amdgcn_ballot_w64(mine && ci == 0) != 0;
+    const bool has_own = __builtin_amdgcn_ballot_w64(mine && ci == own) != 0;
+    int m = 0;
+    if (!has0) {
+        if (lane == 0) sel_lds[0] = 0;
+        m = 1;
+    }
+    if (mine) sel_lds[m + __popcll(take & lanes_below)] = ci;
+    m += __popcll(take);
+    if (!has_own && own != 0 && own < n) {
+        if (lane == 0) sel_lds[m] = own;
+        m += 1;
+    }
+    return m;
+}
+
 }  // namespace sparda
