@@ -54,3 +54,23 @@ def test_graph_decoder_refuses_cpu_models_and_unsupported_backends():
         GraphDecoder(SparDAResearchModel(cfg).to(torch.bfloat16), 1, 512)  # CPU weights: no fallback
     with pytest.raises(TypeError):
         GraphDecoder(SparDAResearchModel(cfg), 1, 512)  # fp32
+
+
+def test_rope_known_answers():
+    # tests/test_attention.py:11-21 of the reference: position 0 is the identity
+    from model.rope import RotaryEmbedding, apply_rope, rope_tables
+    cos, sin = rope_tables(64, 16)
+    assert cos.shape == (16, 32) and sin.shape == (16, 32)
+    assert torch.equal(cos[0], torch.ones(32)) and torch.equal(sin[0], torch.zeros(32))
+    x = torch.randn(2, 1, 3, 64)
+    assert torch.equal(apply_rope(x, cos, sin, offset=0), x)
+    # rotate-half pairs (i, i + 32) at angle pos * 10000^(-2i/64)
+    y = apply_rope(x, cos, sin, offset=5)
+    ang = 5 * 10000.0 ** (-torch.arange(0, 64, 2, dtype=torch.float64) / 64)
+    c, s = torch.cos(ang), torch.sin(ang)
+    a, b = x[..., :32].double(), x[..., 32:].double()
+    want = torch.cat((a * c - b * s, b * c + a * s), dim=-1)
+    assert torch.allclose(y.double(), want, atol=1e-5)
+    rot = RotaryEmbedding(64, 16)
+    q, k = rot(x, x[:, :, :1], offset=0)
+    assert q.shape == x.shape and k.shape == (2, 1, 1, 64)
