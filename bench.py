@@ -396,13 +396,14 @@ def bench_offload(args, torch, sparda, synth):
     }
 
 
-def bench_generate(args, torch, sparda, synth):
+def bench_generate(args, torch, sparda, synth, batch=1):
     """Greedy generation after a 16384-token prompt with the 12-layer model of
     bench_model (fused producer, cached prototypes, absolute-position routing,
-    B=1): per-token time of the eager cached decode loop (host-driven, one
-    launch sequence issued per token) and of GraphDecoder (one HIP graph replay
-    per token, positions read from device memory). Both loops start from the
-    same prefill; their generated tokens must agree."""
+    B=1, then B=8 sequences decoded together): per-step time of the eager
+    cached decode loop (host-driven, one launch sequence issued per token) and
+    of GraphDecoder (one HIP graph replay per step, positions read from device
+    memory). Both loops start from the same prefill; their generated tokens
+    must agree."""
     from model.attention import PrototypeKVCache
     from model.config import ModelConfig
     from model.decode_graph import GraphDecoder
@@ -416,7 +417,7 @@ def bench_generate(args, torch, sparda, synth):
     torch.manual_seed(1007)
     model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
     g = torch.Generator().manual_seed(1007)
-    prompt = torch.randint(0, cfg.vocab_size, (1, MT), generator=g).to(dev)
+    prompt = torch.randint(0, cfg.vocab_size, (batch, MT), generator=g).to(dev)
 
     def loop(first_logits, step, n):
         toks, logits = [], first_logits
@@ -437,25 +438,33 @@ def bench_generate(args, torch, sparda, synth):
         return e0.elapsed_time(e1) * 1e3 / G, torch.cat(toks + more, dim=1)
 
     with torch.no_grad():
-        caches = [PrototypeKVCache(1, cap, cfg.n_kv_head, cfg.head_dim, dev, torch.bfloat16, block_size=BS)
+        caches = [PrototypeKVCache(batch, cap, cfg.n_kv_head, cfg.head_dim, dev, torch.bfloat16, block_size=BS)
                   for _ in range(cfg.n_layer)]
         first = model(prompt, kv_caches=caches)["logits"][:, -1]
         us_eager, toks_eager = timed(lambda t: model(t, kv_caches=caches)["logits"][:, -1], first)
         del caches
-        gd = GraphDecoder(model, 1, cap)
+        gd = GraphDecoder(model, batch, cap)
         first = gd.prefill(prompt)
         us_graph, toks_graph = timed(gd.step, first)
         torch.cuda.synchronize()
     assert torch.equal(toks_eager, toks_graph), "graph-replayed generation differs from the eager loop"
     del gd, model
     torch.cuda.empty_cache()
+    if batch != 1:
+        return {"us_per_step_eager": round(us_eager, 1), "us_per_step_graph": round(us_graph, 1),
+                "tok_s_graph": round(batch * 1e6 / us_graph, 1)}
+    b8 = bench_generate(args, torch, sparda, synth, batch=8)
     return {
         "workload": f"greedy generation of {G} tokens after a {MT}-token prompt, 12-layer model of "
                     "model_forward (fused producer, block sums kept in HBM, top-8 + sink + current, "
-                    "absolute-position routing), B=1, bf16; step = one token through all layers incl. LM head",
+                    "absolute-position routing), bf16; step = one token per sequence through all layers "
+                    "incl. LM head; B=1, and B=8 sequences decoded together (*_b8)",
         "us_per_token_eager": round(us_eager, 1),
         "us_per_token_graph": round(us_graph, 1),
         "tok_s_graph": round(1e6 / us_graph, 1),
+        "us_per_step_eager_b8": b8["us_per_step_eager"],
+        "us_per_step_graph_b8": b8["us_per_step_graph"],
+        "tok_s_graph_b8": b8["tok_s_graph"],
         "tokens": G,
         "tokens_agree": True,
     }
@@ -697,7 +706,8 @@ def main():
         f"{mdl['ms_per_forward_fused_producer']:.2f} ms ({mdl['tok_s_fused_producer']:.0f} tok/s)")
     log("graph-replayed generation")
     gen = bench_generate(args, torch, sparda, synth)
-    log(f"generate: eager {gen['us_per_token_eager']:.1f} us/token, graph {gen['us_per_token_graph']:.1f} us/token")
+    log(f"generate: eager {gen['us_per_token_eager']:.1f} us/token, graph {gen['us_per_token_graph']:.1f} us/token; "
+        f"B=8 graph {gen['us_per_step_graph_b8']:.1f} us/step ({gen['tok_s_graph_b8']:.0f} tok/s)")
     log("fused producer")
     prod = bench_producer(args, torch, sparda, synth)
     log(f"producer: fused {prod['us_fused']:.1f} us ({prod['fused_tflops']:.0f} TFLOP/s), "
