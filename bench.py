@@ -262,7 +262,7 @@ def bench_offload(args, torch, sparda, synth):
     from model.model import SparDAResearchModel
     dev = torch.device("cuda")
     W, K = 4, args.offload_steps
-    cap = OB_CTX + 4 * (W + K) + 64
+    cap = OB_CTX + 6 * (W + K) + 64
     cfg = ModelConfig(n_layer=OB_LAYERS, context_length=cap, block_size=BS, top_k_blocks=TOPK,
                       decode_routing="absolute", attention_backend="async_offload", norm_eps=1e-5)
     torch.manual_seed(1004)
@@ -284,7 +284,7 @@ def bench_offload(args, torch, sparda, synth):
             res_caches[li].update(kd, vd)
     torch.cuda.synchronize()
     g = torch.Generator().manual_seed(1006)
-    ids = torch.randint(0, cfg.vocab_size, (4 * (W + K), 1, 1), generator=g).to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (6 * (W + K), 1, 1), generator=g).to(dev)
     it = iter(range(ids.shape[0]))
 
     def run(m, caches, n):
@@ -366,6 +366,30 @@ def bench_offload(args, torch, sparda, synth):
     us_proto_eager = timed(resident, proto_caches)
     us_proto_graph = graph_step_us(resident, proto_caches)
     del proto_caches
+
+    # the offloaded step replayed from a HIP graph (GraphDecoder over the same
+    # host arenas, positions in device memory): the prefetch of layer L+1 on a
+    # side stream under layer L's attention + FFN, and the same step with the
+    # prefetches on the compute stream (no overlap)
+    from model.decode_graph import GraphDecoder
+
+    def offload_graph_us(overlap):
+        gd = GraphDecoder(model, 1, cap, caches=off_caches, overlap=overlap)
+        with torch.no_grad():
+            for _ in range(W):
+                gd.step(ids[next(it)])
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(K // 2):
+                gd.step(ids[next(it)])
+            e1.record()
+            e1.synchronize()
+        del gd
+        return e0.elapsed_time(e1) * 1e3 / (K // 2)
+
+    us_off_graph = offload_graph_us(overlap=True)
+    us_off_graph_serial = offload_graph_us(overlap=False)
     # host link: one 256 MiB pinned host -> device copy
     hb = torch.empty(256 << 20, dtype=torch.uint8).pin_memory()
     db = torch.empty_like(hb, device=dev)
@@ -385,6 +409,8 @@ def bench_offload(args, torch, sparda, synth):
         "us_per_step_gpu_resident_graph": round(us_res_graph, 1),
         "us_per_step_cached_prototypes": round(us_proto_eager, 1),
         "us_per_step_cached_prototypes_graph": round(us_proto_graph, 1),
+        "us_per_step_async_graph": round(us_off_graph, 1),
+        "us_per_step_async_graph_serial_prefetch": round(us_off_graph_serial, 1),
         "steps": K,
         "overlap": round(1.0 - ex / tr, 4) if tr > 0 else None,
         "transfer_us_per_layer": round(tr * 1e3, 2),
@@ -696,7 +722,8 @@ def main():
     log(f"offload: async {off['us_per_step_async']:.1f} us/step, sync {off['us_per_step_sync']:.1f}, "
         f"resident {off['us_per_step_gpu_resident']:.1f} (graph {off['us_per_step_gpu_resident_graph']:.1f}; "
         f"cached prototypes {off['us_per_step_cached_prototypes']:.1f}, graph "
-        f"{off['us_per_step_cached_prototypes_graph']:.1f}); overlap {off['overlap']}, "
+        f"{off['us_per_step_cached_prototypes_graph']:.1f}); async graph {off['us_per_step_async_graph']:.1f} "
+        f"(serial prefetch {off['us_per_step_async_graph_serial_prefetch']:.1f}); overlap {off['overlap']}, "
         f"transfer {off['transfer_us_per_layer']} us/layer, link {off['host_link_gbs']} GB/s")
     log("12-layer forward workload")
     mdl = bench_model(args, torch, sparda, synth)

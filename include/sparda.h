@@ -370,13 +370,24 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
  *   (sb, st, sh, 1); KVCache.update, model/attention/base.py:19-29) and
  *   recomputes the fp32 sums of the block holding p over [p - p % bs, p], as
  *   sparda_block_sums(k, ..., pos = p - p % bs, n = p % bs + 1) does. With
- *   k_new / v_new NULL only the sums are recomputed (v_cache may be NULL).
- * sparda_select_decode_at: sparda_select_decode with len = p + 1, pos = p.
+ *   k_new / v_new NULL only the sums are recomputed (v_cache may be NULL);
+ *   with block_sums NULL only the rows are written.
+ * sparda_select_decode_at: sparda_select_decode with len = p + 1, pos = p;
+ *   with lookahead != 0, len = p, pos = p (the selection a prefetch makes
+ *   before token p is appended, async_offload.py:196-260).
  * sparda_decode_at: sparda_decode_selected with S = p + 1 over the caller's
- *   list (sel / n_sel), or, with sel NULL and window_k > 0, the static window
+ *   list (sel / n_sel; compact != 0: the fetched block buffers of
+ *   sparda_offload_fetch_at; k_new / v_new: the key and value of position p),
+ *   or, with sel NULL and window_k > 0, the static window
  *   {0} U [cb - window_k + 1, cb] (cb = p / bs; every block while cb + 1 <=
  *   window_k + 2) that sparda_decode uses without a forecast, or every block
  *   (sel NULL, window_k 0).
+ * sparda_offload_fetch_at: sparda_offload_fetch (gather kernel) with
+ *   len = *len_dev, clamped into [0, max_seq].
+ * sparda_offload_append_at: appends one token (k / v [B,Hkv,D], strides
+ *   (new_sb, new_sh, 1)) as row *pos_dev of the arena through its device
+ *   mapping (OffloadedKVCache.update, offload.py:67-77) and, with block_sums,
+ *   recomputes that block's sums from the arena, as sparda_append_at does.
  */
 SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
                                  int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
@@ -390,12 +401,20 @@ SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_
                                        const float* block_sums, int64_t B, int64_t Hkv, int64_t D,
                                        int64_t nb_stride, int64_t max_len, const int64_t* pos_dev,
                                        int64_t block_size, int64_t top_k, int routing, float scale,
-                                       int32_t* sel, int32_t* n_sel, int64_t sel_cap, void* stream);
+                                       int32_t* sel, int32_t* n_sel, int64_t sel_cap, int lookahead,
+                                       void* stream);
 SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
-                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel,
-                                const int32_t* n_sel, int64_t sel_cap, int64_t window_k, int64_t B,
+                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                                const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
+                                const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
                                 int64_t block_size, float scale, void* out, int64_t out_sb, void* stream);
+SPARDA_API int sparda_offload_fetch_at(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
+                                       int64_t sel_cap, int64_t block_size, const int64_t* len_dev, void* k_dst,
+                                       void* v_dst, void* stream);
+SPARDA_API int sparda_offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
+                                        int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
+                                        float* block_sums, void* stream);
 
 /*
  * Host-resident KV cache of one layer: pinned host arena (hipHostMalloc,

@@ -266,7 +266,7 @@ SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_
                                        const float* block_sums, int64_t B, int64_t Hkv, int64_t D,
                                        int64_t nb_stride, int64_t max_len, const int64_t* pos_dev,
                                        int64_t block_size, int64_t top_k, int routing, float scale, int32_t* sel,
-                                       int32_t* n_sel, int64_t sel_cap, void* stream) {
+                                       int32_t* n_sel, int64_t sel_cap, int lookahead, void* stream) {
     SPARDA_REQUIRE(pos_dev, SPARDA_ERR_NULL, "select_decode_at: null pos_dev");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
                    "select_decode_at: pos_dev must be 8-byte aligned");
@@ -287,18 +287,21 @@ SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_
     SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "select_decode_at: grid too large");
     return launch_select_decode(forecast, f_dtype, f_sb, f_sh, block_sums, B, Hkv, D, nb_stride, max_len,
                                 max_len - 1, block_size, top_k, routing, scale, sel, n_sel, sel_cap,
-                                static_cast<hipStream_t>(stream), pos_dev);
+                                static_cast<hipStream_t>(stream), pos_dev, lookahead != 0);
 }
 
 SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
-                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel,
-                                const int32_t* n_sel, int64_t sel_cap, int64_t window_k, int64_t B,
+                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                                const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
+                                const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
                                 int64_t block_size, float scale, void* out, int64_t out_sb, void* stream) {
     SPARDA_REQUIRE(q && k && v && out && pos_dev, SPARDA_ERR_NULL, "decode_at: null q/k/v/out/pos_dev");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
                    "decode_at: pos_dev must be 8-byte aligned");
     SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "decode_at: sel and n_sel go together");
+    SPARDA_REQUIRE(!k_new == !v_new, SPARDA_ERR_NULL, "decode_at: k_new and v_new go together");
+    SPARDA_REQUIRE(!compact || sel, SPARDA_ERR_MODE, "decode_at: compact buffers need a selection");
     SPARDA_REQUIRE(!sel || window_k == 0, SPARDA_ERR_MODE, "decode_at: a selection list or a window, not both");
     SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "decode_at: dtype %d unsupported", dtype);
     SPARDA_REQUIRE(B > 0 && max_len > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
@@ -314,9 +317,11 @@ SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const
     const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
     SPARDA_REQUIRE(aligned16(k) && aligned16(v) && kv_sb % ve == 0 && kv_ss % ve == 0 && kv_sh % ve == 0,
                    SPARDA_ERR_STRIDE, "decode_at: K/V rows must be 16-byte aligned");
-    return launch_decode_at(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, sel, n_sel, sel_cap, window_k, B,
-                            max_len, pos_dev, Hq, Hkv, D, block_size, scale, out, out_sb,
-                            static_cast<hipStream_t>(stream));
+    SPARDA_REQUIRE(!k_new || (aligned16(k_new) && aligned16(v_new) && new_sb % ve == 0 && new_sh % ve == 0),
+                   SPARDA_ERR_STRIDE, "decode_at: k_new/v_new rows must be 16-byte aligned");
+    return launch_decode_at(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
+                            k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
+                            out_sb, static_cast<hipStream_t>(stream));
 }
 
 SPARDA_API int sparda_offload_create(int64_t B, int64_t max_seq, int64_t Hkv, int64_t D, int dtype,
@@ -433,8 +438,9 @@ SPARDA_API int sparda_append_at(void* k_cache, void* v_cache, int dtype, int64_t
                                 const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,
                                 int64_t block_size, int64_t nb_stride, float* block_sums, void* stream) {
-    SPARDA_REQUIRE(k_cache && block_sums && pos_dev, SPARDA_ERR_NULL, "append_at: null k_cache/block_sums/pos_dev");
+    SPARDA_REQUIRE(k_cache && pos_dev, SPARDA_ERR_NULL, "append_at: null k_cache/pos_dev");
     SPARDA_REQUIRE(!k_new == !v_new, SPARDA_ERR_NULL, "append_at: k_new and v_new go together");
+    SPARDA_REQUIRE(k_new || block_sums, SPARDA_ERR_NULL, "append_at: nothing to do (no new rows, no block sums)");
     SPARDA_REQUIRE(!k_new || v_cache, SPARDA_ERR_NULL, "append_at: appending needs v_cache");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
                    "append_at: pos_dev must be 8-byte aligned");
@@ -485,6 +491,35 @@ SPARDA_API int sparda_offload_fetch(sparda_offload_t h, const int32_t* sel, cons
                    "offload_fetch: destinations must be 16-byte aligned");
     return offload_fetch(h, sel, n_sel, sel_cap, block_size, len, method, k_dst, v_dst,
                          static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_offload_fetch_at(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
+                                       int64_t sel_cap, int64_t block_size, const int64_t* len_dev, void* k_dst,
+                                       void* v_dst, void* stream) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_fetch_at: null handle");
+    SPARDA_REQUIRE(sel && n_sel && k_dst && v_dst && len_dev, SPARDA_ERR_NULL, "offload_fetch_at: null pointer");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(len_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "offload_fetch_at: len_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(block_size > 0, SPARDA_ERR_SHAPE, "offload_fetch_at: bad block_size");
+    SPARDA_REQUIRE(sel_cap >= 1 && sel_cap <= 65535, SPARDA_ERR_SHAPE, "offload_fetch_at: sel_cap %lld out of range",
+                   (long long)sel_cap);
+    SPARDA_REQUIRE(aligned16(k_dst) && aligned16(v_dst), SPARDA_ERR_STRIDE,
+                   "offload_fetch_at: destinations must be 16-byte aligned");
+    return offload_fetch(h, sel, n_sel, sel_cap, block_size, 0, SPARDA_FETCH_KERNEL, k_dst, v_dst,
+                         static_cast<hipStream_t>(stream), len_dev);
+}
+
+SPARDA_API int sparda_offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
+                                        int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
+                                        float* block_sums, void* stream) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_append_at: null handle");
+    SPARDA_REQUIRE(k && v && pos_dev, SPARDA_ERR_NULL, "offload_append_at: null k/v/pos_dev");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "offload_append_at: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(new_sb >= 0 && new_sh >= 0, SPARDA_ERR_STRIDE, "offload_append_at: negative stride");
+    SPARDA_REQUIRE(!block_sums || block_size > 0, SPARDA_ERR_SHAPE, "offload_append_at: block_size must be > 0");
+    return offload_append_at(h, k, v, new_sb, new_sh, pos_dev, block_sums ? block_size : 1, block_sums,
+                             static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -722,9 +722,10 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
 }
 
 int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
-                     int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel, const int32_t* n_sel,
-                     int64_t cap, int64_t window_k, int64_t B, int64_t S_max, const int64_t* pos_dev, int64_t Hq,
-                     int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
+                     int64_t kv_ss, int64_t kv_sh, int dtype, int compact, const int32_t* sel,
+                     const int32_t* n_sel, int64_t cap, int64_t window_k, const void* k_new, const void* v_new,
+                     int64_t new_sb, int64_t new_sh, int64_t B, int64_t S_max, const int64_t* pos_dev,
+                     int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
                      hipStream_t stream) {
     int mode, cap_i;
     int64_t kk;
@@ -736,7 +737,8 @@ int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, c
         mode = 1, cap_i = 0, kk = 0;
     }
     AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S_max, Hq, Hkv, D, bs, kk, mode, cap_i, scale,
-                 nullptr, sel, n_sel, 0, nullptr, nullptr, 0, 0, nullptr, nullptr, out, out_sb, pos_dev};
+                 nullptr, sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb,
+                 pos_dev};
     return launch_attend(a, stream);
 }
 

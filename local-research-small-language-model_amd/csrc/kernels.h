@@ -61,14 +61,15 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
 int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
                          int64_t H, int64_t D, int64_t nb_stride, int64_t len, int64_t pos, int64_t bs,
                          int64_t k, int routing, float scale, int32_t* sel, int32_t* n_sel, int64_t cap,
-                         hipStream_t stream, const int64_t* pos_dev = nullptr);
+                         hipStream_t stream, const int64_t* pos_dev = nullptr, int lookahead = 0);
 
 // attention at a device-held position: S = *pos_dev + 1 (clamped to S_max);
 // the caller's list (sel), the window of window_k blocks, or every block
 int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
-                     int64_t kv_ss, int64_t kv_sh, int dtype, const int32_t* sel, const int32_t* n_sel,
-                     int64_t cap, int64_t window_k, int64_t B, int64_t S_max, const int64_t* pos_dev, int64_t Hq,
-                     int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
+                     int64_t kv_ss, int64_t kv_sh, int dtype, int compact, const int32_t* sel,
+                     const int32_t* n_sel, int64_t cap, int64_t window_k, const void* k_new, const void* v_new,
+                     int64_t new_sb, int64_t new_sh, int64_t B, int64_t S_max, const int64_t* pos_dev,
+                     int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
                      hipStream_t stream);
 
 // host-resident KV arena (offload.hip)
@@ -91,7 +92,11 @@ int launch_append_at(void* kc, void* vc, int dtype, int64_t sb, int64_t st, int6
                      const void* v_new, int64_t n_sb, int64_t n_sh, int64_t B, int64_t H, int64_t D, int64_t bs,
                      int64_t max_len, int64_t nb_stride, const int64_t* pos_dev, float* sums, hipStream_t stream);
 int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t bs,
-                  int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream);
+                  int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream,
+                  const int64_t* len_dev = nullptr);
+// decode-step append of one token at row *pos_dev of the arena (device mapping) + its block's sums
+int offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t n_sb, int64_t n_sh,
+                      const int64_t* pos_dev, int64_t bs, float* sums, hipStream_t stream);
 
 int launch_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
                    const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,

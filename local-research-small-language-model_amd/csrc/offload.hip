@@ -201,7 +201,8 @@ append_at_kernel(void* __restrict__ kc, void* __restrict__ vc, int64_t sb, int64
     int64_t p = *pos_dev;
     p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
     const int64_t j = p / bs;
-    const int64_t s_hi = k_new != nullptr ? p : p + 1;  // rows read from the cache
+    // rows read from the cache (none when only the new row is written)
+    const int64_t s_hi = sums == nullptr ? j * bs : (k_new != nullptr ? p : p + 1);
     E* kce = static_cast<E*>(kc);
     for (int64_t e = threadIdx.x; e < H * D; e += blockDim.x) {
         const int64_t g = e / D, d = e % D;
@@ -223,7 +224,7 @@ append_at_kernel(void* __restrict__ kc, void* __restrict__ vc, int64_t sb, int64
             static_cast<E*>(vc)[base + p * st] = static_cast<const E*>(v_new)[ni];
             acc = acc + load_elem<DT>(k_new, ni);
         }
-        sums[((b * nb_stride + j) * H + g) * D + d] = acc;
+        if (sums != nullptr) sums[((b * nb_stride + j) * H + g) * D + d] = acc;
     }
 }
 
@@ -270,6 +271,14 @@ int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb,
                              stream);
 }
 
+int offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t n_sb, int64_t n_sh,
+                      const int64_t* pos_dev, int64_t bs, float* sums, hipStream_t stream) {
+    // the arena through its device mapping: [B][H][Smax][D] -> strides (H*Smax*D, D, Smax*D)
+    return launch_append_at(h->dev, h->dev + arena_bytes(h), h->dtype, h->H * h->Smax * h->D, h->D, h->Smax * h->D,
+                            k, v, n_sb, n_sh, h->B, h->H, h->D, bs, h->Smax, cdiv(h->Smax, bs), pos_dev, sums,
+                            stream);
+}
+
 int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sums, hipStream_t stream) {
     // the arena read through its device mapping: [B][H][Smax][D] -> strides (H*Smax*D, D, Smax*D)
     return launch_block_sums(h->dev, h->dtype, h->H * h->Smax * h->D, h->D, h->Smax * h->D, 0, len, h->B, h->H,
@@ -304,7 +313,7 @@ __global__ void __launch_bounds__(kSelThreads)
 select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, const float* __restrict__ sums,
                      int64_t H, int64_t nb_stride, int64_t n_present_arg, int64_t pos_arg, int64_t score_pos_arg,
                      int64_t bs, int k, float scale, int32_t* __restrict__ sel, int32_t* __restrict__ n_sel,
-                     int cap, const int64_t* __restrict__ pos_dev, int absolute) {
+                     int cap, const int64_t* __restrict__ pos_dev, int absolute, int lookahead) {
     __shared__ float f_lds[kMaxHeadDim];
     __shared__ uint32_t key_lds[kSelMaxBlocks];
     __shared__ int32_t sel_lds[kMaxSelCap + 2];
@@ -317,12 +326,13 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
     const int lane = tid % kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
     // with pos_dev: a decode step at token p = *pos_dev (clamped into [0, pos_arg]),
-    // len = p + 1; otherwise the host's len / pos
+    // len = p + 1, or with lookahead the prefetch before token p is appended,
+    // len = p; otherwise the host's len / pos
     int64_t pos = pos_arg, n_present = n_present_arg, score_pos = score_pos_arg;
     if (pos_dev != nullptr) {
         const int64_t p = *pos_dev;
         pos = p < 0 ? 0 : (p > pos_arg ? pos_arg : p);
-        n_present = pos / bs + 1;
+        n_present = lookahead ? (pos + bs - 1) / bs : pos / bs + 1;
         score_pos = absolute ? pos : 0;
     }
     const int own = static_cast<int>(pos / bs);
@@ -389,7 +399,7 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
 int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
                          int64_t H, int64_t D, int64_t nb_stride, int64_t len, int64_t pos, int64_t bs,
                          int64_t k, int routing, float scale, int32_t* sel, int32_t* n_sel, int64_t cap,
-                         hipStream_t stream, const int64_t* pos_dev) {
+                         hipStream_t stream, const int64_t* pos_dev, int lookahead) {
     // with pos_dev, len bounds the device length (pos = len - 1 is the largest position)
     const int64_t n_present = cdiv(len, bs);
     const int64_t score_pos = routing == SPARDA_ROUTE_ABSOLUTE ? pos : 0;
@@ -399,7 +409,7 @@ int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, 
     hipLaunchKernelGGL((select_decode_kernel<FDT_, CH_, DH_, P2_>), grid, dim3(kSelThreads), 0, stream, f,  \
                        f_sb, f_sh, sums, H, nb_stride, n_present, pos, score_pos, bs, static_cast<int>(k),  \
                        scale, sel, n_sel, static_cast<int>(cap), pos_dev,                                   \
-                       routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0)
+                       routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0, lookahead)
 #define SPARDA_SEL_P(FDT_, CH_, DH_)                    \
     if (pow2) SPARDA_SEL(FDT_, CH_, DH_, true);         \
     else SPARDA_SEL(FDT_, CH_, DH_, false);
@@ -436,7 +446,14 @@ constexpr int kFetchThreads = 256;
 __global__ void __launch_bounds__(kFetchThreads)
 fetch_blocks_kernel(const char* __restrict__ ak, const char* __restrict__ av, const int32_t* __restrict__ sel,
                     const int32_t* __restrict__ n_sel, int cap, int64_t H, int64_t Smax, int64_t row_bytes,
-                    int64_t bs, int64_t len, char* __restrict__ dk, char* __restrict__ dv) {
+                    int64_t bs, int64_t len_arg, char* __restrict__ dk, char* __restrict__ dv,
+                    const int64_t* __restrict__ len_dev) {
+    // with len_dev the arena length is read when the kernel runs (clamped into [0, Smax])
+    int64_t len = len_arg;
+    if (len_dev != nullptr) {
+        len = *len_dev;
+        len = len < 0 ? 0 : (len > Smax ? Smax : len);
+    }
     const int slot = blockIdx.x;
     const int64_t g = blockIdx.y;
     const int64_t b = blockIdx.z;
@@ -471,14 +488,14 @@ fetch_blocks_kernel(const char* __restrict__ ak, const char* __restrict__ av, co
 }
 
 int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t bs,
-                  int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream) {
+                  int64_t len, int method, void* k_dst, void* v_dst, hipStream_t stream, const int64_t* len_dev) {
     const int64_t row_bytes = h->D * h->esz;
     const size_t ab = arena_bytes(h);
     if (method == SPARDA_FETCH_KERNEL) {
         dim3 grid(static_cast<unsigned>(cap), static_cast<unsigned>(h->H), static_cast<unsigned>(h->B));
         hipLaunchKernelGGL(fetch_blocks_kernel, grid, dim3(kFetchThreads), 0, stream, h->dev, h->dev + ab, sel,
                            n_sel, static_cast<int>(cap), h->H, h->Smax, row_bytes, bs, len,
-                           static_cast<char*>(k_dst), static_cast<char*>(v_dst));
+                           static_cast<char*>(k_dst), static_cast<char*>(v_dst), len_dev);
         return check_hip(hipGetLastError(), "fetch_blocks_kernel");
     }
     // DMA: the selection to the host (one wait on the stream), then one copy

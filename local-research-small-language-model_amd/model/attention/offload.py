@@ -191,6 +191,15 @@ class HipOffloadAttention(BaseAttention):
         xv = self.wv(x).view(B, T, self.n_kv_head, self.head_dim)
         offset = kv_cache.current_len if kv_cache is not None else 0
         xq, xk = rotary_emb(xq, xk, offset=offset)
+        return self.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
+                                      forecast_vector=forecast_vector)
+
+    def forward_projected(self, xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor, kv_cache=None,
+                          is_causal: bool = True, forecast_vector: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The attention after the projections and RoPE (q [B,T,Hq,D], k / v
+        [B,T,Hkv,D] rotated at the cache's position): from forward, or from a
+        block whose fused producer computed them."""
+        T = xq.shape[1]
         if isinstance(kv_cache, OffloadedKVCache) and T == 1:
             return self._offload_decode(xq[:, 0], xk, xv, kv_cache, forecast_vector)
         if kv_cache is not None and T == 1:

@@ -18,63 +18,150 @@ when it runs:
   attention       the selected blocks of a cache holding *pos + 1 tokens
   LM head         logits of the step; *pos += 1 last
 
-so one recorded step serves every token: a step is one graph replay. The
-kernels and their launch shapes are those of the eager cached-prototype
-decode (HipSparseAttention with PrototypeKVCache and the fused producer), so
-a replayed step reproduces the eager step bit for bit while the cache holds
-more than top_k + 2 blocks.
+so one recorded step serves every token: a step is one graph replay.
 
-Requirements: HipSparseAttention layers, bf16 weights, head dim 64, forecast
-dim 64 (the fused producer's shape). Weights are read from the tensors that
-exist when the step is captured: capture (the first ``step``) after loading
-them, or call ``reset_graph`` after changing them.
+Layers of HipAsyncOffloadAttention keep their KV in a pinned host arena
+(AsyncOffloadedKVCache; layer 0 then keeps a GPU-resident KVCache and attends
+densely, as the eager path does). Layer L's block issues the prefetch of
+layer L+1 right after its producer has formed F_L (transformer.py:110-115):
+the selection from layer L+1's block sums (the lookahead before token *pos
+is appended, async_offload.py:196-260) and the gather of the selected blocks
+from the arena into device buffers, then an event that layer L+1 waits for;
+with overlap=True on a side stream, so that the copy over the host link runs
+under layer L's attention and FFN inside the graph. Layer L+1 then appends
+its token into the arena and attends over the fetched blocks with the new
+token supplied separately.
+
+The kernels and their launch shapes are those of the eager decode with the
+fused producer (HipSparseAttention with PrototypeKVCache, or
+HipAsyncOffloadAttention with AsyncOffloadedKVCache), so a replayed step
+reproduces the eager step bit for bit while the cache holds more than
+top_k + 2 blocks (below that the eager path attends every block through
+another wavefront split).
+
+Requirements: HipSparseAttention or HipAsyncOffloadAttention layers, bf16
+weights, head dim 64, forecast dim 64 (the fused producer's shape). Weights
+are read from the tensors that exist when the step is captured: capture (the
+first ``step``) after loading them, or call ``reset_graph`` after changing
+them.
 """
 
-from typing import List, Optional
+from typing import List, Optional, Sequence
 
 import torch
 import torch.nn.functional as F
 
 import sparda
+from model.attention.async_offload import AsyncOffloadedKVCache, HipAsyncOffloadAttention
+from model.attention.base import KVCache
 from model.attention.hip_sparse import HipSparseAttention, PrototypeKVCache
+
+_SPARSE, _RESIDENT_DENSE, _OFFLOAD = "sparse", "resident_dense", "offload"
 
 
 class GraphDecoder:
-    """Owns one PrototypeKVCache per layer and the device-held position."""
+    """Owns (or adopts) one cache per layer and the device-held position.
 
-    def __init__(self, model, batch_size: int, max_seq_len: int):
+    caches: None (a PrototypeKVCache per sparse layer; for offload layers a
+    GPU KVCache at layer 0 and an AsyncOffloadedKVCache elsewhere), or one
+    cache per layer of those types, all holding the same number of tokens
+    (their contents are decoded on from there). overlap=True issues the
+    offload prefetches on a side stream joined by an event before the layer
+    that needs them; the default issues them on the compute stream, which a
+    replayed graph runs faster here (each cross-stream dependency inside the
+    graph costs more than the ~20 us per layer of selection and host-link
+    copy it would hide)."""
+
+    def __init__(self, model, batch_size: int, max_seq_len: int, caches: Optional[Sequence] = None,
+                 overlap: bool = False):
         cfg = model.config
         p = next(model.parameters())
         self.device = p.device
         if not p.is_cuda or p.dtype != torch.bfloat16:
             raise TypeError("GraphDecoder: the model must be bf16 on the GPU")
-        for layer in model.layers:
+        kinds = []
+        for i, layer in enumerate(model.layers):
             a = layer.attention
-            if type(a) is not HipSparseAttention:
-                raise TypeError(f"GraphDecoder: layer {layer.layer_idx} uses {type(a).__name__}, "
-                                "not HipSparseAttention")
+            if type(a) is HipSparseAttention:
+                kinds.append(_SPARSE)
+            elif type(a) is HipAsyncOffloadAttention:
+                kinds.append(_RESIDENT_DENSE if i == 0 else _OFFLOAD)
+            else:
+                raise TypeError(f"GraphDecoder: layer {layer.layer_idx} uses {type(a).__name__}, not "
+                                "HipSparseAttention or HipAsyncOffloadAttention")
             if a.head_dim != 64 or layer.forecast.forecast_dim != 64:
                 raise ValueError("GraphDecoder: head dim and forecast dim must be 64")
         if max_seq_len > cfg.context_length:
             raise ValueError(f"GraphDecoder: max_seq_len {max_seq_len} beyond the context {cfg.context_length}")
         self.model = model
+        self.kinds = kinds
         self.B = batch_size
         self.max_len = max_seq_len
         self.block_size = cfg.block_size
-        self.caches: List[PrototypeKVCache] = [
-            PrototypeKVCache(batch_size, max_seq_len, cfg.n_kv_head, cfg.head_dim, self.device, torch.bfloat16,
-                             block_size=cfg.block_size) for _ in model.layers]
-        self.pos = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.overlap = overlap
+        bs, H, D = cfg.block_size, cfg.n_kv_head, cfg.head_dim
+        if caches is None:
+            caches = []
+            for kind in kinds:
+                if kind == _SPARSE:
+                    caches.append(PrototypeKVCache(batch_size, max_seq_len, H, D, self.device, torch.bfloat16,
+                                                   block_size=bs))
+                elif kind == _RESIDENT_DENSE:
+                    caches.append(KVCache(batch_size, max_seq_len, H, D, self.device, torch.bfloat16))
+                else:
+                    caches.append(AsyncOffloadedKVCache(batch_size, max_seq_len, H, D, self.device, torch.bfloat16,
+                                                        block_size=bs))
+        caches = list(caches)
+        want = {_SPARSE: PrototypeKVCache, _RESIDENT_DENSE: KVCache, _OFFLOAD: AsyncOffloadedKVCache}
+        if len(caches) != len(kinds):
+            raise ValueError("GraphDecoder: one cache per layer")
+        for i, (kind, c) in enumerate(zip(kinds, caches)):
+            if not isinstance(c, want[kind]) or (kind == _SPARSE and c.block_size != bs):
+                raise TypeError(f"GraphDecoder: layer {i} needs a {want[kind].__name__}")
+            cap = c.max_seq_len if kind == _OFFLOAD else c.k.shape[1]
+            nb_ = c.max_batch_size if kind == _OFFLOAD else c.k.shape[0]
+            if cap < max_seq_len or nb_ != batch_size:
+                raise ValueError(f"GraphDecoder: the cache of layer {i} is smaller than {batch_size} x {max_seq_len}")
+        lens = {c.current_len for c in caches}
+        if len(lens) != 1:
+            raise ValueError("GraphDecoder: the caches hold different numbers of tokens")
+        self.caches = caches
+        self.length = lens.pop()
+        self.pos = torch.full((1,), self.length, dtype=torch.int64, device=self.device)
         self.tok = torch.zeros((batch_size, 1), dtype=torch.int64, device=self.device)
-        self.length = 0
         self.cos, self.sin = model.rotary_emb.tables(max_seq_len, self.device)
+        # prefetch buffers and events of the offloaded layers
+        k = cfg.top_k_blocks
+        self._side = torch.cuda.Stream(device=self.device)
+        self._pf = {}
+        for i, kind in enumerate(kinds):
+            if kind == _OFFLOAD:
+                self._pf[i] = dict(
+                    sel=torch.empty((batch_size, H, k + 2), dtype=torch.int32, device=self.device),
+                    n=torch.empty((batch_size, H), dtype=torch.int32, device=self.device),
+                    k=torch.empty((batch_size, H, k + 2, bs, D), dtype=torch.bfloat16, device=self.device),
+                    v=torch.empty((batch_size, H, k + 2, bs, D), dtype=torch.bfloat16, device=self.device),
+                    ev=torch.cuda.Event())
+                caches[i].block_sums(bs)  # start the block sums before anything is captured
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.logits: Optional[torch.Tensor] = None
 
     # -- one decode step, every launch reading *pos --------------------------
-    def _attend(self, a: HipSparseAttention, q: torch.Tensor, cache: PrototypeKVCache,
+    def _attend(self, i: int, a, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 f: Optional[torch.Tensor]) -> torch.Tensor:
         bs = self.block_size
+        cache = self.caches[i]
+        kind = self.kinds[i]
+        if kind == _OFFLOAD:
+            pf = self._pf[i]
+            torch.cuda.current_stream().wait_event(pf["ev"])
+            cache.arena.append_at(k, v, self.pos, bs, cache.block_sums(bs))
+            return sparda.decode_at(q, pf["k"], pf["v"], self.pos, bs, pf["sel"], pf["n"], max_len=self.max_len,
+                                    compact=True, k_new=k[:, 0], v_new=v[:, 0])
+        if kind == _RESIDENT_DENSE:
+            sparda.append_at(cache.k, cache.v, self.pos, bs, None, k, v)
+            return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len)
+        sparda.append_at(cache.k, cache.v, self.pos, bs, cache.block_sums, k, v)
         if a.mode == "dense":
             return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len)
         if a.mode == "static" or f is None:
@@ -83,19 +170,39 @@ class GraphDecoder:
                                              self.max_len, bs, a.top_k_blocks, routing=a.decode_routing)
         return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, sel, n_sel, max_len=self.max_len)
 
+    def _prefetch(self, i: int, f: torch.Tensor):
+        """Selection + gather of layer i's blocks for this step, from layer i-1's forecast."""
+        a = self.model.layers[i].attention
+        cache, pf, bs = self.caches[i], self._pf[i], self.block_size
+        sparda.select_decode_at(f.reshape(self.B, a.n_kv_head, -1), cache.block_sums(bs), self.pos, self.max_len,
+                                bs, a.top_k_blocks, routing=a.decode_routing, sel=pf["sel"], n_sel=pf["n"],
+                                lookahead=True)
+        cache.arena.fetch_at(pf["sel"], pf["n"], bs, self.pos, pf["k"], pf["v"])
+
     def _step(self):
         m = self.model
         B = self.B
+        main = torch.cuda.current_stream()
         x = m.embeddings.embed(self.tok)
         prev_f = None
-        for layer, cache in zip(m.layers, self.caches):
+        n = len(m.layers)
+        for i, layer in enumerate(m.layers):
             a = layer.attention
             fc = layer.forecast
             q, k, v, f = sparda.produce(x, layer._fused_weight(), a.n_head * a.head_dim, a.n_kv_head * a.head_dim,
                                         fc.forecast_heads * fc.forecast_dim, layer.attn_norm.eps, self.cos,
                                         self.sin, f_dtype=x.dtype, pos_dev=self.pos)
-            sparda.append_at(cache.k, cache.v, self.pos, self.block_size, cache.block_sums, k, v)
-            out = self._attend(a, q[:, 0], cache, prev_f)
+            if i + 1 < n and self.kinds[i + 1] == _OFFLOAD:
+                ev = self._pf[i + 1]["ev"]
+                if self.overlap:
+                    self._side.wait_stream(main)
+                    with torch.cuda.stream(self._side):
+                        self._prefetch(i + 1, f)
+                        ev.record(self._side)
+                else:
+                    self._prefetch(i + 1, f)
+                    ev.record(main)
+            out = self._attend(i, a, q[:, 0], k, v, prev_f)
             x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
             x = x + layer.ffn(layer.ffn_norm(x))
             prev_f = f
@@ -108,12 +215,19 @@ class GraphDecoder:
                 layer._fused_weight()  # build the stacked weights outside the graph
             # warm-up step on a side stream (library handles, workspaces), then
             # the position is put back: the replay rewrites the same cache rows
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
+            # and recomputes the same block sums. The prefetch of an offloaded
+            # layer selects before its token is appended, so there the sums of
+            # the current block are rebuilt without the warm-up's token.
+            warm = torch.cuda.Stream()
+            warm.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(warm):
                 self._step()
                 self.pos.sub_(1)
-            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.current_stream().wait_stream(warm)
+            for i, kind in enumerate(self.kinds):
+                if kind == _OFFLOAD:
+                    c = self.caches[i]
+                    c.arena.rebuild_sums(self.length, self.block_size, c.block_sums(self.block_size))
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):

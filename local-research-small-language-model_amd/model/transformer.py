@@ -80,7 +80,8 @@ class TransformerBlock(nn.Module):
 
     def _use_fused_producer(self, x: torch.Tensor, mask) -> bool:
         a = self.attention
-        return (getattr(self.config, "fused_producer", False) and type(a) is HipSparseAttention
+        return (getattr(self.config, "fused_producer", False)
+                and type(a) in (HipSparseAttention, HipOffloadAttention, HipAsyncOffloadAttention)
                 and mask is None and x.is_cuda and x.dtype == torch.bfloat16 and a.head_dim == 64
                 and self.forecast.forecast_dim == 64 and not torch.is_grad_enabled())
 

@@ -77,9 +77,11 @@ SIGNATURES = {
     "sparda_append_at": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                                 _i64, _i64, _p, _p]),
     "sparda_select_decode_at": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64,
-                                       _int, _f32, _p, _p, _i64, _p]),
-    "sparda_decode_at": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _p, _i64, _i64, _i64,
-                                _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
+                                       _int, _f32, _p, _p, _i64, _int, _p]),
+    "sparda_decode_at": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _i64, _p, _p,
+                                _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
+    "sparda_offload_fetch_at": (_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p]),
+    "sparda_offload_append_at": (_int, [_p, _p, _p, _i64, _i64, _p, _i64, _p, _p]),
     "sparda_offload_append": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
     "sparda_offload_rebuild_sums": (_int, [_p, _i64, _i64, _p, _p]),
     "sparda_offload_fetch": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p, _p, _p]),

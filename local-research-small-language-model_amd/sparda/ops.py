@@ -429,23 +429,30 @@ def _pos_ptr(pos_dev: torch.Tensor) -> int:
 
 
 def append_at(k_cache: torch.Tensor, v_cache: Optional[torch.Tensor], pos_dev: torch.Tensor, block_size: int,
-              block_sums: torch.Tensor, k_new: Optional[torch.Tensor] = None,
-              v_new: Optional[torch.Tensor] = None) -> torch.Tensor:
+              block_sums: Optional[torch.Tensor], k_new: Optional[torch.Tensor] = None,
+              v_new: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """Decode-step cache append at token p = pos_dev (a one-element int64 device
     tensor, read when the kernel runs): k_new / v_new ([B,1,Hkv,D] or
     [B,Hkv,D]) written as row p of the caches [B,Smax,Hkv,D] (KVCache.update,
     model/attention/base.py:19-29), and the fp32 sums of the block holding p
     recomputed over [p - p % bs, p] in block_sums (in place; returned). Without
-    k_new / v_new only the sums are recomputed."""
+    k_new / v_new only the sums are recomputed; without block_sums only the
+    rows are written."""
     dev = require_device(k_cache, v_cache, block_sums, pos_dev, k_new, v_new)
     _inference_only(k_cache, v_cache, k_new, v_new)
-    if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
-        raise TypeError("sparda: block sums must be contiguous float32")
     if k_cache.stride(-1) != 1:
         raise ValueError("sparda: the cache's last dimension must be contiguous")
     B, S, Hkv, D = k_cache.shape
-    if tuple(block_sums.shape[:1]) != (B,) or tuple(block_sums.shape[2:]) != (Hkv, D):
-        raise AssertionError(f"Mismatch: cache {tuple(k_cache.shape)} vs block sums {tuple(block_sums.shape)}")
+    if block_sums is None:
+        if k_new is None:
+            raise ValueError("sparda: append_at needs new rows or block sums")
+        nbs = (S + block_size - 1) // block_size
+    else:
+        if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
+            raise TypeError("sparda: block sums must be contiguous float32")
+        if tuple(block_sums.shape[:1]) != (B,) or tuple(block_sums.shape[2:]) != (Hkv, D):
+            raise AssertionError(f"Mismatch: cache {tuple(k_cache.shape)} vs block sums {tuple(block_sums.shape)}")
+        nbs = block_sums.shape[1]
     nsb = nsh = 0
     if (k_new is None) != (v_new is None):
         raise ValueError("sparda: k_new and v_new go together")
@@ -459,21 +466,24 @@ def append_at(k_cache: torch.Tensor, v_cache: Optional[torch.Tensor], pos_dev: t
         if k_new.stride() != v_new.stride():
             raise ValueError("sparda: k_new and v_new must share strides")
         nsb, nsh, _ = k_new.stride()
-    max_len = min(S, block_sums.shape[1] * block_size)
+    max_len = min(S, nbs * block_size)
     sb, st, sh, _ = k_cache.stride()
     call("sparda_append_at", k_cache.data_ptr(), v_cache.data_ptr() if v_cache is not None else None,
          _dtype_code(k_cache), sb, st, sh, k_new.data_ptr() if k_new is not None else None,
          v_new.data_ptr() if v_new is not None else None, nsb, nsh, B, Hkv, D, max_len, _pos_ptr(pos_dev),
-         block_size, block_sums.shape[1], block_sums.data_ptr(), _stream(dev))
+         block_size, nbs, block_sums.data_ptr() if block_sums is not None else None, _stream(dev))
     return block_sums
 
 
 def select_decode_at(forecast: torch.Tensor, block_sums: torch.Tensor, pos_dev: torch.Tensor, max_len: int,
                      block_size: int, top_k: int, routing: str = "reference", scale: Optional[float] = None,
-                     sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None):
+                     sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None,
+                     lookahead: bool = False):
     """select_decode for the decode step at token p = pos_dev (a one-element
     int64 device tensor, read when the kernel runs): length p + 1, query
-    position p; p is clamped below max_len."""
+    position p; with lookahead, length p (the prefetch issued before token p
+    is appended, model/attention/async_offload.py:196-260). p is clamped below
+    max_len."""
     dev = require_device(forecast, block_sums, pos_dev, sel, n_sel)
     if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
         raise TypeError("sparda: block_sums must be contiguous float32")
@@ -490,33 +500,54 @@ def select_decode_at(forecast: torch.Tensor, block_sums: torch.Tensor, pos_dev: 
     call("sparda_select_decode_at", forecast.data_ptr(), _dtype_code(forecast), fsb, fsh, block_sums.data_ptr(),
          B, Hkv, D, nbs, max_len, _pos_ptr(pos_dev), block_size, top_k,
          _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE, float(scale),
-         sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], _stream(dev))
+         sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], int(bool(lookahead)), _stream(dev))
     return sel, n_sel
 
 
 def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.Tensor, block_size: int,
               sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None, window: int = 0,
               max_len: Optional[int] = None, scale: Optional[float] = None,
-              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+              out: Optional[torch.Tensor] = None, compact: bool = False, k_new: Optional[torch.Tensor] = None,
+              v_new: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Decode attention of q [B,Hq,D] at token p = pos_dev (a one-element int64
     device tensor, read when the kernel runs) over the caches [B,Smax,Hkv,D]
     holding p + 1 tokens: the blocks sel[b,g,:n_sel], or with sel None the
     static window of `window` blocks (+ sink; every block while the cache has
-    at most window + 2), or every block (window 0). p is clamped below max_len
-    (default: the cache capacity)."""
-    dev = require_device(q, k, v, pos_dev, sel, n_sel)
-    _inference_only(q, k, v)
+    at most window + 2), or every block (window 0). compact: k / v are fetched
+    block buffers [B,Hkv,cap,bs,D] (slot i = block sel[b,g,i]); k_new / v_new
+    [B,Hkv,D]: the key and value of position p. p is clamped below max_len
+    (default: the cache capacity; required with compact)."""
+    dev = require_device(q, k, v, pos_dev, sel, n_sel, k_new, v_new)
+    _inference_only(q, k, v, k_new, v_new)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("sparda: q, k and v must share a dtype")
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     if k.stride() != v.stride():
         raise ValueError("sparda: k and v must share strides")
     B, Hq, D = q.shape
-    Hkv = k.shape[2]
-    if max_len is None:
-        max_len = k.shape[1]
-    if not 0 < max_len <= k.shape[1]:
-        raise ValueError(f"sparda: max_len={max_len} outside the cache (capacity {k.shape[1]})")
+    if compact:
+        if sel is None or max_len is None:
+            raise ValueError("sparda: compact block buffers need a selection and max_len")
+        _, Hkv, cap_, bs_, _ = k.shape
+        if bs_ != block_size or cap_ != sel.shape[-1]:
+            raise ValueError("sparda: compact buffers must be [B,Hkv,sel_cap,block_size,D]")
+        kv_sb, kv_sh, _, kv_ss, _ = k.stride()
+    else:
+        Hkv = k.shape[2]
+        if max_len is None:
+            max_len = k.shape[1]
+        if not 0 < max_len <= k.shape[1]:
+            raise ValueError(f"sparda: max_len={max_len} outside the cache (capacity {k.shape[1]})")
+        kv_sb, kv_ss, kv_sh, _ = k.stride()
+    nsb = nsh = 0
+    if (k_new is None) != (v_new is None):
+        raise ValueError("sparda: k_new and v_new go together")
+    if k_new is not None:
+        k_new = _rowmajor(k_new.reshape(B, Hkv, D))
+        v_new = _rowmajor(v_new.reshape(B, Hkv, D))
+        if k_new.stride() != v_new.stride():
+            raise ValueError("sparda: k_new and v_new must share strides")
+        nsb, nsh, _ = k_new.stride()
     cap = 0
     if sel is not None:
         if sel.dtype != torch.int32 or n_sel is None or n_sel.dtype != torch.int32:
@@ -527,12 +558,13 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
         scale = default_scale(D)
     if out is None:
         out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
-    kv_sb, kv_ss, kv_sh, _ = k.stride()
     qsb, qsh, _ = q.stride()
     call("sparda_decode_at", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
-         _dtype_code(q), sel.data_ptr() if sel is not None else None,
-         n_sel.data_ptr() if n_sel is not None else None, cap, int(window), B, max_len, _pos_ptr(pos_dev),
-         Hq, Hkv, D, block_size, float(scale), out.data_ptr(), out.stride(0), _stream(dev))
+         _dtype_code(q), int(bool(compact)), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap, int(window),
+         k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
+         nsb, nsh, B, max_len, _pos_ptr(pos_dev), Hq, Hkv, D, block_size, float(scale), out.data_ptr(),
+         out.stride(0), _stream(dev))
     return out
 
 
@@ -665,3 +697,38 @@ class OffloadArena:
             raise TypeError("sparda: fetch destinations must have the arena dtype")
         call("sparda_offload_fetch", self.handle, sel.contiguous().data_ptr(), n_sel.contiguous().data_ptr(),
              cap, block_size, length, method, k_dst.data_ptr(), v_dst.data_ptr(), _stream(dev))
+
+    def fetch_at(self, sel: torch.Tensor, n_sel: torch.Tensor, block_size: int, len_dev: torch.Tensor,
+                 k_dst: torch.Tensor, v_dst: torch.Tensor) -> None:
+        """fetch (gather kernel) with the arena length read from device memory
+        (len_dev: a one-element int64 GPU tensor, clamped into [0, max_seq])."""
+        dev = require_device(sel, n_sel, k_dst, v_dst, len_dev)
+        if not (k_dst.is_contiguous() and v_dst.is_contiguous()):
+            raise ValueError("sparda: fetch destinations must be contiguous")
+        cap = sel.shape[-1]
+        if tuple(k_dst.shape) != (self.B, self.Hkv, cap, block_size, self.D) or k_dst.shape != v_dst.shape:
+            raise ValueError("sparda: fetch destinations must be [B,Hkv,sel_cap,block_size,D]")
+        if k_dst.dtype != self.dtype or v_dst.dtype != self.dtype:
+            raise TypeError("sparda: fetch destinations must have the arena dtype")
+        if not (sel.is_contiguous() and n_sel.is_contiguous()):
+            raise ValueError("sparda: sel / n_sel must be contiguous")
+        call("sparda_offload_fetch_at", self.handle, sel.data_ptr(), n_sel.data_ptr(), cap, block_size,
+             _pos_ptr(len_dev), k_dst.data_ptr(), v_dst.data_ptr(), _stream(dev))
+
+    def append_at(self, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.Tensor, block_size: int = 0,
+                  block_sums: Optional[torch.Tensor] = None) -> None:
+        """One token k, v ([B,1,Hkv,D] or [B,Hkv,D], device) into the arena at row
+        pos_dev (a one-element int64 GPU tensor, read when the kernel runs),
+        with its block's sums recomputed from the arena when block_sums is given."""
+        dev = require_device(k, v, block_sums, pos_dev)
+        if k.dtype != self.dtype or v.dtype != self.dtype:
+            raise TypeError(f"sparda: arena holds {self.dtype}, got {k.dtype}/{v.dtype}")
+        k = _rowmajor(k.reshape(self.B, self.Hkv, self.D))
+        v = _rowmajor(v.reshape(self.B, self.Hkv, self.D))
+        if k.stride() != v.stride():
+            k, v = k.contiguous(), v.contiguous()
+        if block_sums is not None and (block_sums.dtype != torch.float32 or not block_sums.is_contiguous()):
+            raise TypeError("sparda: block sums must be contiguous float32")
+        nsb, nsh, _ = k.stride()
+        call("sparda_offload_append_at", self.handle, k.data_ptr(), v.data_ptr(), nsb, nsh, _pos_ptr(pos_dev),
+             block_size, block_sums.data_ptr() if block_sums is not None else None, _stream(dev))

@@ -135,19 +135,27 @@ def test_device_position_entry_argument_errors():
     _expect(-2, "sparda_append_at", P, P, 1, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 0, Q, 64, 4, P, None)
     _expect(-3, "sparda_append_at", P, P, 5, 256, 256, 64, P, P, 256, 64, 1, 4, 64, 256, Q, 64, 4, P, None)
     # select_decode_at: f, f_dtype, f_sb, f_sh, sums, B, Hkv, D, nb_stride, max_len, pos_dev, bs, k, routing,
-    #                   scale, sel, n_sel, sel_cap, stream
-    _expect(-1, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, None, 64, 8, 1, 0.125, P, P, 10, None)
-    _expect(-2, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 1, 100, Q, 64, 8, 1, 0.125, P, P, 10,
+    #                   scale, sel, n_sel, sel_cap, lookahead, stream
+    _expect(-1, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, None, 64, 8, 1, 0.125, P, P, 10, 0,
+            None)
+    _expect(-2, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 1, 100, Q, 64, 8, 1, 0.125, P, P, 10, 0,
             None)  # nb_stride < ceil(max_len / bs)
-    _expect(-2, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, Q, 64, 8, 1, 0.125, P, P, 9,
+    _expect(-2, "sparda_select_decode_at", P, 1, 1, 1, P, 1, 4, 64, 64, 100, Q, 64, 8, 1, 0.125, P, P, 9, 1,
             None)  # sel_cap < k + 2
-    # decode_at: q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, sel, n_sel, sel_cap, window_k, B, max_len,
-    #            pos_dev, Hq, Hkv, D, bs, scale, out, out_sb, stream
-    _expect(-1, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, None, None, 0, 8, 1, 100, None, 12, 4, 64, 64,
-            0.125, P, 1, None)
-    _expect(-6, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, P, P, 10, 8, 1, 100, Q, 12, 4, 64, 64, 0.125, P,
-            1, None)  # a list and a window
-    _expect(-2, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, None, None, 0, 33, 1, 100, Q, 12, 4, 64, 64,
-            0.125, P, 1, None)  # window > 32
-    _expect(-5, "sparda_decode_at", P, 1, 1, P + 2, P, 8, 8, 8, 1, None, None, 0, 8, 1, 100, Q, 12, 4, 64, 64,
-            0.125, P, 1, None)  # misaligned K
+    # decode_at: q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
+    #            k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, bs, scale, out, out_sb, stream
+    _expect(-1, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, 8, None, None, 0, 0, 1, 100, None,
+            12, 4, 64, 64, 0.125, P, 1, None)
+    _expect(-6, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, P, P, 10, 8, None, None, 0, 0, 1, 100, Q, 12, 4,
+            64, 64, 0.125, P, 1, None)  # a list and a window
+    _expect(-6, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 1, None, None, 0, 8, None, None, 0, 0, 1, 100, Q,
+            12, 4, 64, 64, 0.125, P, 1, None)  # compact buffers without a selection
+    _expect(-1, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, P, P, 10, 0, P, None, 8, 8, 1, 100, Q, 12, 4,
+            64, 64, 0.125, P, 1, None)  # k_new without v_new
+    _expect(-2, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, 33, None, None, 0, 0, 1, 100, Q,
+            12, 4, 64, 64, 0.125, P, 1, None)  # window > 32
+    _expect(-5, "sparda_decode_at", P, 1, 1, P + 2, P, 8, 8, 8, 1, 0, None, None, 0, 8, None, None, 0, 0, 1, 100,
+            Q, 12, 4, 64, 64, 0.125, P, 1, None)  # misaligned K
+    # offload entries at a device position (handle checks come first)
+    _expect(-7, "sparda_offload_fetch_at", None, P, P, 10, 64, Q, P, P, None)
+    _expect(-7, "sparda_offload_append_at", None, P, P, 256, 64, Q, 64, P, None)

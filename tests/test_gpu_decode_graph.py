@@ -185,3 +185,40 @@ def test_graph_generation_equals_eager_generation_and_replays_after_reset():
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"temperature {temperature}"
     assert gd.graph is not None  # the second generation replayed the step recorded by the first
+
+
+@pytest.mark.parametrize("routing", ["absolute", "reference"])
+def test_graph_replayed_offload_steps_equal_eager_async_offload(routing):
+    case(f"graph-replayed offload decode (prefetch on a side stream), {routing}")
+    from model.attention import AsyncOffloadedKVCache, KVCache
+    cfg = ModelConfig(n_layer=3, context_length=2048, block_size=64, top_k_blocks=8, decode_routing=routing,
+                      attention_backend="async_offload", fused_producer=True, norm_eps=1e-5)
+    torch.manual_seed(24)
+    model = SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval()
+    B, T0, n, cap = 2, 900, 100, 1100
+    g = torch.Generator().manual_seed(25)
+    ids = torch.randint(0, cfg.vocab_size, (B, T0 + n), generator=g).to(DEV)
+    caches = [KVCache(B, cap, cfg.n_kv_head, cfg.head_dim, DEV, torch.bfloat16)] + [
+        AsyncOffloadedKVCache(B, cap, cfg.n_kv_head, cfg.head_dim, DEV, torch.bfloat16, block_size=64)
+        for _ in range(cfg.n_layer - 1)]
+    gd = GraphDecoder(model, B, cap, overlap=True)
+    serial = GraphDecoder(model, B, cap, overlap=False)
+    with torch.no_grad():
+        want = [model(ids[:, :T0], kv_caches=caches)["logits"][:, -1]]
+        for t in range(T0, T0 + n):
+            want.append(model(ids[:, t:t + 1], kv_caches=caches)["logits"][:, -1])
+        got = [gd.prefill(ids[:, :T0])]
+        got_s = [serial.prefill(ids[:, :T0])]
+        for t in range(T0, T0 + n):
+            got.append(gd.step(ids[:, t:t + 1]).clone())
+            got_s.append(serial.step(ids[:, t:t + 1]).clone())
+    torch.cuda.synchronize()
+    for i, (a, b, c) in enumerate(zip(got, got_s, want)):
+        assert torch.equal(a, c), f"step {i}: max diff {(a.float() - c.float()).abs().max().item()}"
+        assert torch.equal(b, c), f"serial step {i}"
+    L = T0 + n
+    assert torch.equal(gd.caches[0].k[:, :L], caches[0].k[:, :L])
+    for c, e in zip(gd.caches[1:], caches[1:]):
+        assert c.current_len == e.current_len == L
+        assert torch.equal(c.cpu_k[:, :L], e.cpu_k[:, :L]) and torch.equal(c.cpu_v[:, :L], e.cpu_v[:, :L])
+        assert torch.equal(c.block_sums(64), e.block_sums(64))
