@@ -21,6 +21,11 @@ What it restates (citations into tyborra/local-research-Small-Language-Model):
                    model/attention/sparse.py:255-281, computed per query row in
                    float64 over exactly the allowed keys (never an O(T^2) mask)
 * ``attention_decode`` / ``decode_step`` — model/attention/sparse.py:99-183
+* ``teacher_block_scores`` — TeacherBlockSelector.forward steps 1-3,
+                   model/forecast.py:160-184 (head mean, block sums, causal 0)
+* ``dense_weights`` / ``teacher_block_mass`` — the dense softmax weights the
+                   teacher consumes (model/attention/dense.py with
+                   return_attn_weights), float64, then the block mass
 
 The compressor, scorer and top-k run in C (``sparda_oracle.c``) so that the
 fp32 summation / fma order is exactly the documented one; everything else is
