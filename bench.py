@@ -125,7 +125,7 @@ def bench_prefill(args, torch, sparda, synth):
             step(ev)
         evs[-1][3].synchronize()
         torch.cuda.synchronize()
-        ms_step = evs[0][0].elapsed_time(evs[-1][3]) / args.steps
+        ms_step_eager = evs[0][0].elapsed_time(evs[-1][3]) / args.steps
         ms_compress = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
         ms_route = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
         ms_attn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
@@ -136,6 +136,31 @@ def bench_prefill(args, torch, sparda, synth):
         t = torch.arange(PT, device="cuda")
         keys = (n.to(torch.int64) - 1) * BS + (t % BS + 1)
         pairs = int(keys.sum().item()) * (HQ // HKV)
+        # the step as a serving loop issues it: the three launches recorded once
+        # in a HIP graph, replayed once per step (no launch gaps from the host)
+        ref = out.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), "graph-replayed prefill step differs from the eager step"
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        torch.cuda.synchronize()
+        ms_step = e0.elapsed_time(e1) / args.steps
+        del g
     flops = 4 * D * pairs
     tflops = flops / (ms_attn * 1e-3) / 1e12
     comp_bytes = PB * PT * HKV * D * 2 + PB * (PT // BS) * HKV * D * 4
@@ -143,6 +168,7 @@ def bench_prefill(args, torch, sparda, synth):
     return {
         "ms_per_step": ms_step,
         "tok_s": PB * PT / (ms_step * 1e-3),
+        "ms_per_step_eager": ms_step_eager,
         "attn_ms": ms_attn,
         "attn_useful_flop": flops,
         "attn_tflops": tflops,
