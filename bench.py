@@ -693,6 +693,33 @@ def pmc_workload(args, torch, sparda, synth):
     return {"copy_bytes": COPY_BYTES}
 
 
+def cpu_decode_baseline(args, torch, synth):
+    """The reference's decode step restated op for op (oracle/reference_path.py:
+    whole-cache recompression, selection, topk compaction, gather, masked SDPA)
+    on the host cores, at the decode workload (B=8, 16K cache, bf16)."""
+    from oracle import reference_path as R
+    threads = args.cpu_threads or torch.get_num_threads()
+    torch.set_num_threads(threads)
+    x = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002)
+    q = x["q"][:, :, None, :]
+    k, v = x["k_cache"].transpose(1, 2), x["v_cache"].transpose(1, 2)
+    f = x["forecast"][:, None]
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        R.sparse_decode(q, k, v, DS, f, BS, TOPK)
+        first = time.perf_counter() - t0
+        reps = max(1, min(64, int(10.0 / max(first, 1e-3))))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            R.sparse_decode(q, k, v, DS, f, BS, TOPK)
+        dt = (time.perf_counter() - t0) / reps
+    return {"value": round(dt * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"the decode workload (B=8, 16K cache, bf16) through the reference's decode step restated "
+                      f"op for op in PyTorch (whole-cache recompression, selection with the reference's row-0 "
+                      f"mask, topk compaction, gather, masked SDPA); {reps} timed step(s) after 1 warm-up, "
+                      f"torch threads={threads}"}
+
+
 def cpu_baseline(args, torch, synth):
     """Reference path restated op for op (oracle/reference_path.py), host CPU."""
     from oracle import reference_path as R
@@ -769,11 +796,13 @@ def main():
     tch = bench_teacher(args, torch, sparda, synth)
     log(f"teacher: kernel {tch['us_kernel']:.1f} us ({tch['kernel_tflops']:.0f} TFLOP/s), materialised torch "
         f"{tch['us_materialised_torch']:.1f} us")
-    cpu = None
+    cpu = cpu_dec = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         cpu = cpu_baseline(args, torch, synth)
         log(f"cpu: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+        cpu_dec = cpu_decode_baseline(args, torch, synth)
+        log(f"cpu decode: {cpu_dec['value']:.1f} us/step on {cpu_dec['cores']} threads")
 
     traffic = load_traffic()
     t_attn = traffic.get("prefill_mfma_kernel")
@@ -808,6 +837,7 @@ def main():
             "steps": args.decode_steps,
             "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(dec["gbs"] / PEAK_HBM_GBS, 4), "traffic": t_dec},
+            "cpu_baseline": cpu_dec,
             "bytes_per_step": dec["bytes_per_step"],
             "k_stream_bytes": dec["k_stream_bytes"],
             "gathered_bytes": dec["gathered_bytes"],
