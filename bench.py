@@ -464,7 +464,7 @@ def bench_generate(args, torch, sparda, synth, batch=1):
     G, W = args.generate_steps, 8
     cap = MT + G + W + 64
     cfg = ModelConfig(n_layer=12, context_length=cap, block_size=BS, top_k_blocks=TOPK,
-                      attention_backend="hip_sparse", norm_eps=1e-5, fused_producer=True,
+                      attention_backend="hip_sparse", norm_eps=1e-5, fused_producer=True, fused_ffn=True,
                       decode_routing="absolute")
     torch.manual_seed(1007)
     model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
@@ -508,7 +508,7 @@ def bench_generate(args, torch, sparda, synth, batch=1):
     b8 = bench_generate(args, torch, sparda, synth, batch=8)
     return {
         "workload": f"greedy generation of {G} tokens after a {MT}-token prompt, 12-layer model of "
-                    "model_forward (fused producer, block sums kept in HBM, top-8 + sink + current, "
+                    "model_forward (fused producer and FFN, block sums kept in HBM, top-8 + sink + current, "
                     "absolute-position routing), bf16; step = one token per sequence through all layers "
                     "incl. LM head; B=1, and B=8 sequences decoded together (*_b8)",
         "us_per_token_eager": round(us_eager, 1),

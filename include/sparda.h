@@ -311,6 +311,25 @@ SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w
                               void* v, void* f, int f_dtype, void* stream);
 
 /*
+ * Feed-forward half of a block for decode-sized batches, fused: RMSNorm +
+ * SwiGLU + residual. Replaces, for the HIP model, ffn_norm -> SwiGLU -> add of
+ * TransformerBlock.forward (model/transformer.py:18-31, 126-129;
+ * model/norm.py:15-21) when M = B*T <= 16.
+ *   x: [M, C] bf16 rows (stride x_stride_row), C a multiple of 128 up to 1024.
+ *   w_gate_up: [2F, C] bf16 = [w_gate; w_up] with the RMSNorm weight folded
+ *     into the columns (w[f, c] * norm_weight[c]); w_down: [C, F] bf16, F a
+ *     multiple of 128 up to 2048.
+ *   act: [M, F] bf16 scratch (the SwiGLU activation); out: [M, C] bf16
+ *     (stride out_stride_row), out = x + w_down . (silu(g) * u),
+ *     g / u = (x . w_gate_up rows) / sqrt(mean(x^2) + eps), each projection,
+ *     silu, product and the down projection rounded to bf16 as the unfused
+ *     sequence rounds them.
+ */
+SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void* w_gate_up, const void* w_down,
+                                 int64_t M, int64_t C, int64_t F, float eps, void* act, void* out,
+                                 int64_t out_stride_row, void* stream);
+
+/*
  * fp32 block sums of a device KV cache, kept current across decode steps so
  * that decode selection (sparda_select_decode) reads the sums instead of
  * recompressing the whole cache every step as the reference's decode does

@@ -434,6 +434,23 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
                         k, v, f, f_dtype, stream);
 }
 
+SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void* w_gate_up, const void* w_down,
+                                 int64_t M, int64_t C, int64_t F, float eps, void* act, void* out,
+                                 int64_t out_stride_row, void* stream) {
+    SPARDA_REQUIRE(x && w_gate_up && w_down && act && out, SPARDA_ERR_NULL, "ffn_decode: null pointer");
+    SPARDA_REQUIRE(M >= 1 && M <= 16, SPARDA_ERR_SHAPE, "ffn_decode: %lld rows (decode batches of 1..16)",
+                   (long long)M);
+    SPARDA_REQUIRE(C >= 128 && C % 128 == 0 && C <= 1024, SPARDA_ERR_SHAPE,
+                   "ffn_decode: model width %lld must be a multiple of 128 up to 1024", (long long)C);
+    SPARDA_REQUIRE(F >= 128 && F % 128 == 0 && F <= 2048, SPARDA_ERR_SHAPE,
+                   "ffn_decode: hidden width %lld must be a multiple of 128 up to 2048", (long long)F);
+    SPARDA_REQUIRE(x_stride_row >= C && x_stride_row % 8 == 0 && out_stride_row >= C && out_stride_row % 8 == 0 &&
+                       aligned16(x) && aligned16(w_gate_up) && aligned16(w_down) && aligned16(act) && aligned16(out),
+                   SPARDA_ERR_STRIDE, "ffn_decode: rows and weights must be 16-byte aligned");
+    return launch_ffn_decode(x, x_stride_row, w_gate_up, w_down, M, C, F, eps, act, out, out_stride_row,
+                             static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_append_at(void* k_cache, void* v_cache, int dtype, int64_t sb, int64_t st, int64_t sh,
                                 const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,

@@ -191,6 +191,15 @@ __device__ __forceinline__ void block_sum(const void* __restrict__ kc, int64_t b
 namespace sparda {
 int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);
+// sum over each 16-lane group of a wavefront
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __shfl_xor(v, 8, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 1, 16);
+    return v;
+}
+
 }  // namespace sparda
 
 #define SPARDA_REQUIRE(cond, code, ...)                        \

@@ -21,6 +21,10 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
                    const int64_t* pos_dev = nullptr, int64_t rope_len = 0);
 
+// decode-sized feed-forward half of a block: RMSNorm (folded) + SwiGLU + residual
+int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const void* w_down, int64_t M,
+                      int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream);
+
 int launch_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb,
                         int64_t k_st, int64_t k_sh, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int causal,
                         float scale, float* mass, hipStream_t stream);

@@ -22,6 +22,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "mfma.h"
+#include "rows.h"
 
 namespace sparda {
 
@@ -183,25 +184,17 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// Decode shapes (M <= kRowsMax rows, a few tokens): the tiled kernel would run
-// N/128 workgroups and stream all of W' through a dozen CUs. Here a workgroup
-// owns 16 columns of one head (8 RoPE pairs: d0+p and d0+p+32, p < 8), so
-// N/16 workgroups share the weight read; a 16-lane group per column holds the
-// column's row of W' in registers (C/128 16-byte chunks per lane) and takes
-// the dot product with every x row, reduced across the group. The same lanes
-// see all of x's row, so each group also forms sum(x^2) for 1/rms. Results go
-// through LDS to the threads that rotate and store the pairs.
+// Decode shapes (M <= kRowsMaxM rows, a few tokens): the tiled kernel would
+// run N/128 workgroups and stream all of W' through a dozen CUs. Here a
+// workgroup owns 16 columns of one head (8 RoPE pairs: d0+p and d0+p+32,
+// p < 8), so N/16 workgroups share the weight read; the x rows are staged in
+// LDS, a 16-lane group per column holds the column's row of W' in registers
+// (C/128 16-byte chunks per lane) and takes the dot product with every x row,
+// reduced across the group. The same lanes see all of x's row, so each group
+// also forms sum(x^2) for 1/rms. Results go through LDS to the threads that
+// rotate and store the pairs.
 // ---------------------------------------------------------------------------
-constexpr int kRowsMax = 16;        // rows handled by the decode kernel
 constexpr int kRowsChunks = 16;     // C / 128 <= 16 (C <= 2048)
-
-__device__ __forceinline__ float row16_sum(float v) {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
-    return v;
-}
 
 template <int FDT>
 __global__ void __launch_bounds__(kPThreads)
@@ -210,7 +203,8 @@ produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t
                     const float* __restrict__ sinv, int64_t T, int64_t pos0, uint16_t* __restrict__ q,
                     uint16_t* __restrict__ k, uint16_t* __restrict__ v, void* __restrict__ f,
                     const int64_t* __restrict__ pos_dev, int64_t rope_len) {
-    __shared__ float ylds[kRowsMax][16];
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][C]
+    __shared__ float ylds[kRowsMaxM][16];
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
     const int wave = tid / kWave;
@@ -220,36 +214,23 @@ produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t
     const int d0 = (blockIdx.x % 4) * 8;
     const int n = nh + d0 + lc / 2 + 32 * (lc % 2);  // row of W'
     const int nch = C / 128;
-    uint4 wreg[kRowsChunks];
+    uint4 wreg[1][kRowsChunks];
     const uint16_t* wr = w + static_cast<int64_t>(n) * C + li * 8;
 #pragma unroll
     for (int i = 0; i < kRowsChunks; ++i)
-        if (i < nch) wreg[i] = *reinterpret_cast<const uint4*>(wr + i * 128);
-    for (int m = 0; m < M; ++m) {
-        const uint16_t* xr = x + m * x_st + li * 8;
-        float acc = 0.0f, ss = 0.0f;
+        if (i < nch) wreg[0][i] = *reinterpret_cast<const uint4*>(wr + i * 128);
+    stage_rows(x, x_st, M, C, xs);
+    float acc[1][kRowsMaxM], ss[kRowsMaxM];
 #pragma unroll
-        for (int i = 0; i < kRowsChunks; ++i) {
-            if (i < nch) {
-                const uint4 xv = *reinterpret_cast<const uint4*>(xr + i * 128);
-                const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-                const uint32_t ww[4] = {wreg[i].x, wreg[i].y, wreg[i].z, wreg[i].w};
+    for (int m = 0; m < kRowsMaxM; ++m) acc[0][m] = ss[m] = 0.0f;
+    rows_dot<1, kRowsChunks, true>(xs, M, C, nch, li, wreg, acc, ss);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x0 = __builtin_bit_cast(float, xw[e] << 16);
-                    const float x1 = __builtin_bit_cast(float, xw[e] & 0xFFFF0000u);
-                    const float w0 = __builtin_bit_cast(float, ww[e] << 16);
-                    const float w1 = __builtin_bit_cast(float, ww[e] & 0xFFFF0000u);
-                    acc = __builtin_fmaf(x0, w0, acc);
-                    acc = __builtin_fmaf(x1, w1, acc);
-                    ss = __builtin_fmaf(x0, x0, ss);
-                    ss = __builtin_fmaf(x1, x1, ss);
-                }
-            }
+    for (int m = 0; m < kRowsMaxM; ++m) {
+        if (m < M) {
+            const float a = row16_sum(acc[0][m]);
+            const float s2 = row16_sum(ss[m]);
+            if (li == 0) ylds[m][lc] = a / __builtin_sqrtf(s2 / static_cast<float>(C) + eps);
         }
-        acc = row16_sum(acc);
-        ss = row16_sum(ss);
-        if (li == 0) ylds[m][lc] = acc / __builtin_sqrtf(ss / static_cast<float>(C) + eps);
     }
     __syncthreads();
 
@@ -288,9 +269,10 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
                    const int64_t* pos_dev, int64_t rope_len) {
     const int64_t N = Nq + 2 * Nk + Nf;
-    if (M <= kRowsMax && C % 128 == 0 && C / 128 <= kRowsChunks) {
+    if (M <= kRowsMaxM && C % 128 == 0 && C / 128 <= kRowsChunks) {
+        const size_t lds = static_cast<size_t>(M * C) * 2;
 #define SPARDA_PRODUCE_ROWS(FDT_)                                                                            \
-    hipLaunchKernelGGL((produce_rows_kernel<FDT_>), dim3(static_cast<unsigned>(N / 16)), dim3(kPThreads), 0,  \
+    hipLaunchKernelGGL((produce_rows_kernel<FDT_>), dim3(static_cast<unsigned>(N / 16)), dim3(kPThreads), lds, \
                        stream, static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w),        \
                        static_cast<int>(M), static_cast<int>(C), static_cast<int>(Nq), static_cast<int>(Nk),  \
                        static_cast<int>(Nf), eps, cosv, sinv, T, pos0, static_cast<uint16_t*>(q),             \

@@ -45,8 +45,13 @@ class ModelConfig:
 
     # HIP model only: compute RMSNorm + the q / k / v / forecast projections +
     # RoPE of each block in one kernel (sparda.produce) when the attention
-    # backend is the GPU-resident one and the activations are bf16.
+    # backend is one of the HIP ones and the activations are bf16.
     fused_producer: bool = False
+
+    # HIP model only: for decode-sized batches (B*T <= 16 rows, bf16, no
+    # autograd) compute ffn_norm + SwiGLU + the residual add of each block in
+    # two kernels (sparda.ffn_decode).
+    fused_ffn: bool = False
 
     def __post_init__(self):
         assert self.n_embd == self.n_head * self.head_dim, (

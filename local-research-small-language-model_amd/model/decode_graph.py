@@ -204,7 +204,7 @@ class GraphDecoder:
                     ev.record(main)
             out = self._attend(i, a, q[:, 0], k, v, prev_f)
             x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
-            x = x + layer.ffn(layer.ffn_norm(x))
+            x = layer.ffn_residual(x)
             prev_f = f
         self.logits = m.embeddings.project(m.final_norm(x))[:, -1, :]
         self.pos.add_(1)
@@ -213,6 +213,7 @@ class GraphDecoder:
         with torch.no_grad():
             for layer in self.model.layers:
                 layer._fused_weight()  # build the stacked weights outside the graph
+                layer._fused_ffn_weight()
             # warm-up step on a side stream (library handles, workspaces), then
             # the position is put back: the replay rewrites the same cache rows
             # and recomputes the same block sums. The prefetch of an offloaded

@@ -77,6 +77,8 @@ class TransformerBlock(nn.Module):
         self.ffn = SwiGLU(config.n_embd, config.ffn_dim)
         self._fused_w = None
         self._fused_key = None
+        self._ffn_w = None
+        self._ffn_key = None
 
     def _use_fused_producer(self, x: torch.Tensor, mask) -> bool:
         a = self.attention
@@ -97,6 +99,32 @@ class TransformerBlock(nn.Module):
                 self._fused_w = w.to(torch.bfloat16).contiguous()
             self._fused_key = key
         return self._fused_w
+
+    def _use_fused_ffn(self, x: torch.Tensor) -> bool:
+        C = x.shape[-1]
+        F_ = self.ffn.w_gate.out_features
+        return (getattr(self.config, "fused_ffn", False) and x.is_cuda and x.dtype == torch.bfloat16
+                and not torch.is_grad_enabled() and x.shape[0] * x.shape[1] <= 16
+                and C % 128 == 0 and C <= 1024 and F_ % 128 == 0 and F_ <= 2048)
+
+    def _fused_ffn_weight(self) -> torch.Tensor:
+        """[w_gate; w_up] with the FFN RMSNorm weight folded into the columns,
+        rebuilt when any of the parameters changed."""
+        ws = (self.ffn.w_gate.weight, self.ffn.w_up.weight, self.ffn_norm.weight)
+        key = tuple((t.data_ptr(), t._version) for t in ws)
+        if key != self._ffn_key:
+            with torch.no_grad():
+                w = torch.cat([ws[0].float(), ws[1].float()], dim=0) * ws[2].float()[None, :]
+                self._ffn_w = w.to(torch.bfloat16).contiguous()
+            self._ffn_key = key
+        return self._ffn_w
+
+    def ffn_residual(self, x: torch.Tensor) -> torch.Tensor:
+        """x + SwiGLU(ffn_norm(x)) (transformer.py:126-129); one fused pair of
+        kernels for decode-sized batches when the config asks for it."""
+        if self._use_fused_ffn(x):
+            return sparda.ffn_decode(x, self._fused_ffn_weight(), self.ffn.w_down.weight, self.ffn_norm.eps)
+        return x + self.ffn(self.ffn_norm(x))
 
     def forward(self, x: torch.Tensor, rotary_emb: RotaryEmbedding, kv_cache: Optional[KVCache] = None,
                 mask: Optional[torch.Tensor] = None, is_causal: bool = True,
@@ -121,8 +149,7 @@ class TransformerBlock(nn.Module):
             attn_out = a.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
                                            forecast_vector=prev_layer_forecast)
             x = x + attn_out
-            x = x + self.ffn(self.ffn_norm(x))
-            return x, current_forecast
+            return self.ffn_residual(x), current_forecast
         normed_x = self.attn_norm(x)
         current_forecast = self.forecast(normed_x)
         if next_layer_block is not None and next_kv_cache is not None:
@@ -131,5 +158,4 @@ class TransformerBlock(nn.Module):
         attn_out = self.attention(normed_x, rotary_emb=rotary_emb, kv_cache=kv_cache, mask=mask,
                                   is_causal=is_causal, forecast_vector=prev_layer_forecast)
         x = x + attn_out
-        x = x + self.ffn(self.ffn_norm(x))
-        return x, current_forecast
+        return self.ffn_residual(x), current_forecast

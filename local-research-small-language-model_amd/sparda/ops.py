@@ -421,6 +421,34 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
     return q, k, v, f
 
 
+def ffn_decode(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor, eps: float,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x + SwiGLU(RMSNorm(x)) for decode-sized batches (model/transformer.py:18-31,
+    126-129; model/norm.py:15-21): x [B,T,C] bf16 with B*T <= 16, w_gate_up
+    [2F, C] = [w_gate; w_up] * norm_weight (folded into the columns), w_down
+    [C, F], all bf16. Returns [B,T,C] bf16."""
+    dev = require_device(x, w_gate_up, w_down, out)
+    _inference_only(x, w_gate_up, w_down)
+    if not (x.dtype == w_gate_up.dtype == w_down.dtype == torch.bfloat16):
+        raise TypeError("sparda: ffn_decode takes bf16 activations and weights")
+    B, T, C = x.shape
+    x2 = x.reshape(B * T, C)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8:
+        x2 = x2.contiguous()
+    F = w_gate_up.shape[0] // 2
+    w_gate_up, w_down = w_gate_up.contiguous(), w_down.contiguous()
+    if tuple(w_gate_up.shape) != (2 * F, C) or tuple(w_down.shape) != (C, F):
+        raise AssertionError(f"Mismatch: w_gate_up {tuple(w_gate_up.shape)}, w_down {tuple(w_down.shape)} "
+                             f"for width {C}")
+    act = torch.empty((B * T, F), dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty((B, T, C), dtype=torch.bfloat16, device=dev)
+    o2 = out.view(B * T, C)
+    call("sparda_ffn_decode", x2.data_ptr(), x2.stride(0), w_gate_up.data_ptr(), w_down.data_ptr(), B * T, C, F,
+         float(eps), act.data_ptr(), o2.data_ptr(), o2.stride(0), _stream(dev))
+    return out
+
+
 def _pos_ptr(pos_dev: torch.Tensor) -> int:
     """Address of a device-held position: one int64 element on the GPU."""
     if pos_dev.dtype != torch.int64 or pos_dev.numel() != 1 or not pos_dev.is_cuda:

@@ -159,3 +159,13 @@ def test_device_position_entry_argument_errors():
     # offload entries at a device position (handle checks come first)
     _expect(-7, "sparda_offload_fetch_at", None, P, P, 10, 64, Q, P, P, None)
     _expect(-7, "sparda_offload_append_at", None, P, P, 256, 64, Q, 64, P, None)
+
+
+def test_ffn_decode_argument_errors():
+    P = 4096
+    # x, x_stride, w_gate_up, w_down, M, C, F, eps, act, out, out_stride, stream
+    _expect(-1, "sparda_ffn_decode", None, 768, P, P, 1, 768, 2048, 1e-5, P, P, 768, None)
+    _expect(-2, "sparda_ffn_decode", P, 768, P, P, 17, 768, 2048, 1e-5, P, P, 768, None)   # 17 rows
+    _expect(-2, "sparda_ffn_decode", P, 768, P, P, 1, 800, 2048, 1e-5, P, P, 800, None)    # C % 128
+    _expect(-2, "sparda_ffn_decode", P, 768, P, P, 1, 768, 4096, 1e-5, P, P, 768, None)    # F > 2048
+    _expect(-5, "sparda_ffn_decode", P + 2, 768, P, P, 1, 768, 2048, 1e-5, P, P, 768, None)

@@ -133,19 +133,19 @@ def test_produce_at_device_position_equals_host_position():
         assert torch.equal(a, b)
 
 
-def _model(mode, routing, n_layer=3, ctx=2048):
+def _model(mode, routing, n_layer=3, ctx=2048, fused_ffn=False):
     backend = {"forecast": "hip_sparse", "static": "static_sparse", "dense": "dense"}[mode]
     cfg = ModelConfig(n_layer=n_layer, context_length=ctx, block_size=64, top_k_blocks=8, decode_routing=routing,
-                      attention_backend=backend, fused_producer=True, norm_eps=1e-5)
+                      attention_backend=backend, fused_producer=True, fused_ffn=fused_ffn, norm_eps=1e-5)
     torch.manual_seed(21)
     return SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval(), cfg
 
 
-@pytest.mark.parametrize("mode,routing", [("forecast", "reference"), ("forecast", "absolute"),
-                                          ("static", "reference")])
-def test_graph_replayed_steps_equal_eager_cached_decode(mode, routing):
-    case(f"graph-replayed decode steps, {mode} {routing}")
-    model, cfg = _model(mode, routing)
+@pytest.mark.parametrize("mode,routing,fused_ffn", [("forecast", "reference", False), ("forecast", "absolute", False),
+                                                    ("static", "reference", False), ("forecast", "absolute", True)])
+def test_graph_replayed_steps_equal_eager_cached_decode(mode, routing, fused_ffn):
+    case(f"graph-replayed decode steps, {mode} {routing} fused_ffn={fused_ffn}")
+    model, cfg = _model(mode, routing, fused_ffn=fused_ffn)
     B, T0, n, cap = 2, 900, 100, 1100  # 15 blocks at the start, crossing 960 and 1024
     g = torch.Generator().manual_seed(22)
     ids = torch.randint(0, cfg.vocab_size, (B, T0 + n), generator=g).to(DEV)
@@ -192,7 +192,8 @@ def test_graph_replayed_offload_steps_equal_eager_async_offload(routing):
     case(f"graph-replayed offload decode (prefetch on a side stream), {routing}")
     from model.attention import AsyncOffloadedKVCache, KVCache
     cfg = ModelConfig(n_layer=3, context_length=2048, block_size=64, top_k_blocks=8, decode_routing=routing,
-                      attention_backend="async_offload", fused_producer=True, norm_eps=1e-5)
+                      attention_backend="async_offload", fused_producer=True, fused_ffn=routing == "absolute",
+                      norm_eps=1e-5)
     torch.manual_seed(24)
     model = SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval()
     B, T0, n, cap = 2, 900, 100, 1100

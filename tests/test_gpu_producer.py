@@ -110,3 +110,57 @@ def test_model_with_fused_producer_matches_unfused():
             m.layers[1].attn_norm.weight.mul_(1.5)
         _no_less_accurate(fused(ids[:, :300])["logits"], plain(ids[:, :300])["logits"],
                           ref(ids[:, :300])["logits"], "logits after a weight update")
+
+
+def _ffn_reference(x, wg, wu, wd, norm_w, eps):
+    """fp32: x + w_down(silu(w_gate(n)) * w_up(n)), n = RMSNorm(x) * norm_w."""
+    xf = x.float()
+    n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * norm_w.float()
+    g = n @ wg.float().t()
+    u = n @ wu.float().t()
+    return xf + (torch.nn.functional.silu(g) * u) @ wd.float().t()
+
+
+@pytest.mark.parametrize("M,C,F", [(1, 768, 2048), (16, 768, 2048), (5, 256, 512), (3, 1024, 128)])
+def test_ffn_decode_matches_fp32_reference(M, C, F):
+    case(f"ffn_decode M={M} C={C} F={F}")
+    torch.manual_seed(M * 1000 + C)
+    x = (torch.randn(M, 1, C) * 0.7).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(F, C) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(F, C) * 0.02).to(torch.bfloat16).to(DEV)
+    wd = (torch.randn(C, F) * 0.02).to(torch.bfloat16).to(DEV)
+    nw = (1.0 + 0.1 * torch.randn(C)).to(torch.bfloat16).to(DEV)
+    wgu = (torch.cat([wg.float(), wu.float()]) * nw.float()[None, :]).to(torch.bfloat16)
+    got = sparda.ffn_decode(x, wgu, wd, 1e-5)
+    ref = _ffn_reference(x, wg, wu, wd, nw, 1e-5)
+    assert_close_out(np32(got), ref.cpu().numpy(), torch.bfloat16, what="ffn_decode")
+    # (B, T) = (M, 1) and (1, M) rows are the same rows
+    got2 = sparda.ffn_decode(x.view(1, M, C), wgu, wd, 1e-5)
+    assert torch.equal(got2.view(M, 1, C), got)
+
+
+def test_model_with_fused_ffn_matches_unfused():
+    case("cached decode with / without the fused FFN (dense attention), vs fp32")
+    plain, fused = _pair(True), _pair(True, fused_ffn=True)
+    fused.load_state_dict(plain.state_dict())
+    ref = _pair(False).float()
+    ref.load_state_dict({k: v.float() for k, v in plain.state_dict().items()})
+    probe = torch.zeros(2, 1, 768, device=DEV, dtype=torch.bfloat16)
+    assert not fused.layers[1]._use_fused_ffn(probe)  # autograd on: unfused
+    with torch.no_grad():
+        assert fused.layers[1]._use_fused_ffn(probe)
+        assert not fused.layers[1]._use_fused_ffn(torch.zeros(2, 9, 768, device=DEV, dtype=torch.bfloat16))
+    g = torch.Generator().manual_seed(10)
+    ids = torch.randint(0, plain.config.vocab_size, (2, 700), generator=g).to(DEV)
+    with torch.no_grad():
+        caches = [[KVCache(2, 800, 4, 64, DEV, dt) for _ in range(2)]
+                  for dt in (torch.bfloat16, torch.bfloat16, torch.float32)]
+        for m, c in zip((plain, fused, ref), caches):
+            m(ids[:, :650], kv_caches=c)
+        for t in range(650, 660):
+            a, b, r = (m(ids[:, t:t + 1], kv_caches=c)["logits"] for m, c in zip((plain, fused, ref), caches))
+            _no_less_accurate(b, a, r, f"decode logits {t}")
+        for m in (plain, fused, ref):
+            m.layers[0].ffn_norm.weight.mul_(1.5)  # the folded weight follows parameter updates
+        a, b, r = (m(ids[:, 660:661], kv_caches=c)["logits"] for m, c in zip((plain, fused, ref), caches))
+        _no_less_accurate(b, a, r, "decode logits after a weight update")
