@@ -223,13 +223,12 @@ def bench_decode(args, torch, sparda, synth):
                             BS, TOPK, routing="absolute", workspace=ws)
         assert torch.equal(ref, outs[0]), "graph replay differs from eager decode"
         # cached prototypes: block sums kept in HBM, the step recomputes the
-        # current block's sums (64 tokens), selects from the sums and attends
-        # in place -- no whole-cache compression
+        # current block's sums (64 tokens), then one launch scores the blocks
+        # from the sums, selects and attends in place -- no whole-cache
+        # compression
         nb = DS // BS
         cb = (DS - 1) // BS
         sums = [torch.zeros((DB, nb, HKV, D), dtype=torch.float32, device="cuda") for _ in range(N_CACHES)]
-        sels = [torch.empty((DB, HKV, TOPK + 2), dtype=torch.int32, device="cuda") for _ in range(N_CACHES)]
-        nsel = [torch.empty((DB, HKV), dtype=torch.int32, device="cuda") for _ in range(N_CACHES)]
         outs_c = [torch.empty((DB, HQ * D), dtype=torch.bfloat16, device="cuda") for _ in range(N_CACHES)]
         for i, c in enumerate(caches):
             sparda.block_sums(c["k_cache"], 0, DS, BS, sums[i])
@@ -238,9 +237,8 @@ def bench_decode(args, torch, sparda, synth):
             j = i % N_CACHES
             c = caches[j]
             sparda.block_sums(c["k_cache"], cb * BS, DS - cb * BS, BS, sums[j])
-            sparda.select_decode(c["forecast"], sums[j], DS, DS - 1, BS, TOPK, routing="absolute",
-                                 sel=sels[j], n_sel=nsel[j])
-            sparda.decode_selected(c["q"], c["k_cache"], c["v_cache"], DS, BS, sels[j], nsel[j], out=outs_c[j])
+            sparda.decode_sums(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], sums[j], BS, TOPK,
+                               routing="absolute", out=outs_c[j])
 
         for i in range(8):
             one_cached(i)
@@ -259,8 +257,15 @@ def bench_decode(args, torch, sparda, synth):
         gc.replay()
         torch.cuda.synchronize()
         cached_us = events_ms(gc.replay, 3, torch) * 1e3 / args.decode_steps
-        assert torch.equal(sels[0], sparda.select_decode(caches[0]["forecast"], sums[0], DS, DS - 1, BS, TOPK,
-                                                         routing="absolute")[0])
+        # the cached step's selection equals the faithful step's, its output the
+        # attention over that selection
+        c0 = caches[0]
+        _, ex = sparda.decode(c0["q"], c0["k_cache"], c0["v_cache"], DS, c0["forecast"], BS, TOPK,
+                              routing="absolute", workspace=ws, want_sel=True)
+        o4, s4, n4 = sparda.decode_sums(c0["q"], c0["k_cache"], c0["v_cache"], DS, c0["forecast"], sums[0], BS,
+                                        TOPK, routing="absolute", want_sel=True)
+        assert torch.equal(s4, ex["sel"]) and torch.equal(n4, ex["n_sel"]), "cached selection differs"
+        assert torch.equal(o4, outs_c[0]), "graph-replayed cached step differs from the eager one"
     k_stream = DB * DS * HKV * D * 2
     small = DB * HQ * D * 2 * 2 + DB * HKV * D * 2 + DB * HKV * (DS // BS) * 4 * 2
     total = k_stream + gathered + small

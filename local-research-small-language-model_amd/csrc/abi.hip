@@ -434,6 +434,41 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
                         k, v, f, f_dtype, stream);
 }
 
+SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                  int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const void* forecast,
+                                  int f_dtype, int64_t f_sb, int64_t f_sh, const float* block_sums,
+                                  int64_t nb_stride, int64_t B, int64_t S, const int64_t* pos_dev, int64_t Hq,
+                                  int64_t Hkv, int64_t D, int64_t block_size, int64_t top_k, int routing,
+                                  float scale, float route_scale, int32_t* sel_out, int32_t* n_sel_out, void* out,
+                                  int64_t out_sb, void* stream) {
+    SPARDA_REQUIRE(q && k && v && out && forecast && block_sums, SPARDA_ERR_NULL, "decode_sums: null pointer");
+    SPARDA_REQUIRE(!sel_out == !n_sel_out, SPARDA_ERR_NULL, "decode_sums: sel_out and n_sel_out go together");
+    SPARDA_REQUIRE(!pos_dev || (reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "decode_sums: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(dtype_ok(dtype) && dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "decode_sums: dtype %d / %d unsupported",
+                   dtype, f_dtype);
+    SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
+                   "decode_sums: unknown routing %d", routing);
+    SPARDA_REQUIRE(B > 0 && S > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "decode_sums: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "decode_sums: head dim %lld not in {16,32,64,128}",
+                   (long long)D);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "decode_sums: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "decode_sums: top_k out of range");
+    SPARDA_REQUIRE(nb_stride >= cdiv(S, block_size) && cdiv(S, block_size) <= 4096, SPARDA_ERR_SHAPE,
+                   "decode_sums: need ceil(S/bs) <= nb_stride and <= 4096 blocks");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
+                   "decode_sums: block_sums must be 16-byte aligned");
+    SPARDA_REQUIRE(B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "decode_sums: grid too large");
+    const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
+    SPARDA_REQUIRE(aligned16(k) && aligned16(v) && kv_sb % ve == 0 && kv_ss % ve == 0 && kv_sh % ve == 0,
+                   SPARDA_ERR_STRIDE, "decode_sums: K/V rows must be 16-byte aligned");
+    return launch_decode_sums(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, forecast, f_dtype, f_sb, f_sh,
+                              block_sums, nb_stride, B, S, pos_dev, Hq, Hkv, D, block_size, top_k, routing, scale,
+                              route_scale, sel_out, n_sel_out, out, out_sb, static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void* w_gate_up, const void* w_down,
                                  int64_t M, int64_t C, int64_t F, float eps, void* act, void* out,
                                  int64_t out_stride_row, void* stream) {

@@ -107,8 +107,10 @@ decode_score_kernel(const void* __restrict__ kc, int64_t kv_sb, int64_t kv_ss, i
 // workgroup per (sequence, KV head), W wavefronts; wavefront w serves the
 // selected blocks w, w+W, ... sel_mode: 0 top-k of the launch-1 scores,
 // 1 dense (all blocks), 2 window {0} U [cb-k+1, cb] (every block while
-// cb+1 <= k+2), 3 the caller's list. With pos_dev the length comes from
-// device memory (S = *pos_dev + 1, clamped to the S argument).
+// cb+1 <= k+2), 3 the caller's list, 4 top-k of scores formed here from
+// block sums (cached prototypes; every block while cb+1 <= k+2). With pos_dev
+// the length comes from device memory (S = *pos_dev + 1, clamped to the S
+// argument).
 // For a block, lane i holds key row j*bs + i of K in registers and stages
 // the V row in the wave's LDS region (16-byte loads); it scores the R query
 // heads of the group (4 at a time), keeps a running (m, l, o) per head over
@@ -153,7 +155,9 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      int compact, const void* __restrict__ k_new, const void* __restrict__ v_new,
                      int64_t new_sb, int64_t new_sh,
                      int32_t* __restrict__ sel_out, int32_t* __restrict__ n_sel_out,
-                     void* __restrict__ out, int64_t out_sb, const int64_t* __restrict__ pos_dev) {
+                     void* __restrict__ out, int64_t out_sb, const int64_t* __restrict__ pos_dev,
+                     const float* __restrict__ sums, int64_t nb_stride, const void* __restrict__ fsel,
+                     int fsel_bf16, int64_t fs_sb, int64_t fs_sh, int absolute, float fscale, int pow2) {
     using E = typename KvElem<DT>::T;
     constexpr int VR = v_row_elems<DT, DH>();
     constexpr int KW = DT == SPARDA_BF16 ? DH / 2 : DH;  // K row words per lane
@@ -163,6 +167,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     __shared__ int32_t sel_lds[kMaxSlots + 6];
     __shared__ uint32_t ck_lds[kWave];  // selection candidates (keys, block indices)
     __shared__ int32_t ci_lds[kWave];
+    __shared__ float fsel_lds[DH];      // forecast of the selection from block sums
     __shared__ int n_lds;
 
     const int g = blockIdx.x;
@@ -191,9 +196,43 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             q_lds[e] = load_elem<DT>(q, b * q_sb + static_cast<int64_t>(g * R + hh) * q_sh + d) * scale_log2;
         }
     }
+    // sel_mode 4: every thread scores present blocks from the block sums (as
+    // select_decode_kernel does), keys parked in the dynamic region until the
+    // selection is made
+    uint32_t* key_lds = reinterpret_cast<uint32_t*>(dyn);
+    const bool dense4 = cb + 1 <= k + 2;
+    constexpr int kSumBatch = DH / 4 < 4 ? DH / 4 : 4;  // 16-byte loads in flight per score (register budget)
+    if (sel_mode == 4) {
+        for (int d = threadIdx.x; d < DH; d += blockDim.x) {
+            const int64_t fi = b * fs_sb + g * fs_sh + d;
+            fsel_lds[d] = fsel_bf16 ? load_elem<SPARDA_BF16>(fsel, fi) : load_elem<SPARDA_F32>(fsel, fi);
+        }
+        __syncthreads();
+        if (!dense4) {
+            const float den = static_cast<float>(bs);
+            const float inv = 1.0f / den;
+            const int limit = absolute ? cb : 0;
+            for (int j = threadIdx.x; j <= cb; j += blockDim.x) {
+                const float* sp = sums + ((b * nb_stride + j) * H + g) * DH;
+                const float sc = j > limit ? -__builtin_inff()
+                                           : (pow2 ? score_from_sum<DH, true, kSumBatch>(sp, fsel_lds, den, inv, fscale)
+                                                   : score_from_sum<DH, false, kSumBatch>(sp, fsel_lds, den, inv,
+                                                                                          fscale));
+                key_lds[j] = order_key(sc);
+            }
+        }
+        __syncthreads();
+    }
     if (wave == 0) {
         int m = 0;
-        if (sel_mode == 0) {
+        if (sel_mode == 4) {
+            if (dense4) {
+                m = cb + 1;  // every block 0..cb
+                if (lane < m) sel_lds[lane] = lane;
+            } else {
+                m = select_keys_upto<CH>(key_lds, cb + 1, k, cb, sel_lds, lane, ck_lds, ci_lds);
+            }
+        } else if (sel_mode == 0) {
             const float* srow = ws_scores + bg * NB;
             uint32_t kreg[CH];
 #pragma unroll
@@ -589,6 +628,10 @@ struct AttendArgs {
     int32_t* sel_out; int32_t* n_sel_out;
     void* out; int64_t out_sb;
     const int64_t* pos_dev = nullptr;  // S = *pos_dev + 1, S the bound (window / list modes)
+    // sel_mode 4: selection from block sums [B, nb_stride, Hkv, D] and a forecast [B, Hkv, D]
+    const float* sums = nullptr; int64_t nb_stride = 0;
+    const void* fsel = nullptr; int fsel_bf16 = 0; int64_t fs_sb = 0, fs_sh = 0;
+    int absolute = 0; float fscale = 0.0f;
 };
 
 static int launch_attend(const AttendArgs& a, hipStream_t stream) {
@@ -602,6 +645,7 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     const bool mf = a.dtype == SPARDA_BF16 && a.D == 64 && a.bs == 64 && (a.q_sb % 8) == 0 &&
                     (a.q_sh % 8) == 0 && (reinterpret_cast<uintptr_t>(a.q) & 15u) == 0;
     constexpr size_t kLdsBudget = 150 * 1024;
+    const int pow2 = (a.bs & (a.bs - 1)) == 0 ? 1 : 0;
     dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
 #define SPARDA_ATT(DT_, DH_, CH_)                                                                        \
     do {                                                                                                 \
@@ -619,12 +663,14 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
         const size_t pb = static_cast<size_t>(R) * (DH_ + 2) * 4;                                        \
         int waves = max_blocks < kAttendMaxWaves ? static_cast<int>(max_blocks) : kAttendMaxWaves;       \
         while (waves > 1 && ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb > kLdsBudget) --waves; \
-        const size_t lds = ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb;                  \
+        size_t lds = ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb;                        \
+        if (a.sel_mode == 4 && lds < static_cast<size_t>(NB) * 4) lds = static_cast<size_t>(NB) * 4;       \
         hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_, MF_>), grid2, dim3(waves * kWave), lds, stream, \
                            a.q, a.q_sb, a.q_sh, a.kc, a.vc, a.kv_sb, a.kv_ss, a.kv_sh, a.S, Hq_i, Hkv_i,  \
                            static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
-                           a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb, a.pos_dev);      \
+                           a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb, a.pos_dev, a.sums, \
+                           a.nb_stride, a.fsel, a.fsel_bf16, a.fs_sb, a.fs_sh, a.absolute, a.fscale, pow2);      \
     } while (0)
 #define SPARDA_ATT_C(DT_, DH_)                            \
     if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
@@ -718,6 +764,26 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
     AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S, Hq, Hkv, D, bs, cap > 2 ? cap - 2 : 0,
                  sel == nullptr ? 1 : 3, static_cast<int>(sel == nullptr ? 0 : cap), scale, nullptr,
                  sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb};
+    return launch_attend(a, stream);
+}
+
+int launch_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
+                       int64_t kv_ss, int64_t kv_sh, int dtype, const void* f, int f_dtype, int64_t f_sb,
+                       int64_t f_sh, const float* sums, int64_t nb_stride, int64_t B, int64_t S,
+                       const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int64_t top_k,
+                       int routing, float scale, float fscale, int32_t* sel_out, int32_t* n_sel_out, void* out,
+                       int64_t out_sb, hipStream_t stream) {
+    AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S, Hq, Hkv, D, bs, top_k, 4,
+                 static_cast<int>(top_k + 2), scale, nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0, 0,
+                 sel_out, n_sel_out, out, out_sb, pos_dev};
+    a.sums = sums;
+    a.nb_stride = nb_stride;
+    a.fsel = f;
+    a.fsel_bf16 = f_dtype == SPARDA_BF16 ? 1 : 0;
+    a.fs_sb = f_sb;
+    a.fs_sh = f_sh;
+    a.absolute = routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0;
+    a.fscale = fscale;
     return launch_attend(a, stream);
 }
 

@@ -295,19 +295,6 @@ int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sum
 constexpr int kSelThreads = 256;
 constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
 
-// top-k selection over the first n keys of key_lds, CH keys per lane
-template <int CH>
-__device__ __forceinline__ int select_keys(const uint32_t* key_lds, int n, int k, int own, int32_t* sel_lds,
-                                           int lane, uint32_t* ck_lds, int32_t* ci_lds) {
-    uint32_t kreg[CH];
-#pragma unroll
-    for (int e = 0; e < CH; ++e) {
-        const int j = e * kWave + lane;
-        kreg[e] = j < n ? key_lds[j] : 0u;
-    }
-    return wave_select_pre<CH>(kreg, n, k, own, sel_lds, ck_lds, ci_lds);
-}
-
 template <int FDT, int CH, int DH, bool POW2>
 __global__ void __launch_bounds__(kSelThreads)
 select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, const float* __restrict__ sums,
@@ -348,22 +335,9 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
         const float inv = 1.0f / den;
         const int64_t limit = score_pos / bs;
         for (int64_t j = tid; j < n_present; j += kSelThreads) {
-            float s = -__builtin_inff();
-            if (j <= limit) {
-                const float4* p = reinterpret_cast<const float4*>(sums + ((b * nb_stride + j) * H + g) * DH);
-                float4 v[DH / 4];
-#pragma unroll
-                for (int c = 0; c < DH / 4; ++c) v[c] = p[c];
-                float acc = 0.0f;
-#pragma unroll
-                for (int c = 0; c < DH / 4; ++c) {
-                    const float x[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc = __fmaf_rn(f_lds[4 * c + e], POW2 ? x[e] * inv : x[e] / den, acc);
-                }
-                s = acc * scale;
-            }
+            const float s = j <= limit ? score_from_sum<DH, POW2>(sums + ((b * nb_stride + j) * H + g) * DH, f_lds,
+                                                                 den, inv, scale)
+                                       : -__builtin_inff();
             key_lds[j] = order_key(s);
         }
     }
@@ -374,15 +348,7 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
             m = own + 1;
             if (lane < m) sel_lds[lane] = lane;
         } else {
-            // the smallest key-register count holding n_present keys (a device-held
-            // length may be far below the bound CH was chosen for)
-            const int n = static_cast<int>(n_present);
-            if (CH >= 64 && n > 1024)
-                m = select_keys<(CH >= 64 ? 64 : CH)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
-            else if (CH >= 16 && n > 256)
-                m = select_keys<(CH >= 16 ? 16 : CH)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
-            else
-                m = select_keys<4>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+            m = select_keys_upto<CH>(key_lds, static_cast<int>(n_present), k, own, sel_lds, lane, ck_lds, ci_lds);
             if (own >= n_present) {  // the own block holds no token yet: it has no score but is attended
                 if (lane == 0) sel_lds[m] = own;
                 m += 1;

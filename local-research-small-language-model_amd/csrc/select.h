@@ -298,4 +298,58 @@ __device__ __forceinline__ int wave_select_pre(const uint32_t (&kreg)[CH], int n
     return m;
 }
 
+// Decode score of one block from its fp32 sum: p = sum / bs, then the
+// canonical fma chain over d (f . p, d ascending), times scale. BATCH 16-byte
+// loads are issued before the part of the chain that consumes them (all DH/4
+// by default). For a power-of-two bs, sum * (1/bs) is the same correctly
+// rounded value as sum / bs (the reciprocal is exact), at the cost of one
+// multiply.
+template <int DH, bool POW2, int BATCH = DH / 4>
+__device__ __forceinline__ float score_from_sum(const float* __restrict__ sum, const float* f_lds, float den,
+                                                float inv, float scale) {
+    static_assert((DH / 4) % BATCH == 0, "BATCH must divide DH/4");
+    const float4* p = reinterpret_cast<const float4*>(sum);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c0 = 0; c0 < DH / 4; c0 += BATCH) {
+        float4 v[BATCH];
+#pragma unroll
+        for (int c = 0; c < BATCH; ++c) v[c] = p[c0 + c];
+#pragma unroll
+        for (int c = 0; c < BATCH; ++c) {
+            const float x[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc = __fmaf_rn(f_lds[4 * (c0 + c) + e], POW2 ? x[e] * inv : x[e] / den, acc);
+        }
+    }
+    return acc * scale;
+}
+
+// top-k selection over the first n keys of key_lds, CH keys per lane
+template <int CH>
+__device__ __forceinline__ int select_keys(const uint32_t* key_lds, int n, int k, int own, int32_t* sel_lds,
+                                           int lane, uint32_t* ck_lds, int32_t* ci_lds) {
+    uint32_t kreg[CH];
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+        const int j = e * kWave + lane;
+        kreg[e] = j < n ? key_lds[j] : 0u;
+    }
+    return wave_select_pre<CH>(kreg, n, k, own, sel_lds, ck_lds, ci_lds);
+}
+
+// select_keys with the smallest key-register count (4, 16 or 64, at most
+// CHMAX) holding n keys: a length known only on the device may be far below
+// the bound CHMAX was chosen for
+template <int CHMAX>
+__device__ __forceinline__ int select_keys_upto(const uint32_t* key_lds, int n, int k, int own, int32_t* sel_lds,
+                                                int lane, uint32_t* ck_lds, int32_t* ci_lds) {
+    if (CHMAX >= 64 && n > 1024)
+        return select_keys<(CHMAX >= 64 ? 64 : CHMAX)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+    if (CHMAX >= 16 && n > 256)
+        return select_keys<(CHMAX >= 16 ? 16 : CHMAX)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+    return select_keys<4>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+}
+
 }  // namespace sparda

@@ -89,11 +89,9 @@ class HipSparseAttention(BaseAttention):
         if f is not None:
             f = f.reshape(B, self.n_kv_head, -1)
         if f is not None and isinstance(cache, PrototypeKVCache) and cache.block_size == self.block_size:
-            # cached prototypes: select from the block sums, attend in place
-            S = cache.current_len
-            sel, n_sel = sparda.select_decode(f, cache.block_sums, S, S - 1, self.block_size,
-                                              self.top_k_blocks, routing=self.decode_routing)
-            out = sparda.decode_selected(xq[:, 0], cache.k, cache.v, S, self.block_size, sel, n_sel)
+            # cached prototypes: select from the block sums and attend in place, one launch
+            out = sparda.decode_sums(xq[:, 0], cache.k, cache.v, cache.current_len, f, cache.block_sums,
+                                     self.block_size, self.top_k_blocks, routing=self.decode_routing)
             return self.wo(out.view(B, 1, self.n_head * self.head_dim))
         out = sparda.decode(xq[:, 0], cache.k, cache.v, cache.current_len, f, self.block_size,
                             self.top_k_blocks, routing=self.decode_routing, workspace=self._ws)

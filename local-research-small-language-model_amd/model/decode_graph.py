@@ -12,10 +12,11 @@ when it runs:
   fused producer  RMSNorm + q/k/v/forecast projections + RoPE at *pos
   cache append    k / v row *pos written, and the fp32 sums of the block
                   holding it recomputed from its first token (one launch)
-  selection       layer 0 and static layers: the static window; forecast
-                  layers: top-k of the previous layer's forecast against the
-                  cached prototypes (block sums / bs), sink and own block
-  attention       the selected blocks of a cache holding *pos + 1 tokens
+  selection and   layer 0 and static layers: the static window; forecast
+  attention       layers: top-k of the previous layer's forecast against the
+                  cached prototypes (block sums / bs), sink and own block,
+                  scored and selected inside the attention launch; the
+                  selected blocks of a cache holding *pos + 1 tokens
   LM head         logits of the step; *pos += 1 last
 
 so one recorded step serves every token: a step is one graph replay.
@@ -166,9 +167,8 @@ class GraphDecoder:
             return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len)
         if a.mode == "static" or f is None:
             return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=a.top_k_blocks, max_len=self.max_len)
-        sel, n_sel = sparda.select_decode_at(f.reshape(self.B, a.n_kv_head, -1), cache.block_sums, self.pos,
-                                             self.max_len, bs, a.top_k_blocks, routing=a.decode_routing)
-        return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, sel, n_sel, max_len=self.max_len)
+        return sparda.decode_sums(q, cache.k, cache.v, self.max_len, f, cache.block_sums, bs, a.top_k_blocks,
+                                  routing=a.decode_routing, pos_dev=self.pos)
 
     def _prefetch(self, i: int, f: torch.Tensor):
         """Selection + gather of layer i's blocks for this step, from layer i-1's forecast."""

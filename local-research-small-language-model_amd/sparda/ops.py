@@ -421,6 +421,60 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
     return q, k, v, f
 
 
+def decode_sums(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, forecast: torch.Tensor,
+                block_sums: torch.Tensor, block_size: int, top_k: int, routing: str = "reference",
+                pos_dev: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                want_sel: bool = False, out: Optional[torch.Tensor] = None):
+    """One decode step with cached prototypes in a single launch: the blocks
+    are scored from the fp32 block sums [B,NBmax,Hkv,D] (sum / bs = the
+    prototypes of model/forecast.py:66-78), the top-k + sink + own block
+    selected (model/attention/sparse.py:126-154; every block while the cache
+    holds at most top_k + 2 blocks) and attended in place, inside the attention
+    kernel. q [B,Hq,D] at position S-1, caches [B,Smax,Hkv,D] holding [0, S),
+    forecast [B,Hkv,D]. With pos_dev (a one-element int64 GPU tensor) the
+    length is *pos_dev + 1, read when the kernel runs, S its bound.
+    Returns out [B,Hq*D], or (out, sel, n_sel) with want_sel."""
+    dev = require_device(q, k, v, forecast, block_sums, pos_dev)
+    _inference_only(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q and the caches must share a dtype")
+    if block_sums.dtype != torch.float32 or not block_sums.is_contiguous():
+        raise TypeError("sparda: block_sums must be contiguous float32")
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    if k.stride() != v.stride():
+        raise ValueError("sparda: k_cache and v_cache must share strides")
+    B, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if S > k.shape[1] or S <= 0:
+        raise ValueError(f"sparda: S={S} outside the cache (capacity {k.shape[1]})")
+    if routing not in ("reference", "absolute"):
+        raise ValueError(f"sparda: routing must be 'reference' or 'absolute', got {routing!r}")
+    forecast = _rowmajor(forecast.reshape(B, Hkv, -1) if forecast.dim() != 3 else forecast)
+    if forecast.shape[-1] != D or tuple(block_sums.shape[2:]) != (Hkv, D) or block_sums.shape[0] != B:
+        raise AssertionError(f"Mismatch: forecast {tuple(forecast.shape)} / block sums {tuple(block_sums.shape)} "
+                             f"for head dim {D}")
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
+    sel = n_sel = None
+    if want_sel:
+        sel = torch.empty((B, Hkv, top_k + 2), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, Hkv), dtype=torch.int32, device=dev)
+    qsb, qsh, _ = q.stride()
+    ksb, kss, ksh, _ = k.stride()
+    fsb, fsh, _ = forecast.stride()
+    call("sparda_decode_sums", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), ksb, kss, ksh, _dtype_code(q),
+         forecast.data_ptr(), _dtype_code(forecast), fsb, fsh, block_sums.data_ptr(), block_sums.shape[1], B, S,
+         _pos_ptr(pos_dev) if pos_dev is not None else None, Hq, Hkv, D, block_size, top_k,
+         _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE, float(scale),
+         float(default_scale(forecast.shape[-1])), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, out.data_ptr(), out.stride(0), _stream(dev))
+    if want_sel:
+        return out, sel, n_sel
+    return out
+
+
 def ffn_decode(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor, eps: float,
                out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """x + SwiGLU(RMSNorm(x)) for decode-sized batches (model/transformer.py:18-31,

@@ -169,3 +169,19 @@ def test_ffn_decode_argument_errors():
     _expect(-2, "sparda_ffn_decode", P, 768, P, P, 1, 800, 2048, 1e-5, P, P, 800, None)    # C % 128
     _expect(-2, "sparda_ffn_decode", P, 768, P, P, 1, 768, 4096, 1e-5, P, P, 768, None)    # F > 2048
     _expect(-5, "sparda_ffn_decode", P + 2, 768, P, P, 1, 768, 2048, 1e-5, P, P, 768, None)
+
+
+def test_decode_sums_argument_errors():
+    P = 4096
+    # q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, f, f_dtype, f_sb, f_sh, sums, nb_stride, B, S, pos_dev,
+    # Hq, Hkv, D, bs, top_k, routing, scale, route_scale, sel_out, n_sel_out, out, out_sb, stream
+    _expect(-1, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, None, 1, 1, 1, P, 64, 1, 100, None, 12, 4, 64, 64,
+            8, 1, 0.125, 0.125, None, None, P, 1, None)
+    _expect(-6, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 64, 1, 100, None, 12, 4, 64, 64,
+            8, 5, 0.125, 0.125, None, None, P, 1, None)  # unknown routing
+    _expect(-2, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 1, 1, 100, None, 12, 4, 64, 64,
+            8, 1, 0.125, 0.125, None, None, P, 1, None)  # nb_stride < ceil(S / bs)
+    _expect(-2, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 64, 1, 100, None, 12, 4, 64, 64,
+            40, 1, 0.125, 0.125, None, None, P, 1, None)  # top_k > 32
+    _expect(-5, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P + 4, 64, 1, 100, None, 12, 4, 64,
+            64, 8, 1, 0.125, 0.125, None, None, P, 1, None)  # misaligned block sums

@@ -107,3 +107,31 @@ def test_backend_decode_through_prototype_cache_equals_plain_cache(routing):
             assert_close_out(np32(b), np32(a), torch.float32, what=f"step {t}")
     nb = (T + 70 + 63) // 64
     assert torch.equal(proto.block_sums[:, :nb] / 64, sparda.compress(proto.k[:, :T + 70], 64))
+
+
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+@pytest.mark.parametrize("S,dtype", [(16384, torch.bfloat16), (16448, torch.bfloat16), (5000, torch.float32),
+                                     (300, torch.bfloat16)])
+def test_decode_sums_equals_separate_selection_and_attention(routing, S, dtype):
+    case(f"decode_sums (selection inside the attention launch) S={S} {dtype} {routing}")
+    B, Hq, Hkv, D, bs, k = 4, 12, 4, 64, 64, 8
+    x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=dtype, seed=41)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    nb = (S + bs - 1) // bs
+    sums = torch.zeros((B, nb + 5, Hkv, D), device=DEV)
+    sparda.block_sums(d["k_cache"], 0, S, bs, sums)
+    sel, n = sparda.select_decode(d["forecast"], sums, S, S - 1, bs, k, routing=routing)
+    want = sparda.decode_selected(d["q"], d["k_cache"], d["v_cache"], S, bs, sel, n)
+    out, sel4, n4 = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], sums, bs, k,
+                                       routing=routing, want_sel=True)
+    torch.cuda.synchronize()
+    assert torch.equal(n4, n) and torch.equal(sel4, sel)
+    if nb > k + 2:  # the same list through the same attention: bit-equal
+        assert torch.equal(out, want)
+    else:           # every block: decode_selected takes its own wavefront split
+        assert_close_out(np32(out), np32(want), dtype, what="dense fallback")
+    # at a device-held position, bounded by the cache capacity
+    pos = torch.full((1,), S - 1, dtype=torch.int64, device=DEV)
+    out_d = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], d["k_cache"].shape[1], d["forecast"], sums, bs,
+                               k, routing=routing, pos_dev=pos)
+    assert torch.equal(out_d, out)
