@@ -34,9 +34,9 @@ class RotaryEmbedding(nn.Module):
         self.head_dim = head_dim
         self.theta = theta
         self.max_seq_len = max_seq_len
-        cos, sin = rope_tables(head_dim, max_seq_len, theta)
-        self.register_buffer("cos", cos, persistent=False)
-        self.register_buffer("sin", sin, persistent=False)
+        # plain fp32 attributes, not buffers: Module.to(dtype) would round
+        # buffers to the model dtype; tables() moves them to the device in use
+        self.cos, self.sin = rope_tables(head_dim, max_seq_len, theta)
 
     def tables(self, need: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
         """fp32 cos, sin [L, head_dim/2] on `device`, L >= need."""
