@@ -221,6 +221,31 @@ def test_prefill_full_size_sampled_rows():
     _prefill_case(4, 4096, 12, 4, 64, 64, 8, torch.bfloat16, seed=1001, rows=rows)
 
 
+def test_prefill_long_context_16k_sampled_rows_and_selection_invariants():
+    # T = 16384 (256 blocks): the reference switches to its chunked path above
+    # 8192 tokens; this build keeps the per-token rule, checked here against the
+    # oracle on sampled rows, plus the invariants of every selection list
+    case("prefill B=1 T=16384 sampled")
+    T, bs, k = 16384, 64, 8
+    r = np.random.default_rng(5)
+    rows = sorted({(0, int(t)) for t in r.integers(0, T, 160)} | {(0, t) for t in (0, 63, 64, 8191, 8192, T - 1)})
+    _prefill_case(1, T, 12, 4, 64, bs, k, torch.bfloat16, seed=1005, rows=rows)
+    x = synth.prefill_inputs(1, T, 12, 4, 64, dtype=torch.bfloat16, seed=1005)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    _, _, sel, n = sparda.route(d["forecast"], sparda.compress(d["k"], bs), bs, k, want_topk=False, want_sel=True)
+    sel, n = sel.cpu().numpy(), n.cpu().numpy()
+    own = np.arange(T) // bs
+    assert (n >= 1).all() and (n <= k + 2).all()
+    assert (sel[..., 0] == 0).all()                                        # sink first
+    last = np.take_along_axis(sel, (n - 1)[..., None].astype(np.int64), -1)[..., 0]
+    assert (last == own[None, None, :]).all()                              # own block last
+    valid = np.arange(sel.shape[-1])[None, None, None, :] < n[..., None]
+    assert (np.where(valid, sel, 0) <= own[None, None, :, None]).all()     # causal
+    d_sel = np.diff(np.where(valid, sel, 1 << 30), axis=-1)
+    assert (d_sel[valid[..., 1:]] > 0).all()                               # ascending, no duplicates
+    assert (n[..., own >= k - 1] >= k).all()                               # k distinct picks once k blocks exist
+
+
 def test_prefill_topk_covering_all_blocks_equals_dense():
     case("prefill k>=NB == dense")
     x = synth.prefill_inputs(1, 640, 12, 4, 64, dtype=torch.bfloat16, seed=80)
