@@ -223,3 +223,23 @@ def test_graph_replayed_offload_steps_equal_eager_async_offload(routing):
         assert c.current_len == e.current_len == L
         assert torch.equal(c.cpu_k[:, :L], e.cpu_k[:, :L]) and torch.equal(c.cpu_v[:, :L], e.cpu_v[:, :L])
         assert torch.equal(c.block_sums(64), e.block_sums(64))
+
+
+def test_graph_decoder_sixteen_sequences_and_capacity_limit():
+    case("graph-replayed decode, 16 sequences (the largest decode-shape batch), up to the capacity")
+    model, cfg = _model("forecast", "absolute", n_layer=2, fused_ffn=True)
+    B, T0, cap = 16, 700, 712
+    g = torch.Generator().manual_seed(26)
+    ids = torch.randint(0, cfg.vocab_size, (B, cap), generator=g).to(DEV)
+    caches = [PrototypeKVCache(B, cap, cfg.n_kv_head, cfg.head_dim, DEV, torch.bfloat16, block_size=64)
+              for _ in range(cfg.n_layer)]
+    gd = GraphDecoder(model, B, cap)
+    with torch.no_grad():
+        model(ids[:, :T0], kv_caches=caches)
+        gd.prefill(ids[:, :T0])
+        for t in range(T0, cap):
+            want = model(ids[:, t:t + 1], kv_caches=caches)["logits"][:, -1]
+            got = gd.step(ids[:, t:t + 1])
+            assert torch.equal(got, want), f"position {t}"
+        with pytest.raises(ValueError):
+            gd.step(ids[:, :1])  # the caches are full
