@@ -135,3 +135,28 @@ def test_decode_sums_equals_separate_selection_and_attention(routing, S, dtype):
     out_d = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], d["k_cache"].shape[1], d["forecast"], sums, bs,
                                k, routing=routing, pos_dev=pos)
     assert torch.equal(out_d, out)
+
+
+def test_head_major_cache_layout_gives_the_same_decode():
+    # the kernels take element strides: a head-major cache ([B,Hkv,S,D] storage,
+    # each (head, block) one contiguous 8 KiB run) decodes exactly as the
+    # reference's token-major [B,S,Hkv,D] one
+    case("decode over a head-major (block-contiguous) cache")
+    B, S, Hq, Hkv, D, bs, k = 2, 5000, 12, 4, 64, 64, 8
+    x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=torch.bfloat16, seed=43)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    hk = d["k_cache"].transpose(1, 2).contiguous().transpose(1, 2)
+    hv = d["v_cache"].transpose(1, 2).contiguous().transpose(1, 2)
+    assert hk.stride() == (Hkv * S * D, D, S * D, 1)
+    for routing in ("reference", "absolute"):
+        a = sparda.decode(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], bs, k, routing=routing)
+        b = sparda.decode(d["q"], hk, hv, S, d["forecast"], bs, k, routing=routing)
+        assert torch.equal(a, b)
+    sa = torch.zeros((B, (S + bs - 1) // bs, Hkv, D), device=DEV)
+    sb = torch.zeros_like(sa)
+    sparda.block_sums(d["k_cache"], 0, S, bs, sa)
+    sparda.block_sums(hk, 0, S, bs, sb)
+    assert torch.equal(sa, sb)
+    a = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], sa, bs, k, routing="absolute")
+    b = sparda.decode_sums(d["q"], hk, hv, S, d["forecast"], sb, bs, k, routing="absolute")
+    assert torch.equal(a, b)
