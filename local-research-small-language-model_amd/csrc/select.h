@@ -222,13 +222,16 @@ __device__ __forceinline__ int wave_select(const uint32_t (&kreg)[CH], int n, in
     return m;
 }
 
-// The k-th largest of one key per lane (keys of empty lanes 0).
+// The k-th largest of one key per lane (keys of empty lanes 0): the largest
+// T with count(v >= T) >= k, two bits per round (the three candidate counts
+// of a round are independent ballots, so a round costs little more than one).
 __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
     uint32_t T = 0;
 #pragma unroll 4
-    for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t c = T | (1u << bit);
-        T = ballot_count(v >= c) >= k ? c : T;
+    for (int bit = 30; bit >= 0; bit -= 2) {
+        const uint32_t c1 = T | (1u << bit), c2 = T | (2u << bit), c3 = T | (3u << bit);
+        const int n1 = ballot_count(v >= c1), n2 = ballot_count(v >= c2), n3 = ballot_count(v >= c3);
+        T = n3 >= k ? c3 : (n2 >= k ? c2 : (n1 >= k ? c1 : T));
     }
     return T;
 }

@@ -108,9 +108,11 @@ def kernels(asm_text: str):
             out[cur] = []
             continue
         if cur is not None:
-            out[cur].append(l)
-            if "s_endpgm" in l:
+            # a kernel may end in several s_endpgm (early exits): read to its end label
+            if l.startswith(".Lfunc_end"):
                 cur = None
+                continue
+            out[cur].append(l)
     return out
 
 
