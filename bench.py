@@ -222,10 +222,10 @@ def bench_decode(args, torch, sparda, synth):
         ref = sparda.decode(caches[0]["q"], caches[0]["k_cache"], caches[0]["v_cache"], DS, caches[0]["forecast"],
                             BS, TOPK, routing="absolute", workspace=ws)
         assert torch.equal(ref, outs[0]), "graph replay differs from eager decode"
-        # cached prototypes: block sums kept in HBM, the step recomputes the
-        # current block's sums (64 tokens), then one launch scores the blocks
-        # from the sums, selects and attends in place -- no whole-cache
-        # compression
+        # cached prototypes: block sums kept in HBM; one launch recomputes the
+        # current block's sums (64 tokens), scores the blocks from the sums,
+        # selects and attends in place -- no whole-cache compression. Also
+        # timed with the sums update as a separate launch before it.
         nb = DS // BS
         cb = (DS - 1) // BS
         sums = [torch.zeros((DB, nb, HKV, D), dtype=torch.float32, device="cuda") for _ in range(N_CACHES)]
@@ -233,30 +233,35 @@ def bench_decode(args, torch, sparda, synth):
         for i, c in enumerate(caches):
             sparda.block_sums(c["k_cache"], 0, DS, BS, sums[i])
 
-        def one_cached(i):
+        def one_cached(i, separate=False):
             j = i % N_CACHES
             c = caches[j]
-            sparda.block_sums(c["k_cache"], cb * BS, DS - cb * BS, BS, sums[j])
+            if separate:
+                sparda.block_sums(c["k_cache"], cb * BS, DS - cb * BS, BS, sums[j])
             sparda.decode_sums(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], sums[j], BS, TOPK,
-                               routing="absolute", out=outs_c[j])
+                               routing="absolute", out=outs_c[j], update_current=not separate)
+
+        def replayed(separate):
+            gc = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for i in range(4):
+                    one_cached(i, separate)
+            torch.cuda.current_stream().wait_stream(side)
+            with torch.cuda.graph(gc):
+                for i in range(args.decode_steps):
+                    one_cached(i, separate)
+            gc.replay()
+            torch.cuda.synchronize()
+            return events_ms(gc.replay, 3, torch) * 1e3 / args.decode_steps
 
         for i in range(8):
             one_cached(i)
         torch.cuda.synchronize()
         eager_c_us = events_ms(lambda: [one_cached(i) for i in range(args.decode_steps)], 1, torch) * 1e3 / args.decode_steps
-        gc = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for i in range(4):
-                one_cached(i)
-        torch.cuda.current_stream().wait_stream(side)
-        with torch.cuda.graph(gc):
-            for i in range(args.decode_steps):
-                one_cached(i)
-        gc.replay()
-        torch.cuda.synchronize()
-        cached_us = events_ms(gc.replay, 3, torch) * 1e3 / args.decode_steps
+        cached_sep_us = replayed(True)
+        cached_us = replayed(False)
         # the cached step's selection equals the faithful step's, its output the
         # attention over that selection
         c0 = caches[0]
@@ -279,6 +284,7 @@ def bench_decode(args, torch, sparda, synth):
         "gathered_bytes": gathered,
         "us_per_step_cached_protos": cached_us,
         "us_per_step_cached_protos_eager": eager_c_us,
+        "us_per_step_cached_protos_separate_sums": cached_sep_us,
         "cached_bytes_per_step": cached_total,
     }
 
@@ -847,10 +853,12 @@ def main():
             "k_stream_bytes": dec["k_stream_bytes"],
             "gathered_bytes": dec["gathered_bytes"],
             "cached_prototypes": {
-                "workload": "the same step with fp32 block sums kept in HBM: recompute the current block's "
-                            "sums, select from the sums, attend in place (no whole-cache compression)",
+                "workload": "the same step with fp32 block sums kept in HBM: one launch recomputes the current "
+                            "block's sums, selects from the sums and attends in place (no whole-cache "
+                            "compression); *_separate_sums: the sums update as a launch of its own",
                 "us_per_step": round(dec["us_per_step_cached_protos"], 3),
                 "us_per_step_eager": round(dec["us_per_step_cached_protos_eager"], 3),
+                "us_per_step_separate_sums": round(dec["us_per_step_cached_protos_separate_sums"], 3),
                 "bytes_per_step": dec["cached_bytes_per_step"],
             },
         },

@@ -371,6 +371,41 @@ SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f
                                     int32_t* sel, int32_t* n_sel, int64_t sel_cap, void* stream);
 
 /*
+ * One decode step with cached prototypes, in a single launch. Replaces the
+ * decode branch of SparseAttention.forward after the projections
+ * (model/attention/sparse.py:99-183) for a cache whose fp32 block sums are kept
+ * current (PrototypeKVCache): instead of recompressing all S keys
+ * (sparse.py:133-135) the blocks are scored from the sums (prototype = sum /
+ * bs, model/forecast.py:66-78, scored as sparda_select_decode does), the
+ * ascending {0, cb} U top-k selected (sparse.py:126-154; every block 0..cb
+ * while cb + 1 <= top_k + 2) and attended in place (sparse.py:157-181).
+ *   q: [B,Hq,D] at position S-1; k/v: [B,Smax,Hkv,D] strides (kv_sb, kv_ss,
+ *     kv_sh, 1), rows 16-byte aligned; forecast: [B,Hkv,D] strides (f_sb,
+ *     f_sh, 1); D in {16, 32, 64, 128}
+ *   block_sums: [B,nb_stride,Hkv,D] fp32, 16-byte aligned, covering [0, S).
+ *     With update_current != 0 the sums of the current block cb are first
+ *     recomputed from its rows [cb*bs, S) in row order (what sparda_block_sums
+ *     with pos = cb*bs does) and stored, so a caller that appended the token
+ *     at S-1 needs no separate sums launch; the other blocks must be current.
+ *   pos_dev: NULL, or an 8-byte aligned int64 in device memory: then the
+ *     query is token *pos_dev (S = *pos_dev + 1, clamped into [1, S]) read
+ *     when the kernel runs
+ *   route_scale: the score scale (1/sqrt(D) in the reference); scale: the
+ *     attention scale
+ *   sel_out/n_sel_out: optional [B,Hkv,top_k+2] / [B,Hkv] int32 (together)
+ *   out: [B,Hq*D] of dtype, stride out_sb
+ */
+SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                  int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype,
+                                  const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                                  float* block_sums, int64_t nb_stride, int update_current,
+                                  int64_t B, int64_t S, const int64_t* pos_dev,
+                                  int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, int64_t top_k,
+                                  int routing, float scale, float route_scale,
+                                  int32_t* sel_out, int32_t* n_sel_out, void* out, int64_t out_sb,
+                                  void* stream);
+
+/*
  * Decode steps at a device-held position, so that one recorded sequence of
  * launches (a HIP graph) serves every step of a generation loop. The
  * reference's loop (SparDAResearchModel.generate, model/model.py:159-195, one

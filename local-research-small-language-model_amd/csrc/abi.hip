@@ -436,8 +436,9 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
 
 SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
                                   int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const void* forecast,
-                                  int f_dtype, int64_t f_sb, int64_t f_sh, const float* block_sums,
-                                  int64_t nb_stride, int64_t B, int64_t S, const int64_t* pos_dev, int64_t Hq,
+                                  int f_dtype, int64_t f_sb, int64_t f_sh, float* block_sums,
+                                  int64_t nb_stride, int update_current, int64_t B, int64_t S,
+                                  const int64_t* pos_dev, int64_t Hq,
                                   int64_t Hkv, int64_t D, int64_t block_size, int64_t top_k, int routing,
                                   float scale, float route_scale, int32_t* sel_out, int32_t* n_sel_out, void* out,
                                   int64_t out_sb, void* stream) {
@@ -465,7 +466,8 @@ SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, con
     SPARDA_REQUIRE(aligned16(k) && aligned16(v) && kv_sb % ve == 0 && kv_ss % ve == 0 && kv_sh % ve == 0,
                    SPARDA_ERR_STRIDE, "decode_sums: K/V rows must be 16-byte aligned");
     return launch_decode_sums(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, forecast, f_dtype, f_sb, f_sh,
-                              block_sums, nb_stride, B, S, pos_dev, Hq, Hkv, D, block_size, top_k, routing, scale,
+                              block_sums, nb_stride, update_current, B, S, pos_dev, Hq, Hkv, D, block_size, top_k,
+                              routing, scale,
                               route_scale, sel_out, n_sel_out, out, out_sb, static_cast<hipStream_t>(stream));
 }
 

@@ -156,7 +156,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      int64_t new_sb, int64_t new_sh,
                      int32_t* __restrict__ sel_out, int32_t* __restrict__ n_sel_out,
                      void* __restrict__ out, int64_t out_sb, const int64_t* __restrict__ pos_dev,
-                     const float* __restrict__ sums, int64_t nb_stride, const void* __restrict__ fsel,
+                     float* sums, int64_t nb_stride, int update_sums, const void* __restrict__ fsel,
                      int fsel_bf16, int64_t fs_sb, int64_t fs_sh, int absolute, float fscale, int pow2) {
     using E = typename KvElem<DT>::T;
     constexpr int VR = v_row_elems<DT, DH>();
@@ -206,6 +206,33 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
         for (int d = threadIdx.x; d < DH; d += blockDim.x) {
             const int64_t fi = b * fs_sb + g * fs_sh + d;
             fsel_lds[d] = fsel_bf16 ? load_elem<SPARDA_BF16>(fsel, fi) : load_elem<SPARDA_F32>(fsel, fi);
+        }
+        if (update_sums && threadIdx.x < DH / 2) {
+            // the current block's sums of head g from its rows [cb*bs, S), in
+            // row order (block_sums_kernel's order), 32 row loads in flight
+            const int dd = 2 * static_cast<int>(threadIdx.x);
+            const int64_t s0 = static_cast<int64_t>(cb) * bs;
+            const int nr = static_cast<int>(S - s0);
+            const int64_t base = b * kv_sb + g * kv_sh + dd;
+            float a0 = 0.0f, a1 = 0.0f;
+            for (int c0 = 0; c0 < nr; c0 += 32) {
+                float buf[32][2];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int r = c0 + i < nr ? c0 + i : nr - 1;
+                    load_vec<DT, 2>(kc, base + (s0 + r) * kv_ss, buf[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    if (c0 + i < nr) {
+                        a0 = a0 + buf[i][0];
+                        a1 = a1 + buf[i][1];
+                    }
+                }
+            }
+            float* cur = sums + ((b * nb_stride + cb) * H + g) * DH + dd;
+            cur[0] = a0;
+            cur[1] = a1;
         }
         __syncthreads();
         if (!dense4) {
@@ -628,8 +655,9 @@ struct AttendArgs {
     int32_t* sel_out; int32_t* n_sel_out;
     void* out; int64_t out_sb;
     const int64_t* pos_dev = nullptr;  // S = *pos_dev + 1, S the bound (window / list modes)
-    // sel_mode 4: selection from block sums [B, nb_stride, Hkv, D] and a forecast [B, Hkv, D]
-    const float* sums = nullptr; int64_t nb_stride = 0;
+    // sel_mode 4: selection from block sums [B, nb_stride, Hkv, D] and a forecast [B, Hkv, D];
+    // update_sums: recompute the current block's sums first
+    float* sums = nullptr; int64_t nb_stride = 0; int update_sums = 0;
     const void* fsel = nullptr; int fsel_bf16 = 0; int64_t fs_sb = 0, fs_sh = 0;
     int absolute = 0; float fscale = 0.0f;
 };
@@ -670,7 +698,8 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
                            static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
                            a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb, a.pos_dev, a.sums, \
-                           a.nb_stride, a.fsel, a.fsel_bf16, a.fs_sb, a.fs_sh, a.absolute, a.fscale, pow2);      \
+                           a.nb_stride, a.update_sums, a.fsel, a.fsel_bf16, a.fs_sb, a.fs_sh, a.absolute,       \
+                           a.fscale, pow2);                                                                    \
     } while (0)
 #define SPARDA_ATT_C(DT_, DH_)                            \
     if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
@@ -769,7 +798,7 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
 
 int launch_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
                        int64_t kv_ss, int64_t kv_sh, int dtype, const void* f, int f_dtype, int64_t f_sb,
-                       int64_t f_sh, const float* sums, int64_t nb_stride, int64_t B, int64_t S,
+                       int64_t f_sh, float* sums, int64_t nb_stride, int update_sums, int64_t B, int64_t S,
                        const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int64_t top_k,
                        int routing, float scale, float fscale, int32_t* sel_out, int32_t* n_sel_out, void* out,
                        int64_t out_sb, hipStream_t stream) {
@@ -778,6 +807,7 @@ int launch_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
                  sel_out, n_sel_out, out, out_sb, pos_dev};
     a.sums = sums;
     a.nb_stride = nb_stride;
+    a.update_sums = update_sums;
     a.fsel = f;
     a.fsel_bf16 = f_dtype == SPARDA_BF16 ? 1 : 0;
     a.fs_sb = f_sb;

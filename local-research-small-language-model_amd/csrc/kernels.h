@@ -71,7 +71,7 @@ int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, 
 // (S = host length, or *pos_dev + 1 clamped to S)
 int launch_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
                        int64_t kv_ss, int64_t kv_sh, int dtype, const void* f, int f_dtype, int64_t f_sb,
-                       int64_t f_sh, const float* sums, int64_t nb_stride, int64_t B, int64_t S,
+                       int64_t f_sh, float* sums, int64_t nb_stride, int update_sums, int64_t B, int64_t S,
                        const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int64_t top_k,
                        int routing, float scale, float fscale, int32_t* sel_out, int32_t* n_sel_out, void* out,
                        int64_t out_sb, hipStream_t stream);

@@ -36,7 +36,13 @@ class PrototypeKVCache(KVCache):
     decode step selects blocks from the sums instead of recompressing all S
     keys (model/attention/sparse.py:133-135). Each update recomputes the
     blocks it touches from their first token, so the sums equal a fresh
-    compression bit for bit."""
+    compression bit for bit.
+
+    A single-token append inside the current block leaves that block's sums
+    to the next decode launch (``current_block_stale``; decode_sums with
+    update_current recomputes them there); any other update, or a consumer
+    that reads ``block_sums`` directly after ``refresh_sums()``, sees them
+    current."""
 
     def __init__(self, max_batch_size: int, max_seq_len: int, n_kv_head: int, head_dim: int,
                  device: torch.device, dtype: torch.dtype, block_size: int = 64):
@@ -45,13 +51,31 @@ class PrototypeKVCache(KVCache):
         nb = (max_seq_len + block_size - 1) // block_size
         self.block_sums = torch.zeros((max_batch_size, nb, n_kv_head, head_dim), device=device,
                                       dtype=torch.float32)
+        self.current_block_stale = False
+
+    def refresh_sums(self) -> None:
+        """Bring the current block's sums up to date (after deferred appends)."""
+        if self.current_block_stale and self.current_len > 0:
+            first = ((self.current_len - 1) // self.block_size) * self.block_size
+            sparda.block_sums(self.k, first, self.current_len - first, self.block_size, self.block_sums)
+        self.current_block_stale = False
 
     def update(self, xk: torch.Tensor, xv: torch.Tensor):
         pos = self.current_len
+        same_block = pos > 0 and pos % self.block_size != 0
+        if not (xk.shape[1] == 1 and (same_block or not self.current_block_stale)):
+            self.refresh_sums()  # a deferred block that this update would leave behind
         out = super().update(xk, xv)
-        first = (pos // self.block_size) * self.block_size
-        sparda.block_sums(self.k, first, self.current_len - first, self.block_size, self.block_sums)
+        if xk.shape[1] == 1:
+            self.current_block_stale = True  # the decode launch recomputes it
+        else:
+            first = (pos // self.block_size) * self.block_size
+            sparda.block_sums(self.k, first, self.current_len - first, self.block_size, self.block_sums)
         return out
+
+    def reset(self):
+        super().reset()
+        self.current_block_stale = False
 
 
 class HipSparseAttention(BaseAttention):
@@ -91,7 +115,9 @@ class HipSparseAttention(BaseAttention):
         if f is not None and isinstance(cache, PrototypeKVCache) and cache.block_size == self.block_size:
             # cached prototypes: select from the block sums and attend in place, one launch
             out = sparda.decode_sums(xq[:, 0], cache.k, cache.v, cache.current_len, f, cache.block_sums,
-                                     self.block_size, self.top_k_blocks, routing=self.decode_routing)
+                                     self.block_size, self.top_k_blocks, routing=self.decode_routing,
+                                     update_current=cache.current_block_stale)
+            cache.current_block_stale = False
             return self.wo(out.view(B, 1, self.n_head * self.head_dim))
         out = sparda.decode(xq[:, 0], cache.k, cache.v, cache.current_len, f, self.block_size,
                             self.top_k_blocks, routing=self.decode_routing, workspace=self._ws)

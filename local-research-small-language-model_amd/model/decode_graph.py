@@ -126,6 +126,9 @@ class GraphDecoder:
         lens = {c.current_len for c in caches}
         if len(lens) != 1:
             raise ValueError("GraphDecoder: the caches hold different numbers of tokens")
+        for c in caches:
+            if isinstance(c, PrototypeKVCache):
+                c.refresh_sums()  # the recorded appends keep the sums current from here on
         self.caches = caches
         self.length = lens.pop()
         self.pos = torch.full((1,), self.length, dtype=torch.int64, device=self.device)
@@ -253,6 +256,9 @@ class GraphDecoder:
         if T >= self.max_len:
             raise ValueError(f"GraphDecoder: prompt of {T} leaves no room in {self.max_len}")
         logits = self.model(input_ids, kv_caches=self.caches)["logits"][:, -1, :]
+        for c in self.caches:
+            if isinstance(c, PrototypeKVCache):
+                c.refresh_sums()
         self.pos.fill_(T)
         self.length = T
         return logits

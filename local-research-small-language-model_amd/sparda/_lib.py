@@ -81,8 +81,8 @@ SIGNATURES = {
     "sparda_decode_at": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _i64, _p, _p,
                                 _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
     "sparda_decode_sums": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _p, _i64,
-                                  _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f32, _p, _p, _p, _i64,
-                                  _p]),
+                                  _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f32, _p, _p, _p,
+                                  _i64, _p]),
     "sparda_ffn_decode": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _i64, _p]),
     "sparda_offload_fetch_at": (_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p]),
     "sparda_offload_append_at": (_int, [_p, _p, _p, _i64, _i64, _p, _i64, _p, _p]),

@@ -424,7 +424,7 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
 def decode_sums(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, forecast: torch.Tensor,
                 block_sums: torch.Tensor, block_size: int, top_k: int, routing: str = "reference",
                 pos_dev: Optional[torch.Tensor] = None, scale: Optional[float] = None,
-                want_sel: bool = False, out: Optional[torch.Tensor] = None):
+                want_sel: bool = False, out: Optional[torch.Tensor] = None, update_current: bool = False):
     """One decode step with cached prototypes in a single launch: the blocks
     are scored from the fp32 block sums [B,NBmax,Hkv,D] (sum / bs = the
     prototypes of model/forecast.py:66-78), the top-k + sink + own block
@@ -432,7 +432,10 @@ def decode_sums(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, forec
     holds at most top_k + 2 blocks) and attended in place, inside the attention
     kernel. q [B,Hq,D] at position S-1, caches [B,Smax,Hkv,D] holding [0, S),
     forecast [B,Hkv,D]. With pos_dev (a one-element int64 GPU tensor) the
-    length is *pos_dev + 1, read when the kernel runs, S its bound.
+    length is *pos_dev + 1, read when the kernel runs, S its bound. With
+    update_current the sums of the block holding position S-1 are first
+    recomputed from its rows (as block_sums(k, cb*bs, S - cb*bs, ...) does)
+    and stored, so the caller needs no separate sums update after appending.
     Returns out [B,Hq*D], or (out, sel, n_sel) with want_sel."""
     dev = require_device(q, k, v, forecast, block_sums, pos_dev)
     _inference_only(q, k, v)
@@ -465,7 +468,8 @@ def decode_sums(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, forec
     ksb, kss, ksh, _ = k.stride()
     fsb, fsh, _ = forecast.stride()
     call("sparda_decode_sums", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), ksb, kss, ksh, _dtype_code(q),
-         forecast.data_ptr(), _dtype_code(forecast), fsb, fsh, block_sums.data_ptr(), block_sums.shape[1], B, S,
+         forecast.data_ptr(), _dtype_code(forecast), fsb, fsh, block_sums.data_ptr(), block_sums.shape[1],
+         1 if update_current else 0, B, S,
          _pos_ptr(pos_dev) if pos_dev is not None else None, Hq, Hkv, D, block_size, top_k,
          _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE, float(scale),
          float(default_scale(forecast.shape[-1])), sel.data_ptr() if sel is not None else None,

@@ -32,6 +32,20 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
 
 
+def test_every_exported_symbol_is_declared():
+    # the reverse: nothing the library exports (and the binding uses) is
+    # missing from the header a C caller compiles against
+    import subprocess
+    syms = set(header_symbols())
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True)
+    if out.returncode != 0:
+        pytest.skip("nm not available")
+    exported = set(re.findall(r"\b(sparda_\w+)$", out.stdout, flags=re.M))
+    assert exported, "no sparda_* symbols found in the library"
+    assert exported <= syms, f"exported but not declared in sparda.h: {sorted(exported - syms)}"
+    assert set(_lib.SIGNATURES) <= syms, f"bound but not declared: {sorted(set(_lib.SIGNATURES) - syms)}"
+
+
 def _expect(code, name, *args):
     with pytest.raises(sparda.SpardaArgumentError) as ei:
         _lib.call(name, *args)
@@ -173,15 +187,15 @@ def test_ffn_decode_argument_errors():
 
 def test_decode_sums_argument_errors():
     P = 4096
-    # q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, f, f_dtype, f_sb, f_sh, sums, nb_stride, B, S, pos_dev,
+    # q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, f, f_dtype, f_sb, f_sh, sums, nb_stride, update, B, S, pos_dev,
     # Hq, Hkv, D, bs, top_k, routing, scale, route_scale, sel_out, n_sel_out, out, out_sb, stream
-    _expect(-1, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, None, 1, 1, 1, P, 64, 1, 100, None, 12, 4, 64, 64,
+    _expect(-1, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, None, 1, 1, 1, P, 64, 0, 1, 100, None, 12, 4, 64, 64,
             8, 1, 0.125, 0.125, None, None, P, 1, None)
-    _expect(-6, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 64, 1, 100, None, 12, 4, 64, 64,
+    _expect(-6, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 64, 0, 1, 100, None, 12, 4, 64, 64,
             8, 5, 0.125, 0.125, None, None, P, 1, None)  # unknown routing
-    _expect(-2, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 1, 1, 100, None, 12, 4, 64, 64,
+    _expect(-2, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 1, 0, 1, 100, None, 12, 4, 64, 64,
             8, 1, 0.125, 0.125, None, None, P, 1, None)  # nb_stride < ceil(S / bs)
-    _expect(-2, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 64, 1, 100, None, 12, 4, 64, 64,
+    _expect(-2, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P, 64, 0, 1, 100, None, 12, 4, 64, 64,
             40, 1, 0.125, 0.125, None, None, P, 1, None)  # top_k > 32
-    _expect(-5, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P + 4, 64, 1, 100, None, 12, 4, 64,
+    _expect(-5, "sparda_decode_sums", P, 1, 1, P, P, 8, 8, 8, 1, P, 1, 1, 1, P + 4, 64, 0, 1, 100, None, 12, 4, 64,
             64, 8, 1, 0.125, 0.125, None, None, P, 1, None)  # misaligned block sums

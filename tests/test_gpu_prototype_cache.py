@@ -51,6 +51,9 @@ def test_prototype_cache_incremental_updates_equal_one_shot():
     cache.update(k[:, :1000], v[:, :1000])
     for t in range(1000, 1100):  # one token at a time, crossing blocks 15 -> 17
         cache.update(k[:, t:t + 1], v[:, t:t + 1])
+    # single-token appends leave the current block to the next decode launch
+    assert cache.current_block_stale
+    cache.refresh_sums()
     fresh = torch.zeros_like(cache.block_sums)
     sparda.block_sums(cache.k, 0, 1100, bs, fresh)
     nb = (1100 + bs - 1) // bs
@@ -160,3 +163,40 @@ def test_head_major_cache_layout_gives_the_same_decode():
     a = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], sa, bs, k, routing="absolute")
     b = sparda.decode_sums(d["q"], hk, hv, S, d["forecast"], sb, bs, k, routing="absolute")
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("S,dtype", [(5000, torch.bfloat16), (4096, torch.bfloat16), (4097, torch.bfloat16),
+                                     (300, torch.bfloat16), (2000, torch.float32)])
+def test_decode_sums_updating_the_current_block(S, dtype):
+    # the launch that recomputes the current block's sums first equals a
+    # separate block_sums update followed by the plain launch, bit for bit,
+    # and leaves the sums equal to a fresh computation
+    case(f"decode_sums update_current S={S} {dtype}")
+    B, Hq, Hkv, D, bs, k = 3, 12, 4, 64, 64, 8
+    x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=dtype, seed=47)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    nb = (S + bs - 1) // bs
+    cb = (S - 1) // bs
+    fresh = torch.zeros((B, nb + 2, Hkv, D), device=DEV)
+    sparda.block_sums(d["k_cache"], 0, S, bs, fresh)
+    stale = torch.zeros_like(fresh)
+    sparda.block_sums(d["k_cache"], 0, S - 1, bs, stale)  # the sums before token S-1 was appended
+    if cb * bs < S - 1:
+        assert not torch.equal(stale[:, cb], fresh[:, cb])
+    for routing in ("reference", "absolute"):
+        want, sel_w, n_w = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], fresh, bs, k,
+                                              routing=routing, want_sel=True)
+        sums = stale.clone()
+        got, sel_g, n_g = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], S, d["forecast"], sums, bs, k,
+                                             routing=routing, want_sel=True, update_current=True)
+        torch.cuda.synchronize()
+        assert torch.equal(sums, fresh)
+        assert torch.equal(n_g, n_w) and torch.equal(sel_g, sel_w)
+        assert torch.equal(got, want)
+        # at a device-held position
+        sums = stale.clone()
+        pos = torch.full((1,), S - 1, dtype=torch.int64, device=DEV)
+        got_d = sparda.decode_sums(d["q"], d["k_cache"], d["v_cache"], d["k_cache"].shape[1], d["forecast"], sums,
+                                   bs, k, routing=routing, pos_dev=pos, update_current=True)
+        torch.cuda.synchronize()
+        assert torch.equal(sums, fresh) and torch.equal(got_d, want)
