@@ -330,6 +330,20 @@ SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void
                                  int64_t out_stride_row, void* stream);
 
 /*
+ * The attention's output projection and residual of a decode-sized batch in
+ * one kernel: out = x + attn . wo^T (TransformerBlock.forward,
+ * model/transformer.py:118-126: x + attention(...) whose last step is
+ * self.wo(...), model/attention/sparse.py:183), rounded as the unfused pair
+ * rounds (the projection to bf16, then the sum).
+ *   a: [M, K] bf16 (stride a_stride_row), M in 1..16, K a multiple of 128 up
+ *     to 2048; w: [N, K] bf16 contiguous (nn.Linear layout), N a multiple of 16
+ *   res / out: [M, N] bf16 (strides res_stride_row / out_stride_row)
+ */
+SPARDA_API int sparda_rows_residual(const void* a, int64_t a_stride_row, const void* w, int64_t M, int64_t K,
+                                    int64_t N, const void* res, int64_t res_stride_row, void* out,
+                                    int64_t out_stride_row, void* stream);
+
+/*
  * fp32 block sums of a device KV cache, kept current across decode steps so
  * that decode selection (sparda_select_decode) reads the sums instead of
  * recompressing the whole cache every step as the reference's decode does
@@ -419,6 +433,13 @@ SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, con
  * never reads out of bounds, but its results are those of the clamped one.
  *
  * sparda_produce_at: sparda_produce with positions *pos_dev + t.
+ * sparda_produce_cache_at: sparda_produce_at that also writes the rotated key
+ *   and the value of row m as row p = *pos_dev + m % T (clamped into
+ *   [0, max_len)) of sequence m / T in the caches [B,Smax,Hkv,64] bf16
+ *   (strides (sb, st, sh, 1)), the append of KVCache.update
+ *   (model/attention/base.py:19-29) done by the producer; decode-sized
+ *   batches only (M <= 16). The block sums are left to the decode launch
+ *   (sparda_decode_sums with update_current).
  * sparda_append_at: per sequence, writes k_new / v_new ([B,Hkv,D], strides
  *   (new_sb, new_sh, 1)) as row p of the caches [B,Smax,Hkv,D] (strides
  *   (sb, st, sh, 1); KVCache.update, model/attention/base.py:19-29) and
@@ -447,6 +468,12 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
                                  int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
                                  const float* rope_sin, int64_t rope_len, int64_t T, const int64_t* pos_dev,
                                  void* q, void* k, void* v, void* f, int f_dtype, void* stream);
+SPARDA_API int sparda_produce_cache_at(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                                       int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                                       const float* rope_sin, int64_t rope_len, int64_t T, const int64_t* pos_dev,
+                                       void* q, void* k, void* v, void* f, int f_dtype, void* k_cache,
+                                       void* v_cache, int64_t sb, int64_t st, int64_t sh, int64_t max_len,
+                                       void* stream);
 SPARDA_API int sparda_append_at(void* k_cache, void* v_cache, int dtype, int64_t sb, int64_t st, int64_t sh,
                                 const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t Hkv, int64_t D, int64_t max_len, const int64_t* pos_dev,

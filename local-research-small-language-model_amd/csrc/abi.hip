@@ -393,7 +393,8 @@ SPARDA_API int sparda_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, in
 static int produce_impl(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C, int64_t Nq,
                         int64_t Nk, int64_t Nf, float eps, const float* rope_cos, const float* rope_sin,
                         int64_t rope_len, int64_t T, int64_t pos0, const int64_t* pos_dev, void* q, void* k,
-                        void* v, void* f, int f_dtype, void* stream) {
+                        void* v, void* f, int f_dtype, void* stream, void* kc = nullptr, void* vc = nullptr,
+                        int64_t c_sb = 0, int64_t c_st = 0, int64_t c_sh = 0, int64_t cap = 0) {
     SPARDA_REQUIRE(x && w && rope_cos && rope_sin && q && k && v && f, SPARDA_ERR_NULL, "produce: null pointer");
     SPARDA_REQUIRE(f_dtype == SPARDA_F32 || f_dtype == SPARDA_BF16, SPARDA_ERR_DTYPE,
                    "produce: forecast dtype %d unsupported", f_dtype);
@@ -414,7 +415,8 @@ static int produce_impl(const void* x, int64_t x_stride_row, const void* w, int6
                    SPARDA_ERR_STRIDE, "produce: x rows and w must be 16-byte aligned");
     SPARDA_REQUIRE(M / 128 < (int64_t(1) << 31), SPARDA_ERR_SHAPE, "produce: too many rows");
     return launch_produce(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, T, pos0, q, k, v, f,
-                          f_dtype, static_cast<hipStream_t>(stream), pos_dev, rope_len);
+                          f_dtype, static_cast<hipStream_t>(stream), pos_dev, rope_len, kc, vc, c_sb, c_st, c_sh,
+                          cap);
 }
 
 SPARDA_API int sparda_produce(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
@@ -432,6 +434,21 @@ SPARDA_API int sparda_produce_at(const void* x, int64_t x_stride_row, const void
     SPARDA_REQUIRE(pos_dev, SPARDA_ERR_NULL, "produce_at: null pos_dev");
     return produce_impl(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, rope_len, T, 0, pos_dev, q,
                         k, v, f, f_dtype, stream);
+}
+
+SPARDA_API int sparda_produce_cache_at(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                                       int64_t Nq, int64_t Nk, int64_t Nf, float eps, const float* rope_cos,
+                                       const float* rope_sin, int64_t rope_len, int64_t T, const int64_t* pos_dev,
+                                       void* q, void* k, void* v, void* f, int f_dtype, void* k_cache,
+                                       void* v_cache, int64_t sb, int64_t st, int64_t sh, int64_t max_len,
+                                       void* stream) {
+    SPARDA_REQUIRE(pos_dev && k_cache && v_cache, SPARDA_ERR_NULL, "produce_cache_at: null pos_dev or cache");
+    SPARDA_REQUIRE(M >= 1 && M <= 16 && C % 128 == 0 && C / 128 <= 16, SPARDA_ERR_SHAPE,
+                   "produce_cache_at: decode-sized batches only (M <= 16 rows, C a multiple of 128 up to 2048)");
+    SPARDA_REQUIRE(max_len >= 1 && sb > 0 && st > 0 && sh > 0, SPARDA_ERR_SHAPE,
+                   "produce_cache_at: cache strides and capacity must be positive");
+    return produce_impl(x, x_stride_row, w, M, C, Nq, Nk, Nf, eps, rope_cos, rope_sin, rope_len, T, 0, pos_dev, q,
+                        k, v, f, f_dtype, stream, k_cache, v_cache, sb, st, sh, max_len);
 }
 
 SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
@@ -486,6 +503,23 @@ SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void
                    SPARDA_ERR_STRIDE, "ffn_decode: rows and weights must be 16-byte aligned");
     return launch_ffn_decode(x, x_stride_row, w_gate_up, w_down, M, C, F, eps, act, out, out_stride_row,
                              static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_rows_residual(const void* a, int64_t a_stride_row, const void* w, int64_t M, int64_t K,
+                                    int64_t N, const void* res, int64_t res_stride_row, void* out,
+                                    int64_t out_stride_row, void* stream) {
+    SPARDA_REQUIRE(a && w && res && out, SPARDA_ERR_NULL, "rows_residual: null pointer");
+    SPARDA_REQUIRE(M >= 1 && M <= 16, SPARDA_ERR_SHAPE, "rows_residual: %lld rows (decode batches of 1..16)",
+                   (long long)M);
+    SPARDA_REQUIRE(K >= 128 && K % 128 == 0 && K <= 2048, SPARDA_ERR_SHAPE,
+                   "rows_residual: input width %lld must be a multiple of 128 up to 2048", (long long)K);
+    SPARDA_REQUIRE(N >= 16 && N % 16 == 0, SPARDA_ERR_SHAPE, "rows_residual: output width %lld must be a multiple "
+                   "of 16", (long long)N);
+    SPARDA_REQUIRE(a_stride_row >= K && a_stride_row % 8 == 0 && res_stride_row >= N && out_stride_row >= N &&
+                       aligned16(a) && aligned16(w),
+                   SPARDA_ERR_STRIDE, "rows_residual: input rows and weights must be 16-byte aligned");
+    return launch_rows_residual(a, a_stride_row, w, M, K, N, res, res_stride_row, out, out_stride_row,
+                                static_cast<hipStream_t>(stream));
 }
 
 SPARDA_API int sparda_append_at(void* k_cache, void* v_cache, int dtype, int64_t sb, int64_t st, int64_t sh,

@@ -136,4 +136,14 @@ int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const 
     return check_hip(hipGetLastError(), "ffn_down_kernel");
 }
 
+int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, int64_t K, int64_t N,
+                         const void* res, int64_t res_st, void* out, int64_t out_st, hipStream_t stream) {
+    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads),
+                       static_cast<size_t>(M * K) * 2, stream, static_cast<const uint16_t*>(a), a_st,
+                       static_cast<const uint16_t*>(w), static_cast<int>(M), static_cast<int>(K),
+                       static_cast<int>(N), static_cast<const uint16_t*>(res), res_st, static_cast<uint16_t*>(out),
+                       out_st);
+    return check_hip(hipGetLastError(), "ffn_down_kernel");
+}
+
 }  // namespace sparda

@@ -19,9 +19,13 @@ int launch_route(const void* f, int fdtype, int64_t fsb, int64_t fst, int64_t fs
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
-                   const int64_t* pos_dev = nullptr, int64_t rope_len = 0);
+                   const int64_t* pos_dev = nullptr, int64_t rope_len = 0, void* kc = nullptr,
+                   void* vc = nullptr, int64_t c_sb = 0, int64_t c_st = 0, int64_t c_sh = 0, int64_t cap = 0);
 
 // decode-sized feed-forward half of a block: RMSNorm (folded) + SwiGLU + residual
+// out[m] = bf16(res[m] + bf16(a[m] . W^T)) for M <= 16 rows: W [N, K] bf16, K <= 2048
+int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, int64_t K, int64_t N,
+                         const void* res, int64_t res_st, void* out, int64_t out_st, hipStream_t stream);
 int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const void* w_down, int64_t M,
                       int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream);
 

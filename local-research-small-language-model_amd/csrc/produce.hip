@@ -202,7 +202,8 @@ produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t
                     int Nq, int Nk, int Nf, float eps, const float* __restrict__ cosv,
                     const float* __restrict__ sinv, int64_t T, int64_t pos0, uint16_t* __restrict__ q,
                     uint16_t* __restrict__ k, uint16_t* __restrict__ v, void* __restrict__ f,
-                    const int64_t* __restrict__ pos_dev, int64_t rope_len) {
+                    const int64_t* __restrict__ pos_dev, int64_t rope_len, uint16_t* __restrict__ kc,
+                    uint16_t* __restrict__ vc, int64_t c_sb, int64_t c_st, int64_t c_sh, int64_t cap) {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][C]
     __shared__ float ylds[kRowsMaxM][16];
     const int tid = threadIdx.x;
@@ -261,13 +262,23 @@ produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t
         else if (region == 1) { store_out<SPARDA_BF16>(k, base, y1); store_out<SPARDA_BF16>(k, base + 32, y2); }
         else if (region == 2) { store_out<SPARDA_BF16>(v, base, y1); store_out<SPARDA_BF16>(v, base + 32, y2); }
         else { store_out<FDT>(f, base, y1); store_out<FDT>(f, base + 32, y2); }
+        if (kc != nullptr && (region == 1 || region == 2)) {
+            // the new key / value also as row p of sequence m / T in the caches
+            int64_t p = pos_base + m % T;
+            p = p < 0 ? 0 : (p > cap - 1 ? cap - 1 : p);
+            const int64_t ci = (m / T) * c_sb + p * c_st + head * c_sh + d;
+            uint16_t* dst = region == 1 ? kc : vc;
+            store_out<SPARDA_BF16>(dst, ci, y1);
+            store_out<SPARDA_BF16>(dst, ci + 32, y2);
+        }
     }
 }
 
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,
-                   const int64_t* pos_dev, int64_t rope_len) {
+                   const int64_t* pos_dev, int64_t rope_len, void* kc, void* vc, int64_t c_sb, int64_t c_st,
+                   int64_t c_sh, int64_t cap) {
     const int64_t N = Nq + 2 * Nk + Nf;
     if (M <= kRowsMaxM && C % 128 == 0 && C / 128 <= kRowsChunks) {
         const size_t lds = static_cast<size_t>(M * C) * 2;
@@ -276,12 +287,15 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                        stream, static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w),        \
                        static_cast<int>(M), static_cast<int>(C), static_cast<int>(Nq), static_cast<int>(Nk),  \
                        static_cast<int>(Nf), eps, cosv, sinv, T, pos0, static_cast<uint16_t*>(q),             \
-                       static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), f, pos_dev, rope_len)
+                       static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), f, pos_dev, rope_len,             \
+                       static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), c_sb, c_st, c_sh, cap)
         if (f_dtype == SPARDA_F32) SPARDA_PRODUCE_ROWS(SPARDA_F32);
         else SPARDA_PRODUCE_ROWS(SPARDA_BF16);
 #undef SPARDA_PRODUCE_ROWS
         return check_hip(hipGetLastError(), "produce_rows_kernel");
     }
+    if (kc != nullptr) return set_error(SPARDA_ERR_SHAPE, "produce: cache rows are written for M <= %d only",
+                                        kRowsMaxM);
     dim3 grid(static_cast<unsigned>(cdiv(M, kPBM)), static_cast<unsigned>(N / kPBN));
 #define SPARDA_PRODUCE(FDT_)                                                                              \
     hipLaunchKernelGGL((produce_kernel<FDT_>), grid, dim3(kPThreads), 0, stream,                          \

@@ -102,13 +102,22 @@ class HipSparseAttention(BaseAttention):
         self._ws = None
 
     # -- decode ------------------------------------------------------------
-    def _decode(self, xq: torch.Tensor, cache: KVCache, forecast_vector: Optional[torch.Tensor]):
+    def _project(self, out: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """wo of a decode step's output [B, Hq*D]; with residual, residual +
+        wo(out) in one kernel (sparda.rows_residual)."""
+        o = out.view(out.shape[0], 1, self.n_head * self.head_dim)
+        if residual is None:
+            return self.wo(o)
+        return sparda.rows_residual(o, self.wo.weight, residual)
+
+    def _decode(self, xq: torch.Tensor, cache: KVCache, forecast_vector: Optional[torch.Tensor],
+                residual: Optional[torch.Tensor] = None):
         B = xq.shape[0]
         if self._ws is None or self._ws.device != xq.device:
             self._ws = sparda.DecodeWorkspace(xq.device)
         if self.mode == "dense":
             out = sparda.decode_selected(xq[:, 0], cache.k, cache.v, cache.current_len, self.block_size)
-            return self.wo(out.view(B, 1, self.n_head * self.head_dim))
+            return self._project(out, residual)
         f = forecast_vector if (self.mode == "forecast" and forecast_vector is not None) else None
         if f is not None:
             f = f.reshape(B, self.n_kv_head, -1)
@@ -118,10 +127,10 @@ class HipSparseAttention(BaseAttention):
                                      self.block_size, self.top_k_blocks, routing=self.decode_routing,
                                      update_current=cache.current_block_stale)
             cache.current_block_stale = False
-            return self.wo(out.view(B, 1, self.n_head * self.head_dim))
+            return self._project(out, residual)
         out = sparda.decode(xq[:, 0], cache.k, cache.v, cache.current_len, f, self.block_size,
                             self.top_k_blocks, routing=self.decode_routing, workspace=self._ws)
-        return self.wo(out.view(B, 1, self.n_head * self.head_dim))
+        return self._project(out, residual)
 
     # -- prefill -----------------------------------------------------------
     def _prefill(self, xq, xk, xv, forecast_vector, is_causal):
@@ -161,14 +170,19 @@ class HipSparseAttention(BaseAttention):
 
     def forward_projected(self, xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
                           kv_cache: Optional[KVCache] = None, is_causal: bool = True,
-                          forecast_vector: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          forecast_vector: Optional[torch.Tensor] = None,
+                          residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The attention after the projections and RoPE: xq [B,T,Hq,D], xk / xv
         [B,T,Hkv,D] (already rotated at the cache's current position). Entered
-        from forward, or directly by a block whose fused producer computed them."""
+        from forward, or directly by a block whose fused producer computed them.
+        With residual (single-token decode only) the result is residual +
+        attention, the projection and the sum in one kernel."""
         T = xq.shape[1]
         if kv_cache is not None and T == 1:
             kv_cache.update(xk, xv)
-            return self._decode(xq, kv_cache, forecast_vector)
+            return self._decode(xq, kv_cache, forecast_vector, residual)
+        if residual is not None:
+            raise ValueError("forward_projected: residual is for single-token decode steps")
         if kv_cache is not None:
             if kv_cache.current_len != 0:
                 raise NotImplementedError("prefill into a non-empty cache is not supported")

@@ -151,6 +151,11 @@ class GraphDecoder:
         self.logits: Optional[torch.Tensor] = None
 
     # -- one decode step, every launch reading *pos --------------------------
+    def _producer_appends(self, i: int, a, f: Optional[torch.Tensor]) -> bool:
+        """Layer i's producer writes the new row into its cache and the decode
+        launch re-sums the current block (the forecast-routed sparse layers)."""
+        return self.kinds[i] == _SPARSE and a.mode not in ("dense", "static") and f is not None
+
     def _attend(self, i: int, a, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 f: Optional[torch.Tensor]) -> torch.Tensor:
         bs = self.block_size
@@ -165,13 +170,13 @@ class GraphDecoder:
         if kind == _RESIDENT_DENSE:
             sparda.append_at(cache.k, cache.v, self.pos, bs, None, k, v)
             return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len)
+        if self._producer_appends(i, a, f):
+            return sparda.decode_sums(q, cache.k, cache.v, self.max_len, f, cache.block_sums, bs, a.top_k_blocks,
+                                      routing=a.decode_routing, pos_dev=self.pos, update_current=True)
+        # dense / static-window layers: the append keeps the block sums current
         sparda.append_at(cache.k, cache.v, self.pos, bs, cache.block_sums, k, v)
-        if a.mode == "dense":
-            return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len)
-        if a.mode == "static" or f is None:
-            return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=a.top_k_blocks, max_len=self.max_len)
-        return sparda.decode_sums(q, cache.k, cache.v, self.max_len, f, cache.block_sums, bs, a.top_k_blocks,
-                                  routing=a.decode_routing, pos_dev=self.pos)
+        window = 0 if a.mode == "dense" else a.top_k_blocks
+        return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=window, max_len=self.max_len)
 
     def _prefetch(self, i: int, f: torch.Tensor):
         """Selection + gather of layer i's blocks for this step, from layer i-1's forecast."""
@@ -192,9 +197,11 @@ class GraphDecoder:
         for i, layer in enumerate(m.layers):
             a = layer.attention
             fc = layer.forecast
+            cache = self.caches[i]
+            kc, vc = (cache.k, cache.v) if self._producer_appends(i, a, prev_f) else (None, None)
             q, k, v, f = sparda.produce(x, layer._fused_weight(), a.n_head * a.head_dim, a.n_kv_head * a.head_dim,
                                         fc.forecast_heads * fc.forecast_dim, layer.attn_norm.eps, self.cos,
-                                        self.sin, f_dtype=x.dtype, pos_dev=self.pos)
+                                        self.sin, f_dtype=x.dtype, pos_dev=self.pos, k_cache=kc, v_cache=vc)
             if i + 1 < n and self.kinds[i + 1] == _OFFLOAD:
                 ev = self._pf[i + 1]["ev"]
                 if self.overlap:
@@ -206,7 +213,10 @@ class GraphDecoder:
                     self._prefetch(i + 1, f)
                     ev.record(main)
             out = self._attend(i, a, q[:, 0], k, v, prev_f)
-            x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
+            if layer._use_fused_wo(x, 1, self.caches[i]):
+                x = sparda.rows_residual(out.view(B, 1, a.n_head * a.head_dim), a.wo.weight, x)
+            else:
+                x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
             x = layer.ffn_residual(x)
             prev_f = f
         self.logits = m.embeddings.project(m.final_norm(x))[:, -1, :]

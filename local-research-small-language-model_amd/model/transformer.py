@@ -119,6 +119,13 @@ class TransformerBlock(nn.Module):
             self._ffn_key = key
         return self._ffn_w
 
+    def _use_fused_wo(self, x: torch.Tensor, T: int, kv_cache) -> bool:
+        """x + wo(attention) as one kernel: single-token decode steps of the
+        sparse backend, under the same switch and size limits as the FFN."""
+        return (T == 1 and kv_cache is not None and type(self.attention) is HipSparseAttention
+                and getattr(self.config, "fused_producer", False) and self._use_fused_ffn(x) and self.attention.n_head * self.attention.head_dim % 128 == 0
+                and self.attention.n_head * self.attention.head_dim <= 2048)
+
     def ffn_residual(self, x: torch.Tensor) -> torch.Tensor:
         """x + SwiGLU(ffn_norm(x)) (transformer.py:126-129); one fused pair of
         kernels for decode-sized batches when the config asks for it."""
@@ -146,9 +153,12 @@ class TransformerBlock(nn.Module):
                 if hasattr(next_layer_block.attention, "prefetch"):
                     next_layer_block.attention.prefetch(forecast_vector=current_forecast,
                                                         offload_cache=next_kv_cache)
-            attn_out = a.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
-                                           forecast_vector=prev_layer_forecast)
-            x = x + attn_out
+            if self._use_fused_wo(x, T, kv_cache):
+                x = a.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
+                                        forecast_vector=prev_layer_forecast, residual=x)
+            else:
+                x = x + a.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
+                                            forecast_vector=prev_layer_forecast)
             return self.ffn_residual(x), current_forecast
         normed_x = self.attn_norm(x)
         current_forecast = self.forecast(normed_x)

@@ -74,6 +74,8 @@ SIGNATURES = {
                                  _p, _p]),
     "sparda_produce_at": (_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64, _i64, _p,
                                  _p, _p, _p, _p, _int, _p]),
+    "sparda_produce_cache_at": (_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64, _i64, _p,
+                                       _p, _p, _p, _p, _int, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "sparda_append_at": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                                 _i64, _i64, _p, _p]),
     "sparda_select_decode_at": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64,
@@ -84,6 +86,7 @@ SIGNATURES = {
                                   _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f32, _p, _p, _p,
                                   _i64, _p]),
     "sparda_ffn_decode": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _i64, _p]),
+    "sparda_rows_residual": (_int, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p]),
     "sparda_offload_fetch_at": (_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p]),
     "sparda_offload_append_at": (_int, [_p, _p, _p, _i64, _i64, _p, _i64, _p, _p]),
     "sparda_offload_append": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),

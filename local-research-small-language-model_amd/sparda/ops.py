@@ -376,7 +376,8 @@ def teacher_block_mass(q: torch.Tensor, k: torch.Tensor, block_size: int = 64, c
 
 def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: int, eps: float,
             rope_cos: torch.Tensor, rope_sin: torch.Tensor, pos0: int = 0,
-            f_dtype: torch.dtype = torch.bfloat16, pos_dev: Optional[torch.Tensor] = None):
+            f_dtype: torch.dtype = torch.bfloat16, pos_dev: Optional[torch.Tensor] = None,
+            k_cache: Optional[torch.Tensor] = None, v_cache: Optional[torch.Tensor] = None):
     """RMSNorm + q / k / v / forecast projections + RoPE in one kernel
     (model/transformer.py:104-107; model/norm.py:15-21; model/forecast.py:30-40;
     model/attention/base.py:38-52; model/rope.py:34-65).
@@ -388,7 +389,11 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
 
     pos_dev: a one-element int64 device tensor holding the first position,
     read when the kernel runs (pos0 must then be 0; positions are clamped into
-    the tables), for launches recorded once and replayed every decode step."""
+    the tables), for launches recorded once and replayed every decode step.
+    With pos_dev, k_cache / v_cache ([B,Smax,n_kv/64,64] bf16) also receive
+    the new keys and values as rows *pos_dev + t (the cache append of
+    KVCache.update, model/attention/base.py:19-29; decode-sized batches,
+    B*T <= 16); block sums are then the decode launch's to update."""
     dev = require_device(x, w_stacked, rope_cos, rope_sin, pos_dev)
     _inference_only(x, w_stacked)
     if x.dtype != torch.bfloat16 or w_stacked.dtype != torch.bfloat16:
@@ -408,6 +413,22 @@ def produce(x: torch.Tensor, w_stacked: torch.Tensor, n_q: int, n_kv: int, n_f: 
     k = torch.empty((B, T, n_kv // 64, 64), dtype=torch.bfloat16, device=dev)
     v = torch.empty_like(k)
     f = torch.empty((B, T, n_f // 64, 64), dtype=f_dtype, device=dev)
+    if (k_cache is None) != (v_cache is None):
+        raise ValueError("sparda: k_cache and v_cache go together")
+    if k_cache is not None:
+        if pos_dev is None or pos0 != 0:
+            raise ValueError("sparda: writing the caches needs pos_dev (and pos0 = 0)")
+        require_device(k_cache, v_cache)
+        if not (k_cache.dtype == v_cache.dtype == torch.bfloat16) or k_cache.stride() != v_cache.stride():
+            raise TypeError("sparda: the caches must be bf16 with equal strides")
+        if k_cache.shape[0] != B or tuple(k_cache.shape[2:]) != (n_kv // 64, 64) or k_cache.stride(-1) != 1:
+            raise AssertionError(f"Mismatch: cache {tuple(k_cache.shape)} for {B} sequences, {n_kv // 64} heads")
+        sb, st, sh, _ = k_cache.stride()
+        call("sparda_produce_cache_at", x2.data_ptr(), x2.stride(0), w_stacked.data_ptr(), B * T, C, n_q, n_kv,
+             n_f, float(eps), rope_cos.data_ptr(), rope_sin.data_ptr(), rope_cos.shape[0], T, _pos_ptr(pos_dev),
+             q.data_ptr(), k.data_ptr(), v.data_ptr(), f.data_ptr(), _DT[f_dtype], k_cache.data_ptr(),
+             v_cache.data_ptr(), sb, st, sh, k_cache.shape[1], _stream(dev))
+        return q, k, v, f
     if pos_dev is not None:
         if pos0 != 0:
             raise ValueError("sparda: produce takes pos0 or pos_dev, not both")
@@ -504,6 +525,36 @@ def ffn_decode(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor, e
     o2 = out.view(B * T, C)
     call("sparda_ffn_decode", x2.data_ptr(), x2.stride(0), w_gate_up.data_ptr(), w_down.data_ptr(), B * T, C, F,
          float(eps), act.data_ptr(), o2.data_ptr(), o2.stride(0), _stream(dev))
+    return out
+
+
+def rows_residual(a: torch.Tensor, w: torch.Tensor, res: torch.Tensor,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """res + a . w^T for decode-sized batches in one kernel: the attention's
+    output projection and residual (model/transformer.py:118-126 with
+    model/attention/sparse.py:183). a [B,T,K], w [N,K], res [B,T,N], all bf16,
+    B*T <= 16. The projection is rounded to bf16 before the sum, as the
+    unfused pair does. Returns [B,T,N] bf16."""
+    dev = require_device(a, w, res, out)
+    _inference_only(a, w, res)
+    if not (a.dtype == w.dtype == res.dtype == torch.bfloat16):
+        raise TypeError("sparda: rows_residual takes bf16 activations and weights")
+    B, T, K = a.shape
+    N = w.shape[0]
+    if tuple(w.shape) != (N, K) or tuple(res.shape) != (B, T, N):
+        raise AssertionError(f"Mismatch: a {tuple(a.shape)}, w {tuple(w.shape)}, res {tuple(res.shape)}")
+    a2 = a.reshape(B * T, K)
+    if a2.stride(-1) != 1 or a2.stride(0) % 8:
+        a2 = a2.contiguous()
+    r2 = res.reshape(B * T, N)
+    if r2.stride(-1) != 1:
+        r2 = r2.contiguous()
+    w = w.contiguous()
+    if out is None:
+        out = torch.empty((B, T, N), dtype=torch.bfloat16, device=dev)
+    o2 = out.view(B * T, N)
+    call("sparda_rows_residual", a2.data_ptr(), a2.stride(0), w.data_ptr(), B * T, K, N, r2.data_ptr(),
+         r2.stride(0), o2.data_ptr(), o2.stride(0), _stream(dev))
     return out
 
 

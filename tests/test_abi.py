@@ -74,6 +74,18 @@ def test_argument_errors_are_reported_before_any_hip_call():
             None, None, None, None, P, 1, P * 2, 16, None)  # workspace too small
     _expect(-6, "sparda_decode", P, 1, 1, P, P, 8, 8, 8, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 5, 0.125,
             None, None, None, None, P, 1, P * 2, 1 << 20, None)  # unknown routing
+    # x, x_st, w, M, C, Nq, Nk, Nf, eps, cos, sin, rope_len, T, pos_dev, q, k, v, f, f_dtype,
+    # k_cache, v_cache, sb, st, sh, max_len, stream
+    _expect(-1, "sparda_produce_cache_at", P, 768, P, 1, 768, 768, 256, 256, 1e-5, P, P, 64, 1, P, P, P, P, P, 1,
+            None, P, 8, 8, 8, 64, None)  # no k_cache
+    _expect(-2, "sparda_produce_cache_at", P, 768, P, 17, 768, 768, 256, 256, 1e-5, P, P, 64, 1, P, P, P, P, P, 1,
+            P, P, 8, 8, 8, 64, None)  # M > 16
+    # a, a_st, w, M, K, N, res, res_st, out, out_st, stream
+    _expect(-1, "sparda_rows_residual", None, 768, P, 1, 768, 768, P, 768, P, 768, None)
+    _expect(-2, "sparda_rows_residual", P, 768, P, 17, 768, 768, P, 768, P, 768, None)   # M > 16
+    _expect(-2, "sparda_rows_residual", P, 768, P, 1, 700, 768, P, 768, P, 768, None)   # K % 128
+    _expect(-2, "sparda_rows_residual", P, 768, P, 1, 768, 760, P, 768, P, 768, None)   # N % 16
+    _expect(-5, "sparda_rows_residual", P + 4, 768, P, 1, 768, 768, P, 768, P, 768, None)  # misaligned a
 
 
 def test_decode_workspace_size_formula():

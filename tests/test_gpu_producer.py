@@ -164,3 +164,43 @@ def test_model_with_fused_ffn_matches_unfused():
             m.layers[0].ffn_norm.weight.mul_(1.5)  # the folded weight follows parameter updates
         a, b, r = (m(ids[:, 660:661], kv_caches=c)["logits"] for m, c in zip((plain, fused, ref), caches))
         _no_less_accurate(b, a, r, "decode logits after a weight update")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 768, 768), (8, 768, 768), (16, 2048, 256), (3, 128, 16)])
+def test_rows_residual_op(M, K, N):
+    # res + a . w^T with the projection rounded to bf16 first, against the
+    # same two roundings around an fp32 product
+    g = torch.Generator().manual_seed(M * 131 + K)
+    a = torch.randn(M, 1, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(DEV)
+    res = torch.randn(M, 1, N, generator=g).to(torch.bfloat16).to(DEV)
+    got = sparda.rows_residual(a, w, res)
+    proj = (a.float().reshape(M, K) @ w.float().T).to(torch.bfloat16)
+    want = (res.float().reshape(M, N) + proj.float()).to(torch.bfloat16)
+    diff = (got.reshape(M, N).float() - want.float()).abs()
+    # accumulation order only: within one bf16 rounding step of the projection and the sum
+    tol = want.float().abs() * 2 ** -7 + proj.float().abs() * 2 ** -7 + 1e-3
+    assert bool((diff <= tol).all()), f"max diff {diff.max().item()}"
+
+
+def test_produce_writes_the_cache_rows():
+    # the cache-writing producer equals produce_at followed by a row copy into
+    # the caches; rows outside position p stay untouched
+    case_B, C, nq, nkv, nf = 4, 768, 768, 256, 256
+    g = torch.Generator().manual_seed(61)
+    x = torch.randn(case_B, 1, C, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(nq + 2 * nkv + nf, C, generator=g) / C ** 0.5).to(torch.bfloat16).to(DEV)
+    cos, sin = rope_tables(64, 300)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    for p in (0, 77, 299):
+        pos = torch.full((1,), p, dtype=torch.int64, device=DEV)
+        kc = torch.randn(case_B, 300, nkv // 64, 64, device=DEV).to(torch.bfloat16)
+        vc = torch.randn_like(kc)
+        k0, v0 = kc.clone(), vc.clone()
+        q1, k1, v1, f1 = sparda.produce(x, w, nq, nkv, nf, 1e-5, cos, sin, pos_dev=pos)
+        q2, k2, v2, f2 = sparda.produce(x, w, nq, nkv, nf, 1e-5, cos, sin, pos_dev=pos, k_cache=kc, v_cache=vc)
+        torch.cuda.synchronize()
+        assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2) and torch.equal(f1, f2)
+        assert torch.equal(kc[:, p], k1[:, 0]) and torch.equal(vc[:, p], v1[:, 0])
+        rest = [t for t in range(300) if t != p]
+        assert torch.equal(kc[:, rest], k0[:, rest]) and torch.equal(vc[:, rest], v0[:, rest])
