@@ -703,6 +703,7 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     } while (0)
 #define SPARDA_ATT_C(DT_, DH_)                            \
     if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
+    else if (NB <= 512) SPARDA_ATT(DT_, DH_, 8);          \
     else if (NB <= 1024) SPARDA_ATT(DT_, DH_, 16);        \
     else SPARDA_ATT(DT_, DH_, 64);
 #define SPARDA_ATT_D(DT_)                                         \

@@ -342,7 +342,7 @@ __device__ __forceinline__ int select_keys(const uint32_t* key_lds, int n, int k
     return wave_select_pre<CH>(kreg, n, k, own, sel_lds, ck_lds, ci_lds);
 }
 
-// select_keys with the smallest key-register count (4, 16 or 64, at most
+// select_keys with the smallest key-register count (4, 8, 16 or 64, at most
 // CHMAX) holding n keys: a length known only on the device may be far below
 // the bound CHMAX was chosen for
 template <int CHMAX>
@@ -350,8 +350,10 @@ __device__ __forceinline__ int select_keys_upto(const uint32_t* key_lds, int n, 
                                                 int lane, uint32_t* ck_lds, int32_t* ci_lds) {
     if (CHMAX >= 64 && n > 1024)
         return select_keys<(CHMAX >= 64 ? 64 : CHMAX)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
-    if (CHMAX >= 16 && n > 256)
+    if (CHMAX >= 16 && n > 512)
         return select_keys<(CHMAX >= 16 ? 16 : CHMAX)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
+    if (CHMAX >= 8 && n > 256)
+        return select_keys<(CHMAX >= 8 ? 8 : CHMAX)>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
     return select_keys<4>(key_lds, n, k, own, sel_lds, lane, ck_lds, ci_lds);
 }
 

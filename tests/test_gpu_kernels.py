@@ -288,6 +288,13 @@ def test_decode_16k_cache(routing):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+def test_decode_between_256_and_512_blocks(routing):
+    # 313 blocks: the selection runs on eight key registers per lane
+    case(f"decode S=20000 {routing}")
+    _decode_case(2, 20000, 12, 4, 64, 64, 8, torch.bfloat16, routing, seed=20000)
+
+
 @pytest.mark.parametrize("S", [1, 63, 64, 65, 600, 1000, 5000])
 def test_decode_lengths_fp32(S):
     case(f"decode fp32 S={S}")
