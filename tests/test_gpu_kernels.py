@@ -246,6 +246,32 @@ def test_prefill_long_context_16k_sampled_rows_and_selection_invariants():
     assert (n[..., own >= k - 1] >= k).all()                               # k distinct picks once k blocks exist
 
 
+def test_prefill_at_the_largest_block_count_sampled_rows():
+    # T = 65536: 1024 blocks, the most the matrix-core prefill's per-token
+    # selection bitmasks hold; sampled rows against the oracle
+    case("prefill B=1 T=65536 sampled")
+    T, bs, k = 65536, 64, 8
+    r = np.random.default_rng(9)
+    ts = sorted({int(t) for t in r.integers(0, T, 96)} | {0, 63, 64, 32768, T - 64, T - 1})
+    x = synth.prefill_inputs(1, T, 12, 4, 64, dtype=torch.bfloat16, seed=1009)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    _, _, sel, n = sparda.route(d["forecast"], sparda.compress(d["k"], bs), bs, k, want_topk=False, want_sel=True)
+    out = sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs)
+    torch.cuda.synchronize()
+    sel, n = sel.cpu().numpy(), n.cpu().numpy()
+    protos = O.compress(np32(x["k"]), bs)
+    f = np32(x["forecast"])
+    for t in ts:  # the oracle's selection of row t alone (its position passed explicitly)
+        _, _, s_o, n_o = O.route(f[:, t:t + 1], protos, bs, k, True, score_pos0=t, query_pos0=t)
+        assert np.array_equal(n[:, :, t], n_o[:, :, 0]) and np.array_equal(sel[:, :, t], s_o[:, :, 0]), f"row {t}"
+    rows = [(0, t) for t in ts]
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel, n, bs, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(out), want, torch.bfloat16, mask)
+
+
 def test_prefill_topk_covering_all_blocks_equals_dense():
     case("prefill k>=NB == dense")
     x = synth.prefill_inputs(1, 640, 12, 4, 64, dtype=torch.bfloat16, seed=80)
