@@ -321,6 +321,12 @@ def test_decode_between_256_and_512_blocks(routing):
     _decode_case(2, 20000, 12, 4, 64, 64, 8, torch.bfloat16, routing, seed=20000)
 
 
+def test_decode_beyond_1024_blocks():
+    # 1563 blocks: 64 key registers per lane
+    case("decode S=100000 absolute")
+    _decode_case(1, 100000, 12, 4, 64, 64, 8, torch.bfloat16, "absolute", seed=100000)
+
+
 @pytest.mark.parametrize("S", [1, 63, 64, 65, 600, 1000, 5000])
 def test_decode_lengths_fp32(S):
     case(f"decode fp32 S={S}")
