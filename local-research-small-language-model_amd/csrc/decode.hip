@@ -207,10 +207,14 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             const int64_t fi = b * fs_sb + g * fs_sh + d;
             fsel_lds[d] = fsel_bf16 ? load_elem<SPARDA_BF16>(fsel, fi) : load_elem<SPARDA_F32>(fsel, fi);
         }
-        if (update_sums && threadIdx.x < DH / 2) {
+        __syncthreads();  // fsel_lds
+        // the last DH/2 threads re-sum the current block while the others
+        // score the blocks before it; its score follows in wave 0
+        const int rs0 = static_cast<int>(blockDim.x) - DH / 2;
+        if (update_sums && static_cast<int>(threadIdx.x) >= rs0) {
             // the current block's sums of head g from its rows [cb*bs, S), in
             // row order (block_sums_kernel's order), 32 row loads in flight
-            const int dd = 2 * static_cast<int>(threadIdx.x);
+            const int dd = 2 * (static_cast<int>(threadIdx.x) - rs0);
             const int64_t s0 = static_cast<int64_t>(cb) * bs;
             const int nr = static_cast<int>(S - s0);
             const int64_t base = b * kv_sb + g * kv_sh + dd;
@@ -234,12 +238,12 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             cur[0] = a0;
             cur[1] = a1;
         }
-        __syncthreads();
         if (!dense4) {
             const float den = static_cast<float>(bs);
             const float inv = 1.0f / den;
             const int limit = absolute ? cb : 0;
-            for (int j = threadIdx.x; j <= cb; j += blockDim.x) {
+            const int jend = update_sums ? cb - 1 : cb;  // the current block is scored after the re-sum
+            for (int j = threadIdx.x; j <= jend; j += blockDim.x) {
                 const float* sp = sums + ((b * nb_stride + j) * H + g) * DH;
                 const float sc = j > limit ? -__builtin_inff()
                                            : (pow2 ? score_from_sum<DH, true, kSumBatch>(sp, fsel_lds, den, inv, fscale)
@@ -252,6 +256,20 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     }
     if (wave == 0) {
         int m = 0;
+        if (sel_mode == 4 && update_sums && !dense4) {
+            // the current block's key from its fresh sums (stored before the barrier)
+            if (lane == 0) {
+                const float den = static_cast<float>(bs);
+                const float* sp = sums + ((b * nb_stride + cb) * H + g) * DH;
+                const float sc = cb > (absolute ? cb : 0)
+                                     ? -__builtin_inff()
+                                     : (pow2 ? score_from_sum<DH, true, kSumBatch>(sp, fsel_lds, den, 1.0f / den, fscale)
+                                             : score_from_sum<DH, false, kSumBatch>(sp, fsel_lds, den, 1.0f / den,
+                                                                                    fscale));
+                key_lds[cb] = order_key(sc);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
         if (sel_mode == 4) {
             if (dense4) {
                 m = cb + 1;  // every block 0..cb
