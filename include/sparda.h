@@ -330,6 +330,20 @@ SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void
                                  int64_t out_stride_row, void* stream);
 
 /*
+ * The final RMSNorm and the output projection of a decode-sized batch in one
+ * kernel: logits = final_norm(x) . W^T (SparDAResearchModel.forward,
+ * model/model.py:79-157, with the tied embedding weight; RMSNorm as
+ * model/norm.py:15-21), as out[m, n] = (x[m] . W'[n]) / sqrt(mean(x[m]^2) + eps)
+ * in fp32, rounded to bf16 once, with W' = W * norm_weight (folded into the
+ * columns by the caller).
+ *   x: [M, C] bf16 (stride x_stride_row), M in 1..16, C a multiple of 128 up
+ *     to 1024; w: [N, C] bf16 contiguous, N a multiple of 16
+ *   out: [M, N] bf16 (stride out_stride_row)
+ */
+SPARDA_API int sparda_norm_gemv(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                                int64_t N, float eps, void* out, int64_t out_stride_row, void* stream);
+
+/*
  * The attention's output projection and residual of a decode-sized batch in
  * one kernel: out = x + attn . wo^T (TransformerBlock.forward,
  * model/transformer.py:118-126: x + attention(...) whose last step is

@@ -505,6 +505,20 @@ SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void
                              static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_norm_gemv(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,
+                                int64_t N, float eps, void* out, int64_t out_stride_row, void* stream) {
+    SPARDA_REQUIRE(x && w && out, SPARDA_ERR_NULL, "norm_gemv: null pointer");
+    SPARDA_REQUIRE(M >= 1 && M <= 16, SPARDA_ERR_SHAPE, "norm_gemv: %lld rows (decode batches of 1..16)",
+                   (long long)M);
+    SPARDA_REQUIRE(C >= 128 && C % 128 == 0 && C <= 1024, SPARDA_ERR_SHAPE,
+                   "norm_gemv: width %lld must be a multiple of 128 up to 1024", (long long)C);
+    SPARDA_REQUIRE(N >= 16 && N % 16 == 0 && N / 16 < (int64_t(1) << 31), SPARDA_ERR_SHAPE,
+                   "norm_gemv: %lld outputs, need a multiple of 16", (long long)N);
+    SPARDA_REQUIRE(x_stride_row >= C && x_stride_row % 8 == 0 && out_stride_row >= N && aligned16(x) && aligned16(w),
+                   SPARDA_ERR_STRIDE, "norm_gemv: rows and weights must be 16-byte aligned");
+    return launch_norm_gemv(x, x_stride_row, w, M, C, N, eps, out, out_stride_row, static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_rows_residual(const void* a, int64_t a_stride_row, const void* w, int64_t M, int64_t K,
                                     int64_t N, const void* res, int64_t res_stride_row, void* out,
                                     int64_t out_stride_row, void* stream) {

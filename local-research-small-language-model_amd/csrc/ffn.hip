@@ -136,6 +136,55 @@ int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const 
     return check_hip(hipGetLastError(), "ffn_down_kernel");
 }
 
+// grid N/16: out[m, n] = bf16((x[m, :] . W'[n, :]) / rms(x[m])), W' [N, C] with the
+// norm weight folded into its columns: the final RMSNorm and the output
+// projection of a decode step in one launch
+__global__ void __launch_bounds__(kFfnThreads)
+norm_gemv_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __restrict__ w, int M, int C,
+                 float eps, uint16_t* __restrict__ out, int64_t out_st) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][C]
+    __shared__ float ylds[kRowsMaxM][16];
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int li = lane % 16;
+    const int lc = 4 * (tid / kWave) + lane / 16;
+    const int n = blockIdx.x * 16 + lc;
+    const int nch = C / 128;
+    uint4 wr[1][kFfnGuChunks];
+    const uint16_t* wrow = w + static_cast<int64_t>(n) * C + li * 8;
+#pragma unroll
+    for (int i = 0; i < kFfnGuChunks; ++i)
+        if (i < nch) wr[0][i] = *reinterpret_cast<const uint4*>(wrow + i * 128);
+    stage_rows(x, x_st, M, C, xs);
+    float acc[1][kRowsMaxM], ss[kRowsMaxM];
+#pragma unroll
+    for (int m = 0; m < kRowsMaxM; ++m) acc[0][m] = ss[m] = 0.0f;
+    rows_dot<1, kFfnGuChunks, true>(xs, M, C, nch, li, wr, acc, ss);
+#pragma unroll
+    for (int m = 0; m < kRowsMaxM; ++m) {
+        if (m < M) {
+            const float a = row16_sum(acc[0][m]);
+            const float s2 = row16_sum(ss[m]);
+            if (li == 0) ylds[m][lc] = a / __builtin_sqrtf(s2 / static_cast<float>(C) + eps);
+        }
+    }
+    __syncthreads();
+    for (int t = tid; t < M * 16; t += kFfnThreads) {
+        const int m = t / 16, c = t % 16;
+        out[m * out_st + static_cast<int64_t>(blockIdx.x) * 16 + c] =
+            __builtin_bit_cast(uint16_t, static_cast<__bf16>(ylds[m][c]));
+    }
+}
+
+int launch_norm_gemv(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t N, float eps,
+                     void* out, int64_t out_st, hipStream_t stream) {
+    hipLaunchKernelGGL(norm_gemv_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads),
+                       static_cast<size_t>(M * C) * 2, stream, static_cast<const uint16_t*>(x), x_st,
+                       static_cast<const uint16_t*>(w), static_cast<int>(M), static_cast<int>(C), eps,
+                       static_cast<uint16_t*>(out), out_st);
+    return check_hip(hipGetLastError(), "norm_gemv_kernel");
+}
+
 int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, int64_t K, int64_t N,
                          const void* res, int64_t res_st, void* out, int64_t out_st, hipStream_t stream) {
     hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads),

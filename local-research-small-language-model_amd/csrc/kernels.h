@@ -23,6 +23,9 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                    void* vc = nullptr, int64_t c_sb = 0, int64_t c_st = 0, int64_t c_sh = 0, int64_t cap = 0);
 
 // decode-sized feed-forward half of a block: RMSNorm (folded) + SwiGLU + residual
+// out[m, n] = bf16((x[m] . W'[n]) / rms(x[m])) for M <= 16 rows: W' [N, C] bf16, C <= 1024
+int launch_norm_gemv(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t N, float eps,
+                     void* out, int64_t out_st, hipStream_t stream);
 // out[m] = bf16(res[m] + bf16(a[m] . W^T)) for M <= 16 rows: W [N, K] bf16, K <= 2048
 int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, int64_t K, int64_t N,
                          const void* res, int64_t res_st, void* out, int64_t out_st, hipStream_t stream);

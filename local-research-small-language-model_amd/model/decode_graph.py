@@ -219,7 +219,7 @@ class GraphDecoder:
                 x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
             x = layer.ffn_residual(x)
             prev_f = f
-        self.logits = m.embeddings.project(m.final_norm(x))[:, -1, :]
+        self.logits = m.logits(x)[:, -1, :]
         self.pos.add_(1)
 
     def _capture(self):

@@ -16,6 +16,8 @@ from model.norm import RMSNorm
 from model.rope import RotaryEmbedding
 from model.transformer import TransformerBlock
 
+import sparda
+
 
 class SparDAResearchModel(nn.Module):
     def __init__(self, config: ModelConfig):
@@ -27,6 +29,8 @@ class SparDAResearchModel(nn.Module):
         self.layers = nn.ModuleList([TransformerBlock(config, layer_idx=i) for i in range(config.n_layer)])
         self.final_norm = RMSNorm(config.n_embd, eps=config.norm_eps)
         self.apply(self._init_weights)
+        self._head_key = None
+        self._head_w: Optional[torch.Tensor] = None
 
     def _init_weights(self, module: nn.Module):
         if isinstance(module, nn.Linear):
@@ -41,6 +45,27 @@ class SparDAResearchModel(nn.Module):
         emb = self.embeddings.weight.numel()
         return {"total": total, "trainable": sum(p.numel() for p in self.parameters() if p.requires_grad),
                 "embeddings": emb, "layers": total - emb}
+
+    def _folded_head(self) -> torch.Tensor:
+        """The tied output weight with the final RMSNorm weight folded into its
+        columns, rebuilt when either changed."""
+        ws = (self.embeddings.weight, self.final_norm.weight)
+        key = tuple((t.data_ptr(), t._version) for t in ws)
+        if key != self._head_key:
+            with torch.no_grad():
+                self._head_w = (ws[0].float() * ws[1].float()[None, :]).to(torch.bfloat16).contiguous()
+            self._head_key = key
+        return self._head_w
+
+    def logits(self, x: torch.Tensor) -> torch.Tensor:
+        """final_norm + tied output projection (model/model.py:79-157); one
+        kernel for decode-sized bf16 batches under ``fused_ffn``."""
+        C = x.shape[-1]
+        if (getattr(self.config, "fused_ffn", False) and x.is_cuda and x.dtype == torch.bfloat16
+                and not torch.is_grad_enabled() and x.shape[0] * x.shape[1] <= 16 and C % 128 == 0
+                and C <= 1024 and self.config.vocab_size % 16 == 0):
+            return sparda.norm_gemv(x, self._folded_head(), self.final_norm.eps)
+        return self.embeddings.project(self.final_norm(x))
 
     def forward(self, input_ids: torch.Tensor, targets: Optional[torch.Tensor] = None,
                 kv_caches: Optional[List] = None, return_forecasts: bool = False) -> Dict[str, torch.Tensor]:
@@ -59,7 +84,7 @@ class SparDAResearchModel(nn.Module):
             if return_forecasts:
                 forecasts.append(current_forecast)
             prev_forecast = current_forecast
-        logits = self.embeddings.project(self.final_norm(x))
+        logits = self.logits(x)
         out = {"logits": logits}
         if return_forecasts:
             out["forecasts"] = forecasts

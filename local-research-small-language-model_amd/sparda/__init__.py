@@ -6,7 +6,7 @@ from ._lib import (BF16, F32, FETCH_DMA, FETCH_KERNEL, ROUTE_ABSOLUTE, ROUTE_REF
                    SpardaError, load)
 from .ops import (DecodeWorkspace, OffloadArena, append_at, block_sums, compress, decode, decode_at,
                   decode_selected, decode_sums, decode_workspace_bytes, default_scale, ffn_decode, gather_blocks, prefill, produce,
-                  rows_residual,
+                  norm_gemv, rows_residual,
                   require_device, route, select_decode, select_decode_at, select_fixed, teacher_block_mass,
                   topk_scores)
 
@@ -16,5 +16,5 @@ __all__ = [
     "load", "DecodeWorkspace", "compress", "decode", "decode_workspace_bytes", "default_scale",
     "gather_blocks", "prefill", "require_device", "route", "select_fixed", "topk_scores",
     "OffloadArena", "decode_selected", "select_decode", "block_sums", "produce", "teacher_block_mass",
-    "append_at", "select_decode_at", "decode_at", "ffn_decode", "decode_sums", "rows_residual",
+    "append_at", "select_decode_at", "decode_at", "ffn_decode", "decode_sums", "rows_residual", "norm_gemv",
 ]

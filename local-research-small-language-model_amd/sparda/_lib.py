@@ -87,6 +87,7 @@ SIGNATURES = {
                                   _i64, _p]),
     "sparda_ffn_decode": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _i64, _p]),
     "sparda_rows_residual": (_int, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p]),
+    "sparda_norm_gemv": (_int, [_p, _i64, _p, _i64, _i64, _i64, _f32, _p, _i64, _p]),
     "sparda_offload_fetch_at": (_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p]),
     "sparda_offload_append_at": (_int, [_p, _p, _p, _i64, _i64, _p, _i64, _p, _p]),
     "sparda_offload_append": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),

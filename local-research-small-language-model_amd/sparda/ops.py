@@ -558,6 +558,32 @@ def rows_residual(a: torch.Tensor, w: torch.Tensor, res: torch.Tensor,
     return out
 
 
+def norm_gemv(x: torch.Tensor, w_folded: torch.Tensor, eps: float,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """final_norm(x) . W^T for decode-sized batches in one kernel (the model's
+    last RMSNorm and its tied output projection, model/model.py:79-157 with
+    model/norm.py:15-21): x [B,T,C] bf16 with B*T <= 16, w_folded [N,C] bf16 =
+    W * norm_weight (folded into the columns). Returns [B,T,N] bf16."""
+    dev = require_device(x, w_folded, out)
+    _inference_only(x, w_folded)
+    if not (x.dtype == w_folded.dtype == torch.bfloat16):
+        raise TypeError("sparda: norm_gemv takes bf16 activations and weights")
+    B, T, C = x.shape
+    N = w_folded.shape[0]
+    if tuple(w_folded.shape) != (N, C):
+        raise AssertionError(f"Mismatch: weight {tuple(w_folded.shape)} for width {C}")
+    x2 = x.reshape(B * T, C)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8:
+        x2 = x2.contiguous()
+    w_folded = w_folded.contiguous()
+    if out is None:
+        out = torch.empty((B, T, N), dtype=torch.bfloat16, device=dev)
+    o2 = out.view(B * T, N)
+    call("sparda_norm_gemv", x2.data_ptr(), x2.stride(0), w_folded.data_ptr(), B * T, C, N, float(eps),
+         o2.data_ptr(), o2.stride(0), _stream(dev))
+    return out
+
+
 def _pos_ptr(pos_dev: torch.Tensor) -> int:
     """Address of a device-held position: one int64 element on the GPU."""
     if pos_dev.dtype != torch.int64 or pos_dev.numel() != 1 or not pos_dev.is_cuda:

@@ -80,6 +80,10 @@ def test_argument_errors_are_reported_before_any_hip_call():
             None, P, 8, 8, 8, 64, None)  # no k_cache
     _expect(-2, "sparda_produce_cache_at", P, 768, P, 17, 768, 768, 256, 256, 1e-5, P, P, 64, 1, P, P, P, P, P, 1,
             P, P, 8, 8, 8, 64, None)  # M > 16
+    # x, x_st, w, M, C, N, eps, out, out_st, stream
+    _expect(-1, "sparda_norm_gemv", None, 768, P, 1, 768, 32000, 1e-6, P, 32000, None)
+    _expect(-2, "sparda_norm_gemv", P, 768, P, 1, 768, 32001, 1e-6, P, 32001, None)   # N % 16
+    _expect(-2, "sparda_norm_gemv", P, 2048, P, 1, 2048, 32000, 1e-6, P, 32000, None)  # C > 1024
     # a, a_st, w, M, K, N, res, res_st, out, out_st, stream
     _expect(-1, "sparda_rows_residual", None, 768, P, 1, 768, 768, P, 768, P, 768, None)
     _expect(-2, "sparda_rows_residual", P, 768, P, 17, 768, 768, P, 768, P, 768, None)   # M > 16

@@ -204,3 +204,20 @@ def test_produce_writes_the_cache_rows():
         assert torch.equal(kc[:, p], k1[:, 0]) and torch.equal(vc[:, p], v1[:, 0])
         rest = [t for t in range(300) if t != p]
         assert torch.equal(kc[:, rest], k0[:, rest]) and torch.equal(vc[:, rest], v0[:, rest])
+
+
+@pytest.mark.parametrize("M,C,N", [(1, 768, 32000), (8, 768, 4096), (16, 1024, 160)])
+def test_norm_gemv_op(M, C, N):
+    # final RMSNorm + output projection, against the fp32 product of the
+    # folded weight divided by rms(x), one bf16 rounding
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, 1, C, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, C, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    nw = (1.0 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(DEV)
+    wf = (w.float() * nw.float()[None, :]).to(torch.bfloat16)
+    got = sparda.norm_gemv(x, wf, 1e-6)
+    xf = x.float().reshape(M, C)
+    want = (xf @ wf.float().T) / torch.sqrt((xf * xf).mean(-1, keepdim=True) + 1e-6)
+    diff = (got.reshape(M, N).float() - want).abs()
+    tol = want.abs() * 2 ** -7 + 1e-3
+    assert bool((diff <= tol).all()), f"max diff {diff.max().item()}"
