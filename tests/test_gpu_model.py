@@ -201,6 +201,8 @@ def test_async_prefetch_absolute_matches_oracle_and_stale_prefetch_is_dropped():
         fv = torch.randn(2, 1, cfg.forecast_heads, cfg.forecast_dim, device=DEV).to(torch.bfloat16)
         attn.track_overlap = True
         assert attn.prefetch(fv, cache)
+        # the selection is written on the transfer stream: wait for its event before reading it here
+        torch.cuda.current_stream().wait_event(attn.prefetch_event)
         sel = attn.prefetched_sel_indices.clone()
         out = attn(x[:, T:T + 1], rot, kv_cache=cache, forecast_vector=fv)
         xq, xk, xv = _project(attn, rot, x[:, T:T + 1], offset=T)
