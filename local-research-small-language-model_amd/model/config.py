@@ -54,13 +54,13 @@ class ModelConfig:
     fused_ffn: bool = False
 
     def __post_init__(self):
-        assert self.n_embd == self.n_head * self.head_dim, (
-            f"n_embd ({self.n_embd}) must equal n_head ({self.n_head}) * head_dim ({self.head_dim})"
-        )
-        assert self.n_head % self.n_kv_head == 0, (
-            f"n_head ({self.n_head}) must be divisible by n_kv_head ({self.n_kv_head})"
-        )
-        assert self.decode_routing in ("reference", "absolute"), (
-            f"decode_routing must be 'reference' or 'absolute', got {self.decode_routing!r}"
-        )
+        if self.n_head * self.head_dim != self.n_embd:
+            raise AssertionError(f"{self.n_head} query heads of dim {self.head_dim} do not tile "
+                                 f"the {self.n_embd}-wide residual stream")
+        if self.n_head % self.n_kv_head:
+            raise AssertionError(f"{self.n_kv_head} key/value heads cannot be shared evenly by "
+                                 f"{self.n_head} query heads")
+        if self.decode_routing not in ("reference", "absolute"):
+            raise AssertionError(f"unknown decode_routing {self.decode_routing!r} "
+                                 "(expected 'reference' or 'absolute')")
         self.num_queries_per_kv = self.n_head // self.n_kv_head

@@ -20,6 +20,10 @@ import sparda
 
 
 class SparDAResearchModel(nn.Module):
+    """Token embedding -> n_layer forecast-routed blocks -> final RMSNorm ->
+    tied output projection. Parameter names and count are the reference's, so
+    its state dicts load unchanged."""
+
     def __init__(self, config: ModelConfig):
         super().__init__()
         self.config = config
@@ -28,23 +32,29 @@ class SparDAResearchModel(nn.Module):
                                           theta=config.rope_theta)
         self.layers = nn.ModuleList([TransformerBlock(config, layer_idx=i) for i in range(config.n_layer)])
         self.final_norm = RMSNorm(config.n_embd, eps=config.norm_eps)
-        self.apply(self._init_weights)
+        self._draw_projection_weights()
         self._head_key = None
         self._head_w: Optional[torch.Tensor] = None
 
-    def _init_weights(self, module: nn.Module):
-        if isinstance(module, nn.Linear):
-            nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
-            if module.bias is not None:
-                nn.init.zeros_(module.bias)
-        elif isinstance(module, nn.Embedding):
-            nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
+    @torch.no_grad()
+    def _draw_projection_weights(self) -> None:
+        """Every projection of the model is a bias-free ``nn.Linear``; each
+        weight is drawn from N(0, initializer_range^2), in module order. The
+        tied embedding draws its own table when it is built and the norm
+        weights start at one."""
+        std = self.config.initializer_range
+        for proj in self.modules():
+            if isinstance(proj, nn.Linear):
+                proj.weight.normal_(0.0, std)
 
     def count_parameters(self) -> Dict[str, int]:
-        total = sum(p.numel() for p in self.parameters())
-        emb = self.embeddings.weight.numel()
-        return {"total": total, "trainable": sum(p.numel() for p in self.parameters() if p.requires_grad),
-                "embeddings": emb, "layers": total - emb}
+        """Parameter counts: the whole model, the trainable part, the shared
+        embedding table, and everything else."""
+        sizes = [(p.numel(), p.requires_grad) for p in self.parameters()]
+        total = sum(n for n, _ in sizes)
+        table = self.embeddings.weight.numel()
+        return {"total": total, "trainable": sum(n for n, g in sizes if g),
+                "embeddings": table, "layers": total - table}
 
     def _folded_head(self) -> torch.Tensor:
         """The tied output weight with the final RMSNorm weight folded into its
@@ -69,29 +79,32 @@ class SparDAResearchModel(nn.Module):
 
     def forward(self, input_ids: torch.Tensor, targets: Optional[torch.Tensor] = None,
                 kv_caches: Optional[List] = None, return_forecasts: bool = False) -> Dict[str, torch.Tensor]:
-        """input_ids [B,T] -> {"logits" [B,T,V], "loss"?, "forecasts"?} (model/model.py:79-157)."""
-        x = self.embeddings.embed(input_ids)
-        forecasts: List[torch.Tensor] = []
-        prev_forecast: Optional[torch.Tensor] = None
+        """input_ids [B,T] -> {"logits" [B,T,V], "loss"?, "forecasts"?} (model/model.py:79-157).
+
+        Block i receives the forecast block i-1 emitted (None for block 0),
+        its own cache, and block i+1 with that block's cache so it can issue
+        the next layer's prefetch before its own attention."""
         n = len(self.layers)
-        for i, layer in enumerate(self.layers):
-            kv_cache = kv_caches[i] if kv_caches is not None else None
-            next_layer = self.layers[i + 1] if i + 1 < n else None
-            next_cache = kv_caches[i + 1] if (kv_caches is not None and i + 1 < len(kv_caches)) else None
-            x, current_forecast = layer(x=x, rotary_emb=self.rotary_emb, kv_cache=kv_cache, mask=None,
-                                        is_causal=True, prev_layer_forecast=prev_forecast,
-                                        next_layer_block=next_layer, next_kv_cache=next_cache)
-            if return_forecasts:
-                forecasts.append(current_forecast)
-            prev_forecast = current_forecast
-        logits = self.logits(x)
-        out = {"logits": logits}
+        caches: List = list(kv_caches) if kv_caches is not None else []
+        caches += [None] * (n + 1 - len(caches))
+        followers = list(self.layers)[1:] + [None]
+        h = self.embeddings.embed(input_ids)
+        emitted: List[torch.Tensor] = []
+        forecast: Optional[torch.Tensor] = None
+        for block, follower, cache, follower_cache in zip(self.layers, followers, caches, caches[1:]):
+            h, forecast_out = block(x=h, rotary_emb=self.rotary_emb, kv_cache=cache, mask=None, is_causal=True,
+                                    prev_layer_forecast=forecast, next_layer_block=follower,
+                                    next_kv_cache=follower_cache if follower is not None else None)
+            forecast = forecast_out
+            emitted.append(forecast_out)
+        result: Dict[str, torch.Tensor] = {"logits": self.logits(h)}
         if return_forecasts:
-            out["forecasts"] = forecasts
+            result["forecasts"] = emitted
         if targets is not None:
-            out["loss"] = F.cross_entropy(logits.view(-1, self.config.vocab_size), targets.view(-1),
-                                          ignore_index=-100)
-        return out
+            vocab = self.config.vocab_size
+            result["loss"] = F.cross_entropy(result["logits"].reshape(-1, vocab), targets.reshape(-1),
+                                             ignore_index=-100)
+        return result
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 50, temperature: float = 0.8,

@@ -23,6 +23,18 @@ def test_library_loads_and_reports_version():
     assert lib.sparda_version() == 100
 
 
+def test_the_loaded_library_is_the_in_tree_build():
+    # the mapping the process holds is the file next to the binding, unless
+    # SPARDA_LIBRARY overrides it on purpose
+    if os.environ.get("SPARDA_LIBRARY"):
+        pytest.skip("SPARDA_LIBRARY overrides the library path")
+    in_tree = os.path.join(ROOT, "local-research-small-language-model_amd", "sparda", "libsparda.so")
+    sparda.load()
+    maps = open("/proc/self/maps").read()
+    mapped = {line.split()[-1] for line in maps.splitlines() if line.endswith("libsparda.so")}
+    assert mapped and all(os.path.samefile(m, in_tree) for m in mapped), mapped
+
+
 def test_every_declared_symbol_is_exported_and_bound():
     lib = sparda.load()
     syms = header_symbols()

@@ -309,7 +309,7 @@ def test_decode_16k_cache(routing):
     case(f"decode 16K {routing}")
     d, out, ex = _decode_case(8, 16384, 12, 4, 64, 64, 8, torch.bfloat16, routing, seed=1002)
     assert np.array_equal(ex["protos"].cpu().numpy(), O.compress(np32(d["k_cache"]), 64))
-    # a second call on the same workspace (arrival counters reset) is identical
+    # a second call (nothing survives a call in the workspace) is identical
     out2 = sparda.decode(d["q"], d["k_cache"], d["v_cache"], 16384, d["forecast"], 64, 8, routing=routing)
     assert torch.equal(out, out2)
 
