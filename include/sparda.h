@@ -245,6 +245,30 @@ SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh,
                              void* stream);
 
 /*
+ * sparda_decode without a workspace argument. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops and harnesses that forbid hipMalloc). The
+ * step's block scores live in a static device array of 1 MiB per GPU
+ * (B * Hkv * ceil(S/block_size) <= 262,144 scores; larger steps return
+ * SPARDA_ERR_CAPACITY). The call itself allocates nothing; the caller passes
+ * every input and output as for sparda_decode, whose arguments and results
+ * this matches exactly. Uses the current device's array: the stream must
+ * belong to the current device, and calls that overlap in time on one GPU
+ * race on the array.
+ */
+SPARDA_API int sparda_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                     const void* k_cache, const void* v_cache,
+                                     int64_t kv_sb, int64_t kv_ss, int64_t kv_sh,
+                                     int dtype,
+                                     const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
+                                     int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                                     int64_t block_size, int64_t top_k, int routing, float scale,
+                                     const float* protos_in, float* protos_out,
+                                     int32_t* sel_out, int32_t* n_sel_out,
+                                     void* out, int64_t out_sb,
+                                     void* stream);
+
+/*
  * Single-token decode attention over a given block selection.
  * Replaces the gather + validity mask + SDPA over selected blocks of
  * SparseAttention._forward_decode_gather (model/attention/sparse.py:154-181)

@@ -29,6 +29,35 @@ static bool head_dim_ok(int64_t d) { return d == 16 || d == 32 || d == 64 || d =
 constexpr int64_t kMaxTopK = 32;
 constexpr int64_t kMaxGroupAbi = 16;
 
+int check_decode_args(const void* q, const void* k_cache, const void* v_cache, int64_t kv_sb, int64_t kv_ss,
+                      int64_t kv_sh, int dtype, const void* forecast, int f_dtype, int64_t B, int64_t S, int64_t Hq,
+                      int64_t Hkv, int64_t D, int64_t block_size, int64_t top_k, int routing,
+                      const int32_t* sel_out, const int32_t* n_sel_out, const void* out) {
+    SPARDA_REQUIRE(q && k_cache && v_cache && out, SPARDA_ERR_NULL, "decode: null q/k/v/out");
+    SPARDA_REQUIRE(!sel_out == !n_sel_out, SPARDA_ERR_NULL, "decode: sel_out and n_sel_out go together");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "decode: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(!forecast || dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "decode: forecast dtype %d", f_dtype);
+    SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
+                   "decode: unknown routing %d", routing);
+    SPARDA_REQUIRE(B > 0 && S > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "decode: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "decode: head dim %lld not in {16,32,64,128}",
+                   (long long)D);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "decode: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "decode: top_k out of range");
+    SPARDA_REQUIRE(Hkv * D <= 2048, SPARDA_ERR_SHAPE, "decode: Hkv*D > 2048");
+    const int64_t NB = cdiv(S, block_size);
+    SPARDA_REQUIRE(NB <= 4096, SPARDA_ERR_SHAPE, "decode: more than 4096 blocks");
+    SPARDA_REQUIRE(B <= 65535, SPARDA_ERR_SHAPE, "decode: B too large");
+    const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
+    const bool al = (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 && kv_sb % ve == 0 && kv_ss % ve == 0 &&
+                    kv_sh % ve == 0;
+    SPARDA_REQUIRE(al, SPARDA_ERR_STRIDE, "decode: K/V cache rows must be 16-byte aligned");
+    return 0;
+}
+
 }  // namespace sparda
 
 using namespace sparda;
@@ -167,31 +196,10 @@ SPARDA_API int sparda_decode(const void* q, int64_t q_sb, int64_t q_sh, const vo
                              int64_t top_k, int routing, float scale, const float* protos_in,
                              float* protos_out, int32_t* sel_out, int32_t* n_sel_out, void* out,
                              int64_t out_sb, void* workspace, size_t workspace_bytes, void* stream) {
-    SPARDA_REQUIRE(q && k_cache && v_cache && out, SPARDA_ERR_NULL, "decode: null q/k/v/out");
+    const int rc = check_decode_args(q, k_cache, v_cache, kv_sb, kv_ss, kv_sh, dtype, forecast, f_dtype, B, S, Hq,
+                                     Hkv, D, block_size, top_k, routing, sel_out, n_sel_out, out);
+    if (rc) return rc;
     SPARDA_REQUIRE(workspace, SPARDA_ERR_WORKSPACE, "decode: workspace is required");
-    SPARDA_REQUIRE(!sel_out == !n_sel_out, SPARDA_ERR_NULL, "decode: sel_out and n_sel_out go together");
-    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "decode: dtype %d unsupported", dtype);
-    SPARDA_REQUIRE(!forecast || dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "decode: forecast dtype %d", f_dtype);
-    SPARDA_REQUIRE(routing == SPARDA_ROUTE_REFERENCE || routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
-                   "decode: unknown routing %d", routing);
-    SPARDA_REQUIRE(B > 0 && S > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
-                   "decode: sizes must be positive");
-    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "decode: head dim %lld not in {16,32,64,128}",
-                   (long long)D);
-    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
-                   "decode: Hq must be a multiple of Hkv with ratio <= 16");
-    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "decode: top_k out of range");
-    SPARDA_REQUIRE(Hkv * D <= 2048, SPARDA_ERR_SHAPE, "decode: Hkv*D > 2048");
-    const int64_t NB = cdiv(S, block_size);
-    SPARDA_REQUIRE(NB <= 4096, SPARDA_ERR_SHAPE, "decode: more than 4096 blocks");
-    SPARDA_REQUIRE(B <= 65535, SPARDA_ERR_SHAPE, "decode: B too large");
-    {
-        const int64_t ve = 16 / (dtype == SPARDA_F32 ? 4 : 2);
-        const bool al = (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
-                        (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 && kv_sb % ve == 0 &&
-                        kv_ss % ve == 0 && kv_sh % ve == 0;
-        SPARDA_REQUIRE(al, SPARDA_ERR_STRIDE, "decode: K/V cache rows must be 16-byte aligned");
-    }
     const DecodeWs ws = decode_ws_layout(workspace, B, S, Hq, Hkv, D, block_size, top_k);
     SPARDA_REQUIRE(workspace_bytes >= ws.bytes, SPARDA_ERR_WORKSPACE, "decode: workspace %zu < %zu bytes",
                    workspace_bytes, ws.bytes);

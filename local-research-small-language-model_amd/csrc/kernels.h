@@ -55,6 +55,12 @@ struct DecodeWs {
 DecodeWs decode_ws_layout(void* base, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
                           int64_t bs, int64_t k);
 
+// Argument checks of one decode step (before any HIP call); 0 or a negative status.
+int check_decode_args(const void* q, const void* k_cache, const void* v_cache, int64_t kv_sb, int64_t kv_ss,
+                      int64_t kv_sh, int dtype, const void* forecast, int f_dtype, int64_t B, int64_t S, int64_t Hq,
+                      int64_t Hkv, int64_t D, int64_t block_size, int64_t top_k, int routing,
+                      const int32_t* sel_out, const int32_t* n_sel_out, const void* out);
+
 int launch_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kc, const void* vc,
                   int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, const void* f, int fdtype,
                   int64_t f_sb, int64_t f_sh, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,

@@ -59,6 +59,9 @@ SIGNATURES = {
     "sparda_decode": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _i64,
                              _i64, _i64, _i64, _i64, _i64, _i64, _int, _f32, _p, _p, _p, _p, _p, _i64,
                              _p, _size, _p]),
+    "sparda_decode_noalloc": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _i64,
+                                     _i64, _i64, _i64, _i64, _i64, _i64, _int, _f32, _p, _p, _p, _p, _p, _i64,
+                                     _p]),
     "sparda_decode_selected": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _p, _p,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
     "sparda_select_decode": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
