@@ -1,0 +1,618 @@
+// bf16 block-sparse GQA prefill over compacted tiles (D = 64, bs = 64,
+// at most 10 selected blocks per token).
+//
+// One workgroup (4 wavefronts) serves one (sequence b, KV head g, query block
+// qb): 64 query tokens x R = Hq/Hkv query heads = 64R columns, column
+// c = token * R + head. Every query token picks its own blocks, so a KV block
+// is attended by only some of the window's columns. For each block j in the
+// union of the window's selections, the columns that selected j are packed,
+// in token order, into tiles of 16 (the N side of v_mfma_f32_16x16x32_bf16):
+//     S^T[key, slot] = K[key, :] . Q[col(slot), :]          (8 MFMA)
+//     P = exp2(S^T * scale * log2 e - m_ref[col])            (VALU, bf16)
+//     O^T[d, slot]  += V^T[d, key] . P^T[key, slot]          (8 MFMA, C = acc)
+// so a tile wastes only its padding slots (and the masked half of the causal
+// diagonal block, whose key sub-tiles past the tile's last token are skipped).
+//
+// Accumulation. P is taken against a fixed per-column reference m_ref, the
+// larger of the column's scores with the first key of its smallest selected
+// block (the sink, for router lists) and with its own key (when its own block
+// is selected): both are allowed keys, so m_ref never exceeds the row maximum
+// and the row keeps a term P = 1. Contributions are then plain sums (no
+// rescaling), accumulated in fp32 in LDS (acc[col][d], row sums lsum[col]).
+// Work items (a block and up to three of its tiles) are taken by the waves
+// from a shared counter in block order; a column's contributions are added in
+// ascending block order, each tile waiting until the column's earlier blocks
+// have been added (vers[col] = blocks added so far), so the result does not
+// depend on timing. A column whose row sum passes 2^64 (a score more than 64
+// log2-units above m_ref) trips a flag; the workgroup then takes the exact
+// row maxima in a scores-only pass and redoes the window with them.
+//
+// K A operands are read straight from memory; V is staged per wavefront in
+// LDS, half a block at a time (XOR-swizzled 16-byte chunks), and read
+// transposed with ds_read_b64_tr_b16.
+#include "common.h"
+#include "kernels.h"
+#include "mfma.h"
+
+namespace sparda {
+
+namespace {
+
+constexpr int kCT = 256;                        // threads per workgroup
+constexpr int kCWaves = kCT / kWave;            // 4
+constexpr int kCWin = 64;                       // query tokens per workgroup
+constexpr int kCMaxCap = 10;                    // selection entries per token
+constexpr int kCMaxUnion = kCWin * kCMaxCap;    // distinct blocks a window can select
+constexpr int kCMaxNB = 1024;                   // KV blocks (bitmap set-up)
+constexpr int kCChunk = 3;                      // tiles per work item
+constexpr float kCLog2e = 1.4426950408889634f;
+constexpr float kCGuard = 18446744073709551616.0f;  // 2^64
+constexpr uint32_t kCSpinLimit = 1u << 20;
+constexpr int kSentinel = 0x7fffffff;
+
+template <int R>
+struct CompactSmem {
+    static constexpr int kCols = kCWin * R;
+    static constexpr int kMaxItems = (R * kCMaxUnion) / 16 + kCMaxUnion;
+    // fp32 accumulators, slab layout: acc[s * kCols + col] = O[col][4s .. 4s+3].
+    // During the set-up the same bytes hold the per-block token bitmaps, the
+    // block -> union map and per-token facts.
+    float4 acc[16 * kCols];
+    uint16_t vstage[kCWaves][32 * 64];          // half a V block per wave, swizzled
+    unsigned long long umask[kCMaxUnion];       // tokens selecting union block u
+    uint32_t items[kMaxItems];                  // u | first tile << 16
+    float mref[kCols];                          // log2 units
+    float lsum[kCols];                          // row sums (exact-max pass: order keys)
+    int32_t vers[kCols];                        // blocks added to the column so far
+    uint16_t ulist[kCMaxUnion];                 // block index of union entry u
+    uint16_t uofs[kCMaxUnion + 1];              // rank records of u start here
+    uint8_t rankbuf[kCMaxUnion];                // rank of block u in a token's list
+    uint8_t tokrank[kCWaves][64];               // selecting token of each rank
+    int n_union, n_items, next_item, flag;
+#ifdef SPARDA_PC_DEBUG
+    int dbg_rank[kCols];
+    int dbg_spin[kCols];
+#endif
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz(int r) { return 2 * ((r >> 1) & 3); }
+// element index of (local row r, element col) in a swizzled V half-stage
+__device__ __forceinline__ int vidx(int r, int col) { return r * 64 + (((col >> 3) ^ swz(r)) << 3) + (col & 7); }
+
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+}  // namespace
+
+template <int R>
+__global__ void __launch_bounds__(kCT, 2)
+prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                       const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                       int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                       const int32_t* __restrict__ sel, const int32_t* __restrict__ n_sel, int64_t cap,
+                       int64_t T, int H, int64_t NBq, int causal, float scale_log2,
+                       uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st) {
+    using Smem = CompactSmem<R>;
+    constexpr int kCols = Smem::kCols;
+    __shared__ Smem sm;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    const int col16 = lane % 16;
+    const int grp = lane / 16;
+    const uint64_t below = (1ull << lane) - 1ull;
+
+    // heaviest query blocks first; consecutive ids cycle through (b, g)
+    const int64_t BH = static_cast<int64_t>(gridDim.x) / NBq;
+    const int64_t bg = blockIdx.x % BH;
+    const int64_t qb = NBq - 1 - blockIdx.x / BH;
+    const int b = static_cast<int>(bg / H);
+    const int g = static_cast<int>(bg % H);
+    const int64_t t0 = qb * 64;
+    const int64_t NB = cdiv(T, 64);
+    const int t_valid = static_cast<int>(T - t0 < 64 ? T - t0 : 64);
+    const int jmax = static_cast<int>(causal ? qb : NB - 1);  // highest block a token here may attend
+    const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
+    const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
+    const uint16_t* qbase = q + b * q_sb + t0 * q_st + static_cast<int64_t>(g * R) * q_sh;
+
+    unsigned long long* bitmap = reinterpret_cast<unsigned long long*>(sm.acc);          // [kCMaxNB]
+    uint16_t* jmap = reinterpret_cast<uint16_t*>(bitmap + kCMaxNB);                       // [kCMaxNB]
+    int16_t* tokfirst = reinterpret_cast<int16_t*>(jmap + kCMaxNB);                      // [64]
+    uint8_t* tokown = reinterpret_cast<uint8_t*>(tokfirst + 64);                         // [64]
+
+    // ---- set-up 1: this thread's column rows (reference maxima) and token list ----
+    const int ctok = tid / R, chead = tid % R;
+    const bool ccol = tid < kCols && ctok < t_valid;
+    u32x4 qr[8], kd[8], k0[8];
+    if (ccol) {
+        const uint16_t* qp = qbase + ctok * q_st + chead * q_sh;
+        const uint16_t* kp = kbase + (t0 + ctok) * kv_st;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            qr[i] = *reinterpret_cast<const u32x4*>(qp + 8 * i);
+            kd[i] = *reinterpret_cast<const u32x4*>(kp + 8 * i);
+            k0[i] = *reinterpret_cast<const u32x4*>(kbase + 8 * i);
+        }
+    }
+    int lst[kCMaxCap];
+#pragma unroll
+    for (int i = 0; i < kCMaxCap; ++i) lst[i] = kSentinel;
+    if (tid < t_valid) {
+        const int64_t r = (static_cast<int64_t>(b) * H + g) * T + t0 + tid;
+        const int64_t nr = n_sel[r];
+        const int n = static_cast<int>(nr < 0 ? 0 : (nr > cap ? cap : nr));
+        const int32_t* row = sel + r * cap;
+#pragma unroll
+        for (int i = 0; i < kCMaxCap; ++i) {
+            if (i < n) {
+                const int j = row[i];
+                lst[i] = (j >= 0 && j <= jmax) ? j : kSentinel;
+            }
+        }
+        // ascending, duplicates dropped (odd-even transposition sort, twice)
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+            for (int rd = 0; rd < kCMaxCap; ++rd)
+#pragma unroll
+                for (int i = rd & 1; i + 1 < kCMaxCap; i += 2) {
+                    const int a = lst[i], c = lst[i + 1];
+                    lst[i] = a < c ? a : c;
+                    lst[i + 1] = a < c ? c : a;
+                }
+            if (pass == 0) {
+#pragma unroll
+                for (int i = kCMaxCap - 1; i > 0; --i)
+                    if (lst[i] == lst[i - 1]) lst[i] = kSentinel;
+            }
+        }
+    }
+    for (int i = tid; i <= jmax; i += kCT) bitmap[i] = 0ull;
+    __syncthreads();
+    if (tid < t_valid) {
+        const int own = static_cast<int>((t0 + tid) / 64);
+        bool has_own = false;
+#pragma unroll
+        for (int i = 0; i < kCMaxCap; ++i) {
+            if (lst[i] != kSentinel) {
+                atomicOr(&bitmap[lst[i]], 1ull << tid);
+                has_own = has_own || lst[i] == own;
+            }
+        }
+        tokfirst[tid] = static_cast<int16_t>(lst[0] != kSentinel ? lst[0] : -1);
+        tokown[tid] = has_own ? 1 : 0;
+    }
+    __syncthreads();
+
+    // ---- set-up 2: union of the selected blocks, work items, rank offsets (wave 0) ----
+    if (wave == 0) {
+        int nu = 0, ni = 0, nrk = 0;
+        for (int c0 = 0; c0 <= jmax; c0 += kWave) {
+            const int j = c0 + lane;
+            const unsigned long long M = j <= jmax ? bitmap[j] : 0ull;
+            const bool nz = M != 0ull;
+            const uint64_t bal = __ballot(nz);
+            const int nt = __popcll(M);
+            const int tiles = (R * nt + 15) / 16;
+            const int chunks = nz ? (tiles + kCChunk - 1) / kCChunk : 0;
+            const int rk = nz ? nt : 0;
+            // inclusive prefix sums over the lanes
+            int sc = chunks, sr = rk;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int a = __shfl_up(sc, o, kWave), c = __shfl_up(sr, o, kWave);
+                if (lane >= o) {
+                    sc += a;
+                    sr += c;
+                }
+            }
+            if (nz) {
+                const int pos = nu + __popcll(bal & below);
+                const int item0 = ni + sc - chunks;
+                sm.ulist[pos] = static_cast<uint16_t>(j);
+                sm.umask[pos] = M;
+                sm.uofs[pos] = static_cast<uint16_t>(nrk + sr - rk);
+                jmap[j] = static_cast<uint16_t>(pos);
+                for (int cc = 0; cc < chunks; ++cc)
+                    sm.items[item0 + cc] = static_cast<uint32_t>(pos) | (static_cast<uint32_t>(cc * kCChunk) << 16);
+            }
+            nu += __popcll(bal);
+            ni += __shfl(sc, kWave - 1, kWave);
+            nrk += __shfl(sr, kWave - 1, kWave);
+        }
+        if (lane == 0) {
+            sm.n_union = nu;
+            sm.n_items = ni;
+            sm.uofs[nu] = static_cast<uint16_t>(nrk);
+            sm.next_item = 0;
+            sm.flag = 0;
+        }
+    }
+    __syncthreads();
+
+    // ---- set-up 3: ranks (position of each block in a token's list) and m_ref ----
+    if (tid < t_valid) {
+#pragma unroll
+        for (int i = 0; i < kCMaxCap; ++i) {
+            if (lst[i] != kSentinel) {
+                const int u = jmap[lst[i]];
+                const int p = __popcll(sm.umask[u] & ((1ull << tid) - 1ull));
+                sm.rankbuf[sm.uofs[u] + p] = static_cast<uint8_t>(i);
+            }
+        }
+    }
+    if (tid < kCols) {
+        float mr = 0.0f;
+        if (ccol) {
+            auto dot = [&](const u32x4 (&a)[8], const u32x4 (&c)[8]) __attribute__((always_inline)) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        acc = __builtin_fmaf(__uint_as_float(a[i][w] << 16), __uint_as_float(c[i][w] << 16), acc);
+                        acc = __builtin_fmaf(__uint_as_float(a[i][w] & 0xffff0000u),
+                                             __uint_as_float(c[i][w] & 0xffff0000u), acc);
+                    }
+                }
+                return acc;
+            };
+            const int first = tokfirst[ctok];
+            float s;
+            if (first == 0) {
+                s = dot(qr, k0);
+            } else {  // the first key of the smallest selected block (not the sink)
+                u32x4 kf[8];
+                const int fb = first < 0 ? 0 : first;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    kf[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(fb) * 64 * kv_st + 8 * i);
+                s = dot(qr, kf);
+            }
+            if (tokown[ctok]) s = __builtin_fmaxf(s, dot(qr, kd));
+            mr = s * scale_log2;
+        }
+        sm.mref[tid] = mr;
+        sm.lsum[tid] = 0.0f;
+        sm.vers[tid] = 0;
+    }
+    __syncthreads();  // the set-up aliases in acc are dead from here
+    for (int i = tid; i < 16 * kCols; i += kCT) sm.acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#ifdef SPARDA_PC_DEBUG
+    for (int i = tid; i < kCols; i += kCT) {
+        sm.dbg_rank[i] = -1;
+        sm.dbg_spin[i] = -1;
+    }
+#endif
+    __syncthreads();
+
+    // ---- the tiles ----
+    bf16x8 ones_a;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
+    const int64_t last_row = T - 1;
+
+    auto grab = [&]() -> int {
+        int it = 0;
+        if (lane == 0) it = atomicAdd(&sm.next_item, 1);
+        return __builtin_amdgcn_readfirstlane(it);
+    };
+    // K A operands (key 16n + col16, dims 32kk + 8grp ..) and V rows (chunk lane + 64i:
+    // row (lane + 64i) / 8, 16-byte column lane % 8) of union block u; rows past T
+    // read row T-1 (finite, masked)
+    auto load_k = [&](int item, u32x4 (&kr)[8]) __attribute__((always_inline)) {
+        const int64_t j = sm.ulist[item & 0xffff];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            int64_t row = j * 64 + 16 * n + col16;
+            row = row < last_row ? row : last_row;
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+                kr[2 * n + kk] = *reinterpret_cast<const u32x4*>(kbase + row * kv_st + 32 * kk + 8 * grp);
+        }
+    };
+    auto load_v = [&](int item, u32x4 (&vr)[8]) __attribute__((always_inline)) {
+        const int64_t j = sm.ulist[item & 0xffff];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int64_t row = j * 64 + (lane + 64 * i) / 8;
+            row = row < last_row ? row : last_row;
+            vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * kv_st + (lane % 8) * 8);
+        }
+    };
+
+    uint16_t* vst = sm.vstage[wave];
+    uint8_t* trk = sm.tokrank[wave];
+    const int rsub = 4 * grp + col16 / 4;
+    const int csub = 4 * (col16 % 4);
+
+    // one work item (packed word: union entry u | first tile i0 << 16): tiles
+    // [i0, i0 + kCChunk) of union block u, K operands in kr, V rows in vr
+    // (reloaded with the V rows of item word nxt once staged); MAXPASS: scores
+    // only, column maxima
+    auto process = [&](int item, const u32x4 (&kr)[8], u32x4 (&vr)[8], int nxt,
+                       bool maxpass) __attribute__((always_inline)) {
+        const int u = item & 0xffff;
+        const int i0 = item >> 16;
+        const int j = sm.ulist[u];
+        const unsigned long long M = sm.umask[u];
+        const int ncol = R * __popcll(M);
+        const int tiles = (ncol + 15) / 16;
+        const int i1 = i0 + kCChunk < tiles ? i0 + kCChunk : tiles;
+        const int rofs = sm.uofs[u];
+        if ((M >> lane) & 1ull) trk[__popcll(M & below)] = static_cast<uint8_t>(lane);
+        // V^T operands: stage each half of the block, read it transposed
+        bf16x8 va[4][2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = lane / 8 + 8 * i;
+                *reinterpret_cast<u32x4*>(vst + vidx(r, (lane % 8) * 8)) = vr[4 * m + i];
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const i16x4 lo = lds_read_tr(vst + vidx(rsub, 16 * dt + csub));
+                const i16x4 hi = lds_read_tr(vst + vidx(rsub + 16, 16 * dt + csub));
+                va[dt][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        load_v(nxt, vr);  // unconditional (nxt repeats item at the end): the registers stay registers
+        const bool diag = causal && j == qb;
+        const int lim_tail = (!causal && (static_cast<int64_t>(j) + 1) * 64 > T) ? static_cast<int>(T - j * 64LL) : 64;
+        for (int i = i0; i < i1; ++i) {
+            const int e = 16 * i + col16;
+            const bool valid = e < ncol;
+            const int ei = valid ? e : ncol - 1;  // padding slots repeat the last column, masked
+            const int tr = ei / R;
+            const int h = ei % R;
+            const int tk = trk[tr];
+            const int c = tk * R + h;
+            const uint16_t* qp = qbase + tk * q_st + h * q_sh + 8 * grp;
+            const bf16x8 qb0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp));
+            const bf16x8 qb1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + 32));
+            // causal diagonal: key sub-tiles past the tile's last token are all masked
+            int thi = 63;
+            if (diag) {
+                const int last = (16 * i + 15 < ncol ? 16 * i + 15 : ncol - 1) / R;
+                thi = trk[last];
+            }
+            const int nmax = thi / 16;
+            f32x4 s[4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                if (n <= nmax) {
+                    s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n]), qb0, s[n], 0, 0, 0);
+                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n + 1]), qb1, s[n], 0,
+                                                                   0, 0);
+                } else {
+                    s[n] = f32x4{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+                }
+            }
+            if (diag || lim_tail < 64) {
+                const int lim = diag ? tk : lim_tail - 1;  // keys <= lim are allowed
+#pragma unroll
+                for (int n = 0; n < 4; ++n)
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii)
+                        if (16 * n + 4 * grp + ii > lim) s[n][ii] = -__builtin_inff();
+            }
+            if (maxpass) {
+                float mx = max16_nn(s);
+                mx = pair32_max(pair16_max(mx));
+                if (valid && grp == 0)
+                    atomicMax(reinterpret_cast<uint32_t*>(sm.lsum) + c, order_key(mx * scale_log2));
+                continue;
+            }
+            const float neg = valid ? -sm.mref[c] : -__builtin_inff();
+            uint4 pw[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                bf16x8 pb;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    pb[ii] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m][ii], scale_log2, neg)));
+                    pb[4 + ii] =
+                        static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m + 1][ii], scale_log2, neg)));
+                }
+                pw[m] = __builtin_bit_cast(uint4, pb);
+            }
+            const int rank = sm.rankbuf[rofs + tr];
+            // wait until the column's earlier blocks have been added
+            const bool owner = valid && grp == 0;
+            uint32_t spins = 0;
+            for (;; ++spins) {
+                const bool ready = !owner || __hip_atomic_load(&sm.vers[c], __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_WORKGROUP) >= rank;
+                if (__ballot(!ready) == 0ull) break;
+                if (spins >= kCSpinLimit) {
+                    if (lane == 0) atomicOr(&sm.flag, 2);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+#ifdef SPARDA_PC_DEBUG
+            if (owner) {
+                sm.dbg_rank[c] = rank;
+                sm.dbg_spin[c] = rofs * 64 + tr;
+            }
+#endif
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            f32x4 o[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const float4 a = valid ? sm.acc[(4 * dt + grp) * kCols + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+                o[dt] = f32x4{a.x, a.y, a.z, a.w};
+            }
+            f32x4 ol = f32x4{owner ? sm.lsum[c] : 0.f, 0.f, 0.f, 0.f};
+            const bool upper = thi >= 32;  // keys 32..63 can hold allowed keys
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[0]), o[dt], 0, 0, 0);
+                if (upper)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]), o[dt], 0,
+                                                                    0, 0);
+            }
+            ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[0]), ol, 0, 0, 0);
+            if (upper) ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[1]), ol, 0, 0, 0);
+            if (valid) {
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) sm.acc[(4 * dt + grp) * kCols + c] = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+            }
+            if (owner) {
+                sm.lsum[c] = ol[0];
+                if (!(ol[0] <= kCGuard)) atomicOr(&sm.flag, 1);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (owner) __hip_atomic_store(&sm.vers[c], rank + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    };
+
+    // every wave takes items until none is left; K of the next item is loaded
+    // while the current one is computed (two register sets), V right after the
+    // current V is staged
+    auto run = [&](bool maxpass) {
+        const int n_items = sm.n_items;
+        // work item index -> packed item word (union entry | first tile << 16);
+        // past the end: the current word again (loads stay in bounds)
+        auto word = [&](int idx, int fallback) -> int {
+            return idx < n_items ? static_cast<int>(sm.items[idx]) : fallback;
+        };
+        u32x4 kA[8], kB[8], vr[8];
+        int cur_i = grab();
+        if (cur_i >= n_items) return;
+        int cur = word(cur_i, 0);
+        load_k(cur, kA);
+        load_v(cur, vr);
+        while (true) {
+            int nxt_i = grab();
+            int nxt = word(nxt_i, cur);
+            load_k(nxt, kB);
+            process(cur, kA, vr, nxt, maxpass);
+            if (nxt_i >= n_items) break;
+            cur = nxt;
+            nxt_i = grab();
+            nxt = word(nxt_i, cur);
+            load_k(nxt, kA);
+            process(cur, kB, vr, nxt, maxpass);
+            if (nxt_i >= n_items) break;
+            cur = nxt;
+        }
+    };
+
+    run(false);
+    __syncthreads();
+    if (sm.flag & 1) {
+        // a score ran more than 64 log2-units above m_ref: exact row maxima
+        // (order keys of max(m_ref, every allowed score)), then the window again
+        for (int c = tid; c < kCols; c += kCT) reinterpret_cast<uint32_t*>(sm.lsum)[c] = order_key(sm.mref[c]);
+        if (tid == 0) sm.next_item = 0;
+        __syncthreads();
+        run(true);
+        __syncthreads();
+        for (int c = tid; c < kCols; c += kCT) {
+            sm.mref[c] = key_to_float(reinterpret_cast<uint32_t*>(sm.lsum)[c]);
+            sm.lsum[c] = 0.0f;
+            sm.vers[c] = 0;
+        }
+        for (int i = tid; i < 16 * kCols; i += kCT) sm.acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid == 0) {
+            sm.next_item = 0;
+            sm.flag &= ~1;
+        }
+        __syncthreads();
+        run(false);
+        __syncthreads();
+    }
+
+    // ---- epilogue: out[b, t, h*64 + d] = O / l, 16-byte stores ----
+    const bool broken = (sm.flag & 2) != 0;  // a wait ran out (never expected): poison the window
+    for (int e = tid; e < kCols * 8; e += kCT) {
+        const int c = e / 8, ch = e % 8;
+        const int tk = c / R, h = c % R;
+        if (tk >= t_valid) continue;
+        const float4 a = sm.acc[(2 * ch) * kCols + c];
+        const float4 bq = sm.acc[(2 * ch + 1) * kCols + c];
+        const float inv = broken ? __builtin_nanf("") : 1.0f / sm.lsum[c];
+        bf16x8 w;
+#ifdef SPARDA_PC_DEBUG
+        if (ch == 0) {
+            w[0] = static_cast<__bf16>(static_cast<float>(sm.flag));
+            w[1] = static_cast<__bf16>(static_cast<float>(sm.n_union));
+            w[2] = static_cast<__bf16>(static_cast<float>(sm.n_items));
+            w[3] = static_cast<__bf16>(sm.lsum[c]);
+            w[4] = static_cast<__bf16>(sm.mref[c]);
+            w[5] = static_cast<__bf16>(static_cast<float>(sm.vers[c]));
+            w[6] = static_cast<__bf16>(a.x);
+            w[7] = static_cast<__bf16>(static_cast<float>(sm.next_item));
+            w[5] = static_cast<__bf16>(static_cast<float>(sm.dbg_rank[c]));
+            w[6] = static_cast<__bf16>(static_cast<float>(sm.dbg_spin[c]));
+            w[3] = static_cast<__bf16>(static_cast<float>(sm.rankbuf[tk]));
+            w[4] = static_cast<__bf16>(static_cast<float>(sm.uofs[0]));
+            uint16_t* op = out + b * out_sb + (t0 + tk) * out_st + static_cast<int64_t>(g * R + h) * 64;
+            *reinterpret_cast<uint4*>(op) = __builtin_bit_cast(uint4, w);
+            continue;
+        }
+#endif
+        w[0] = static_cast<__bf16>(a.x * inv);
+        w[1] = static_cast<__bf16>(a.y * inv);
+        w[2] = static_cast<__bf16>(a.z * inv);
+        w[3] = static_cast<__bf16>(a.w * inv);
+        w[4] = static_cast<__bf16>(bq.x * inv);
+        w[5] = static_cast<__bf16>(bq.y * inv);
+        w[6] = static_cast<__bf16>(bq.z * inv);
+        w[7] = static_cast<__bf16>(bq.w * inv);
+        uint16_t* op = out + b * out_sb + (t0 + tk) * out_st + static_cast<int64_t>(g * R + h) * 64 + 8 * ch;
+        *reinterpret_cast<uint4*>(op) = __builtin_bit_cast(uint4, w);
+    }
+}
+
+bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs,
+                               const int32_t* sel, int64_t cap, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                               int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st,
+                               const void* q, const void* k, const void* v, const void* out) {
+    if (dtype != SPARDA_BF16 || D != 64 || bs != 64 || sel == nullptr) return false;
+    if (cap < 1 || cap > kCMaxCap || cdiv(T, 64) > kCMaxNB) return false;
+    if (Hq % Hkv != 0) return false;
+    const int64_t R = Hq / Hkv;
+    if (R < 1 || R > 4) return false;
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out)) return false;
+    if ((q_sb % 8) || (q_st % 8) || (q_sh % 8) || (kv_sb % 8) || (kv_st % 8) || (kv_sh % 8)) return false;
+    if ((out_sb % 8) || (out_st % 8)) return false;
+    return true;
+}
+
+int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                           const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                           const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
+                           int64_t Hq, int64_t Hkv, int causal, float scale, void* out,
+                           int64_t out_sb, int64_t out_st, hipStream_t stream) {
+    const int64_t NBq = cdiv(T, 64);
+    const int64_t R = Hq / Hkv;
+    dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
+    const float sl = scale * kCLog2e;
+#define SPARDA_PC(R_)                                                                                        \
+    hipLaunchKernelGGL((prefill_compact_kernel<R_>), grid, dim3(kCT), 0, stream,                             \
+                       static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k),    \
+                       static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, sel, n_sel, cap, T,              \
+                       static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st)
+    switch (R) {
+        case 1: SPARDA_PC(1); break;
+        case 2: SPARDA_PC(2); break;
+        case 3: SPARDA_PC(3); break;
+        default: SPARDA_PC(4); break;
+    }
+#undef SPARDA_PC
+    return check_hip(hipGetLastError(), "prefill_compact_kernel");
+}
+
+}  // namespace sparda

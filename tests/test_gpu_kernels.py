@@ -273,6 +273,8 @@ def test_prefill_at_the_largest_block_count_sampled_rows():
 
 
 def test_prefill_topk_covering_all_blocks_equals_dense():
+    # k >= NB selects every causal block: the compacted per-token kernel and the
+    # dense kernel (no lists) compute the same attention
     case("prefill k>=NB == dense")
     x = synth.prefill_inputs(1, 640, 12, 4, 64, dtype=torch.bfloat16, seed=80)
     d = {n: t.to(DEV) for n, t in x.items()}
@@ -280,7 +282,102 @@ def test_prefill_topk_covering_all_blocks_equals_dense():
     _, _, sel, n = sparda.route(d["forecast"], protos, 64, 10, want_topk=False, want_sel=True)
     a = sparda.prefill(d["q"], d["k"], d["v"], sel, n, 64)
     b = sparda.prefill(d["q"], d["k"], d["v"], None, None, 64)
-    assert torch.equal(a, b)
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), None, None, 64, True)
+    assert_close_out(np32(a), want, torch.bfloat16)
+    assert_close_out(np32(b), want, torch.bfloat16)
+    assert (a.float() - b.float()).abs().max().item() <= 2e-2
+
+
+def test_prefill_is_deterministic():
+    # columns receive their blocks' contributions in block order whatever the
+    # timing of the wavefronts: repeated launches agree bit for bit
+    case("prefill repeat B=4 T=4096")
+    x = synth.prefill_inputs(4, 4096, 12, 4, 64, dtype=torch.bfloat16, seed=1001)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    _, _, sel, n = sparda.route(d["forecast"], sparda.compress(d["k"], 64), 64, 8, want_topk=False, want_sel=True)
+    a = sparda.prefill(d["q"], d["k"], d["v"], sel, n, 64)
+    for _ in range(3):
+        assert torch.equal(sparda.prefill(d["q"], d["k"], d["v"], sel, n, 64), a)
+
+
+def _lists(rows, B, Hkv, T, cap):
+    sel = np.full((B, Hkv, T, cap), -1, np.int32)
+    n = np.zeros((B, Hkv, T), np.int32)
+    for (b, g, t), lst in rows.items():
+        sel[b, g, t, :len(lst)] = lst
+        n[b, g, t] = len(lst)
+    return sel, n
+
+
+def _clean(sel, n, T, bs, causal):
+    # set semantics of the kernel's contract: blocks outside [0, NB) (or past the
+    # query's own block when causal) attend nothing, repeats count once
+    NB = (T + bs - 1) // bs
+    out = np.full_like(sel, -1)
+    no = np.zeros_like(n)
+    B, H, TT, cap = sel.shape
+    for b in range(B):
+        for g in range(H):
+            for t in range(TT):
+                top = t // bs if causal else NB - 1
+                keep = sorted({int(j) for j in sel[b, g, t, :n[b, g, t]] if 0 <= j <= top})
+                out[b, g, t, :len(keep)] = keep
+                no[b, g, t] = len(keep)
+    return out, no
+
+
+def test_prefill_irregular_selection_lists():
+    # unsorted lists, repeats, negative and future entries, lists without the sink
+    # or the own block (the reference maximum then comes from another allowed key)
+    case("prefill irregular lists T=640")
+    B, T, Hq, Hkv, bs, cap = 1, 640, 12, 4, 64, 10
+    x = synth.prefill_inputs(B, T, Hq, Hkv, 64, dtype=torch.bfloat16, seed=91)
+    rng = np.random.default_rng(91)
+    rows = {}
+    for g in range(Hkv):
+        for t in range(T):
+            own = t // bs
+            lst = list(rng.choice(own + 1, size=min(own + 1, int(rng.integers(1, 6))), replace=False))
+            r = rng.random()
+            if r < 0.2:
+                lst = lst + [lst[0]]                  # repeat
+            elif r < 0.3:
+                lst = [-1] + lst                      # negative entry
+            elif r < 0.4 and own + 1 < T // bs:
+                lst = lst + [own + 1]                 # a future block
+            rows[(0, g, t)] = [int(j) for j in lst][:cap]
+    sel, n = _lists(rows, B, Hkv, T, cap)
+    d = {k_: t_.to(DEV) for k_, t_ in x.items()}
+    out = sparda.prefill(d["q"], d["k"], d["v"], torch.from_numpy(sel).to(DEV), torch.from_numpy(n).to(DEV), bs)
+    cs, cn = _clean(sel, n, T, bs, True)
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), cs, cn, bs, True)
+    assert_close_out(np32(out), want, torch.bfloat16)
+
+
+def test_prefill_scores_far_above_the_reference_maximum():
+    # a key scoring ~150 log2-units above both the sink and the diagonal key
+    # trips the row-sum guard: the window is redone with its exact row maxima
+    case("prefill exact-max fallback")
+    B, T, Hq, Hkv, bs = 1, 256, 3, 1, 64
+    x = synth.prefill_inputs(B, T, Hq, Hkv, 64, dtype=torch.float32, seed=93)
+    q, k, v = x["q"].clone(), x["k"].clone(), x["v"].clone()
+    e1 = torch.zeros(64)
+    e1[0] = 20.0
+    t_hot, s_hot = 200, 70      # token 200 (block 3) and a key of block 1
+    q[0, t_hot, :, :] = e1
+    k[0, t_hot, 0] = -e1        # its own key
+    k[0, 0, 0] = -e1            # the sink key
+    k[0, s_hot, 0] = e1         # dot = 400 -> 50 natural units above 0, 100 above the references
+    q, k, v = (t_.to(torch.bfloat16) for t_ in (q, k, v))
+    rows = {(0, 0, t): sorted({0, t // bs} | ({1} if t // bs >= 1 else set())) for t in range(T)}
+    sel, n = _lists(rows, B, Hkv, T, 4)
+    out = sparda.prefill(q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(sel).to(DEV),
+                         torch.from_numpy(n).to(DEV), bs)
+    want = O.attention_prefill(np32(q), np32(k), np32(v), sel, n, bs, True)
+    assert_close_out(np32(out), want, torch.bfloat16)
+    # the hot row is (almost) exactly v[s_hot]
+    hot = np32(out)[0, t_hot].reshape(Hq, 64)
+    assert np.abs(hot - np32(v)[0, s_hot, 0][None, :]).max() <= 2e-2
 
 
 # ---------------------------------------------------------------------------
