@@ -13,19 +13,20 @@
 // so a tile wastes only its padding slots (and the masked half of the causal
 // diagonal block, whose key sub-tiles past the tile's last token are skipped).
 //
-// Accumulation. P is taken against a fixed per-column reference m_ref, the
-// larger of the column's scores with the first key of its smallest selected
-// block (the sink, for router lists) and with its own key (when its own block
-// is selected): both are allowed keys, so m_ref never exceeds the row maximum
-// and the row keeps a term P = 1. Contributions are then plain sums (no
-// rescaling), accumulated in fp32 in LDS (acc[col][d], row sums lsum[col]).
-// Work items (a block and up to three of its tiles) are taken by the waves
-// from a shared counter in block order; a column's contributions are added in
-// ascending block order, each tile waiting until the column's earlier blocks
-// have been added (vers[col] = blocks added so far), so the result does not
-// depend on timing. A column whose row sum passes 2^64 (a score more than 64
-// log2-units above m_ref) trips a flag; the workgroup then takes the exact
-// row maxima in a scores-only pass and redoes the window with them.
+// Accumulation. P is taken against a fixed per-column reference m_ref: the
+// column maximum of the column's first selected block (its smallest block,
+// the sink for router lists), set by the tile that processes that block. It is
+// a score of an allowed key, so it never exceeds the row maximum and the row
+// keeps a term P = 1. Contributions are then plain sums (no rescaling): each
+// tile's O^T and row sums are formed from zero and added into fp32
+// accumulators acc[col][d], lsum[col] in LDS. Work items (a block and up to
+// three of its tiles) are taken by the waves from a shared counter in block
+// order; a column's contributions are added in ascending block order, each
+// tile waiting until the column's earlier blocks have been added (vers[col] =
+// blocks added so far), so the result does not depend on timing. A block
+// whose row sum passes 2^64 (a score more than 64 log2-units above the
+// reference) trips a flag; the workgroup then takes the exact row maxima in a
+// scores-only pass and redoes the window against them.
 //
 // K A operands are read straight from memory; V is staged per wavefront in
 // LDS, half a block at a time (XOR-swizzled 16-byte chunks), and read
@@ -44,7 +45,7 @@ constexpr int kCWin = 64;                       // query tokens per workgroup
 constexpr int kCMaxCap = 10;                    // selection entries per token
 constexpr int kCMaxUnion = kCWin * kCMaxCap;    // distinct blocks a window can select
 constexpr int kCMaxNB = 1024;                   // KV blocks (bitmap set-up)
-constexpr int kCChunk = 3;                      // tiles per work item
+constexpr int kCChunk = 2;                      // tiles per work item
 constexpr float kCLog2e = 1.4426950408889634f;
 constexpr float kCGuard = 18446744073709551616.0f;  // 2^64
 constexpr uint32_t kCSpinLimit = 1u << 20;
@@ -69,10 +70,6 @@ struct CompactSmem {
     uint8_t rankbuf[kCMaxUnion];                // rank of block u in a token's list
     uint8_t tokrank[kCWaves][64];               // selecting token of each rank
     int n_union, n_items, next_item, flag;
-#ifdef SPARDA_PC_DEBUG
-    int dbg_rank[kCols];
-    int dbg_spin[kCols];
-#endif
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -87,8 +84,9 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 
 }  // namespace
 
+// two workgroups per CU for R <= 3 (their LDS fits twice); one for R = 4
 template <int R>
-__global__ void __launch_bounds__(kCT, 2)
+__global__ void __launch_bounds__(kCT, R <= 3 ? 2 : 1)
 prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                        const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                        int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
@@ -118,42 +116,27 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const uint16_t* qbase = q + b * q_sb + t0 * q_st + static_cast<int64_t>(g * R) * q_sh;
+    // element offsets inside a window / a block fit in 32 bits (checked by the host)
+    const int q_st32 = static_cast<int>(q_st), q_sh32 = static_cast<int>(q_sh), kv_st32 = static_cast<int>(kv_st);
 
-    unsigned long long* bitmap = reinterpret_cast<unsigned long long*>(sm.acc);          // [kCMaxNB]
-    uint16_t* jmap = reinterpret_cast<uint16_t*>(bitmap + kCMaxNB);                       // [kCMaxNB]
-    int16_t* tokfirst = reinterpret_cast<int16_t*>(jmap + kCMaxNB);                      // [64]
-    uint8_t* tokown = reinterpret_cast<uint8_t*>(tokfirst + 64);                         // [64]
+    unsigned long long* bitmap = reinterpret_cast<unsigned long long*>(sm.acc);  // [kCMaxNB], set-up only
+    uint16_t* jmap = reinterpret_cast<uint16_t*>(bitmap + kCMaxNB);               // [kCMaxNB], set-up only
 
-    // ---- set-up 1: this thread's column rows (reference maxima) and token list ----
-    const int ctok = tid / R, chead = tid % R;
-    const bool ccol = tid < kCols && ctok < t_valid;
-    u32x4 qr[8], kd[8], k0[8];
-    if (ccol) {
-        const uint16_t* qp = qbase + ctok * q_st + chead * q_sh;
-        const uint16_t* kp = kbase + (t0 + ctok) * kv_st;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            qr[i] = *reinterpret_cast<const u32x4*>(qp + 8 * i);
-            kd[i] = *reinterpret_cast<const u32x4*>(kp + 8 * i);
-            k0[i] = *reinterpret_cast<const u32x4*>(kbase + 8 * i);
-        }
-    }
+    // ---- set-up 1: this thread's token list (sorted, repeats and out-of-range entries dropped) ----
     int lst[kCMaxCap];
 #pragma unroll
     for (int i = 0; i < kCMaxCap; ++i) lst[i] = kSentinel;
     if (tid < t_valid) {
         const int64_t r = (static_cast<int64_t>(b) * H + g) * T + t0 + tid;
+        const int32_t* row = sel + r * cap;
+        int raw[kCMaxCap];
+#pragma unroll
+        for (int i = 0; i < kCMaxCap; ++i) raw[i] = i < cap ? row[i] : -1;  // issued with the count's load
         const int64_t nr = n_sel[r];
         const int n = static_cast<int>(nr < 0 ? 0 : (nr > cap ? cap : nr));
-        const int32_t* row = sel + r * cap;
 #pragma unroll
-        for (int i = 0; i < kCMaxCap; ++i) {
-            if (i < n) {
-                const int j = row[i];
-                lst[i] = (j >= 0 && j <= jmax) ? j : kSentinel;
-            }
-        }
-        // ascending, duplicates dropped (odd-even transposition sort, twice)
+        for (int i = 0; i < kCMaxCap; ++i) lst[i] = (i < n && raw[i] >= 0 && raw[i] <= jmax) ? raw[i] : kSentinel;
+        // ascending, repeats dropped (odd-even transposition sort, twice)
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
@@ -174,17 +157,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     for (int i = tid; i <= jmax; i += kCT) bitmap[i] = 0ull;
     __syncthreads();
     if (tid < t_valid) {
-        const int own = static_cast<int>((t0 + tid) / 64);
-        bool has_own = false;
 #pragma unroll
-        for (int i = 0; i < kCMaxCap; ++i) {
-            if (lst[i] != kSentinel) {
-                atomicOr(&bitmap[lst[i]], 1ull << tid);
-                has_own = has_own || lst[i] == own;
-            }
-        }
-        tokfirst[tid] = static_cast<int16_t>(lst[0] != kSentinel ? lst[0] : -1);
-        tokown[tid] = has_own ? 1 : 0;
+        for (int i = 0; i < kCMaxCap; ++i)
+            if (lst[i] != kSentinel) atomicOr(&bitmap[lst[i]], 1ull << tid);
     }
     __syncthreads();
 
@@ -200,8 +175,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             const int tiles = (R * nt + 15) / 16;
             const int chunks = nz ? (tiles + kCChunk - 1) / kCChunk : 0;
             const int rk = nz ? nt : 0;
-            // inclusive prefix sums over the lanes
-            int sc = chunks, sr = rk;
+            int sc = chunks, sr = rk;  // inclusive prefix sums over the lanes
 #pragma unroll
             for (int o = 1; o < kWave; o <<= 1) {
                 const int a = __shfl_up(sc, o, kWave), c = __shfl_up(sr, o, kWave);
@@ -234,7 +208,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     }
     __syncthreads();
 
-    // ---- set-up 3: ranks (position of each block in a token's list) and m_ref ----
+    // ---- set-up 3: ranks (position of each block in a token's list) ----
     if (tid < t_valid) {
 #pragma unroll
         for (int i = 0; i < kCMaxCap; ++i) {
@@ -245,83 +219,64 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             }
         }
     }
-    if (tid < kCols) {
-        float mr = 0.0f;
-        if (ccol) {
-            auto dot = [&](const u32x4 (&a)[8], const u32x4 (&c)[8]) __attribute__((always_inline)) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) {
-                        acc = __builtin_fmaf(__uint_as_float(a[i][w] << 16), __uint_as_float(c[i][w] << 16), acc);
-                        acc = __builtin_fmaf(__uint_as_float(a[i][w] & 0xffff0000u),
-                                             __uint_as_float(c[i][w] & 0xffff0000u), acc);
-                    }
-                }
-                return acc;
-            };
-            const int first = tokfirst[ctok];
-            float s;
-            if (first == 0) {
-                s = dot(qr, k0);
-            } else {  // the first key of the smallest selected block (not the sink)
-                u32x4 kf[8];
-                const int fb = first < 0 ? 0 : first;
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    kf[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(fb) * 64 * kv_st + 8 * i);
-                s = dot(qr, kf);
-            }
-            if (tokown[ctok]) s = __builtin_fmaxf(s, dot(qr, kd));
-            mr = s * scale_log2;
-        }
-        sm.mref[tid] = mr;
-        sm.lsum[tid] = 0.0f;
-        sm.vers[tid] = 0;
+    for (int c = tid; c < kCols; c += kCT) {
+        sm.mref[c] = 0.0f;
+        sm.lsum[c] = 0.0f;
+        sm.vers[c] = 0;
     }
     __syncthreads();  // the set-up aliases in acc are dead from here
     for (int i = tid; i < 16 * kCols; i += kCT) sm.acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-#ifdef SPARDA_PC_DEBUG
-    for (int i = tid; i < kCols; i += kCT) {
-        sm.dbg_rank[i] = -1;
-        sm.dbg_spin[i] = -1;
-    }
-#endif
     __syncthreads();
 
     // ---- the tiles ----
     bf16x8 ones_a;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
+    // per-lane element offsets inside a block: K A operand (key 16n + col16,
+    // dims 32kk + 8grp), V rows (chunk lane + 64i: row lane/8 + 8i, 16-byte column lane%8)
+    const int koff = col16 * kv_st32 + 8 * grp;
+    const int voff = (lane / 8) * kv_st32 + (lane % 8) * 8;
     const int64_t last_row = T - 1;
 
-    auto grab = [&]() -> int {
+    auto grab = [&]() __attribute__((always_inline)) -> int {
         int it = 0;
         if (lane == 0) it = atomicAdd(&sm.next_item, 1);
         return __builtin_amdgcn_readfirstlane(it);
     };
-    // K A operands (key 16n + col16, dims 32kk + 8grp ..) and V rows (chunk lane + 64i:
-    // row (lane + 64i) / 8, 16-byte column lane % 8) of union block u; rows past T
-    // read row T-1 (finite, masked)
+    // rows past T (a ragged last block) read row T-1: finite values, masked
     auto load_k = [&](int item, u32x4 (&kr)[8]) __attribute__((always_inline)) {
-        const int64_t j = sm.ulist[item & 0xffff];
+        const int64_t r0 = static_cast<int64_t>(sm.ulist[item & 0xffff]) * 64;
+        if (r0 + 64 <= T) {
+            const uint16_t* blk = kbase + r0 * kv_st;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            int64_t row = j * 64 + 16 * n + col16;
-            row = row < last_row ? row : last_row;
+            for (int n = 0; n < 4; ++n)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-                kr[2 * n + kk] = *reinterpret_cast<const u32x4*>(kbase + row * kv_st + 32 * kk + 8 * grp);
+                for (int kk = 0; kk < 2; ++kk)
+                    kr[2 * n + kk] = *reinterpret_cast<const u32x4*>(blk + koff + 16 * n * kv_st32 + 32 * kk);
+        } else {
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                int64_t row = r0 + 16 * n + col16;
+                row = row < last_row ? row : last_row;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    kr[2 * n + kk] = *reinterpret_cast<const u32x4*>(kbase + row * kv_st + 32 * kk + 8 * grp);
+            }
         }
     };
     auto load_v = [&](int item, u32x4 (&vr)[8]) __attribute__((always_inline)) {
-        const int64_t j = sm.ulist[item & 0xffff];
+        const int64_t r0 = static_cast<int64_t>(sm.ulist[item & 0xffff]) * 64;
+        if (r0 + 64 <= T) {
+            const uint16_t* blk = vbase + r0 * kv_st;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int64_t row = j * 64 + (lane + 64 * i) / 8;
-            row = row < last_row ? row : last_row;
-            vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * kv_st + (lane % 8) * 8);
+            for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const u32x4*>(blk + voff + 8 * i * kv_st32);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                int64_t row = r0 + lane / 8 + 8 * i;
+                row = row < last_row ? row : last_row;
+                vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * kv_st + (lane % 8) * 8);
+            }
         }
     };
 
@@ -330,21 +285,84 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     const int rsub = 4 * grp + col16 / 4;
     const int csub = 4 * (col16 % 4);
 
-    // one work item (packed word: union entry u | first tile i0 << 16): tiles
-    // [i0, i0 + kCChunk) of union block u, K operands in kr, V rows in vr
-    // (reloaded with the V rows of item word nxt once staged); MAXPASS: scores
-    // only, column maxima
-    auto process = [&](int item, const u32x4 (&kr)[8], u32x4 (&vr)[8], int nxt,
-                       bool maxpass) __attribute__((always_inline)) {
+    // column of slot col16 in tile i of the current item
+    struct Slot {
+        int tr;     // rank of the slot's token among the block's selecting tokens
+        int c;      // window column (token * R + head)
+        int qoff;   // element offset of the slot's q row (+ 8 grp) from qbase
+        bool valid;
+    };
+    auto slot = [&](int i, int ncol) __attribute__((always_inline)) -> Slot {
+        const int e = 16 * i + col16;
+        Slot s_;
+        s_.valid = e < ncol;
+        const int ei = s_.valid ? e : ncol - 1;  // padding slots repeat the last column, masked
+        s_.tr = ei / R;
+        const int h = ei - s_.tr * R;
+        const int tk = trk[s_.tr];
+        s_.c = tk * R + h;
+        s_.qoff = tk * q_st32 + h * q_sh32 + 8 * grp;
+        return s_;
+    };
+
+    // one work item (packed word: union entry u | first tile i0 << 16): the
+    // up to kCChunk tiles [i0, i1) of union block u, processed phase by phase
+    // so that their latencies overlap: q loads, S = K Q^T, references and P,
+    // O = V^T P^T, then one wait and one read-add-write of every column.
+    // kr holds the block's K operands and is reloaded with item word nxt's
+    // once the products are issued; vr holds its V rows and is reloaded with
+    // nxt's once staged.
+    // mode 0: P against the column's reference, which the column's first block
+    //         sets to its own column maximum; 1: scores only, exact column
+    //         maxima; 2: P against the exact maxima of mode 1
+    auto process = [&](int item, u32x4 (&kr)[8], u32x4 (&vr)[8], int nxt, int mode) __attribute__((always_inline)) {
         const int u = item & 0xffff;
         const int i0 = item >> 16;
         const int j = sm.ulist[u];
         const unsigned long long M = sm.umask[u];
         const int ncol = R * __popcll(M);
         const int tiles = (ncol + 15) / 16;
-        const int i1 = i0 + kCChunk < tiles ? i0 + kCChunk : tiles;
+        const int nt = (i0 + kCChunk < tiles ? i0 + kCChunk : tiles) - i0;  // 1 .. kCChunk
         const int rofs = sm.uofs[u];
         if ((M >> lane) & 1ull) trk[__popcll(M & below)] = static_cast<uint8_t>(lane);
+        __builtin_amdgcn_wave_barrier();
+        const bool diag = causal && j == qb;
+        const int lim_tail = (!causal && (static_cast<int64_t>(j) + 1) * 64 > T) ? static_cast<int>(T - j * 64LL) : 64;
+        const bool masked = diag || lim_tail < 64;  // causal diagonal or ragged tail block
+
+        Slot sl[kCChunk];
+        u32x4 qa[kCChunk], qc[kCChunk];
+        int rank[kCChunk], thi[kCChunk];
+#pragma unroll
+        for (int t = 0; t < kCChunk; ++t) {
+            if (t < nt) {
+                sl[t] = slot(i0 + t, ncol);
+                qa[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff);
+                qc[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff + 32);
+                rank[t] = sm.rankbuf[rofs + sl[t].tr];
+                // causal diagonal: key sub-tiles past the tile's last token are all masked
+                const int last = 16 * (i0 + t) + 15 < ncol ? 16 * (i0 + t) + 15 : ncol - 1;
+                thi[t] = diag ? __builtin_amdgcn_readfirstlane(trk[last / R]) : 63;
+            }
+        }
+        // S^T = K Q^T for every tile
+        f32x4 s[kCChunk][4];
+#pragma unroll
+        for (int t = 0; t < kCChunk; ++t) {
+            if (t < nt) {
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    s[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (16 * n <= thi[t]) {
+                        s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n]),
+                                                                          __builtin_bit_cast(bf16x8, qa[t]), s[t][n], 0, 0, 0);
+                        s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n + 1]),
+                                                                          __builtin_bit_cast(bf16x8, qc[t]), s[t][n], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        load_k(nxt, kr);  // the next item's K operands, in flight from here
         // V^T operands: stage each half of the block, read it transposed
         bf16x8 va[4][2];
 #pragma unroll
@@ -365,73 +383,52 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         }
         __builtin_amdgcn_wave_barrier();
         load_v(nxt, vr);  // unconditional (nxt repeats item at the end): the registers stay registers
-        const bool diag = causal && j == qb;
-        const int lim_tail = (!causal && (static_cast<int64_t>(j) + 1) * 64 > T) ? static_cast<int>(T - j * 64LL) : 64;
-        for (int i = i0; i < i1; ++i) {
-            const int e = 16 * i + col16;
-            const bool valid = e < ncol;
-            const int ei = valid ? e : ncol - 1;  // padding slots repeat the last column, masked
-            const int tr = ei / R;
-            const int h = ei % R;
-            const int tk = trk[tr];
-            const int c = tk * R + h;
-            const uint16_t* qp = qbase + tk * q_st + h * q_sh + 8 * grp;
-            const bf16x8 qb0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp));
-            const bf16x8 qb1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + 32));
-            // causal diagonal: key sub-tiles past the tile's last token are all masked
-            int thi = 63;
-            if (diag) {
-                const int last = (16 * i + 15 < ncol ? 16 * i + 15 : ncol - 1) / R;
-                thi = trk[last];
-            }
-            const int nmax = thi / 16;
-            f32x4 s[4];
+
+        // masks, references, P
+        bool own[kCChunk];
+        uint4 pw[kCChunk][2];
+        bool any_first = false, any_later = false;
 #pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                if (n <= nmax) {
-                    s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n]), qb0, s[n], 0, 0, 0);
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n + 1]), qb1, s[n], 0,
-                                                                   0, 0);
-                } else {
-                    s[n] = f32x4{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+        for (int t = 0; t < kCChunk; ++t) {
+            if (t < nt) {
+                own[t] = sl[t].valid && grp == 0;
+                if (masked) {
+                    const int lim = diag ? sl[t].c / R : lim_tail - 1;  // keys <= lim are allowed
+#pragma unroll
+                    for (int n = 0; n < 4; ++n)
+#pragma unroll
+                        for (int ii = 0; ii < 4; ++ii)
+                            if (16 * n + 4 * grp + ii > lim) s[t][n][ii] = -__builtin_inff();
+                }
+                any_first = any_first || (sl[t].valid && rank[t] == 0);
+                any_later = any_later || (own[t] && rank[t] > 0);
+            }
+        }
+        float cm[kCChunk];
+        if (mode == 1 || __ballot(any_first) != 0ull) {
+#pragma unroll
+            for (int t = 0; t < kCChunk; ++t) {
+                if (t < nt) {
+                    const float x = max16_nn(s[t]);
+                    cm[t] = pair32_max(pair16_max(x)) * scale_log2;
                 }
             }
-            if (diag || lim_tail < 64) {
-                const int lim = diag ? tk : lim_tail - 1;  // keys <= lim are allowed
+        }
+        if (mode == 1) {
 #pragma unroll
-                for (int n = 0; n < 4; ++n)
+            for (int t = 0; t < kCChunk; ++t)
+                if (t < nt && own[t]) atomicMax(reinterpret_cast<uint32_t*>(sm.lsum) + sl[t].c, order_key(cm[t]));
+            return;
+        }
+        if (mode == 0 && __ballot(any_later) != 0ull) {
+            // later blocks: their columns' first blocks have set the references
+            for (uint32_t spins = 0;; ++spins) {
+                bool ready = true;
 #pragma unroll
-                    for (int ii = 0; ii < 4; ++ii)
-                        if (16 * n + 4 * grp + ii > lim) s[n][ii] = -__builtin_inff();
-            }
-            if (maxpass) {
-                float mx = max16_nn(s);
-                mx = pair32_max(pair16_max(mx));
-                if (valid && grp == 0)
-                    atomicMax(reinterpret_cast<uint32_t*>(sm.lsum) + c, order_key(mx * scale_log2));
-                continue;
-            }
-            const float neg = valid ? -sm.mref[c] : -__builtin_inff();
-            uint4 pw[2];
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                bf16x8 pb;
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    pb[ii] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m][ii], scale_log2, neg)));
-                    pb[4 + ii] =
-                        static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m + 1][ii], scale_log2, neg)));
-                }
-                pw[m] = __builtin_bit_cast(uint4, pb);
-            }
-            const int rank = sm.rankbuf[rofs + tr];
-            // wait until the column's earlier blocks have been added
-            const bool owner = valid && grp == 0;
-            uint32_t spins = 0;
-            for (;; ++spins) {
-                const bool ready = !owner || __hip_atomic_load(&sm.vers[c], __ATOMIC_RELAXED,
-                                                               __HIP_MEMORY_SCOPE_WORKGROUP) >= rank;
+                for (int t = 0; t < kCChunk; ++t)
+                    if (t < nt && own[t] && rank[t] > 0)
+                        ready = ready && __hip_atomic_load(&sm.vers[sl[t].c], __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_WORKGROUP) >= 1;
                 if (__ballot(!ready) == 0ull) break;
                 if (spins >= kCSpinLimit) {
                     if (lane == 0) atomicOr(&sm.flag, 2);
@@ -439,84 +436,124 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
-#ifdef SPARDA_PC_DEBUG
-            if (owner) {
-                sm.dbg_rank[c] = rank;
-                sm.dbg_spin[c] = rofs * 64 + tr;
-            }
-#endif
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-            f32x4 o[4];
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                const float4 a = valid ? sm.acc[(4 * dt + grp) * kCols + c] : make_float4(0.f, 0.f, 0.f, 0.f);
-                o[dt] = f32x4{a.x, a.y, a.z, a.w};
-            }
-            f32x4 ol = f32x4{owner ? sm.lsum[c] : 0.f, 0.f, 0.f, 0.f};
-            const bool upper = thi >= 32;  // keys 32..63 can hold allowed keys
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[0]), o[dt], 0, 0, 0);
-                if (upper)
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]), o[dt], 0,
-                                                                    0, 0);
-            }
-            ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[0]), ol, 0, 0, 0);
-            if (upper) ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[1]), ol, 0, 0, 0);
-            if (valid) {
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) sm.acc[(4 * dt + grp) * kCols + c] = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
-            }
-            if (owner) {
-                sm.lsum[c] = ol[0];
-                if (!(ol[0] <= kCGuard)) atomicOr(&sm.flag, 1);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (owner) __hip_atomic_store(&sm.vers[c], rank + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+#pragma unroll
+        for (int t = 0; t < kCChunk; ++t) {
+            if (t < nt) {
+                const bool first = mode == 0 && sl[t].valid && rank[t] == 0;
+                const float m = first ? cm[t] : sm.mref[sl[t].c];
+                if (first && own[t]) sm.mref[sl[t].c] = m;
+                const float neg = sl[t].valid ? -m : -__builtin_inff();
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm) {
+                    bf16x8 pb;
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+                        pb[ii] = static_cast<__bf16>(
+                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][2 * mm][ii], scale_log2, neg)));
+                        pb[4 + ii] = static_cast<__bf16>(
+                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][2 * mm + 1][ii], scale_log2, neg)));
+                    }
+                    pw[t][mm] = __builtin_bit_cast(uint4, pb);
+                }
+            }
+        }
+        // O^T = V^T P^T and the row sums, from zero
+        f32x4 o[kCChunk][4], ol[kCChunk];
+#pragma unroll
+        for (int t = 0; t < kCChunk; ++t) {
+            if (t < nt) {
+                const bool upper = thi[t] >= 32;  // keys 32..63 can hold allowed keys
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[t][0]),
+                                                                       f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    if (upper)
+                        o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[t][1]),
+                                                                           o[t][dt], 0, 0, 0);
+                }
+                ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][0]),
+                                                                f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if (upper)
+                    ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][1]), ol[t],
+                                                                    0, 0, 0);
+            }
+        }
+        // add into every column after its earlier blocks (read-add-write, in block order)
+        for (uint32_t spins = 0;; ++spins) {
+            bool ready = true;
+#pragma unroll
+            for (int t = 0; t < kCChunk; ++t)
+                if (t < nt && own[t])
+                    ready = ready && __hip_atomic_load(&sm.vers[sl[t].c], __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_WORKGROUP) >= rank[t];
+            if (__ballot(!ready) == 0ull) break;
+            if (spins >= kCSpinLimit) {
+                if (lane == 0) atomicOr(&sm.flag, 2);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+        for (int t = 0; t < kCChunk; ++t) {
+            if (t < nt) {
+                if (sl[t].valid) {
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt) {
+                        float4* a = &sm.acc[(4 * dt + grp) * kCols + sl[t].c];
+                        const float4 w = *a;
+                        *a = make_float4(w.x + o[t][dt][0], w.y + o[t][dt][1], w.z + o[t][dt][2], w.w + o[t][dt][3]);
+                    }
+                }
+                if (own[t]) {
+                    sm.lsum[sl[t].c] += ol[t][0];
+                    if (!(ol[t][0] <= kCGuard)) atomicOr(&sm.flag, 1);
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+#pragma unroll
+        for (int t = 0; t < kCChunk; ++t)
+            if (t < nt && own[t])
+                __hip_atomic_store(&sm.vers[sl[t].c], rank[t] + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
 
-    // every wave takes items until none is left; K of the next item is loaded
-    // while the current one is computed (two register sets), V right after the
-    // current V is staged
-    auto run = [&](bool maxpass) {
+    // every wave takes items until none is left; each item's K and V are
+    // loaded while the item before it is computed
+    auto run = [&](int mode) {
         const int n_items = sm.n_items;
-        // work item index -> packed item word (union entry | first tile << 16);
-        // past the end: the current word again (loads stay in bounds)
+        // work item index -> packed item word; past the end: the current word
+        // again (loads stay in bounds)
         auto word = [&](int idx, int fallback) -> int {
             return idx < n_items ? static_cast<int>(sm.items[idx]) : fallback;
         };
-        u32x4 kA[8], kB[8], vr[8];
+        u32x4 kr[8], vr[8];
         int cur_i = grab();
         if (cur_i >= n_items) return;
         int cur = word(cur_i, 0);
-        load_k(cur, kA);
+        load_k(cur, kr);
         load_v(cur, vr);
         while (true) {
-            int nxt_i = grab();
-            int nxt = word(nxt_i, cur);
-            load_k(nxt, kB);
-            process(cur, kA, vr, nxt, maxpass);
-            if (nxt_i >= n_items) break;
-            cur = nxt;
-            nxt_i = grab();
-            nxt = word(nxt_i, cur);
-            load_k(nxt, kA);
-            process(cur, kB, vr, nxt, maxpass);
+            const int nxt_i = grab();
+            const int nxt = word(nxt_i, cur);
+            process(cur, kr, vr, nxt, mode);
             if (nxt_i >= n_items) break;
             cur = nxt;
         }
     };
 
-    run(false);
+    run(0);
     __syncthreads();
     if (sm.flag & 1) {
-        // a score ran more than 64 log2-units above m_ref: exact row maxima
-        // (order keys of max(m_ref, every allowed score)), then the window again
+        // a block's row sum passed 2^64: a score more than 64 log2-units above
+        // the column's reference. Exact maxima (order keys of max(reference,
+        // every allowed score)), then the window again against them.
         for (int c = tid; c < kCols; c += kCT) reinterpret_cast<uint32_t*>(sm.lsum)[c] = order_key(sm.mref[c]);
         if (tid == 0) sm.next_item = 0;
         __syncthreads();
-        run(true);
+        run(1);
         __syncthreads();
         for (int c = tid; c < kCols; c += kCT) {
             sm.mref[c] = key_to_float(reinterpret_cast<uint32_t*>(sm.lsum)[c]);
@@ -529,7 +566,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             sm.flag &= ~1;
         }
         __syncthreads();
-        run(false);
+        run(2);
         __syncthreads();
     }
 
@@ -543,25 +580,6 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         const float4 bq = sm.acc[(2 * ch + 1) * kCols + c];
         const float inv = broken ? __builtin_nanf("") : 1.0f / sm.lsum[c];
         bf16x8 w;
-#ifdef SPARDA_PC_DEBUG
-        if (ch == 0) {
-            w[0] = static_cast<__bf16>(static_cast<float>(sm.flag));
-            w[1] = static_cast<__bf16>(static_cast<float>(sm.n_union));
-            w[2] = static_cast<__bf16>(static_cast<float>(sm.n_items));
-            w[3] = static_cast<__bf16>(sm.lsum[c]);
-            w[4] = static_cast<__bf16>(sm.mref[c]);
-            w[5] = static_cast<__bf16>(static_cast<float>(sm.vers[c]));
-            w[6] = static_cast<__bf16>(a.x);
-            w[7] = static_cast<__bf16>(static_cast<float>(sm.next_item));
-            w[5] = static_cast<__bf16>(static_cast<float>(sm.dbg_rank[c]));
-            w[6] = static_cast<__bf16>(static_cast<float>(sm.dbg_spin[c]));
-            w[3] = static_cast<__bf16>(static_cast<float>(sm.rankbuf[tk]));
-            w[4] = static_cast<__bf16>(static_cast<float>(sm.uofs[0]));
-            uint16_t* op = out + b * out_sb + (t0 + tk) * out_st + static_cast<int64_t>(g * R + h) * 64;
-            *reinterpret_cast<uint4*>(op) = __builtin_bit_cast(uint4, w);
-            continue;
-        }
-#endif
         w[0] = static_cast<__bf16>(a.x * inv);
         w[1] = static_cast<__bf16>(a.y * inv);
         w[2] = static_cast<__bf16>(a.z * inv);
@@ -588,6 +606,8 @@ bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, in
     if (!al16(q) || !al16(k) || !al16(v) || !al16(out)) return false;
     if ((q_sb % 8) || (q_st % 8) || (q_sh % 8) || (kv_sb % 8) || (kv_st % 8) || (kv_sh % 8)) return false;
     if ((out_sb % 8) || (out_st % 8)) return false;
+    // window- and block-relative element offsets are 32-bit in the kernel
+    if (64 * q_st + R * q_sh + 64 >= (int64_t(1) << 30) || 64 * kv_st + 64 >= (int64_t(1) << 30)) return false;
     return true;
 }
 
