@@ -203,6 +203,37 @@ SPARDA_API int sparda_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t
                               void* out, int64_t out_sb, int64_t out_st,
                               void* stream);
 
+/*
+ * Block-sparse GQA prefill with an explicit additive mask and, optionally, the
+ * attention weights. Replaces the masked-SDPA path of
+ * SparseAttention._forward_masked_sdpa with `mask` and return_attn_weights
+ * (model/attention/sparse.py:206-221 dense, 255-281 sparse), and the dense
+ * backend's weights output used by scripts/benchmark_forecast.py:86-93.
+ *   allowed(b,g,t,s) as in sparda_prefill (sel == NULL: every block;
+ *   repeated or out-of-range list entries count once / not at all);
+ *   score = q.k_s * scale + mask[b,h,t,s] on allowed keys, -inf elsewhere;
+ *   weights[b,h,t,s] = softmax_s(score) (0 outside the allowed set),
+ *   out[b,t,h*D+d] = sum_s weights[b,h,t,s] v_s[d].
+ *   mask: optional, fp32 or the input dtype, element strides (m_sb, m_sh,
+ *     m_st, m_ss) over [B, Hq, T, T] (0 to broadcast a dimension), h the
+ *     query head; natural-log units, as added before the reference's softmax.
+ *   weights: optional [B,Hq,T,T] of dtype, strides (w_sb, w_sh, w_st, 1).
+ * A general (VALU) kernel: for the evaluation and debugging callers of these
+ * options, not the sparse fast path (sparda_prefill).
+ */
+SPARDA_API int sparda_prefill_masked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                                     const void* k, const void* v,
+                                     int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                                     int dtype,
+                                     const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
+                                     int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                     int64_t block_size, int causal, float scale,
+                                     const void* mask, int mask_dtype,
+                                     int64_t m_sb, int64_t m_sh, int64_t m_st, int64_t m_ss,
+                                     void* out, int64_t out_sb, int64_t out_st,
+                                     void* weights, int64_t w_sb, int64_t w_sh, int64_t w_st,
+                                     void* stream);
+
 /* Workspace bytes sparda_decode needs for these sizes. */
 SPARDA_API size_t sparda_decode_workspace_bytes(int64_t B, int64_t S, int64_t Hq,
                                                 int64_t Hkv, int64_t D,

@@ -183,6 +183,35 @@ SPARDA_API int sparda_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t
                           static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_prefill_masked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                                     const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
+                                     const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t B,
+                                     int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size,
+                                     int causal, float scale, const void* mask, int mask_dtype, int64_t m_sb,
+                                     int64_t m_sh, int64_t m_st, int64_t m_ss, void* out, int64_t out_sb,
+                                     int64_t out_st, void* weights, int64_t w_sb, int64_t w_sh, int64_t w_st,
+                                     void* stream) {
+    SPARDA_REQUIRE(q && k && v && out, SPARDA_ERR_NULL, "prefill_masked: null q/k/v/out");
+    SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "prefill_masked: sel and n_sel go together");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "prefill_masked: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(!mask || dtype_ok(mask_dtype), SPARDA_ERR_DTYPE, "prefill_masked: mask dtype %d", mask_dtype);
+    SPARDA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "prefill_masked: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "prefill_masked: head dim %lld not in {16,32,64,128}",
+                   (long long)D);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "prefill_masked: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(!sel || (sel_cap >= 1 && sel_cap <= kMaxSelCap), SPARDA_ERR_SHAPE,
+                   "prefill_masked: sel_cap must be in [1, %d]", kMaxSelCap);
+    SPARDA_REQUIRE(T < (1ll << 31) && B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "prefill_masked: too large");
+    SPARDA_REQUIRE(m_sb >= 0 && m_sh >= 0 && m_st >= 0 && m_ss >= 0 && w_sb >= 0 && w_sh >= 0 && w_st >= 0,
+                   SPARDA_ERR_STRIDE, "prefill_masked: negative stride");
+    return launch_prefill_weights(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, dtype, sel, n_sel, sel_cap, B, T,
+                                  Hq, Hkv, D, block_size, causal != 0, scale, mask, mask_dtype, m_sb, m_sh, m_st,
+                                  m_ss, out, out_sb, out_st, weights, w_sb, w_sh, w_st,
+                                  static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API size_t sparda_decode_workspace_bytes(int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
                                                 int64_t block_size, int64_t top_k) {
     if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || block_size <= 0 || top_k <= 0) return 0;

@@ -47,6 +47,14 @@ int launch_gather(const void* k, const void* v, int dtype, int64_t sb, int64_t s
                   const int32_t* idx, int64_t B, int64_t H, int64_t S, int64_t D, int64_t n,
                   int64_t bs, void* ko, void* vo, hipStream_t stream);
 
+int launch_prefill_weights(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                           int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype, const int32_t* sel,
+                           const int32_t* n_sel, int64_t cap, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                           int64_t D, int64_t bs, int causal, float scale, const void* mask, int mask_dt,
+                           int64_t m_sb, int64_t m_sh, int64_t m_st, int64_t m_ss, void* out, int64_t out_sb,
+                           int64_t out_st, void* weights, int64_t w_sb, int64_t w_sh, int64_t w_st,
+                           hipStream_t stream);
+
 // Workspace carve-up of the decode step.
 struct DecodeWs {
     float* scores;     // [B*Hkv*NB]

@@ -108,6 +108,188 @@ bool prefill_mfma_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, int64
                             int64_t kv_sh, int64_t out_sb, int64_t out_st, const void* q, const void* k,
                             const void* v, const void* out);
 
+// ---------------------------------------------------------------------------
+// Masked prefill with optional attention weights (the reference's masked SDPA
+// with an explicit additive mask and return_attn_weights, sparse.py:206-221,
+// 255-281). One workgroup per (query token t, KV head g, sequence b), one
+// wavefront per query head of the group (heads w, w+4, ...). The row's
+// allowed keys are its listed blocks (or every block), keys <= t when causal;
+// the additive mask is added to each allowed score. Pass 1 forms the row
+// maximum and the sum of exponentials, pass 2 the normalised probabilities:
+// written to `weights` (zeros elsewhere in the row) and accumulated into the
+// output. Scores in log2 units: q * scale * log2 e . k + mask * log2 e.
+// ---------------------------------------------------------------------------
+constexpr int kWMaxList = 64;  // distinct listed blocks per row (selection capacity <= 34)
+
+template <int DT, int DH>
+__global__ void __launch_bounds__(kPrefillThreads)
+prefill_weights_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                       const void* __restrict__ k, const void* __restrict__ v,
+                       int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                       const int32_t* __restrict__ sel, const int32_t* __restrict__ n_sel, int64_t cap,
+                       int64_t T, int Hq, int H, int bs, int causal, float scale_log2,
+                       const void* __restrict__ mask, int mask_dt, int64_t m_sb, int64_t m_sh, int64_t m_st,
+                       int64_t m_ss, void* __restrict__ out, int64_t out_sb, int64_t out_st,
+                       void* __restrict__ weights, int64_t w_sb, int64_t w_sh, int64_t w_st) {
+    constexpr int KS = DH + 1;
+    __shared__ float k_lds[kChunkKeys * KS];
+    __shared__ float v_lds[kChunkKeys * KS];
+    __shared__ float q_lds[kPrefillMaxGroup * DH];
+    __shared__ float p_lds[kPrefillWaves][kChunkKeys];
+    __shared__ int32_t blocks[kWMaxList];
+    __shared__ int n_blocks;
+
+    const int64_t t = blockIdx.x;
+    const int g = blockIdx.y;
+    const int b = blockIdx.z;
+    const int R = Hq / H;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int64_t NB = cdiv(T, bs);
+    const int64_t row = (static_cast<int64_t>(b) * H + g) * T + t;
+    const int64_t limit = causal ? t + 1 : T;  // keys [0, limit)
+    const float kL2e = kLog2eP;
+
+    // the row's blocks as a set: listed entries inside [0, NB) once each
+    if (threadIdx.x == 0 && sel != nullptr) {
+        int n = 0;
+        if (sel != nullptr) {
+            const int64_t m = n_sel[row] < cap ? n_sel[row] : cap;
+            for (int64_t i = 0; i < m; ++i) {
+                const int32_t j = sel[row * cap + i];
+                bool seen = j < 0 || j >= NB;
+                for (int e = 0; e < n && !seen; ++e) seen = blocks[e] == j;
+                if (!seen && n < kWMaxList) blocks[n++] = j;
+            }
+        }
+        n_blocks = n;
+    }
+    // zero the rows of the weights; the allowed entries are written in pass 2
+    if (weights != nullptr) {
+        for (int64_t e = threadIdx.x; e < static_cast<int64_t>(R) * T; e += kPrefillThreads) {
+            const int hh = static_cast<int>(e / T);
+            const int64_t s = e % T;
+            store_elem<DT>(weights, b * w_sb + static_cast<int64_t>(g * R + hh) * w_sh + t * w_st + s, 0.0f);
+        }
+    }
+    for (int e = threadIdx.x; e < R * DH; e += kPrefillThreads) {
+        const int hh = e / DH, d = e % DH;
+        q_lds[e] = load_elem<DT>(q, b * q_sb + t * q_st + static_cast<int64_t>(g * R + hh) * q_sh + d) * scale_log2;
+    }
+    __syncthreads();
+    const int64_t nblk = sel != nullptr ? n_blocks : NB;  // dense: every block, in order
+
+    auto mask_at = [&](int h, int64_t s) -> float {
+        if (mask == nullptr) return 0.0f;
+        const int64_t mi = b * m_sb + static_cast<int64_t>(h) * m_sh + t * m_st + s * m_ss;
+        return (mask_dt == SPARDA_F32 ? load_elem<SPARDA_F32>(mask, mi) : load_elem<SPARDA_BF16>(mask, mi)) * kL2e;
+    };
+    constexpr int MAXR = kPrefillMaxGroup / kPrefillWaves;
+    float m_row[MAXR], l_row[MAXR];
+    float o_acc[MAXR][HeadAcc<DH>::DPL];
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) {
+        m_row[r] = -__builtin_inff();
+        l_row[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HeadAcc<DH>::DPL; ++i) o_acc[r][i] = 0.0f;
+    }
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int64_t bi = 0; bi < nblk; ++bi) {
+            const int64_t s0 = (sel != nullptr ? static_cast<int64_t>(blocks[bi]) : bi) * bs;
+            int64_t s1 = s0 + bs;
+            if (s1 > limit) s1 = limit;
+            for (int64_t c0 = s0; c0 < s1; c0 += kChunkKeys) {
+                const int nk = static_cast<int>((s1 - c0) < kChunkKeys ? (s1 - c0) : kChunkKeys);
+                __syncthreads();
+                for (int e = threadIdx.x; e < nk * DH; e += kPrefillThreads) {
+                    const int kk = e / DH, d = e % DH;
+                    const int64_t src = b * kv_sb + (c0 + kk) * kv_st + g * kv_sh + d;
+                    k_lds[kk * KS + d] = load_elem<DT>(k, src);
+                    if (pass == 1) v_lds[kk * KS + d] = load_elem<DT>(v, src);
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < MAXR; ++r) {
+                    const int hh = wave + r * kPrefillWaves;
+                    if (hh >= R) continue;
+                    const int h = g * R + hh;
+                    float sc = -__builtin_inff();
+                    if (lane < nk) {
+                        float a = 0.0f;
+#pragma unroll
+                        for (int d = 0; d < DH; ++d) a = fmaf(q_lds[hh * DH + d], k_lds[lane * KS + d], a);
+                        sc = a + mask_at(h, c0 + lane);
+                    }
+                    if (pass == 0) {
+                        const float mc = wave_max(sc);
+                        if (mc == -__builtin_inff()) continue;  // wave-uniform
+                        const float m_new = fmaxf(m_row[r], mc);
+                        const float p = sc == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sc - m_new);
+                        l_row[r] = l_row[r] * __builtin_amdgcn_exp2f(m_row[r] - m_new) + wave_sum(p);
+                        m_row[r] = m_new;
+                    } else {
+                        const float p = sc == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sc - m_row[r]) / l_row[r];
+                        if (weights != nullptr && lane < nk)
+                            store_elem<DT>(weights, b * w_sb + static_cast<int64_t>(h) * w_sh + t * w_st + c0 + lane, p);
+                        p_lds[wave][lane] = p;
+                        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                        for (int i = 0; i < HeadAcc<DH>::DPL; ++i) {
+                            const int d = lane + i * kWave;
+                            if (d < DH)
+                                for (int key = 0; key < nk; ++key) o_acc[r][i] = fmaf(p_lds[wave][key], v_lds[key * KS + d], o_acc[r][i]);
+                        }
+                        __builtin_amdgcn_wave_barrier();
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) {
+        const int hh = wave + r * kPrefillWaves;
+        if (hh >= R) continue;
+        const int h = g * R + hh;
+#pragma unroll
+        for (int i = 0; i < HeadAcc<DH>::DPL; ++i) {
+            const int d = lane + i * kWave;
+            if (d < DH) store_elem<DT>(out, b * out_sb + t * out_st + static_cast<int64_t>(h) * DH + d, o_acc[r][i]);
+        }
+    }
+}
+
+int launch_prefill_weights(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                           int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype, const int32_t* sel,
+                           const int32_t* n_sel, int64_t cap, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                           int64_t D, int64_t bs, int causal, float scale, const void* mask, int mask_dt,
+                           int64_t m_sb, int64_t m_sh, int64_t m_st, int64_t m_ss, void* out, int64_t out_sb,
+                           int64_t out_st, void* weights, int64_t w_sb, int64_t w_sh, int64_t w_st,
+                           hipStream_t stream) {
+    dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+    const float sl = scale * kLog2eP;
+#define SPARDA_PW(DT_, DH_)                                                                                   \
+    hipLaunchKernelGGL((prefill_weights_kernel<DT_, DH_>), grid, dim3(kPrefillThreads), 0, stream, q, q_sb, q_st, \
+                       q_sh, k, v, kv_sb, kv_st, kv_sh, sel, n_sel, cap, T, static_cast<int>(Hq),            \
+                       static_cast<int>(Hkv), static_cast<int>(bs), causal, sl, mask, mask_dt, m_sb, m_sh, m_st,  \
+                       m_ss, out, out_sb, out_st, weights, w_sb, w_sh, w_st)
+#define SPARDA_PW_D(DT_)                    \
+    switch (D) {                            \
+        case 16: SPARDA_PW(DT_, 16); break; \
+        case 32: SPARDA_PW(DT_, 32); break; \
+        case 64: SPARDA_PW(DT_, 64); break; \
+        default: SPARDA_PW(DT_, 128); break; \
+    }
+    if (dtype == SPARDA_BF16) {
+        SPARDA_PW_D(SPARDA_BF16);
+    } else {
+        SPARDA_PW_D(SPARDA_F32);
+    }
+#undef SPARDA_PW_D
+#undef SPARDA_PW
+    return check_hip(hipGetLastError(), "prefill_weights_kernel");
+}
+
 bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs,
                                const int32_t* sel, int64_t cap, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st,

@@ -133,32 +133,40 @@ class HipSparseAttention(BaseAttention):
         return self._project(out, residual)
 
     # -- prefill -----------------------------------------------------------
-    def _prefill(self, xq, xk, xv, forecast_vector, is_causal):
+    def _selection(self, xq, xk, forecast_vector, is_causal):
+        """The allowed-block lists of a prefill (sparse.py:201-253): None for
+        the dense fallback, else router lists (forecast) or the static window
+        {0} U [own-k, own]; without causality every listed block is attended
+        in full."""
         B, T = xq.shape[:2]
         nb = (T + self.block_size - 1) // self.block_size
         dense = self.mode == "dense" or nb <= 2 or (
             self.mode == "forecast" and (forecast_vector is None or self.layer_idx == 0))
-        if not dense and self.mode == "static" and not is_causal:
-            raise NotImplementedError("static sparse prefill is causal only in the HIP backend")
         if dense:
-            sel = n_sel = None
-        elif self.mode == "forecast":
+            return None, None
+        if self.mode == "forecast":
             protos = sparda.compress(xk, self.block_size)
             _, _, sel, n_sel = sparda.route(forecast_vector, protos, self.block_size, self.top_k_blocks,
                                             causal=is_causal, want_topk=False, want_sel=True)
-        else:
-            sel, n_sel = sparda.select_fixed(sparda.SEL_WINDOW_PREFILL, B, T, self.n_kv_head, nb,
-                                             self.block_size, self.top_k_blocks, 0, device=xq.device)
-        out = sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=is_causal)
-        return self.wo(out)
+            return sel, n_sel
+        return sparda.select_fixed(sparda.SEL_WINDOW_PREFILL, B, T, self.n_kv_head, nb, self.block_size,
+                                   self.top_k_blocks, 0, device=xq.device)
+
+    def _prefill(self, xq, xk, xv, forecast_vector, is_causal, mask=None, return_attn_weights=False):
+        sel, n_sel = self._selection(xq, xk, forecast_vector, is_causal)
+        if mask is None and not return_attn_weights:
+            return self.wo(sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=is_causal))
+        # explicit additive mask and/or the weights (sparse.py:206-221, 255-281)
+        res = sparda.prefill_masked(xq, xk, xv, sel, n_sel, self.block_size, causal=is_causal, mask=mask,
+                                    want_weights=return_attn_weights)
+        if return_attn_weights:
+            out, weights = res
+            return self.wo(out), weights
+        return self.wo(res)
 
     def forward(self, x: torch.Tensor, rotary_emb: RotaryEmbedding, kv_cache: Optional[KVCache] = None,
                 mask: Optional[torch.Tensor] = None, is_causal: bool = True,
                 forecast_vector: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
-        if mask is not None:
-            raise NotImplementedError("explicit additive masks are not supported by the HIP backend")
-        if kwargs.get("return_attn_weights", False):
-            raise NotImplementedError("return_attn_weights is not available from the HIP backend")
         B, T, _ = x.shape
         xq = self.wq(x).view(B, T, self.n_head, self.head_dim)
         xk = self.wk(x).view(B, T, self.n_kv_head, self.head_dim)
@@ -166,17 +174,22 @@ class HipSparseAttention(BaseAttention):
         offset = kv_cache.current_len if kv_cache is not None else 0
         xq, xk = rotary_emb(xq, xk, offset=offset)
         return self.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
-                                      forecast_vector=forecast_vector)
+                                      forecast_vector=forecast_vector, mask=mask,
+                                      return_attn_weights=kwargs.get("return_attn_weights", False))
 
     def forward_projected(self, xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
                           kv_cache: Optional[KVCache] = None, is_causal: bool = True,
                           forecast_vector: Optional[torch.Tensor] = None,
-                          residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          residual: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
+                          return_attn_weights: bool = False):
         """The attention after the projections and RoPE: xq [B,T,Hq,D], xk / xv
         [B,T,Hkv,D] (already rotated at the cache's current position). Entered
         from forward, or directly by a block whose fused producer computed them.
         With residual (single-token decode only) the result is residual +
-        attention, the projection and the sum in one kernel."""
+        attention, the projection and the sum in one kernel. A prefill with an
+        additive mask or return_attn_weights returns (out, weights) as the
+        reference does; a decode step ignores both, as the reference's does
+        (sparse.py:398-410)."""
         T = xq.shape[1]
         if kv_cache is not None and T == 1:
             kv_cache.update(xk, xv)
@@ -187,4 +200,4 @@ class HipSparseAttention(BaseAttention):
             if kv_cache.current_len != 0:
                 raise NotImplementedError("prefill into a non-empty cache is not supported")
             kv_cache.update(xk, xv)
-        return self._prefill(xq, xk, xv, forecast_vector, is_causal)
+        return self._prefill(xq, xk, xv, forecast_vector, is_causal, mask, return_attn_weights)

@@ -214,6 +214,65 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[tor
     return out
 
 
+def prefill_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[torch.Tensor],
+                   n_sel: Optional[torch.Tensor], block_size: int, causal: bool = True,
+                   scale: Optional[float] = None, mask: Optional[torch.Tensor] = None,
+                   want_weights: bool = False, out: Optional[torch.Tensor] = None):
+    """Block-sparse GQA prefill with an additive mask and optionally the
+    attention weights (model/attention/sparse.py:206-221, 255-281).
+
+    q [B,T,Hq,D], k/v [B,T,Hkv,D]; sel/n_sel as for ``prefill`` (None: dense).
+    mask: additive, broadcastable to [B, H, T, T] with H in {1, Hkv, Hq} (a
+    per-KV-head mask applies to that head's query heads, as the reference's
+    repeat_interleave does). Returns out [B,T,Hq*D], and with want_weights
+    also weights [B,Hq,T,T] (q's dtype, zero outside the allowed set).
+    """
+    dev = require_device(q, k, v, sel, n_sel, mask)
+    _inference_only(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q, k, v must share a dtype")
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    if k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty((B, T, Hq * D), dtype=q.dtype, device=dev)
+    cap = 0
+    if sel is not None:
+        sel = sel.to(torch.int32).contiguous()
+        n_sel = n_sel.to(torch.int32).contiguous()
+        cap = sel.shape[-1]
+    mptr, mdt, mst = None, _lib.F32, (0, 0, 0, 0)
+    if mask is not None:
+        if mask.dtype == torch.bool:
+            raise TypeError("sparda: the mask is additive (floating point), as in the reference")
+        m = mask if mask.dim() == 4 else mask.reshape((1,) * (4 - mask.dim()) + tuple(mask.shape))
+        if m.shape[1] == Hkv and Hkv != Hq:
+            m = torch.repeat_interleave(m, Hq // Hkv, dim=1)
+        if m.dtype not in (torch.float32, torch.bfloat16):
+            m = m.float()
+        m = torch.broadcast_to(m, (B, Hq, T, T))
+        mptr, mdt, mst = m.data_ptr(), _dtype_code(m), tuple(m.stride())
+        mask = m  # keep alive through the call
+    w = None
+    wst = (0, 0, 0)
+    if want_weights:
+        w = torch.empty((B, Hq, T, T), dtype=q.dtype, device=dev)
+        wst = w.stride()[:3]
+    qsb, qst, qsh, _ = q.stride()
+    ksb, kst, ksh, _ = k.stride()
+    osb, ost, _ = out.stride()
+    call("sparda_prefill_masked", q.data_ptr(), qsb, qst, qsh, k.data_ptr(), v.data_ptr(), ksb, kst, ksh,
+         _dtype_code(q), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap, B, T, Hq, Hkv, D, block_size,
+         int(causal), float(scale), mptr, mdt, *mst, out.data_ptr(), osb, ost,
+         w.data_ptr() if w is not None else None, *wst, _stream(dev))
+    return (out, w) if want_weights else out
+
+
 class DecodeWorkspace:
     """Device workspace for ``decode``, grown on demand and reused across steps."""
 

@@ -20,6 +20,9 @@ What it restates (citations into tyborra/local-research-Small-Language-Model):
 * ``attention_prefill`` — masked SDPA over the allowed set,
                    model/attention/sparse.py:255-281, computed per query row in
                    float64 over exactly the allowed keys (never an O(T^2) mask)
+* ``attention_prefill_masked`` — the same with an explicit additive mask
+                   and the attention weights (return_attn_weights),
+                   model/attention/sparse.py:206-221, 255-281
 * ``attention_decode`` / ``decode_step`` — model/attention/sparse.py:99-183
 * ``teacher_block_scores`` — TeacherBlockSelector.forward steps 1-3,
                    model/forecast.py:160-184 (head mean, block sums, causal 0)
@@ -264,6 +267,53 @@ def attention_prefill(q, k, v, sel, n_sel, bs: int, causal: bool = True,
             o = _softmax_attend(qr, k[b, keys, g], v[b, keys, g], scale)
             out[b, t, g * R * D:(g + 1) * R * D] = o.reshape(-1)
     return out
+
+
+def attention_prefill_masked(q, k, v, sel, n_sel, bs: int, causal: bool = True, mask=None,
+                             scale: Optional[float] = None, rows=None):
+    """The masked-SDPA path with an explicit additive mask and the attention
+    weights (model/attention/sparse.py:206-221, 255-281), float64.
+
+    Selections have set semantics (repeated entries count once, entries
+    outside [0, NB) attend nothing). mask: broadcastable to [B, Hq, T, T]
+    (natural-log units, added to the allowed scores). Returns (out
+    [B,T,Hq*D], weights [B,Hq,T,T]); rows not evaluated are NaN.
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    R = Hq // Hkv
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    NB = num_blocks(T, bs)
+    m = None if mask is None else np.broadcast_to(np.asarray(mask, np.float64), (B, Hq, T, T))
+    out = np.full((B, T, Hq * D), np.nan)
+    w = np.full((B, Hq, T, T), np.nan)
+    if rows is None:
+        rows = [(b, t) for b in range(B) for t in range(T)]
+    for b, t in rows:
+        limit = t + 1 if causal else T
+        for g in range(Hkv):
+            if sel is None:
+                blocks = range(NB)
+            else:
+                blocks = sorted({int(j) for j in sel[b, g, t, :int(n_sel[b, g, t])] if 0 <= j < NB})
+            keys = _keys_for(blocks, bs, limit)
+            for hh in range(R):
+                h = g * R + hh
+                s = (k[b, keys, g] @ q[b, t, h]) * scale
+                if m is not None:
+                    s = s + m[b, h, t, keys]
+                mx = s.max()
+                p = np.exp(s - mx)
+                p = p / p.sum()
+                row = np.zeros(T)
+                row[keys] = p
+                w[b, h, t] = row
+                out[b, t, h * D:(h + 1) * D] = p @ v[b, keys, g]
+    return out, w
 
 
 def attention_decode(q, kc, vc, S: int, sel, n_sel, bs: int,

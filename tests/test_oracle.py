@@ -391,3 +391,82 @@ def test_prefetch_selection_absolute_equals_router_and_brute_force():
             # with a partial own block the router (own clamped to NB-1 = own) agrees
             _, _, rsel, rn = O.route(f.reshape(B, 1, H, D), P, bs, k, True, L, L)
             assert np.array_equal(rsel[:, :, 0], sel) and np.array_equal(rn[:, :, 0], n)
+
+
+# ---------------------------------------------------------------------------
+# masked prefill with weights (sparse.py:206-221, 255-281)
+# ---------------------------------------------------------------------------
+
+def _small(seed, B=1, T=96, Hq=4, Hkv=2, D=16):
+    r = np.random.default_rng(seed)
+    return (r.standard_normal((B, T, Hq, D)), r.standard_normal((B, T, Hkv, D)),
+            r.standard_normal((B, T, Hkv, D)))
+
+
+def test_masked_prefill_without_mask_equals_prefill():
+    q, k, v = _small(1)
+    f = np.random.default_rng(2).standard_normal((1, 96, 2, 16))
+    _, _, sel, n = O.route(f, O.compress(k, 16), 16, 2, True)
+    out, w = O.attention_prefill_masked(q, k, v, sel, n, 16, True)
+    assert np.allclose(out, O.attention_prefill(q, k, v, sel, n, 16, True), atol=1e-12)
+    # weights: rows sum to one, nothing above the diagonal, out == W V
+    assert np.allclose(w.sum(-1), 1.0)
+    assert (np.triu(w[0, 0], 1) == 0).all()
+    o2 = np.einsum("bhts,bshd->bthd", w, np.repeat(v, 2, axis=2)).reshape(out.shape)
+    assert np.allclose(o2, out, atol=1e-12)
+
+
+def test_masked_prefill_dense_equals_sdpa_with_attn_mask():
+    # library pin: dense, non-causal, additive mask == torch SDPA(attn_mask)
+    q, k, v = _small(3)
+    m = np.random.default_rng(4).standard_normal((1, 4, 96, 96))
+    out, _ = O.attention_prefill_masked(q, k, v, None, None, 16, False, mask=m)
+    tq, tk, tv = (torch.from_numpy(x).permute(0, 2, 1, 3) for x in (q, k, v))
+    tk, tv = (torch.repeat_interleave(x, 2, dim=1) for x in (tk, tv))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=torch.from_numpy(m))
+    assert np.allclose(out, ref.permute(0, 2, 1, 3).reshape(1, 96, 64).numpy(), atol=1e-10)
+
+
+def test_masked_prefill_minus_inf_block_equals_dropping_it():
+    # -inf over one listed block is the list without it; a constant shift of the
+    # mask changes nothing (softmax shift invariance)
+    q, k, v = _small(5)
+    T, bs = 96, 16
+    sel = np.full((1, 2, T, 4), -1, np.int32)
+    n = np.zeros((1, 2, T), np.int32)
+    sel2, n2 = sel.copy(), n.copy()
+    for t in range(T):
+        own = t // bs
+        lst = sorted({0, own} | ({own - 1} if own >= 1 else set()))
+        sel[0, :, t, :len(lst)] = lst
+        n[0, :, t] = len(lst)
+        keep = [j for j in lst if j != 0] or [0]
+        sel2[0, :, t, :len(keep)] = keep
+        n2[0, :, t] = len(keep)
+    m = np.zeros((T, T))
+    m[:, :bs] = -np.inf
+    rows = [(0, t) for t in range(bs, T)]  # rows whose lists keep another block
+    a, _ = O.attention_prefill_masked(q, k, v, sel, n, bs, True, mask=m, rows=rows)
+    b, _ = O.attention_prefill_masked(q, k, v, sel2, n2, bs, True, rows=rows)
+    c, _ = O.attention_prefill_masked(q, k, v, sel, n, bs, True, mask=m + 3.5, rows=rows)
+    assert np.allclose(a[0, bs:], b[0, bs:], atol=1e-12)
+    assert np.allclose(a[0, bs:], c[0, bs:], atol=1e-12)
+
+
+def test_masked_prefill_repeats_and_out_of_range_entries_count_once():
+    q, k, v = _small(6)
+    T, bs = 96, 16
+    sel = np.full((1, 2, T, 6), -1, np.int32)
+    n = np.zeros((1, 2, T), np.int32)
+    clean = sel.copy()
+    nc = n.copy()
+    for t in range(T):
+        own = t // bs
+        sel[0, :, t, :5] = [own, 0, own, -1, 99]
+        n[0, :, t] = 5
+        lst = sorted({0, own})
+        clean[0, :, t, :len(lst)] = lst
+        nc[0, :, t] = len(lst)
+    a, wa = O.attention_prefill_masked(q, k, v, sel, n, bs, True)
+    b = O.attention_prefill(q, k, v, clean, nc, bs, True)
+    assert np.allclose(a, b, atol=1e-12)
