@@ -41,10 +41,15 @@ top_k + 2 blocks (below that the eager path attends every block through
 another wavefront split).
 
 Requirements: HipSparseAttention or HipAsyncOffloadAttention layers, bf16
-weights, head dim 64, forecast dim 64 (the fused producer's shape). Weights
-are read from the tensors that exist when the step is captured: capture (the
-first ``step``) after loading them, or call ``reset_graph`` after changing
-them.
+weights, head dim 64, forecast dim 64 (the fused producer's shape).
+
+The recorded step reads the parameters and the weight copies folded from
+them (each block's stacked producer and FFN weights with their RMSNorm
+weights folded in, and the folded output head) at the addresses they had
+when it was recorded. The decoder holds a reference to every folded copy, so
+that memory stays valid, and keys every parameter by (data_ptr, version): a
+step that finds a parameter replaced or changed in place records the step
+again from the current weights.
 """
 
 from typing import List, Optional, Sequence
@@ -71,10 +76,15 @@ class GraphDecoder:
     that needs them; the default issues them on the compute stream, which a
     replayed graph runs faster here (each cross-stream dependency inside the
     graph costs more than the ~20 us per layer of selection and host-link
-    copy it would hide)."""
+    copy it would hide).
+
+    taps: layers whose attention inputs and output the recorded step keeps in
+    ``tapped[i]`` (q [B,Hq,D], the routing forecast or None, the attention
+    output [B,Hq*D], and for an offloaded layer the prefetched selection),
+    buffers that every replay rewrites, for checking a replayed step."""
 
     def __init__(self, model, batch_size: int, max_seq_len: int, caches: Optional[Sequence] = None,
-                 overlap: bool = False):
+                 overlap: bool = False, taps: Sequence[int] = ()):
         cfg = model.config
         p = next(model.parameters())
         self.device = p.device
@@ -149,6 +159,10 @@ class GraphDecoder:
                 caches[i].block_sums(bs)  # start the block sums before anything is captured
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.logits: Optional[torch.Tensor] = None
+        self._taps = frozenset(taps)
+        self.tapped = {}
+        self._held: List[torch.Tensor] = []
+        self._keys = None
 
     # -- one decode step, every launch reading *pos --------------------------
     def _producer_appends(self, i: int, a, f: Optional[torch.Tensor]) -> bool:
@@ -213,6 +227,11 @@ class GraphDecoder:
                     self._prefetch(i + 1, f)
                     ev.record(main)
             out = self._attend(i, a, q[:, 0], k, v, prev_f)
+            if i in self._taps:
+                t = dict(q=q[:, 0], f=prev_f, out=out)
+                if self.kinds[i] == _OFFLOAD:
+                    t.update(sel=self._pf[i]["sel"], n_sel=self._pf[i]["n"])
+                self.tapped[i] = t
             if layer._use_fused_wo(x, 1, self.caches[i]):
                 x = sparda.rows_residual(out.view(B, 1, a.n_head * a.head_dim), a.wo.weight, x)
             else:
@@ -222,11 +241,17 @@ class GraphDecoder:
         self.logits = m.logits(x)[:, -1, :]
         self.pos.add_(1)
 
+    def _weight_keys(self):
+        return tuple((p.data_ptr(), p._version) for p in self.model.parameters())
+
     def _capture(self):
+        m = self.model
         with torch.no_grad():
-            for layer in self.model.layers:
-                layer._fused_weight()  # build the stacked weights outside the graph
-                layer._fused_ffn_weight()
+            # the folded copies are built outside the graph and held while it lives
+            self._held = [m._folded_head()] if getattr(m.config, "fused_ffn", False) else []
+            for layer in m.layers:
+                self._held += [layer._fused_weight(), layer._fused_ffn_weight()]
+            self._keys = self._weight_keys()
             # warm-up step on a side stream (library handles, workspaces), then
             # the position is put back: the replay rewrites the same cache rows
             # and recomputes the same block sums. The prefetch of an offloaded
@@ -252,6 +277,9 @@ class GraphDecoder:
         """Drop the recorded step (it is captured again by the next ``step``)."""
         self.graph = None
         self.logits = None
+        self.tapped = {}
+        self._held = []
+        self._keys = None
 
     # -- public loop ---------------------------------------------------------
     @torch.no_grad()
@@ -282,6 +310,8 @@ class GraphDecoder:
         if self.length >= self.max_len:
             raise ValueError(f"GraphDecoder: the caches are full ({self.max_len} tokens)")
         self.tok.copy_(tokens.reshape(self.B, 1))
+        if self.graph is not None and self._weight_keys() != self._keys:
+            self.reset_graph()  # a parameter was replaced or changed since the step was recorded
         if self.graph is None:
             self._capture()
         self.graph.replay()

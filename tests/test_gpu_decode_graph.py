@@ -6,9 +6,14 @@ with their host-length counterparts (same kernels, same launch shapes); the
 window mode's every-block fallback on a short cache with the dense decode
 within max-abs 2e-2 / mean-abs 2e-3 (bf16) or 1e-4 (fp32). The replayed
 generation loop is compared with the eager cached-prototype decode of the same
-model: logits of every step bit for bit, sampled tokens identical.
+model: logits of every step bit for bit, sampled tokens identical. A replayed
+step's forecast-routed layers are checked against the oracle from the caches,
+block sums and the q / forecast the replay left behind: the selection
+bit-exact, the attention within the bf16 bar. A parameter changed in place or
+replaced between steps makes the next step record again from the new weights.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -18,6 +23,7 @@ from model.config import ModelConfig
 from model.decode_graph import GraphDecoder
 from model.model import SparDAResearchModel
 from helpers import assert_close_out, np32
+from oracle import sparda_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -244,3 +250,83 @@ def test_graph_decoder_sixteen_sequences_and_capacity_limit():
             assert torch.equal(got, want), f"position {t}"
         with pytest.raises(ValueError):
             gd.step(ids[:, :1])  # the caches are full
+
+
+@pytest.mark.parametrize("backend,routing", [("hip_sparse", "reference"), ("hip_sparse", "absolute"),
+                                             ("async_offload", "reference"), ("async_offload", "absolute")])
+def test_graph_replayed_step_against_the_oracle(backend, routing):
+    # layers 1 and 2 are routed by the forecast of the layer before them; at
+    # each checked step their q, routing forecast and attention output are
+    # read from the replay's own buffers
+    case(f"graph-replayed step vs the oracle, {backend} {routing}")
+    cfg = ModelConfig(n_layer=3, context_length=2048, block_size=64, top_k_blocks=8, decode_routing=routing,
+                      attention_backend=backend, fused_producer=True, fused_ffn=True, norm_eps=1e-5)
+    torch.manual_seed(27)
+    model = SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval()
+    B, T0, n, cap, bs, k = 2, 900, 70, 1100, 64, 8
+    Hkv = cfg.n_kv_head
+    g = torch.Generator().manual_seed(28)
+    ids = torch.randint(0, cfg.vocab_size, (B, T0 + n), generator=g).to(DEV)
+    gd = GraphDecoder(model, B, cap, taps=(1, 2))
+    checked = 0
+    with torch.no_grad():
+        gd.prefill(ids[:, :T0])
+        for t in range(T0, T0 + n):
+            gd.step(ids[:, t:t + 1])
+            if t not in (T0, 959, 960, T0 + n - 1):  # first step, the last row of a block, a new block, last
+                continue
+            torch.cuda.synchronize()
+            S = gd.length
+            for i in (1, 2):
+                case(f"  position {S - 1}, layer {i}")
+                c, tap = gd.caches[i], gd.tapped[i]
+                f = tap["f"].reshape(B, Hkv, -1)
+                if backend == "hip_sparse":
+                    kc, vc = np32(c.k[:, :S]), np32(c.v[:, :S])
+                    sel_o, n_o, _ = O.decode_selection(kc, S, np32(f), bs, k, routing)
+                    # the replay's block sums select what the oracle selects from the keys
+                    sel, n_sel = sparda.select_decode(f, c.block_sums, S, S - 1, bs, k, routing=routing)
+                else:
+                    kc, vc = c.cpu_k[:, :S].float().numpy(), c.cpu_v[:, :S].float().numpy()
+                    # the prefetch selected before the token at S - 1 was appended
+                    sel_o, n_o = O.prefetch_selection(kc, S - 1, S - 1, np32(f), bs, k, routing)
+                    sel, n_sel = tap["sel"], tap["n_sel"]
+                assert np.array_equal(n_sel.cpu().numpy(), n_o)
+                assert np.array_equal(sel.cpu().numpy(), sel_o)
+                want = O.attention_decode(np32(tap["q"]), kc, vc, S, sel_o, n_o, bs)
+                assert_close_out(np32(tap["out"]), want, torch.bfloat16, what=f"layer {i} at {S - 1}")
+                checked += 1
+    assert checked == 8
+
+
+def test_graph_records_again_after_a_weight_change():
+    case("graph-replayed decode after in-place and replacing weight changes")
+    model, cfg = _model("forecast", "absolute", fused_ffn=True)
+    B, T0, n, cap = 2, 700, 30, 1024
+    g = torch.Generator().manual_seed(29)
+    ids = torch.randint(0, cfg.vocab_size, (B, T0 + n), generator=g).to(DEV)
+    caches = [PrototypeKVCache(B, cap, cfg.n_kv_head, cfg.head_dim, DEV, torch.bfloat16, block_size=64)
+              for _ in range(cfg.n_layer)]
+    gd = GraphDecoder(model, B, cap)
+    graphs = []
+    with torch.no_grad():
+        model(ids[:, :T0], kv_caches=caches)
+        gd.prefill(ids[:, :T0])
+        for t in range(T0, T0 + n):
+            if t == T0 + 10:
+                # in place: the folded producer, FFN and head weights are stale
+                model.layers[1].attn_norm.weight.mul_(1.5)
+                model.layers[2].ffn_norm.weight.mul_(0.75)
+                model.final_norm.weight.mul_(1.25)
+                model.embeddings.weight[int(ids[0, t + 1])].mul_(1.5)
+            if t == T0 + 20:
+                # replaced: the recorded step would read the old tensor's memory
+                w = model.layers[0].ffn.w_down.weight
+                model.layers[0].ffn.w_down.weight = torch.nn.Parameter(w * 1.25)
+                model.layers[1].attention.wo.weight = torch.nn.Parameter(model.layers[1].attention.wo.weight * 0.8)
+            want = model(ids[:, t:t + 1], kv_caches=caches)["logits"][:, -1]
+            got = gd.step(ids[:, t:t + 1])
+            if not graphs or graphs[-1] is not gd.graph:
+                graphs.append(gd.graph)
+            assert torch.equal(got, want), f"position {t}: max diff {(got.float() - want.float()).abs().max().item()}"
+    assert len(graphs) == 3  # recorded at the first step and after each change

@@ -164,6 +164,16 @@ def test_model_with_fused_ffn_matches_unfused():
             m.layers[0].ffn_norm.weight.mul_(1.5)  # the folded weight follows parameter updates
         a, b, r = (m(ids[:, 660:661], kv_caches=c)["logits"] for m, c in zip((plain, fused, ref), caches))
         _no_less_accurate(b, a, r, "decode logits after a weight update")
+        # the folded output head follows the final norm and the tied table (one
+        # row scaled: the next token's embedding and that vocabulary column)
+        tok = int(ids[0, 661])
+        head = fused._folded_head()
+        for m in (plain, fused, ref):
+            m.final_norm.weight.mul_(1.25)
+            m.embeddings.weight[tok].mul_(1.5)
+        a, b, r = (m(ids[:, 661:662], kv_caches=c)["logits"] for m, c in zip((plain, fused, ref), caches))
+        assert fused._folded_head() is not head
+        _no_less_accurate(b, a, r, "decode logits after a head update")
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 768, 768), (8, 768, 768), (16, 2048, 256), (3, 128, 16)])
@@ -221,3 +231,12 @@ def test_norm_gemv_op(M, C, N):
     diff = (got.reshape(M, N).float() - want).abs()
     tol = want.abs() * 2 ** -7 + 1e-3
     assert bool((diff <= tol).all()), f"max diff {diff.max().item()}"
+    # against the unfolded composition RMSNorm(x) * g @ W^T in fp32: the folded
+    # weight's one bf16 rounding (unit roundoff 2^-8) bounds the extra error by
+    # 2^-8 * |x / rms| . |W * g|
+    xn = xf / torch.sqrt((xf * xf).mean(-1, keepdim=True) + 1e-6)
+    wg = w.float() * nw.float()[None, :]
+    want2 = xn @ wg.T
+    diff2 = (got.reshape(M, N).float() - want2).abs()
+    tol2 = want2.abs() * 2 ** -7 + 2 ** -8 * (xn.abs() @ wg.abs().T) + 1e-3
+    assert bool((diff2 <= tol2).all()), f"unfolded: max diff {diff2.max().item()}"
