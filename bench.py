@@ -17,7 +17,8 @@ selection lists; the decode step against HBM peak (8 TB/s) with its
 algorithmic bytes. Kernel durations come from HIP events on the launch stream.
 
 cpu_baseline: the op-for-op PyTorch restatement of the reference path
-(O(T^2) masks + masked SDPA) timed on the host cores on a bounded sample.
+(O(T^2) masks + masked SDPA) timed on the host cores, N threads and 1
+thread, warm-up 3 / runs 10, median (the reference's latency protocol).
 
     python bench.py [--steps K] [--warmup W] [--decode-steps N] [--no-cpu-baseline]
 """
@@ -65,8 +66,8 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--offload-steps", type=int, default=32)
     ap.add_argument("--generate-steps", type=int, default=128)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "offload", "model", "producer", "teacher",
-                                       "generate", "pmc"],
+    ap.add_argument("--only", choices=["all", "prefill", "prefill16k", "decode", "offload", "model", "producer",
+                                       "teacher", "generate", "pmc"],
                     default="all",
                     help="run one workload (for profiling); the JSON line needs 'all'")
     return ap.parse_args()
@@ -93,10 +94,13 @@ def load_traffic():
         return {}
 
 
-def bench_prefill(args, torch, sparda, synth):
-    x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
+def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001):
+    """One sparse prefill layer at [B, T] (12/4 heads, D 64, block 64, top-8):
+    eager steps with events around each launch, then the step replayed from a
+    HIP graph."""
+    x = synth.prefill_inputs(B, T, HQ, HKV, D, dtype=torch.bfloat16, seed=seed, device="cuda")
     q, k, v, f = x["q"], x["k"], x["v"], x["forecast"]
-    out = torch.empty((PB, PT, HQ * D), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((B, T, HQ * D), dtype=torch.bfloat16, device="cuda")
 
     state = {}
 
@@ -133,7 +137,7 @@ def bench_prefill(args, torch, sparda, synth):
         assert torch.isfinite(out.float()).all(), "non-finite prefill output"
         # useful work: for each (b, g, t) the allowed keys are full blocks
         # below the own block plus t%bs+1 keys of the own block
-        t = torch.arange(PT, device="cuda")
+        t = torch.arange(T, device="cuda")
         keys = (n.to(torch.int64) - 1) * BS + (t % BS + 1)
         pairs = int(keys.sum().item()) * (HQ // HKV)
         # the step as a serving loop issues it: the three launches recorded once
@@ -163,11 +167,14 @@ def bench_prefill(args, torch, sparda, synth):
         del g
     flops = 4 * D * pairs
     tflops = flops / (ms_attn * 1e-3) / 1e12
-    comp_bytes = PB * PT * HKV * D * 2 + PB * (PT // BS) * HKV * D * 4
-    route_bytes = PB * PT * HKV * D * 2 + PB * (PT // BS) * HKV * D * 4 + PB * HKV * PT * (TOPK + 3) * 4
+    # compressor: read K, write the fp32 prototypes; router: read the forecast
+    # (bf16, [B,T,Hkv,64]) and the prototypes, write the lists and counts
+    nb = (T + BS - 1) // BS
+    comp_bytes = B * T * HKV * D * 2 + B * nb * HKV * D * 4
+    route_bytes = B * T * HKV * D * 2 + B * nb * HKV * D * 4 + B * HKV * T * (TOPK + 3) * 4
     return {
         "ms_per_step": ms_step,
-        "tok_s": PB * PT / (ms_step * 1e-3),
+        "tok_s": B * T / (ms_step * 1e-3),
         "ms_per_step_eager": ms_step_eager,
         "attn_ms": ms_attn,
         "attn_useful_flop": flops,
@@ -176,7 +183,9 @@ def bench_prefill(args, torch, sparda, synth):
         "compress_gbs": comp_bytes / (ms_compress * 1e-3) / 1e9,
         "route_us": ms_route * 1e3,
         "route_gbs": route_bytes / (ms_route * 1e-3) / 1e9,
-        "dense_causal_flop": 4 * D * HQ * PB * PT * (PT + 1) // 2,
+        "compress_frac": comp_bytes / (ms_compress * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "route_frac": route_bytes / (ms_route * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "dense_causal_flop": 4 * D * HQ * B * T * (T + 1) // 2,
     }
 
 
@@ -682,19 +691,22 @@ def bench_teacher(args, torch, sparda, synth):
 
 
 def pmc_workload(args, torch, sparda, synth):
-    """Short eager run for hardware-counter passes: prefill steps, decode steps
-    and a plain device copy of COPY_BYTES (the calibration of FETCH_SIZE /
-    WRITE_SIZE). Counter values are per dispatch."""
+    """Short eager run for hardware-counter passes: prefill steps at B=4 T=4096,
+    then at B=1 T=16384, decode steps and a plain device copy of COPY_BYTES
+    (the calibration of FETCH_SIZE / WRITE_SIZE). Counter values are per
+    dispatch, in this order."""
     x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
+    x16 = synth.prefill_inputs(1, MT, HQ, HKV, D, dtype=torch.bfloat16, seed=1003, device="cuda")
     c = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002, device="cuda")
     ws = sparda.DecodeWorkspace("cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     with torch.no_grad():
-        for _ in range(3):
-            protos = sparda.compress(x["k"], BS)
-            _, _, sel, n = sparda.route(x["forecast"], protos, BS, TOPK, want_topk=False, want_sel=True)
-            sparda.prefill(x["q"], x["k"], x["v"], sel, n, BS)
+        for xs in (x, x16):
+            for _ in range(3):
+                protos = sparda.compress(xs["k"], BS)
+                _, _, sel, n = sparda.route(xs["forecast"], protos, BS, TOPK, want_topk=False, want_sel=True)
+                sparda.prefill(xs["q"], xs["k"], xs["v"], sel, n, BS)
         for _ in range(3):
             sparda.decode(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], BS, TOPK, routing="absolute",
                           workspace=ws)
@@ -704,54 +716,117 @@ def pmc_workload(args, torch, sparda, synth):
     return {"copy_bytes": COPY_BYTES}
 
 
-def cpu_decode_baseline(args, torch, synth):
+def cpu_info():
+    """Host CPU model (/proc/cpuinfo, what lscpu's "Model name" shows), the
+    physical cores and the cores this process may run on."""
+    model, cores = None, set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                k, _, v = ln.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"model": model, "physical_cores": len(cores) or None, "os_cpu_count": os.cpu_count(),
+            "usable_cpus": usable}
+
+
+def cpu_timed(fn, warmup=3, runs=10):
+    """The reference's latency protocol (evaluation/latency.py:30-31,69-74):
+    `warmup` untimed calls, then `runs` calls timed with perf_counter;
+    returns the median and the spread in seconds."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    mid = len(ts) // 2
+    med = ts[mid] if len(ts) % 2 else 0.5 * (ts[mid - 1] + ts[mid])
+    return med, ts[0], ts[-1]
+
+
+def _thread_counts(args, torch):
+    n = args.cpu_threads or torch.get_num_threads()
+    return [n, 1] if n != 1 else [1]
+
+
+def cpu_decode_baseline(args, torch, synth, info):
     """The reference's decode step restated op for op (oracle/reference_path.py:
     whole-cache recompression, selection, topk compaction, gather, masked SDPA)
-    on the host cores, at the decode workload (B=8, 16K cache, bf16)."""
+    on the host cores, at the decode workload (B=8, 16K cache, bf16), routed
+    like the GPU leg (absolute-position causal mask; the reference's row-0 mask
+    is the same operations on another mask row). N threads and 1 thread,
+    warm-up 3 / runs 10 of 8 steps each, median per step."""
     from oracle import reference_path as R
-    threads = args.cpu_threads or torch.get_num_threads()
-    torch.set_num_threads(threads)
     x = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002)
     q = x["q"][:, :, None, :]
     k, v = x["k_cache"].transpose(1, 2), x["v_cache"].transpose(1, 2)
     f = x["forecast"][:, None]
+    steps = 8
+    legs = {}
     with torch.no_grad():
-        t0 = time.perf_counter()
-        R.sparse_decode(q, k, v, DS, f, BS, TOPK)
-        first = time.perf_counter() - t0
-        reps = max(1, min(64, int(10.0 / max(first, 1e-3))))
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            R.sparse_decode(q, k, v, DS, f, BS, TOPK)
-        dt = (time.perf_counter() - t0) / reps
-    return {"value": round(dt * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
-            "sample": f"the decode workload (B=8, 16K cache, bf16) through the reference's decode step restated "
-                      f"op for op in PyTorch (whole-cache recompression, selection with the reference's row-0 "
-                      f"mask, topk compaction, gather, masked SDPA); {reps} timed step(s) after 1 warm-up, "
-                      f"torch threads={threads}"}
+        for n in _thread_counts(args, torch):
+            torch.set_num_threads(n)
+            med, lo, hi = cpu_timed(lambda: [R.sparse_decode(q, k, v, DS, f, BS, TOPK, routing="absolute")
+                                             for _ in range(steps)])
+            legs[n] = (med / steps, lo / steps, hi / steps)
+    torch.set_num_threads(max(legs))
+    n = max(legs)
+    out = {"value": round(legs[n][0] * 1e6, 1), "unit": "us/step", "cores": n, "kind": "port",
+           "sample": f"the decode workload (B=8, 16K cache, bf16) through the reference's decode step restated "
+                     f"op for op in PyTorch (whole-cache recompression, absolute-position routing as the GPU "
+                     f"leg, topk compaction, gather, masked SDPA); warm-up 3, median of 10 runs of {steps} "
+                     f"steps; torch threads={n}",
+           "min_us": round(legs[n][1] * 1e6, 1), "max_us": round(legs[n][2] * 1e6, 1), "cpu": info}
+    if 1 in legs and n != 1:
+        out["value_1_thread"] = round(legs[1][0] * 1e6, 1)
+    return out
 
 
-def cpu_baseline(args, torch, synth):
-    """Reference path restated op for op (oracle/reference_path.py), host CPU."""
+def cpu_baseline(args, torch, synth, info):
+    """Reference prefill path restated op for op (oracle/reference_path.py) on
+    the host cores: the full workload (B=4, T=4096) on N threads; on 1 thread
+    one sequence of it (B=1, T=4096, the same per-sequence work). Warm-up 3 /
+    runs 10, median."""
     from oracle import reference_path as R
-    threads = args.cpu_threads or torch.get_num_threads()
-    torch.set_num_threads(threads)
     x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001)
     q, k, v = (x[n].transpose(1, 2) for n in ("q", "k", "v"))
     f = x["forecast"]
+    legs = {}
     with torch.no_grad():
-        t0 = time.perf_counter()
-        R.sparse_prefill(q, k, v, f, BS, TOPK)
-        first = time.perf_counter() - t0
-        reps = max(1, min(20, int(10.0 / max(first, 1e-3))))
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            R.sparse_prefill(q, k, v, f, BS, TOPK)
-        dt = (time.perf_counter() - t0) / reps
-    return {"value": round(PB * PT / dt, 1), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"the full prefill workload (B={PB}, T={PT}, bf16) through the reference's masked-SDPA "
-                      f"path restated op for op in PyTorch (O(T^2) masks + SDPA); {reps} timed run(s) after "
-                      f"1 warm-up, {dt:.3f} s/run; torch threads={threads}, os.cpu_count()={os.cpu_count()}"}
+        for n in _thread_counts(args, torch):
+            torch.set_num_threads(n)
+            b = PB if n == max(_thread_counts(args, torch)) else 1
+            med, lo, hi = cpu_timed(lambda: R.sparse_prefill(q[:b], k[:b], v[:b], f[:b], BS, TOPK))
+            legs[n] = (b * PT / med, b, med, lo, hi)
+    n = max(legs)
+    torch.set_num_threads(n)
+    out = {"value": round(legs[n][0], 1), "unit": "tok/s", "cores": n, "kind": "port",
+           "sample": f"the full prefill workload (B={PB}, T={PT}, bf16) through the reference's masked-SDPA "
+                     f"path restated op for op in PyTorch (O(T^2) masks + SDPA); warm-up 3, median of 10 runs, "
+                     f"{legs[n][2]:.3f} s/run (min {legs[n][3]:.3f}, max {legs[n][4]:.3f}); torch threads={n}",
+           "cpu": info}
+    if 1 in legs and n != 1:
+        out["value_1_thread"] = round(legs[1][0], 1)
+        out["sample_1_thread"] = f"one sequence (B=1, T={PT}), warm-up 3, median of 10 runs, {legs[1][2]:.3f} s/run"
+    return out
 
 
 def main():
@@ -768,6 +843,7 @@ def main():
     sparda.load()
     if args.only != "all":
         fn = {"prefill": bench_prefill, "decode": bench_decode, "offload": bench_offload,
+              "prefill16k": lambda *a: bench_prefill(*a, B=1, T=MT, seed=1003),
               "model": bench_model, "producer": bench_producer, "teacher": bench_teacher,
               "generate": bench_generate, "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
@@ -777,6 +853,10 @@ def main():
     pre = bench_prefill(args, torch, sparda, synth)
     log(f"prefill: {pre['ms_per_step']:.3f} ms/step, attention {pre['attn_ms']*1e3:.1f} us "
         f"({pre['attn_tflops']:.1f} TFLOP/s useful)")
+    log(f"prefill at T={MT} (one layer of the 12-layer forward's shape)")
+    p16 = bench_prefill(args, torch, sparda, synth, B=1, T=MT, seed=1003)
+    log(f"prefill 16K: {p16['ms_per_step']:.3f} ms/step, attention {p16['attn_ms']*1e3:.1f} us "
+        f"({p16['attn_tflops']:.1f} TFLOP/s useful)")
     log("decode workload")
     dec = bench_decode(args, torch, sparda, synth)
     log(f"decode: {dec['us_per_step']:.2f} us/step ({dec['gbs']:.0f} GB/s), eager {dec['us_per_step_eager']:.2f}; "
@@ -810,13 +890,16 @@ def main():
     cpu = cpu_dec = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        cpu = cpu_baseline(args, torch, synth)
-        log(f"cpu: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
-        cpu_dec = cpu_decode_baseline(args, torch, synth)
-        log(f"cpu decode: {cpu_dec['value']:.1f} us/step on {cpu_dec['cores']} threads")
+        info = cpu_info()
+        cpu = cpu_baseline(args, torch, synth, info)
+        log(f"cpu: {cpu['value']:.1f} tok/s on {cpu['cores']} threads, {cpu.get('value_1_thread')} on 1 "
+            f"({info['model']})")
+        cpu_dec = cpu_decode_baseline(args, torch, synth, info)
+        log(f"cpu decode: {cpu_dec['value']:.1f} us/step on {cpu_dec['cores']} threads, "
+            f"{cpu_dec.get('value_1_thread')} on 1")
 
     traffic = load_traffic()
-    t_attn = traffic.get("prefill_mfma_kernel")
+    t_attn = traffic.get("prefill_attention")
     t_dec = traffic.get("decode_step")
     line = {
         "metric": METRIC,
@@ -839,6 +922,18 @@ def main():
                      "traffic": t_attn},
         "cpu_baseline": cpu,
         "prefill_detail": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre.items()},
+        "prefill_16k": {
+            "workload": f"the same layer at B=1, T={MT} (256 blocks, top-8 + sink + own), the attention shape of "
+                        "one layer of the 12-layer forward; step = compress + route + block-sparse MFMA "
+                        "prefill, HIP graph replay",
+            "ms_per_step": round(p16["ms_per_step"], 4),
+            "tok_s": round(p16["tok_s"], 1),
+            "roofline": {"bound": "mfma", "achieved": round(p16["attn_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(p16["attn_tflops"] / PEAK_BF16_TFLOPS, 4),
+                         "traffic": traffic.get("prefill_attention_16k")},
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16.items()
+               if k not in ("ms_per_step", "tok_s")},
+        },
         "decode": {
             "workload": "decode step @16K: B=8, KV cache [8,16384,4,64] bf16, 256 blocks, top-8 + sink + "
                         "current, absolute-position routing; step = whole-cache compress + route + split-K "

@@ -40,15 +40,17 @@ def block_means(k: torch.Tensor, bs: int) -> torch.Tensor:
 
 
 def select_blocks(forecast: torch.Tensor, reps: torch.Tensor, bs: int, top_k: int,
-                  causal: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
-    """forecast [B,Tq,H,Df], reps [B,NB,H,Df] -> scores [B,H,Tq,NB], topk [B,H,Tq,k]."""
+                  causal: bool = True, query_pos0: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """forecast [B,Tq,H,Df], reps [B,NB,H,Df] -> scores [B,H,Tq,NB], topk [B,H,Tq,k].
+    Row i of the causal mask sits at position query_pos0 + i (0: the
+    reference's row index, forecast.py:123-126)."""
     f = forecast.transpose(1, 2)
     r = reps.transpose(1, 2)
     sc = torch.matmul(f, r.transpose(-1, -2)) * (1.0 / math.sqrt(f.shape[-1]))
     nb = r.shape[2]
     if causal:
         tq = f.shape[2]
-        fut = torch.arange(nb).view(1, 1, 1, nb) > (torch.arange(tq).view(1, 1, tq, 1) // bs)
+        fut = torch.arange(nb).view(1, 1, 1, nb) > ((torch.arange(tq).view(1, 1, tq, 1) + query_pos0) // bs)
         sc = sc.masked_fill(fut, float("-inf"))
     return sc, torch.topk(sc, k=min(top_k, nb), dim=-1).indices
 
@@ -86,10 +88,12 @@ def sparse_prefill(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
 
 
 def sparse_decode(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor, S: int,
-                  forecast: Optional[torch.Tensor], bs: int, top_k: int):
+                  forecast: Optional[torch.Tensor], bs: int, top_k: int, routing: str = "reference"):
     """xq [B,Hq,1,D], xk/xv [B,Hkv,S,D] (S includes the new token), forecast
     [B,1,Hkv,Df] -> (out [B,1,Hq*D], selected block indices [B,Hkv,m],
-    validity [B,Hkv,m])."""
+    validity [B,Hkv,m]). routing "reference" masks the scores at row 0 as
+    sparse.py:139 does; "absolute" at the query's position S - 1 (the same
+    operations, another mask row)."""
     B, Hq, _, D = xq.shape
     Hkv = xk.shape[1]
     rep = Hq // Hkv
@@ -106,7 +110,8 @@ def sparse_decode(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor, S: int,
     mark[:, :, cb] = True
     if forecast is not None:
         reps = block_means(xk.transpose(1, 2), bs)
-        _, top = select_blocks(forecast, reps, bs, top_k, causal=True)
+        _, top = select_blocks(forecast, reps, bs, top_k, causal=True,
+                               query_pos0=S - 1 if routing == "absolute" else 0)
         mark.scatter_(-1, top[:, :, 0, :].clamp(0, nb - 1), True)
     else:
         mark[:, :, max(0, cb - top_k + 1):cb + 1] = True

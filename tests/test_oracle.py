@@ -344,6 +344,17 @@ def test_decode_matches_reference_restatement_on_its_selection():
             assert 0 in s and cb in s and len(s) <= k + 2
     got = O.attention_decode(q, kc, vc, S, sel, n, bs)
     np.testing.assert_allclose(got, out.reshape(B, Hq * D).numpy(), atol=1e-12)
+    # absolute routing masks at the query's position: no -inf ties among the
+    # 19 causal blocks, so the restatement's selection is the oracle's
+    out, idx, valid = R.sparse_decode(t(q)[:, :, None], t(kc).transpose(1, 2), t(vc).transpose(1, 2), S,
+                                      t(f), bs, k, routing="absolute")
+    sel_o, n_o, _ = O.decode_selection(kc, S, f[:, 0], bs, k, "absolute")
+    for b in range(B):
+        for g in range(Hkv):
+            s = sorted(int(j) for j, ok in zip(idx[b, g], valid[b, g]) if ok)
+            assert s == list(sel_o[b, g, :n_o[b, g]])
+    got = O.attention_decode(q, kc, vc, S, sel_o, n_o, bs)
+    np.testing.assert_allclose(got, out.reshape(B, Hq * D).numpy(), atol=1e-12)
 
 
 # ---------------------------------------------------------------------------
