@@ -308,7 +308,7 @@ def bench_offload(args, torch, sparda, synth):
     from model.model import SparDAResearchModel
     dev = torch.device("cuda")
     W, K = 4, args.offload_steps
-    cap = OB_CTX + 6 * (W + K) + 64
+    cap = OB_CTX + 8 * (W + K) + 64
     cfg = ModelConfig(n_layer=OB_LAYERS, context_length=cap, block_size=BS, top_k_blocks=TOPK,
                       decode_routing="absolute", attention_backend="async_offload", norm_eps=1e-5)
     torch.manual_seed(1004)
@@ -330,7 +330,7 @@ def bench_offload(args, torch, sparda, synth):
             res_caches[li].update(kd, vd)
     torch.cuda.synchronize()
     g = torch.Generator().manual_seed(1006)
-    ids = torch.randint(0, cfg.vocab_size, (6 * (W + K), 1, 1), generator=g).to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (8 * (W + K), 1, 1), generator=g).to(dev)
     it = iter(range(ids.shape[0]))
 
     def run(m, caches, n):
@@ -372,6 +372,16 @@ def bench_offload(args, torch, sparda, synth):
     # same caches, synchronous offload (select + fetch on the compute stream)
     us_sync = timed(syncm, off_caches)
     us_res = timed(resident, res_caches)
+    # the fetch as DMA copies (hipMemcpyAsync per run of consecutive blocks;
+    # the host waits for the selection once per fetch), async and sync
+    for m_ in (model, syncm):
+        for layer in m_.layers[1:]:
+            layer.attention.fetch_method = sparda.FETCH_DMA
+    us_async_dma = timed(model, off_caches)
+    us_sync_dma = timed(syncm, off_caches)
+    for m_ in (model, syncm):
+        for layer in m_.layers[1:]:
+            layer.attention.fetch_method = sparda.FETCH_KERNEL
 
     def graph_step_us(m, caches, reps=50):
         """One decode step captured in a HIP graph at a fixed position (each
@@ -451,6 +461,8 @@ def bench_offload(args, torch, sparda, synth):
                     "stream; step = one token through the 12-layer model incl. LM head",
         "us_per_step_async": round(us_async, 1),
         "us_per_step_sync": round(us_sync, 1),
+        "us_per_step_async_dma": round(us_async_dma, 1),
+        "us_per_step_sync_dma": round(us_sync_dma, 1),
         "us_per_step_gpu_resident": round(us_res, 1),
         "us_per_step_gpu_resident_graph": round(us_res_graph, 1),
         "us_per_step_cached_prototypes": round(us_proto_eager, 1),
@@ -868,7 +880,8 @@ def main():
         f"cached prototypes {off['us_per_step_cached_prototypes']:.1f}, graph "
         f"{off['us_per_step_cached_prototypes_graph']:.1f}); async graph {off['us_per_step_async_graph']:.1f} "
         f"(serial prefetch {off['us_per_step_async_graph_serial_prefetch']:.1f}); overlap {off['overlap']}, "
-        f"transfer {off['transfer_us_per_layer']} us/layer, link {off['host_link_gbs']} GB/s")
+        f"transfer {off['transfer_us_per_layer']} us/layer, link {off['host_link_gbs']} GB/s; DMA fetch: async "
+        f"{off['us_per_step_async_dma']:.1f}, sync {off['us_per_step_sync_dma']:.1f}")
     log("12-layer forward workload")
     mdl = bench_model(args, torch, sparda, synth)
     log(f"model: {mdl['ms_per_forward']:.2f} ms per {MT}-token forward ({mdl['tok_s']:.0f} tok/s), "
