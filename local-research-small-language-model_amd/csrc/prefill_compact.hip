@@ -11,7 +11,7 @@
 //     P = exp2(S^T * scale * log2 e - m_ref[col])            (VALU, bf16)
 //     O^T[d, slot]  += V^T[d, key] . P^T[key, slot]          (8 MFMA, C = acc)
 // so a tile wastes only its padding slots (and the masked half of the causal
-// diagonal block, whose key sub-tiles past the tile's last token are skipped).
+// diagonal block).
 //
 // Accumulation. P is taken against a fixed per-column reference m_ref: the
 // column maximum of the column's first selected block (its smallest block,
@@ -332,7 +332,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 
         Slot sl[kCChunk];
         u32x4 qa[kCChunk], qc[kCChunk];
-        int rank[kCChunk], thi[kCChunk];
+        int rank[kCChunk];
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
@@ -340,25 +340,22 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 qa[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff);
                 qc[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff + 32);
                 rank[t] = sm.rankbuf[rofs + sl[t].tr];
-                // causal diagonal: key sub-tiles past the tile's last token are all masked
-                const int last = 16 * (i0 + t) + 15 < ncol ? 16 * (i0 + t) + 15 : ncol - 1;
-                thi[t] = diag ? __builtin_amdgcn_readfirstlane(trk[last / R]) : 63;
             }
         }
-        // S^T = K Q^T for every tile
+        // S^T = K Q^T for every tile (every key sub-tile: on the causal
+        // diagonal the masks below remove what lies past a column's token;
+        // skipping those sub-tiles costs more in branches than it saves)
         f32x4 s[kCChunk][4];
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
 #pragma unroll
                 for (int n = 0; n < 4; ++n) {
-                    s[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    if (16 * n <= thi[t]) {
-                        s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n]),
-                                                                          __builtin_bit_cast(bf16x8, qa[t]), s[t][n], 0, 0, 0);
-                        s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n + 1]),
-                                                                          __builtin_bit_cast(bf16x8, qc[t]), s[t][n], 0, 0, 0);
-                    }
+                    s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n]),
+                                                                      __builtin_bit_cast(bf16x8, qa[t]),
+                                                                      f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n + 1]),
+                                                                      __builtin_bit_cast(bf16x8, qc[t]), s[t][n], 0, 0, 0);
                 }
             }
         }
@@ -464,20 +461,17 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
-                const bool upper = thi[t] >= 32;  // keys 32..63 can hold allowed keys
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) {
                     o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[t][0]),
                                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    if (upper)
-                        o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[t][1]),
-                                                                           o[t][dt], 0, 0, 0);
+                    o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[t][1]),
+                                                                       o[t][dt], 0, 0, 0);
                 }
                 ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][0]),
                                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                if (upper)
-                    ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][1]), ol[t],
-                                                                    0, 0, 0);
+                ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][1]), ol[t],
+                                                                0, 0, 0);
             }
         }
         // add into every column after its earlier blocks (read-add-write, in block order)
