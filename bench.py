@@ -94,8 +94,8 @@ def load_traffic():
         return {}
 
 
-def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001):
-    """One sparse prefill layer at [B, T] (12/4 heads, D 64, block 64, top-8):
+def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK=TOPK):
+    """One sparse prefill layer at [B, T] (12/4 heads, D 64, block BS, top-TOPK):
     eager steps with events around each launch, then the step replayed from a
     HIP graph."""
     x = synth.prefill_inputs(B, T, HQ, HKV, D, dtype=torch.bfloat16, seed=seed, device="cuda")
@@ -869,6 +869,9 @@ def main():
     p16 = bench_prefill(args, torch, sparda, synth, B=1, T=MT, seed=1003)
     log(f"prefill 16K: {p16['ms_per_step']:.3f} ms/step, attention {p16['attn_ms']*1e3:.1f} us "
         f"({p16['attn_tflops']:.1f} TFLOP/s useful)")
+    log("prefill with the reference's default block configuration (32-key blocks, top-4)")
+    p32 = bench_prefill(args, torch, sparda, synth, BS=32, TOPK=4)
+    log(f"prefill bs=32 k=4: {p32['ms_per_step']:.3f} ms/step, attention {p32['attn_ms']*1e3:.1f} us")
     log("decode workload")
     dec = bench_decode(args, torch, sparda, synth)
     log(f"decode: {dec['us_per_step']:.2f} us/step ({dec['gbs']:.0f} GB/s), eager {dec['us_per_step_eager']:.2f}; "
@@ -946,6 +949,15 @@ def main():
                          "traffic": traffic.get("prefill_attention_16k")},
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16.items()
                if k not in ("ms_per_step", "tok_s")},
+        },
+        "prefill_block32": {
+            "workload": f"the prefill layer at B={PB}, T={PT} with the reference's default block configuration "
+                        "(configs/base.yaml: 32-key blocks, top-4; 128 blocks), same step",
+            "ms_per_step": round(p32["ms_per_step"], 4),
+            "tok_s": round(p32["tok_s"], 1),
+            "attn_us": round(p32["attn_ms"] * 1e3, 1),
+            "attn_tflops": round(p32["attn_tflops"], 2),
+            "attn_useful_flop": p32["attn_useful_flop"],
         },
         "decode": {
             "workload": "decode step @16K: B=8, KV cache [8,16384,4,64] bf16, 256 blocks, top-8 + sink + "

@@ -1,5 +1,5 @@
-// bf16 block-sparse GQA prefill over compacted tiles (D = 64, bs = 64,
-// at most 10 selected blocks per token).
+// bf16 block-sparse GQA prefill over compacted tiles (D = 64, KV blocks of
+// BS = 64 or 32 keys, at most 10 selected blocks per token).
 //
 // One workgroup (4 wavefronts) serves one (sequence b, KV head g, query block
 // qb): 64 query tokens x R = Hq/Hkv query heads = 64R columns, column
@@ -78,14 +78,21 @@ __device__ __forceinline__ int swz(int r) { return 2 * ((r >> 1) & 3); }
 // element index of (local row r, element col) in a swizzled V half-stage
 __device__ __forceinline__ int vidx(int r, int col) { return r * 64 + (((col >> 3) ^ swz(r)) << 3) + (col & 7); }
 
+// maximum of a tile column's scores held by this lane (never NaN)
+__device__ __forceinline__ float max_sub_nn(const f32x4 (&s)[4]) { return max16_nn(s); }
+__device__ __forceinline__ float max_sub_nn(const f32x4 (&s)[2]) {
+    return max_nn(max3_nn(max3_nn(s[0][0], s[0][1], s[0][2]), max3_nn(s[0][3], s[1][0], s[1][1]), s[1][2]), s[1][3]);
+}
+
 __device__ __forceinline__ float key_to_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 }  // namespace
 
-// two workgroups per CU for R <= 3 (their LDS fits twice); one for R = 4
-template <int R>
+// two workgroups per CU for R <= 3 (their LDS fits twice); one for R = 4.
+// BS: keys per KV block (64 or 32); the query window is 64 tokens either way.
+template <int R, int BS>
 __global__ void __launch_bounds__(kCT, R <= 3 ? 2 : 1)
 prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                        const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -109,10 +116,14 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     const int64_t qb = NBq - 1 - blockIdx.x / BH;
     const int b = static_cast<int>(bg / H);
     const int g = static_cast<int>(bg % H);
-    const int64_t t0 = qb * 64;
-    const int64_t NB = cdiv(T, 64);
-    const int t_valid = static_cast<int>(T - t0 < 64 ? T - t0 : 64);
-    const int jmax = static_cast<int>(causal ? qb : NB - 1);  // highest block a token here may attend
+    static_assert(BS == 64 || BS == 32, "KV blocks of 64 or 32 keys");
+    constexpr int kSub = BS / 16;  // 16-key sub-tiles of a block (the M side of S^T)
+    constexpr int kHalf = BS / 32; // 32-key halves of a block (the K side of O^T)
+    const int64_t t0 = qb * kCWin;
+    const int64_t NB = cdiv(T, BS);
+    const int t_valid = static_cast<int>(T - t0 < kCWin ? T - t0 : kCWin);
+    // highest block a token here may attend
+    const int jmax = static_cast<int>(causal ? (t0 + t_valid - 1) / BS : NB - 1);
     const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const uint16_t* qbase = q + b * q_sb + t0 * q_st + static_cast<int64_t>(g * R) * q_sh;
@@ -134,8 +145,10 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         for (int i = 0; i < kCMaxCap; ++i) raw[i] = i < cap ? row[i] : -1;  // issued with the count's load
         const int64_t nr = n_sel[r];
         const int n = static_cast<int>(nr < 0 ? 0 : (nr > cap ? cap : nr));
+        // blocks past the token's own (no key of theirs is allowed) are dropped
+        const int tlim = static_cast<int>(causal ? (t0 + tid) / BS : NB - 1);
 #pragma unroll
-        for (int i = 0; i < kCMaxCap; ++i) lst[i] = (i < n && raw[i] >= 0 && raw[i] <= jmax) ? raw[i] : kSentinel;
+        for (int i = 0; i < kCMaxCap; ++i) lst[i] = (i < n && raw[i] >= 0 && raw[i] <= tlim) ? raw[i] : kSentinel;
         // ascending, repeats dropped (odd-even transposition sort, twice)
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
@@ -234,6 +247,8 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
     // per-lane element offsets inside a block: K A operand (key 16n + col16,
     // dims 32kk + 8grp), V rows (chunk lane + 64i: row lane/8 + 8i, 16-byte column lane%8)
+    constexpr int kKR = 2 * kSub;  // K operand registers (u32x4) per block
+    constexpr int kVR = BS / 8;    // V row chunks (u32x4) per lane per block
     const int koff = col16 * kv_st32 + 8 * grp;
     const int voff = (lane / 8) * kv_st32 + (lane % 8) * 8;
     const int64_t last_row = T - 1;
@@ -244,18 +259,18 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         return __builtin_amdgcn_readfirstlane(it);
     };
     // rows past T (a ragged last block) read row T-1: finite values, masked
-    auto load_k = [&](int item, u32x4 (&kr)[8]) __attribute__((always_inline)) {
-        const int64_t r0 = static_cast<int64_t>(sm.ulist[item & 0xffff]) * 64;
-        if (r0 + 64 <= T) {
+    auto load_k = [&](int item, u32x4 (&kr)[kKR]) __attribute__((always_inline)) {
+        const int64_t r0 = static_cast<int64_t>(sm.ulist[item & 0xffff]) * BS;
+        if (r0 + BS <= T) {
             const uint16_t* blk = kbase + r0 * kv_st;
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+            for (int n = 0; n < kSub; ++n)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk)
                     kr[2 * n + kk] = *reinterpret_cast<const u32x4*>(blk + koff + 16 * n * kv_st32 + 32 * kk);
         } else {
 #pragma unroll
-            for (int n = 0; n < 4; ++n) {
+            for (int n = 0; n < kSub; ++n) {
                 int64_t row = r0 + 16 * n + col16;
                 row = row < last_row ? row : last_row;
 #pragma unroll
@@ -264,15 +279,15 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             }
         }
     };
-    auto load_v = [&](int item, u32x4 (&vr)[8]) __attribute__((always_inline)) {
-        const int64_t r0 = static_cast<int64_t>(sm.ulist[item & 0xffff]) * 64;
-        if (r0 + 64 <= T) {
+    auto load_v = [&](int item, u32x4 (&vr)[kVR]) __attribute__((always_inline)) {
+        const int64_t r0 = static_cast<int64_t>(sm.ulist[item & 0xffff]) * BS;
+        if (r0 + BS <= T) {
             const uint16_t* blk = vbase + r0 * kv_st;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const u32x4*>(blk + voff + 8 * i * kv_st32);
+            for (int i = 0; i < kVR; ++i) vr[i] = *reinterpret_cast<const u32x4*>(blk + voff + 8 * i * kv_st32);
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kVR; ++i) {
                 int64_t row = r0 + lane / 8 + 8 * i;
                 row = row < last_row ? row : last_row;
                 vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * kv_st + (lane % 8) * 8);
@@ -315,7 +330,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     // mode 0: P against the column's reference, which the column's first block
     //         sets to its own column maximum; 1: scores only, exact column
     //         maxima; 2: P against the exact maxima of mode 1
-    auto process = [&](int item, u32x4 (&kr)[8], u32x4 (&vr)[8], int nxt, int mode) __attribute__((always_inline)) {
+    auto process = [&](int item, u32x4 (&kr)[kKR], u32x4 (&vr)[kVR], int nxt, int mode) __attribute__((always_inline)) {
         const int u = item & 0xffff;
         const int i0 = item >> 16;
         const int j = sm.ulist[u];
@@ -326,9 +341,12 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         const int rofs = sm.uofs[u];
         if ((M >> lane) & 1ull) trk[__popcll(M & below)] = static_cast<uint8_t>(lane);
         __builtin_amdgcn_wave_barrier();
-        const bool diag = causal && j == qb;
-        const int lim_tail = (!causal && (static_cast<int64_t>(j) + 1) * 64 > T) ? static_cast<int>(T - j * 64LL) : 64;
-        const bool masked = diag || lim_tail < 64;  // causal diagonal or ragged tail block
+        // causal: a block that ends past the window's first token holds keys
+        // beyond some selecting tokens (key j*BS + i is allowed up to token t0 + tk)
+        const bool diag = causal && (static_cast<int64_t>(j) + 1) * BS - 1 > t0;
+        const int dbase = static_cast<int>(t0 - static_cast<int64_t>(j) * BS);
+        const int lim_tail = (!causal && (static_cast<int64_t>(j) + 1) * BS > T) ? static_cast<int>(T - j * static_cast<int64_t>(BS)) : BS;
+        const bool masked = diag || lim_tail < BS;  // causal diagonal or ragged tail block
 
         Slot sl[kCChunk];
         u32x4 qa[kCChunk], qc[kCChunk];
@@ -345,12 +363,12 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         // S^T = K Q^T for every tile (every key sub-tile: on the causal
         // diagonal the masks below remove what lies past a column's token;
         // skipping those sub-tiles costs more in branches than it saves)
-        f32x4 s[kCChunk][4];
+        f32x4 s[kCChunk][kSub];
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
 #pragma unroll
-                for (int n = 0; n < 4; ++n) {
+                for (int n = 0; n < kSub; ++n) {
                     s[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * n]),
                                                                       __builtin_bit_cast(bf16x8, qa[t]),
                                                                       f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -361,9 +379,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         }
         load_k(nxt, kr);  // the next item's K operands, in flight from here
         // V^T operands: stage each half of the block, read it transposed
-        bf16x8 va[4][2];
+        bf16x8 va[4][kHalf];
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
+        for (int m = 0; m < kHalf; ++m) {
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -383,16 +401,16 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 
         // masks, references, P
         bool own[kCChunk];
-        uint4 pw[kCChunk][2];
+        uint4 pw[kCChunk][kHalf];
         bool any_first = false, any_later = false;
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
                 own[t] = sl[t].valid && grp == 0;
                 if (masked) {
-                    const int lim = diag ? sl[t].c / R : lim_tail - 1;  // keys <= lim are allowed
+                    const int lim = diag ? dbase + sl[t].c / R : lim_tail - 1;  // keys <= lim are allowed
 #pragma unroll
-                    for (int n = 0; n < 4; ++n)
+                    for (int n = 0; n < kSub; ++n)
 #pragma unroll
                         for (int ii = 0; ii < 4; ++ii)
                             if (16 * n + 4 * grp + ii > lim) s[t][n][ii] = -__builtin_inff();
@@ -406,7 +424,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 #pragma unroll
             for (int t = 0; t < kCChunk; ++t) {
                 if (t < nt) {
-                    const float x = max16_nn(s[t]);
+                    const float x = max_sub_nn(s[t]);
                     cm[t] = pair32_max(pair16_max(x)) * scale_log2;
                 }
             }
@@ -443,7 +461,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 if (first && own[t]) sm.mref[sl[t].c] = m;
                 const float neg = sl[t].valid ? -m : -__builtin_inff();
 #pragma unroll
-                for (int mm = 0; mm < 2; ++mm) {
+                for (int mm = 0; mm < kHalf; ++mm) {
                     bf16x8 pb;
 #pragma unroll
                     for (int ii = 0; ii < 4; ++ii) {
@@ -465,13 +483,17 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 for (int dt = 0; dt < 4; ++dt) {
                     o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[t][0]),
                                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[t][1]),
-                                                                       o[t][dt], 0, 0, 0);
+#pragma unroll
+                    for (int mm = 1; mm < kHalf; ++mm)
+                        o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            va[dt][mm], __builtin_bit_cast(bf16x8, pw[t][mm]), o[t][dt], 0, 0, 0);
                 }
                 ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][0]),
                                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][1]), ol[t],
-                                                                0, 0, 0);
+#pragma unroll
+                for (int mm = 1; mm < kHalf; ++mm)
+                    ol[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[t][mm]),
+                                                                    ol[t], 0, 0, 0);
             }
         }
         // add into every column after its earlier blocks (read-add-write, in block order)
@@ -523,7 +545,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         auto word = [&](int idx, int fallback) -> int {
             return idx < n_items ? static_cast<int>(sm.items[idx]) : fallback;
         };
-        u32x4 kr[8], vr[8];
+        u32x4 kr[kKR], vr[kVR];
         int cur_i = grab();
         if (cur_i >= n_items) return;
         int cur = word(cur_i, 0);
@@ -591,8 +613,8 @@ bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, in
                                const int32_t* sel, int64_t cap, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st,
                                const void* q, const void* k, const void* v, const void* out) {
-    if (dtype != SPARDA_BF16 || D != 64 || bs != 64 || sel == nullptr) return false;
-    if (cap < 1 || cap > kCMaxCap || cdiv(T, 64) > kCMaxNB) return false;
+    if (dtype != SPARDA_BF16 || D != 64 || (bs != 64 && bs != 32) || sel == nullptr) return false;
+    if (cap < 1 || cap > kCMaxCap || cdiv(T, bs) > kCMaxNB) return false;
     if (Hq % Hkv != 0) return false;
     const int64_t R = Hq / Hkv;
     if (R < 1 || R > 4) return false;
@@ -608,14 +630,16 @@ bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, in
 int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
                            const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
                            const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
-                           int64_t Hq, int64_t Hkv, int causal, float scale, void* out,
+                           int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale, void* out,
                            int64_t out_sb, int64_t out_st, hipStream_t stream) {
-    const int64_t NBq = cdiv(T, 64);
+    const int64_t NBq = cdiv(T, kCWin);  // query windows per (sequence, KV head)
     const int64_t R = Hq / Hkv;
     dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
     const float sl = scale * kCLog2e;
 #define SPARDA_PC(R_)                                                                                        \
-    hipLaunchKernelGGL((prefill_compact_kernel<R_>), grid, dim3(kCT), 0, stream,                             \
+    if (bs == 32) SPARDA_PCB(R_, 32); else SPARDA_PCB(R_, 64)
+#define SPARDA_PCB(R_, BS_)                                                                                  \
+    hipLaunchKernelGGL((prefill_compact_kernel<R_, BS_>), grid, dim3(kCT), 0, stream,                        \
                        static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k),    \
                        static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, sel, n_sel, cap, T,              \
                        static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st)
@@ -625,6 +649,7 @@ int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_
         case 3: SPARDA_PC(3); break;
         default: SPARDA_PC(4); break;
     }
+#undef SPARDA_PCB
 #undef SPARDA_PC
     return check_hip(hipGetLastError(), "prefill_compact_kernel");
 }

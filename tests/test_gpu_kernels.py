@@ -288,16 +288,39 @@ def test_prefill_topk_covering_all_blocks_equals_dense():
     assert (a.float() - b.float()).abs().max().item() <= 2e-2
 
 
-def test_prefill_is_deterministic():
+@pytest.mark.parametrize("bs", [64, 32])
+def test_prefill_is_deterministic(bs):
     # columns receive their blocks' contributions in block order whatever the
     # timing of the wavefronts: repeated launches agree bit for bit
-    case("prefill repeat B=4 T=4096")
+    case(f"prefill repeat B=4 T=4096 bs={bs}")
     x = synth.prefill_inputs(4, 4096, 12, 4, 64, dtype=torch.bfloat16, seed=1001)
     d = {n: t.to(DEV) for n, t in x.items()}
-    _, _, sel, n = sparda.route(d["forecast"], sparda.compress(d["k"], 64), 64, 8, want_topk=False, want_sel=True)
-    a = sparda.prefill(d["q"], d["k"], d["v"], sel, n, 64)
+    k = 8 if bs == 64 else 4
+    _, _, sel, n = sparda.route(d["forecast"], sparda.compress(d["k"], bs), bs, k, want_topk=False, want_sel=True)
+    a = sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs)
     for _ in range(3):
-        assert torch.equal(sparda.prefill(d["q"], d["k"], d["v"], sel, n, 64), a)
+        assert torch.equal(sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs), a)
+
+
+@pytest.mark.parametrize("R", [1, 3, 4])
+def test_prefill_block32_reference_default_config(R):
+    # the reference's default configuration (configs/base.yaml:19-20): blocks of
+    # 32 keys, top-4, on the matrix-core kernel; ragged T, causal and not
+    case(f"prefill bs=32 k=4 R={R} T=1000")
+    _prefill_case(2, 1000, 4 * R, 4, 64, 32, 4, torch.bfloat16, seed=80 + R)
+    _prefill_case(1, 777, 4 * R, 4, 64, 32, 4, torch.bfloat16, seed=90 + R, causal=False)
+
+
+def test_prefill_block32_full_size_sampled_rows_and_dense():
+    # B=4, T=4096 with 32-key blocks (128 blocks), top-4 and top-8, sampled rows;
+    # the dense step (no lists) with bs=32 equals the dense oracle
+    case("prefill B=4 T=4096 bs=32 sampled")
+    r = np.random.default_rng(3)
+    rows = sorted({(int(b), int(t)) for b, t in zip(r.integers(0, 4, 256), r.integers(0, 4096, 256))})
+    rows += [(b, t) for b in range(4) for t in (0, 31, 32, 63, 64, 4095)]
+    _prefill_case(4, 4096, 12, 4, 64, 32, 4, torch.bfloat16, seed=1001, rows=rows)
+    _prefill_case(4, 4096, 12, 4, 64, 32, 8, torch.bfloat16, seed=1001, rows=rows)
+    _prefill_case(1, 700, 12, 4, 64, 32, 4, torch.bfloat16, seed=64, dense=True)
 
 
 def _lists(rows, B, Hkv, T, cap):
@@ -326,11 +349,13 @@ def _clean(sel, n, T, bs, causal):
     return out, no
 
 
-def test_prefill_irregular_selection_lists():
+@pytest.mark.parametrize("bs", [64, 32])
+def test_prefill_irregular_selection_lists(bs):
     # unsorted lists, repeats, negative and future entries, lists without the sink
-    # or the own block (the reference maximum then comes from another allowed key)
-    case("prefill irregular lists T=640")
-    B, T, Hq, Hkv, bs, cap = 1, 640, 12, 4, 64, 10
+    # or the own block (the reference maximum then comes from another allowed key);
+    # with 32-key blocks a future block can lie inside the token's 64-token window
+    case(f"prefill irregular lists T=640 bs={bs}")
+    B, T, Hq, Hkv, cap = 1, 640, 12, 4, 10
     x = synth.prefill_inputs(B, T, Hq, Hkv, 64, dtype=torch.bfloat16, seed=91)
     rng = np.random.default_rng(91)
     rows = {}
