@@ -144,7 +144,7 @@ constexpr int kAttendMaxWaves = 12;
 // wave's LDS region, read transposed), row sums on the matrix cores.
 constexpr int kDVRow = 80;  // V row in LDS for the matrix-core path, bf16 elements
 
-template <int DT, int DH, int CH, bool MF>
+template <int DT, int DH, int CH, bool MF, int MBS = 64>
 __global__ void __launch_bounds__(kAttendMaxWaves * 64)
 decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      const void* __restrict__ kc, const void* __restrict__ vc,
@@ -317,7 +317,11 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
         static_assert(DH == 64, "matrix-core decode path is for head dim 64");
         const int col16 = lane % 16;
         const int grp = lane / 16;
-        constexpr int kBs = 64;
+        constexpr int kBs = MBS;           // keys per block: 64 or 32
+        constexpr int kSub = kBs / 16;     // 16-key sub-tiles (the M side of S^T)
+        constexpr int kHalf = kBs / 32;    // 32-key halves (the K side of O^T)
+        constexpr int kVC = kBs / 8;       // 16-byte V chunks per lane
+        static_assert(kBs == 64 || kBs == 32, "matrix-core decode: blocks of 64 or 32 keys");
         constexpr float kLazy = 8.0f;
         uint16_t* vt = reinterpret_cast<uint16_t*>(wbase);  // [64][kDVRow]
         const uint16_t* qh = static_cast<const uint16_t*>(q);
@@ -358,18 +362,18 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             // the same chunk column lane%8 for every i); rows past S repeat row nk-1
             // (finite values; their P is 0)
             const uint16_t* vrow0 = vh + base + (lane % 8) * 8;
-            uint4 vr[8];
+            uint4 vr[kVC];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kVC; ++i) {
                 int r = (lane + 64 * i) / 8;
                 r = r < nk ? r : nk - 1;
                 vr[i] = *reinterpret_cast<const uint4*>(vrow0 + r * kv_ss);
             }
             // K A operands: key 16n + col16, dims 32kk + 8grp .. +7
             const uint16_t* krow0 = kh + base + 8 * grp;
-            bf16x8 ka[4][2];
+            bf16x8 ka[kSub][2];
 #pragma unroll
-            for (int nn = 0; nn < 4; ++nn) {
+            for (int nn = 0; nn < kSub; ++nn) {
                 int r = 16 * nn + col16;
                 r = r < nk ? r : nk - 1;
 #pragma unroll
@@ -381,7 +385,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 const bf16x8 kn0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(knh + nbase + 8 * grp));
                 const bf16x8 kn1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(knh + nbase + 32 + 8 * grp));
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
+                for (int i = 0; i < kVC; ++i) {
                     // compare the clamped row: rows past S were read from row nk-1
                     int r = (lane + 64 * i) / 8;
                     r = r < nk ? r : nk - 1;
@@ -392,7 +396,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                     vr[i].w = hit ? vn.w : vr[i].w;
                 }
 #pragma unroll
-                for (int nn = 0; nn < 4; ++nn) {
+                for (int nn = 0; nn < kSub; ++nn) {
                     int r = 16 * nn + col16;
                     r = r < nk ? r : nk - 1;
                     const bool hit = r == rnew;
@@ -402,26 +406,26 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             }
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kVC; ++i) {
                 const int c = lane + 64 * i;
                 *reinterpret_cast<uint4*>(vt + (c / 8) * kDVRow + (c % 8) * 8) = vr[i];
             }
             __builtin_amdgcn_wave_barrier();
-            f32x4 sc[4];
+            f32x4 sc[kSub];
 #pragma unroll
-            for (int nn = 0; nn < 4; ++nn) {
+            for (int nn = 0; nn < kSub; ++nn) {
                 sc[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
                 sc[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[nn][0], qb0, sc[nn], 0, 0, 0);
                 sc[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[nn][1], qb1, sc[nn], 0, 0, 0);
             }
-            bf16x8 va[4][2];
+            bf16x8 va[4][kHalf];
             {
                 const int rsub = 4 * grp + col16 / 4;
                 const int csub = 4 * (col16 % 4);
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                    for (int mm = 0; mm < 2; ++mm) {
+                    for (int mm = 0; mm < kHalf; ++mm) {
                         const uint16_t* vb = vt + (32 * mm + rsub) * kDVRow + 16 * dt + csub;
                         const i16x4 lo = lds_read_tr(vb);
                         const i16x4 hi = lds_read_tr(vb + 16 * kDVRow);
@@ -430,20 +434,20 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             }
             if (nk < kBs) {
 #pragma unroll
-                for (int nn = 0; nn < 4; ++nn)
+                for (int nn = 0; nn < kSub; ++nn)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         if (16 * nn + 4 * grp + i >= nk) sc[nn][i] = -__builtin_inff();
             }
-            float mx = max16_nn(sc);
+            float mx = max_sub_nn(sc);
             mx = pair32_max(pair16_max(mx));
             const float cand = mx * scale_log2;
             const float m_new = cand > m_run + kLazy ? cand : m_run;
             const float alpha = m_new != m_run ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
             m_run = m_new;
-            uint4 pw[2];
+            uint4 pw[kHalf];
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm) {
+            for (int mm = 0; mm < kHalf; ++mm) {
                 bf16x8 pb;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -458,12 +462,14 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                 ol *= alpha;
             }
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[0]), o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]), o[dt], 0, 0, 0);
-            }
-            ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[0]), ol, 0, 0, 0);
-            ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[1]), ol, 0, 0, 0);
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int mm = 0; mm < kHalf; ++mm)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][mm], __builtin_bit_cast(bf16x8, pw[mm]), o[dt],
+                                                                    0, 0, 0);
+#pragma unroll
+            for (int mm = 0; mm < kHalf; ++mm)
+                ol = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[mm]), ol, 0, 0, 0);
             __builtin_amdgcn_wave_barrier();  // the next block overwrites vt
         }
         // the wave's partial of head col16: m (log2 units), l (lane group 0, element 0), o[16dt+4grp+i]
@@ -688,7 +694,7 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     // most blocks one workgroup can attend: the selection capacity, or every block when dense
     const int64_t max_blocks = a.sel_mode == 1 ? NB : a.cap;
     // matrix-core block attention: bf16, D = 64, bs = 64, 16-byte aligned q rows
-    const bool mf = a.dtype == SPARDA_BF16 && a.D == 64 && a.bs == 64 && (a.q_sb % 8) == 0 &&
+    const bool mf = a.dtype == SPARDA_BF16 && a.D == 64 && (a.bs == 64 || a.bs == 32) && (a.q_sb % 8) == 0 &&
                     (a.q_sh % 8) == 0 && (reinterpret_cast<uintptr_t>(a.q) & 15u) == 0;
     constexpr size_t kLdsBudget = 150 * 1024;
     const int pow2 = (a.bs & (a.bs - 1)) == 0 ? 1 : 0;
@@ -697,13 +703,14 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     do {                                                                                                 \
         if constexpr (DT_ == SPARDA_BF16 && DH_ == 64) {                                                 \
             if (mf) {                                                                                    \
-                SPARDA_ATT_K(DT_, DH_, CH_, true);                                                       \
+                if (a.bs == 32) SPARDA_ATT_K(DT_, DH_, CH_, true, 32);                                   \
+                else SPARDA_ATT_K(DT_, DH_, CH_, true, 64);                                              \
                 break;                                                                                   \
             }                                                                                            \
         }                                                                                                \
-        SPARDA_ATT_K(DT_, DH_, CH_, false);                                                              \
+        SPARDA_ATT_K(DT_, DH_, CH_, false, 64);                                                          \
     } while (0)
-#define SPARDA_ATT_K(DT_, DH_, CH_, MF_)                                                                 \
+#define SPARDA_ATT_K(DT_, DH_, CH_, MF_, MBS_)                                                           \
     do {                                                                                                 \
         const size_t wb = attend_wave_bytes<DT_, DH_>();                                                 \
         const size_t pb = static_cast<size_t>(R) * (DH_ + 2) * 4;                                        \
@@ -711,7 +718,7 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
         while (waves > 1 && ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb > kLdsBudget) --waves; \
         size_t lds = ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb;                        \
         if (a.sel_mode == 4 && lds < static_cast<size_t>(NB) * 4) lds = static_cast<size_t>(NB) * 4;       \
-        hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_, MF_>), grid2, dim3(waves * kWave), lds, stream, \
+        hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_, MF_, MBS_>), grid2, dim3(waves * kWave), lds, stream, \
                            a.q, a.q_sb, a.q_sh, a.kc, a.vc, a.kv_sb, a.kv_ss, a.kv_sh, a.S, Hq_i, Hkv_i,  \
                            static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \

@@ -52,6 +52,14 @@ __device__ __forceinline__ float max16_nn(const f32x4 (&s)[4]) {
     const float e = max3_nn(s[3][0], s[3][1], s[3][2]);
     return max_nn(max3_nn(a, b, c), max3_nn(d, e, s[3][3]));
 }
+// max of the 8 accumulator values s[0..1][0..3] (a 32-key block): 4 instructions
+__device__ __forceinline__ float max8_nn(const f32x4 (&s)[2]) {
+    return max_nn(max3_nn(max3_nn(s[0][0], s[0][1], s[0][2]), max3_nn(s[0][3], s[1][0], s[1][1]), s[1][2]), s[1][3]);
+}
+// the maximum of a lane's scores of one block: 4 sub-tiles of 16 keys (64-key
+// block) or 2 (32-key block)
+__device__ __forceinline__ float max_sub_nn(const f32x4 (&s)[4]) { return max16_nn(s); }
+__device__ __forceinline__ float max_sub_nn(const f32x4 (&s)[2]) { return max8_nn(s); }
 // max with the lane 16 (SWAP16) or 32 lanes away. One asm block: a VALU write
 // of a register needs two wait states before a permlane swap reads it, and the
 // compiler does not count inline-assembly results as VALU writes, so the copy,

@@ -78,12 +78,6 @@ __device__ __forceinline__ int swz(int r) { return 2 * ((r >> 1) & 3); }
 // element index of (local row r, element col) in a swizzled V half-stage
 __device__ __forceinline__ int vidx(int r, int col) { return r * 64 + (((col >> 3) ^ swz(r)) << 3) + (col & 7); }
 
-// maximum of a tile column's scores held by this lane (never NaN)
-__device__ __forceinline__ float max_sub_nn(const f32x4 (&s)[4]) { return max16_nn(s); }
-__device__ __forceinline__ float max_sub_nn(const f32x4 (&s)[2]) {
-    return max_nn(max3_nn(max3_nn(s[0][0], s[0][1], s[0][2]), max3_nn(s[0][3], s[1][0], s[1][1]), s[1][2]), s[1][3]);
-}
-
 __device__ __forceinline__ float key_to_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }

@@ -472,6 +472,17 @@ def test_decode_cached_prototypes_match():
     assert torch.equal(ex["sel"], ex2["sel"]) and torch.equal(out1, out2)
 
 
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+def test_decode_block32_reference_default_config(routing):
+    # the reference's default configuration (configs/base.yaml:19-20): 32-key
+    # blocks, top-4, on the matrix-core decode; ragged lengths and a cache short
+    # enough that every block is attended
+    case(f"decode bs=32 k=4 {routing}")
+    _decode_case(8, 16384, 12, 4, 64, 32, 4, torch.bfloat16, routing, seed=1102)
+    _decode_case(3, 5001, 12, 4, 64, 32, 4, torch.bfloat16, routing, seed=1103)
+    _decode_case(2, 150, 12, 4, 64, 32, 4, torch.bfloat16, routing, seed=1104)  # NB=5 <= k+2
+
+
 def test_decode_reference_geometry():
     # 8 q heads / 2 kv heads, D=32, bs=16, k=2 (tests/test_sparse_attention.py:14-30)
     case("decode D=32 bs=16 R=4")

@@ -201,12 +201,13 @@ def test_fetch_blocks_exact(arena_bf16, method):
                     assert (kh[b, h, i] == 3.0).all()  # unused slots untouched
 
 
-@pytest.mark.parametrize("method", [sparda.FETCH_KERNEL, sparda.FETCH_DMA])
-def test_offload_decode_step_equals_resident_attention(method):
+@pytest.mark.parametrize("method,bs,k", [(sparda.FETCH_KERNEL, 64, 8), (sparda.FETCH_DMA, 64, 8),
+                                         (sparda.FETCH_KERNEL, 32, 4)])
+def test_offload_decode_step_equals_resident_attention(method, bs, k):
     # the prefetched (compact) blocks + the new token attended = the same
     # selection attended in place on a GPU-resident cache
-    case(f"offload decode step method={method}")
-    B, S, Hq, Hkv, D, bs, k = 1, 8000, 12, 4, 64, 64, 8
+    case(f"offload decode step method={method} bs={bs}")
+    B, S, Hq, Hkv, D = 1, 8000, 12, 4, 64
     x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=torch.bfloat16, seed=60, capacity=8192)
     d = {n_: t.to(DEV) for n_, t in x.items()}
     L = S - 1  # tokens in the cache when the prefetch is issued

@@ -116,9 +116,10 @@ def test_backend_decode_through_prototype_cache_equals_plain_cache(routing):
 @pytest.mark.parametrize("S,dtype", [(16384, torch.bfloat16), (16448, torch.bfloat16), (5000, torch.float32),
                                      (300, torch.bfloat16), (20000, torch.bfloat16), (40000, torch.bfloat16),
                                      (100000, torch.bfloat16)])
-def test_decode_sums_equals_separate_selection_and_attention(routing, S, dtype):
-    case(f"decode_sums (selection inside the attention launch) S={S} {dtype} {routing}")
-    B, Hq, Hkv, D, bs, k = 4, 12, 4, 64, 64, 8
+@pytest.mark.parametrize("bs,k", [(64, 8), (32, 4)])
+def test_decode_sums_equals_separate_selection_and_attention(routing, S, dtype, bs, k):
+    case(f"decode_sums (selection inside the attention launch) S={S} {dtype} {routing} bs={bs}")
+    B, Hq, Hkv, D = 4, 12, 4, 64
     x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=dtype, seed=41)
     d = {n: t.to(DEV) for n, t in x.items()}
     nb = (S + bs - 1) // bs
