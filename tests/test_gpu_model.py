@@ -45,10 +45,11 @@ def _wo64(attn, o):
     return o @ attn.wo.weight.detach().double().cpu().numpy().T
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_sparse_backend_prefill_matches_oracle(dtype):
-    case(f"HipSparseAttention prefill {dtype}")
-    cfg = ModelConfig(block_size=64, top_k_blocks=8, context_length=1024)
+@pytest.mark.parametrize("dtype,bs,k", [(torch.float32, 64, 8), (torch.bfloat16, 64, 8), (torch.bfloat16, 32, 4)])
+def test_sparse_backend_prefill_matches_oracle(dtype, bs, k):
+    # (32, 4): the reference's default block configuration (configs/base.yaml)
+    case(f"HipSparseAttention prefill {dtype} bs={bs} k={k}")
+    cfg = ModelConfig(block_size=bs, top_k_blocks=k, context_length=1024)
     torch.manual_seed(0)
     attn = HipSparseAttention(cfg, layer_idx=1).to(DEV, dtype).eval()
     rot = RotaryEmbedding(cfg.head_dim, 1024).to(DEV)
@@ -57,9 +58,9 @@ def test_sparse_backend_prefill_matches_oracle(dtype):
     with torch.no_grad():
         out = attn(x, rot, forecast_vector=f)
         xq, xk, xv = _project(attn, rot, x)
-    sel, n = O.prefill_selection(np32(xk), np32(f), 64, 8)
+    sel, n = O.prefill_selection(np32(xk), np32(f), bs, k)
     rows = [(0, t) for t in range(0, 1024, 7)]
-    o = O.attention_prefill(np32(xq), np32(xk), np32(xv), sel, n, 64, rows=rows)
+    o = O.attention_prefill(np32(xq), np32(xk), np32(xv), sel, n, bs, rows=rows)
     idx = [t for _, t in rows]
     want = _wo64(attn, o[0, idx])
     tol_dtype = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
