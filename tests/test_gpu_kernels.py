@@ -302,6 +302,15 @@ def test_prefill_is_deterministic(bs):
         assert torch.equal(sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs), a)
 
 
+@pytest.mark.parametrize("bs,k", [(64, 8), (32, 4)])
+def test_prefill_tiny_and_edge_lengths(bs, k):
+    # lengths around one and two blocks and single tokens: the dense fallback
+    # (at most two blocks), the first routed lengths, ragged last blocks
+    for T in (1, 2, bs - 1, bs, bs + 1, 2 * bs + 1, 3 * bs, 5 * bs - 1):
+        case(f"prefill T={T} bs={bs}")
+        _prefill_case(2, T, 12, 4, 64, bs, k, torch.bfloat16, seed=300 + T)
+
+
 @pytest.mark.parametrize("R", [1, 3, 4])
 def test_prefill_block32_reference_default_config(R):
     # the reference's default configuration (configs/base.yaml:19-20): blocks of
