@@ -95,17 +95,30 @@ def load_traffic():
 
 
 def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK=TOPK):
-    """One sparse prefill layer at [B, T] (12/4 heads, D 64, block BS, top-TOPK):
-    eager steps with events around each launch, then the step replayed from a
-    HIP graph."""
+    """One sparse prefill layer at [B, T] (12/4 heads, D 64, block BS, top-TOPK).
+    The step: compress, then the routed prefill (the attention kernel routes its
+    own windows; one launch). Beside it the two-launch form (route, then the
+    prefill on the lists) for the router's own time. Eager steps with events
+    around each launch, then each step replayed from a HIP graph."""
     x = synth.prefill_inputs(B, T, HQ, HKV, D, dtype=torch.bfloat16, seed=seed, device="cuda")
     q, k, v, f = x["q"], x["k"], x["v"], x["forecast"]
     out = torch.empty((B, T, HQ * D), dtype=torch.bfloat16, device="cuda")
-
+    out2 = torch.empty_like(out)
     state = {}
 
-    def step(ev=None):
-        # ev: 4 events bracketing the three launches (same stream as the kernels)
+    def routed(ev=None):
+        # ev: 3 events bracketing the two launches (same stream as the kernels)
+        if ev is not None:
+            ev[0].record()
+        protos = sparda.compress(k, BS)
+        if ev is not None:
+            ev[1].record()
+        sparda.prefill_routed(q, k, v, f, protos, BS, TOPK, out=out)
+        if ev is not None:
+            ev[2].record()
+
+    def two_launch(ev=None):
+        # ev: 4 events bracketing the three launches
         if ev is not None:
             ev[0].record()
         protos = sparda.compress(k, BS)
@@ -114,35 +127,28 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         _, _, sel, n = sparda.route(f, protos, BS, TOPK, want_topk=False, want_sel=True)
         if ev is not None:
             ev[2].record()
-        sparda.prefill(q, k, v, sel, n, BS, out=out)
+        sparda.prefill(q, k, v, sel, n, BS, out=out2)
         if ev is not None:
             ev[3].record()
-        state["sel"], state["n"], state["protos"] = sel, n, protos
+        state["sel"], state["n"] = sel, n
 
-    with torch.no_grad():
+    def eager(step, n_ev):
         for _ in range(args.warmup):
             step()
-        # the timed steps; events around each launch give the per-kernel durations
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_ev)] for _ in range(args.steps)]
         torch.cuda.synchronize()
         for ev in evs:
             step(ev)
-        evs[-1][3].synchronize()
+        evs[-1][-1].synchronize()
         torch.cuda.synchronize()
-        ms_step_eager = evs[0][0].elapsed_time(evs[-1][3]) / args.steps
-        ms_compress = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-        ms_route = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-        ms_attn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
-        sel, n = state["sel"], state["n"]
-        assert torch.isfinite(out.float()).all(), "non-finite prefill output"
-        # useful work: for each (b, g, t) the allowed keys are full blocks
-        # below the own block plus t%bs+1 keys of the own block
-        t = torch.arange(T, device="cuda")
-        keys = (n.to(torch.int64) - 1) * BS + (t % BS + 1)
-        pairs = int(keys.sum().item()) * (HQ // HKV)
-        # the step as a serving loop issues it: the three launches recorded once
-        # in a HIP graph, replayed once per step (no launch gaps from the host)
-        ref = out.clone()
+        total = evs[0][0].elapsed_time(evs[-1][-1]) / args.steps
+        per = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps for i in range(n_ev - 1)]
+        return total, per
+
+    def graphed(step, dst):
+        # the step as a serving loop issues it: its launches recorded once in a
+        # HIP graph, replayed once per step (no launch gaps from the host)
+        ref = dst.clone()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -154,7 +160,7 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
             step()
         g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out, ref), "graph-replayed prefill step differs from the eager step"
+        assert torch.equal(dst, ref), "graph-replayed prefill step differs from the eager step"
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record()
@@ -163,8 +169,22 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         e1.record()
         e1.synchronize()
         torch.cuda.synchronize()
-        ms_step = e0.elapsed_time(e1) / args.steps
         del g
+        return e0.elapsed_time(e1) / args.steps
+
+    with torch.no_grad():
+        ms_step_eager, (ms_compress, ms_attn) = eager(routed, 3)
+        ms_two_eager, (_, ms_route, ms_attn_lists) = eager(two_launch, 4)
+        assert torch.isfinite(out.float()).all(), "non-finite prefill output"
+        assert torch.equal(out, out2), "routed prefill differs from route + prefill"
+        sel, n = state["sel"], state["n"]
+        # useful work: for each (b, g, t) the allowed keys are full blocks
+        # below the own block plus t%bs+1 keys of the own block
+        t = torch.arange(T, device="cuda")
+        keys = (n.to(torch.int64) - 1) * BS + (t % BS + 1)
+        pairs = int(keys.sum().item()) * (HQ // HKV)
+        ms_step = graphed(routed, out)
+        ms_two = graphed(two_launch, out2)
     flops = 4 * D * pairs
     tflops = flops / (ms_attn * 1e-3) / 1e12
     # compressor: read K, write the fp32 prototypes; router: read the forecast
@@ -181,10 +201,15 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         "attn_tflops": tflops,
         "compress_us": ms_compress * 1e3,
         "compress_gbs": comp_bytes / (ms_compress * 1e-3) / 1e9,
+        "compress_frac": comp_bytes / (ms_compress * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "two_launch_ms_per_step": ms_two,
+        "two_launch_ms_per_step_eager": ms_two_eager,
+        "two_launch_tok_s": B * T / (ms_two * 1e-3),
         "route_us": ms_route * 1e3,
         "route_gbs": route_bytes / (ms_route * 1e-3) / 1e9,
-        "compress_frac": comp_bytes / (ms_compress * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "route_frac": route_bytes / (ms_route * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "attn_from_lists_us": ms_attn_lists * 1e3,
+        "attn_from_lists_tflops": flops / (ms_attn_lists * 1e-3) / 1e12,
         "dense_causal_flop": 4 * D * HQ * B * T * (T + 1) // 2,
     }
 
@@ -560,7 +585,7 @@ def bench_model(args, torch, sparda, synth, fused=False):
     layer 0 dense causal, layers 1..11 forecast-routed sparse with layer L's
     forecast routing layer L+1), token ids uniform in [0, 32000). Reports
     tok/s of the whole forward (embeddings to logits) and the time of each
-    layer's attention (projections + RoPE + compress + route + attention +
+    layer's attention (projections + RoPE + compress + routed attention +
     output projection), from HIP events recorded around the attention modules."""
     from model.config import ModelConfig
     from model.model import SparDAResearchModel
@@ -703,8 +728,8 @@ def bench_teacher(args, torch, sparda, synth):
 
 
 def pmc_workload(args, torch, sparda, synth):
-    """Short eager run for hardware-counter passes: prefill steps at B=4 T=4096,
-    then at B=1 T=16384, decode steps and a plain device copy of COPY_BYTES
+    """Short eager run for hardware-counter passes: prefill steps (compress +
+    routed prefill) at B=4 T=4096, then at B=1 T=16384, decode steps and a plain device copy of COPY_BYTES
     (the calibration of FETCH_SIZE / WRITE_SIZE). Counter values are per
     dispatch, in this order."""
     x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
@@ -717,8 +742,7 @@ def pmc_workload(args, torch, sparda, synth):
         for xs in (x, x16):
             for _ in range(3):
                 protos = sparda.compress(xs["k"], BS)
-                _, _, sel, n = sparda.route(xs["forecast"], protos, BS, TOPK, want_topk=False, want_sel=True)
-                sparda.prefill(xs["q"], xs["k"], xs["v"], sel, n, BS)
+                sparda.prefill_routed(xs["q"], xs["k"], xs["v"], xs["forecast"], protos, BS, TOPK)
         for _ in range(3):
             sparda.decode(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], BS, TOPK, routing="absolute",
                           workspace=ws)
@@ -931,7 +955,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "sparse prefill layer: B=4 T=4096 Hq=12 Hkv=4 D=64 block=64 (64 blocks) "
-                               "top-k=8 causal, bf16; step = compress + route + block-sparse MFMA prefill",
+                               "top-k=8 causal, bf16; step = compress + routed block-sparse MFMA prefill (the "
+                               "attention kernel routes its own query windows)",
                    "global_batch": PB, "seq_len": PT, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(pre["attn_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(pre["attn_tflops"] / PEAK_BF16_TFLOPS, 4),
@@ -940,7 +965,7 @@ def main():
         "prefill_detail": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre.items()},
         "prefill_16k": {
             "workload": f"the same layer at B=1, T={MT} (256 blocks, top-8 + sink + own), the attention shape of "
-                        "one layer of the 12-layer forward; step = compress + route + block-sparse MFMA "
+                        "one layer of the 12-layer forward; step = compress + routed block-sparse MFMA "
                         "prefill, HIP graph replay",
             "ms_per_step": round(p16["ms_per_step"], 4),
             "tok_s": round(p16["tok_s"], 1),

@@ -204,6 +204,40 @@ SPARDA_API int sparda_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t
                               void* stream);
 
 /*
+ * Routed block-sparse GQA prefill: sparda_route with score_pos0 = query_pos0
+ * = 0 followed by sparda_prefill on its lists, in one launch where the shape
+ * allows. Replaces the prefill forward of ForecastBlockSelector
+ * (model/forecast.py:89-130) and SparseAttention's selection + masked SDPA
+ * (model/attention/sparse.py:231-281).
+ *   q, k, v, out, scale: as in sparda_prefill
+ *   forecast: [B,T,Hkv,Df] of f_dtype, strides (f_sb, f_st, f_sh, 1)
+ *   protos:   [B,ceil(T/bs),Hkv,Df] fp32 contiguous, 16-byte aligned
+ *             (sparda_compress of k)
+ *   top_k, route_scale: the router's (route_scale is its score scale)
+ *   sel, n_sel: optional [B,Hkv,T,sel_cap] / [B,Hkv,T], sel_cap >=
+ *             min(top_k, NB) + 2: receive exactly what sparda_route writes.
+ * One launch (the attention kernel routes each 64-token window itself, with
+ * the router's code, so lists and output equal the two-call sequence bit for
+ * bit) for bf16, D = Df = 64, bs 32 or 64, min(top_k, NB) <= 8, Hq/Hkv <= 4,
+ * ceil(T/bs) <= 1024, 16-byte aligned rows. Other shapes run the router and
+ * the prefill as two launches and need sel / n_sel as the hand-off buffers
+ * (SPARDA_ERR_SHAPE without them).
+ */
+SPARDA_API int sparda_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                                     const void* k, const void* v,
+                                     int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                                     int dtype,
+                                     const void* forecast, int f_dtype,
+                                     int64_t f_sb, int64_t f_st, int64_t f_sh,
+                                     const float* protos, int64_t Df,
+                                     int64_t top_k, float route_scale,
+                                     int32_t* sel, int32_t* n_sel, int64_t sel_cap,
+                                     int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                     int64_t block_size, int causal, float scale,
+                                     void* out, int64_t out_sb, int64_t out_st,
+                                     void* stream);
+
+/*
  * Block-sparse GQA prefill with an explicit additive mask and, optionally, the
  * attention weights. Replaces the masked-SDPA path of
  * SparseAttention._forward_masked_sdpa with `mask` and return_attn_weights

@@ -183,6 +183,55 @@ SPARDA_API int sparda_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t
                           static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                                     const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
+                                     const void* forecast, int f_dtype, int64_t f_sb, int64_t f_st, int64_t f_sh,
+                                     const float* protos, int64_t Df, int64_t top_k, float route_scale,
+                                     int32_t* sel, int32_t* n_sel, int64_t sel_cap, int64_t B, int64_t T,
+                                     int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, int causal,
+                                     float scale, void* out, int64_t out_sb, int64_t out_st, void* stream) {
+    SPARDA_REQUIRE(q && k && v && out && forecast && protos, SPARDA_ERR_NULL,
+                   "prefill_routed: null q/k/v/out/forecast/protos");
+    SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "prefill_routed: sel and n_sel go together");
+    SPARDA_REQUIRE(dtype_ok(dtype) && dtype_ok(f_dtype), SPARDA_ERR_DTYPE, "prefill_routed: dtype %d / %d unsupported",
+                   dtype, f_dtype);
+    SPARDA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "prefill_routed: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D) && head_dim_ok(Df), SPARDA_ERR_SHAPE,
+                   "prefill_routed: head dim %lld / forecast dim %lld not in {16,32,64,128}", (long long)D,
+                   (long long)Df);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "prefill_routed: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "prefill_routed: top_k %lld not in [1,%lld]",
+                   (long long)top_k, (long long)kMaxTopK);
+    SPARDA_REQUIRE(T < (1ll << 31) && B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "prefill_routed: too large");
+    SPARDA_REQUIRE(f_sb >= 0 && f_st >= 0 && f_sh >= 0, SPARDA_ERR_STRIDE, "prefill_routed: negative stride");
+    SPARDA_REQUIRE(reinterpret_cast<uintptr_t>(protos) % 16 == 0, SPARDA_ERR_STRIDE,
+                   "prefill_routed: prototypes must be 16-byte aligned");
+    const int64_t NB = cdiv(T, block_size);
+    const int64_t ke = top_k < NB ? top_k : NB;
+    SPARDA_REQUIRE(!sel || sel_cap >= ke + 2, SPARDA_ERR_SHAPE, "prefill_routed: sel_cap %lld < %lld",
+                   (long long)sel_cap, (long long)(ke + 2));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (prefill_routed_supported(dtype, f_dtype, T, Hq, Hkv, D, Df, block_size, ke, q_sb, q_st, q_sh, kv_sb, kv_st,
+                                 kv_sh, out_sb, out_st, q, k, v, out, protos)) {
+        CompactRoute rt{forecast, f_sb, f_st, f_sh, protos, static_cast<int>(ke), route_scale,
+                        sel, n_sel, static_cast<int>(sel ? sel_cap : 0)};
+        return launch_prefill_routed(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, f_dtype, rt, B, T, Hq, Hkv,
+                                     block_size, causal != 0, scale, out, out_sb, out_st, st);
+    }
+    // other shapes: the router's lists handed to the prefill through the caller's buffers
+    SPARDA_REQUIRE(sel != nullptr, SPARDA_ERR_SHAPE,
+                   "prefill_routed: this shape takes two launches and needs sel/n_sel as their hand-off buffers");
+    SPARDA_REQUIRE(NB < (1ll << 31), SPARDA_ERR_SHAPE, "prefill_routed: too large");
+    int rc = launch_route(forecast, f_dtype, f_sb, f_st, f_sh, protos, B, T, Hkv, Df, NB, block_size,
+                          static_cast<int>(ke), causal != 0, 0, 0, route_scale, nullptr, nullptr, sel, n_sel,
+                          static_cast<int>(sel_cap), st);
+    if (rc != 0) return rc;
+    return launch_prefill(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, dtype, sel, n_sel, sel_cap, B, T, Hq, Hkv,
+                          D, block_size, causal != 0, scale, out, out_sb, out_st, st);
+}
+
 SPARDA_API int sparda_prefill_masked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
                                      const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
                                      const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t B,

@@ -16,6 +16,26 @@ int launch_route(const void* f, int fdtype, int64_t fsb, int64_t fst, int64_t fs
                  float scale, int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel,
                  int cap, hipStream_t stream);
 
+// forecast routing folded into the compacted bf16 prefill (prefill_compact.hip)
+struct CompactRoute {
+    const void* f;          // forecast [B, T, Hkv, 64], element strides (fsb, fst, fsh, 1)
+    int64_t fsb, fst, fsh;
+    const float* protos;    // [B, ceil(T/bs), Hkv, 64] fp32, contiguous
+    int ke;                 // router picks per token, <= 8
+    float scale;            // router score scale
+    int32_t* sel;           // optional: the router's lists [B, Hkv, T, cap] and counts [B, Hkv, T]
+    int32_t* n_sel;
+    int cap;
+};
+bool prefill_routed_supported(int dtype, int f_dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t Df,
+                              int64_t bs, int64_t ke, int64_t q_sb, int64_t q_st, int64_t q_sh, int64_t kv_sb,
+                              int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st, const void* q,
+                              const void* k, const void* v, const void* out, const float* protos);
+int launch_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                          int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int f_dtype, const CompactRoute& rt,
+                          int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale,
+                          void* out, int64_t out_sb, int64_t out_st, hipStream_t stream);
+
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,

@@ -34,6 +34,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "mfma.h"
+#include "route_rows.h"
 
 namespace sparda {
 
@@ -50,6 +51,8 @@ constexpr float kCLog2e = 1.4426950408889634f;
 constexpr float kCGuard = 18446744073709551616.0f;  // 2^64
 constexpr uint32_t kCSpinLimit = 1u << 20;
 constexpr int kSentinel = 0x7fffffff;
+constexpr int kCRouteK = kCMaxCap - 2;         // router picks per token when the kernel routes
+constexpr int kCRouteDf = 64;                   // forecast dimension when the kernel routes
 
 template <int R>
 struct CompactSmem {
@@ -86,14 +89,18 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 
 // two workgroups per CU for R <= 3 (their LDS fits twice); one for R = 4.
 // BS: keys per KV block (64 or 32); the query window is 64 tokens either way.
-template <int R, int BS>
+// FDT < 0: the token lists come from sel / n_sel. FDT = the forecast's dtype:
+// the kernel routes its own window first (the router's per-set code, so the
+// lists are the router's bit for bit) and, with rt.sel set, also writes them
+// out as the router does.
+template <int R, int BS, int FDT>
 __global__ void __launch_bounds__(kCT, R <= 3 ? 2 : 1)
 prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                        const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                        int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
                        const int32_t* __restrict__ sel, const int32_t* __restrict__ n_sel, int64_t cap,
                        int64_t T, int H, int64_t NBq, int causal, float scale_log2,
-                       uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st) {
+                       uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st, CompactRoute rt) {
     using Smem = CompactSmem<R>;
     constexpr int kCols = Smem::kCols;
     __shared__ Smem sm;
@@ -131,7 +138,28 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     int lst[kCMaxCap];
 #pragma unroll
     for (int i = 0; i < kCMaxCap; ++i) lst[i] = kSentinel;
-    if (tid < t_valid) {
+    // blocks past the token's own (no key of theirs is allowed) are dropped
+    const int tlim = static_cast<int>(causal ? (t0 + tid) / BS : NB - 1);
+    if constexpr (FDT >= 0) {
+        // every wave scores a quarter of the candidate blocks for the window's
+        // 64 tokens; wave 0 merges (through the V staging bytes, unused until
+        // the tiles) and holds token tid's picks in lane tid
+        int32_t picks[kCRouteK];
+        if (route_set<FDT, kCRouteDf, kCRouteK>(rt.f, rt.fsb, rt.fst, rt.fsh, rt.protos, b, g, H, qb, T, NB, BS,
+                                                rt.ke, causal, 0, rt.scale, nullptr, 0,
+                                                reinterpret_cast<double*>(&sm.vstage[0][0]), picks) &&
+            tid < t_valid) {
+            // {0, own} U picks, own = the token's block (prefill positions start at 0)
+            const int own = static_cast<int>((t0 + tid) / BS);
+            int raw[kCMaxCap];
+            raw[0] = 0;
+            raw[1] = own;
+#pragma unroll
+            for (int i = 0; i < kCRouteK; ++i) raw[i + 2] = picks[i];
+#pragma unroll
+            for (int i = 0; i < kCMaxCap; ++i) lst[i] = (raw[i] >= 0 && raw[i] <= tlim) ? raw[i] : kSentinel;
+        }
+    } else if (tid < t_valid) {
         const int64_t r = (static_cast<int64_t>(b) * H + g) * T + t0 + tid;
         const int32_t* row = sel + r * cap;
         int raw[kCMaxCap];
@@ -139,10 +167,10 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         for (int i = 0; i < kCMaxCap; ++i) raw[i] = i < cap ? row[i] : -1;  // issued with the count's load
         const int64_t nr = n_sel[r];
         const int n = static_cast<int>(nr < 0 ? 0 : (nr > cap ? cap : nr));
-        // blocks past the token's own (no key of theirs is allowed) are dropped
-        const int tlim = static_cast<int>(causal ? (t0 + tid) / BS : NB - 1);
 #pragma unroll
         for (int i = 0; i < kCMaxCap; ++i) lst[i] = (i < n && raw[i] >= 0 && raw[i] <= tlim) ? raw[i] : kSentinel;
+    }
+    if (tid < t_valid) {
         // ascending, repeats dropped (odd-even transposition sort, twice)
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
@@ -158,6 +186,21 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 #pragma unroll
                 for (int i = kCMaxCap - 1; i > 0; --i)
                     if (lst[i] == lst[i - 1]) lst[i] = kSentinel;
+            }
+        }
+        if constexpr (FDT >= 0) {
+            if (rt.sel != nullptr) {
+                // the router's output rows: the list, -1 padding, the count
+                const int64_t r = (static_cast<int64_t>(b) * H + g) * T + t0 + tid;
+                int32_t* orow = rt.sel + r * rt.cap;
+                int n = 0;
+#pragma unroll
+                for (int i = 0; i < kCMaxCap; ++i) n += lst[i] != kSentinel;
+#pragma unroll
+                for (int i = 0; i < kCMaxCap; ++i)
+                    if (i < rt.cap) orow[i] = lst[i] != kSentinel ? lst[i] : -1;
+                for (int i = kCMaxCap; i < rt.cap; ++i) orow[i] = -1;
+                rt.n_sel[r] = n;
             }
         }
     }
@@ -603,6 +646,19 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     }
 }
 
+// window- and block-relative element offsets are 32-bit in the kernel; every
+// vector access is 16 bytes
+static bool compact_layout_ok(int64_t R, int64_t q_sb, int64_t q_st, int64_t q_sh, int64_t kv_sb, int64_t kv_st,
+                              int64_t kv_sh, int64_t out_sb, int64_t out_st, const void* q, const void* k,
+                              const void* v, const void* out) {
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out)) return false;
+    if ((q_sb % 8) || (q_st % 8) || (q_sh % 8) || (kv_sb % 8) || (kv_st % 8) || (kv_sh % 8)) return false;
+    if ((out_sb % 8) || (out_st % 8)) return false;
+    if (64 * q_st + R * q_sh + 64 >= (int64_t(1) << 30) || 64 * kv_st + 64 >= (int64_t(1) << 30)) return false;
+    return true;
+}
+
 bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs,
                                const int32_t* sel, int64_t cap, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st,
@@ -612,20 +668,28 @@ bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, in
     if (Hq % Hkv != 0) return false;
     const int64_t R = Hq / Hkv;
     if (R < 1 || R > 4) return false;
-    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (!al16(q) || !al16(k) || !al16(v) || !al16(out)) return false;
-    if ((q_sb % 8) || (q_st % 8) || (q_sh % 8) || (kv_sb % 8) || (kv_st % 8) || (kv_sh % 8)) return false;
-    if ((out_sb % 8) || (out_st % 8)) return false;
-    // window- and block-relative element offsets are 32-bit in the kernel
-    if (64 * q_st + R * q_sh + 64 >= (int64_t(1) << 30) || 64 * kv_st + 64 >= (int64_t(1) << 30)) return false;
-    return true;
+    return compact_layout_ok(R, q_sb, q_st, q_sh, kv_sb, kv_st, kv_sh, out_sb, out_st, q, k, v, out);
 }
 
-int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
-                           const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
-                           const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
-                           int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale, void* out,
-                           int64_t out_sb, int64_t out_st, hipStream_t stream) {
+bool prefill_routed_supported(int dtype, int f_dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t Df,
+                              int64_t bs, int64_t ke, int64_t q_sb, int64_t q_st, int64_t q_sh, int64_t kv_sb,
+                              int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st, const void* q,
+                              const void* k, const void* v, const void* out, const float* protos) {
+    if (dtype != SPARDA_BF16 || D != 64 || (bs != 64 && bs != 32)) return false;
+    if (Df != kCRouteDf || ke < 1 || ke > kCRouteK || (f_dtype != SPARDA_BF16 && f_dtype != SPARDA_F32)) return false;
+    if (cdiv(T, bs) > kCMaxNB || (reinterpret_cast<uintptr_t>(protos) & 15u) != 0) return false;
+    if (Hq % Hkv != 0) return false;
+    const int64_t R = Hq / Hkv;
+    if (R < 1 || R > 4) return false;
+    return compact_layout_ok(R, q_sb, q_st, q_sh, kv_sb, kv_st, kv_sh, out_sb, out_st, q, k, v, out);
+}
+
+template <int FDT>
+static int launch_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                          int64_t kv_sb, int64_t kv_st, int64_t kv_sh, const int32_t* sel, const int32_t* n_sel,
+                          int64_t cap, const CompactRoute& rt, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                          int64_t bs, int causal, float scale, void* out, int64_t out_sb, int64_t out_st,
+                          hipStream_t stream) {
     const int64_t NBq = cdiv(T, kCWin);  // query windows per (sequence, KV head)
     const int64_t R = Hq / Hkv;
     dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
@@ -633,10 +697,10 @@ int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_
 #define SPARDA_PC(R_)                                                                                        \
     if (bs == 32) SPARDA_PCB(R_, 32); else SPARDA_PCB(R_, 64)
 #define SPARDA_PCB(R_, BS_)                                                                                  \
-    hipLaunchKernelGGL((prefill_compact_kernel<R_, BS_>), grid, dim3(kCT), 0, stream,                        \
+    hipLaunchKernelGGL((prefill_compact_kernel<R_, BS_, FDT>), grid, dim3(kCT), 0, stream,                   \
                        static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k),    \
                        static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, sel, n_sel, cap, T,              \
-                       static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st)
+                       static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st, rt)
     switch (R) {
         case 1: SPARDA_PC(1); break;
         case 2: SPARDA_PC(2); break;
@@ -646,6 +710,27 @@ int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_
 #undef SPARDA_PCB
 #undef SPARDA_PC
     return check_hip(hipGetLastError(), "prefill_compact_kernel");
+}
+
+int launch_prefill_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                           const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                           const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
+                           int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale, void* out,
+                           int64_t out_sb, int64_t out_st, hipStream_t stream) {
+    const CompactRoute none{};
+    return launch_compact<-1>(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, sel, n_sel, cap, none, B, T, Hq, Hkv,
+                              bs, causal, scale, out, out_sb, out_st, stream);
+}
+
+int launch_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                          int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int f_dtype, const CompactRoute& rt,
+                          int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale,
+                          void* out, int64_t out_sb, int64_t out_st, hipStream_t stream) {
+    if (f_dtype == SPARDA_F32)
+        return launch_compact<SPARDA_F32>(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, nullptr, nullptr, 0, rt,
+                                          B, T, Hq, Hkv, bs, causal, scale, out, out_sb, out_st, stream);
+    return launch_compact<SPARDA_BF16>(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, nullptr, nullptr, 0, rt, B,
+                                       T, Hq, Hkv, bs, causal, scale, out, out_sb, out_st, stream);
 }
 
 }  // namespace sparda

@@ -10,6 +10,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "select.h"
+#include "route_rows.h"
 
 namespace sparda {
 
@@ -85,60 +86,6 @@ int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, i
 // merged through LDS by one wave (rotating with the set), which writes the
 // rows' outputs.
 // ---------------------------------------------------------------------------
-// N consecutive fp32 values (N in {1, 2, 4, 8}), 4*N-byte aligned
-template <int N>
-__device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&o)[N]) {
-    if constexpr (N == 1) {
-        o[0] = p[0];
-    } else if constexpr (N == 2) {
-        const float2 v = *reinterpret_cast<const float2*>(p);
-        o[0] = v.x; o[1] = v.y;
-    } else {
-#pragma unroll
-        for (int q = 0; q < N; q += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(p + q);
-            o[q] = v.x; o[q + 1] = v.y; o[q + 2] = v.z; o[q + 3] = v.w;
-        }
-    }
-}
-
-// Two fma chains, one step: acc[c] = fma(a, element of lane I of this lane's
-// 16-lane row of p[c], acc[c]), each a v_fmac_f32 with a DPP row_newbcast
-// source (a separate DPP move does not fold into the fma, which is a VOP3 op
-// at that point). A DPP instruction needs two wait states after a VALU write
-// of any register it reads. The compiler does not track that for inline
-// assembly, so the steps carry their own: the two fmas of a step write
-// different accumulators and end with s_nop 0, so an accumulator is read two
-// wait states after its last write, and the steps that first read the
-// prototype registers (FIRST) start with s_nop 1. What the compiler places
-// between steps (spill reloads, copies) is checked on the built code by the
-// test suite.
-template <int I, bool FIRST>
-__device__ __forceinline__ void fma_row_bcast(float (&acc)[2], float a, const float (&p)[2]) {
-    if constexpr (FIRST)
-        asm("s_nop 1\n\tv_fmac_f32_dpp %0, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
-            "v_fmac_f32_dpp %1, %3, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\ts_nop 0"
-            : "+v"(acc[0]), "+v"(acc[1]) : "v"(p[0]), "v"(p[1]), "v"(a), "n"(I));
-    else
-        asm("v_fmac_f32_dpp %0, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
-            "v_fmac_f32_dpp %1, %3, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\ts_nop 0"
-            : "+v"(acc[0]), "+v"(acc[1]) : "v"(p[0]), "v"(p[1]), "v"(a), "n"(I));
-}
-// acc[c] = fma chain over d = E*I + e (I = I0..15, e = 0..E-1) with element d
-// of prototype c taken from lane I of the row (register pc[e][c])
-template <int E, int DF, int C, int I0 = 0>
-__device__ __forceinline__ void row_fma_chains(const float (&fr)[DF], const float (&pc)[E][C],
-                                               float (&acc)[C]) {
-    if constexpr (I0 < 16) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) fma_row_bcast<I0, I0 == 0>(acc, fr[E * I0 + e], pc[e]);
-        row_fma_chains<E, DF, C, I0 + 1>(fr, pc, acc);
-    }
-}
-
-constexpr int kRouteWaves = 4;
-constexpr int kRouteThreads = kRouteWaves * kWave;
-
 template <int FDT, int DF, int KMAX>
 __global__ void __launch_bounds__(kRouteThreads)
 route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t fsh,
@@ -148,94 +95,22 @@ route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t 
                   int32_t* __restrict__ sel, int32_t* __restrict__ n_sel, int cap) {
     extern __shared__ double lists[];  // [kRouteWaves][KMAX][kWave]
     const int lane = threadIdx.x % kWave;
-    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
     const int h = blockIdx.y;
     const int b = blockIdx.z;
     const int64_t NS = cdiv(Tq, kWave);
     const int64_t pair = blockIdx.x;
-    const float* __restrict__ pbh = protos + (static_cast<int64_t>(b) * NB * H + h) * DF;
-    const int64_t pstride = static_cast<int64_t>(H) * DF;
 
     for (int pass = 0; pass < 2; ++pass) {
         const int64_t set = pass == 0 ? pair : NS - 1 - pair;
         if (pass == 1 && set == pair) break;  // odd set count: the middle set has no mirror
-        const int64_t t = set * kWave + lane;
-        const bool active = t < Tq;
-        const int64_t tc = active ? t : Tq - 1;
-        const int64_t t_last = (set * kWave + kWave < Tq ? set * kWave + kWave : Tq) - 1;
-        int64_t limit = causal ? (score_pos0 + tc) / bs : NB - 1;
-        if (limit > NB - 1) limit = NB - 1;
-        int64_t jmax = causal ? (score_pos0 + t_last) / bs : NB - 1;  // uniform
-        if (jmax > NB - 1) jmax = NB - 1;
-
-        float fr[DF];
-        {
-            const int64_t base = b * fsb + tc * fst + h * fsh;
-#pragma unroll
-            for (int d = 0; d < DF; ++d) fr[d] = load_elem<FDT>(f, base + d);
-        }
-        const int64_t row = (static_cast<int64_t>(b) * H + h) * Tq + t;
-        float* srow = (scores != nullptr && active) ? scores + row * NB : nullptr;
-
-        KeyTopK<KMAX> best;
-        best.init();
-        constexpr int E = DF / 16;
-        constexpr int C = 2;  // blocks scored side by side
-        const float* __restrict__ prow = pbh + (lane % 16) * E;
-        float pn[C][E];
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            const int64_t jc = w + c * kRouteWaves;
-            load_f32<E>(prow + (jc < jmax ? jc : jmax) * pstride, pn[c]);
-        }
-        for (int64_t j = w; j <= jmax; j += C * kRouteWaves) {
-            float pc[E][C];
-#pragma unroll
-            for (int c = 0; c < C; ++c) {
-#pragma unroll
-                for (int e = 0; e < E; ++e) pc[e][c] = pn[c][e];
-                const int64_t jn = j + (C + c) * kRouteWaves;
-                load_f32<E>(prow + (jn < jmax ? jn : jmax) * pstride, pn[c]);
-            }
-            float acc[C];
-#pragma unroll
-            for (int c = 0; c < C; ++c) acc[c] = 0.0f;
-            row_fma_chains<E, DF, C>(fr, pc, acc);
-#pragma unroll
-            for (int c = 0; c < C; ++c) {
-                const int64_t jc = j + c * kRouteWaves;
-                const float sc = acc[c] * scale;
-                const bool ok = jc <= limit;  // limit <= jmax
-                if (srow && ok) srow[jc] = sc;
-                best.push(ok ? route_key(sc, static_cast<int32_t>(jc)) : 0.0);
-            }
-        }
-        if (srow) {
-            for (int64_t j = w; j < NB; j += kRouteWaves)
-                if (j > limit) srow[j] = -__builtin_inff();
-        }
-
-        // merge the waves' lists in the merging wave
         const int m = static_cast<int>((2 * pair + pass) % kRouteWaves);
-        __syncthreads();  // the previous set's merger has read its lists
-        if (w != m) {
-#pragma unroll
-            for (int i = 0; i < KMAX; ++i) lists[(w * KMAX + i) * kWave + lane] = best.r[i];
-        }
-        __syncthreads();
-        if (w != m) continue;
-        for (int o = 0; o < kRouteWaves; ++o) {
-            if (o == m) continue;
-            double other[KMAX];
-#pragma unroll
-            for (int i = 0; i < KMAX; ++i) other[i] = lists[(o * KMAX + i) * kWave + lane];
-            best.merge(other);
-        }
-        if (!active) continue;
-        // slots not filled by a candidate take the masked blocks in ascending order
         int32_t picks[KMAX];
-#pragma unroll
-        for (int i = 0; i < KMAX; ++i) picks[i] = (i < ke) ? (best.r[i] == 0.0 ? i : route_key_index(best.r[i])) : -1;
+        if (!route_set<FDT, DF, KMAX>(f, fsb, fst, fsh, protos, b, h, H, set, Tq, NB, bs, ke, causal, score_pos0,
+                                      scale, scores, m, lists, picks))
+            continue;
+        const int64_t t = set * kWave + lane;
+        if (t >= Tq) continue;
+        const int64_t row = (static_cast<int64_t>(b) * H + h) * Tq + t;
         if (topk) {
             int32_t* tr = topk + row * ke;
 #pragma unroll

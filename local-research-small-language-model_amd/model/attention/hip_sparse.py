@@ -3,8 +3,9 @@
 (model/attention/dense.py), with the block gather of
 gather_kv_blocks (model/attention/sparse.py:19-62).
 
-Prefill: compressor -> fused router -> block-sparse prefill kernel (bf16
-MFMA for D = 64, bs = 64; general kernel otherwise). The per-token allowed
+Prefill: compressor, then the router and the block-sparse attention in one
+launch (bf16 MFMA kernel that routes its own query windows, for D = 64 and
+blocks of 32 or 64 keys), or router then prefill kernel for other shapes. The per-token allowed
 set is the reference's masked-SDPA rule (sparse.py:226-281) at every length;
 the reference's chunked path for T > 8192 (sparse.py:284-364, different
 routing semantics) is not reproduced.
@@ -133,6 +134,13 @@ class HipSparseAttention(BaseAttention):
         return self._project(out, residual)
 
     # -- prefill -----------------------------------------------------------
+    def _dense_prefill(self, T, forecast_vector):
+        """The dense fallback of sparse.py:201-224: dense mode, at most two
+        blocks, or forecast mode without a forecast (and at layer 0)."""
+        nb = (T + self.block_size - 1) // self.block_size
+        return self.mode == "dense" or nb <= 2 or (
+            self.mode == "forecast" and (forecast_vector is None or self.layer_idx == 0))
+
     def _selection(self, xq, xk, forecast_vector, is_causal):
         """The allowed-block lists of a prefill (sparse.py:201-253): None for
         the dense fallback, else router lists (forecast) or the static window
@@ -140,9 +148,7 @@ class HipSparseAttention(BaseAttention):
         in full."""
         B, T = xq.shape[:2]
         nb = (T + self.block_size - 1) // self.block_size
-        dense = self.mode == "dense" or nb <= 2 or (
-            self.mode == "forecast" and (forecast_vector is None or self.layer_idx == 0))
-        if dense:
+        if self._dense_prefill(T, forecast_vector):
             return None, None
         if self.mode == "forecast":
             protos = sparda.compress(xk, self.block_size)
@@ -153,6 +159,13 @@ class HipSparseAttention(BaseAttention):
                                    self.top_k_blocks, 0, device=xq.device)
 
     def _prefill(self, xq, xk, xv, forecast_vector, is_causal, mask=None, return_attn_weights=False):
+        if (mask is None and not return_attn_weights and self.mode == "forecast"
+                and not self._dense_prefill(xq.shape[1], forecast_vector)):
+            # compressor, then router and attention in one call (one launch
+            # where the shape allows)
+            protos = sparda.compress(xk, self.block_size)
+            return self.wo(sparda.prefill_routed(xq, xk, xv, forecast_vector, protos, self.block_size,
+                                                 self.top_k_blocks, causal=is_causal))
         sel, n_sel = self._selection(xq, xk, forecast_vector, is_causal)
         if mask is None and not return_attn_weights:
             return self.wo(sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=is_causal))

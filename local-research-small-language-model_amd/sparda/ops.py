@@ -214,6 +214,77 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[tor
     return out
 
 
+def _routed_one_launch(q, k, v, forecast, protos, out, block_size: int, ke: int) -> bool:
+    """Whether sparda_prefill_routed takes its one-launch path for these
+    tensors (a subset of the library's own test: outside it the call gets the
+    hand-off buffers the two-launch path needs)."""
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if q.dtype != torch.bfloat16 or D != 64 or forecast.shape[-1] != 64 or block_size not in (32, 64):
+        return False
+    if forecast.dtype not in (torch.bfloat16, torch.float32) or not 1 <= ke <= 8:
+        return False
+    if Hq % Hkv or not 1 <= Hq // Hkv <= 4 or (T + block_size - 1) // block_size > 1024:
+        return False
+    ts = (q, k, v, out)
+    if any(t.data_ptr() % 16 for t in ts + (protos,)) or any(st % 8 for t in ts for st in t.stride()[:-1]):
+        return False
+    return 64 * q.stride(1) + (Hq // Hkv) * q.stride(2) + 64 < (1 << 30) and 64 * k.stride(1) + 64 < (1 << 30)
+
+
+def prefill_routed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, forecast: torch.Tensor,
+                   protos: torch.Tensor, block_size: int, top_k: int, causal: bool = True,
+                   scale: Optional[float] = None, route_scale: Optional[float] = None, want_sel: bool = False,
+                   out: Optional[torch.Tensor] = None):
+    """Router + block-sparse prefill (model/forecast.py:89-130 then
+    model/attention/sparse.py:231-281): ``route`` at positions 0.. and
+    ``prefill`` on its lists, one launch where the shape allows.
+
+    q [B,T,Hq,D], k/v [B,T,Hkv,D], forecast [B,T,Hkv,Df], protos [B,NB,Hkv,Df]
+    fp32 (``compress`` of k). Returns out [B,T,Hq*D], or (out, sel, n_sel)
+    with want_sel (the lists ``route`` returns with want_sel).
+    """
+    dev = require_device(q, k, v, forecast, protos)
+    _inference_only(q, k, v, forecast)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q, k, v must share a dtype")
+    q, k, v, forecast = _rowmajor(q), _rowmajor(k), _rowmajor(v), _rowmajor(forecast)
+    if k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    if protos.dtype != torch.float32 or not protos.is_contiguous():
+        protos = protos.float().contiguous()
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    Df = forecast.shape[-1]
+    NB = (T + block_size - 1) // block_size
+    if tuple(forecast.shape[:3]) != (B, T, Hkv) or tuple(protos.shape) != (B, NB, Hkv, Df):
+        raise AssertionError(f"Mismatch: forecast {tuple(forecast.shape)} / prototypes {tuple(protos.shape)} "
+                             f"for k {tuple(k.shape)} at block size {block_size}")
+    ke = min(top_k, NB)
+    if scale is None:
+        scale = default_scale(D)
+    if route_scale is None:
+        route_scale = default_scale(Df)
+    if out is None:
+        out = torch.empty((B, T, Hq * D), dtype=q.dtype, device=dev)
+    sel = n_sel = None
+    cap = 0
+    if want_sel or not _routed_one_launch(q, k, v, forecast, protos, out, block_size, ke):
+        cap = ke + 2
+        sel = torch.empty((B, Hkv, T, cap), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, Hkv, T), dtype=torch.int32, device=dev)
+    qsb, qst, qsh, _ = q.stride()
+    ksb, kst, ksh, _ = k.stride()
+    fsb, fst, fsh, _ = forecast.stride()
+    osb, ost, _ = out.stride()
+    call("sparda_prefill_routed", q.data_ptr(), qsb, qst, qsh, k.data_ptr(), v.data_ptr(), ksb, kst, ksh,
+         _dtype_code(q), forecast.data_ptr(), _dtype_code(forecast), fsb, fst, fsh, protos.data_ptr(), Df, top_k,
+         float(route_scale), sel.data_ptr() if sel is not None else None,
+         n_sel.data_ptr() if n_sel is not None else None, cap, B, T, Hq, Hkv, D, block_size, int(causal),
+         float(scale), out.data_ptr(), osb, ost, _stream(dev))
+    return (out, sel, n_sel) if want_sel else out
+
+
 def prefill_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[torch.Tensor],
                    n_sel: Optional[torch.Tensor], block_size: int, causal: bool = True,
                    scale: Optional[float] = None, mask: Optional[torch.Tensor] = None,

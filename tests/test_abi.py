@@ -80,6 +80,17 @@ def test_argument_errors_are_reported_before_any_hip_call():
     _expect(-6, "sparda_select_fixed", 7, 1, 1, 1, 1, 1, 1, 0, P, P, 4, None)
     _expect(-2, "sparda_prefill", P, 1, 1, 1, P, P, 1, 1, 1, 1, None, None, 0, 1, 16, 12, 5, 64, 64, 1, 0.125,
             P, 1, 1, None)  # Hq not a multiple of Hkv
+    # prefill_routed: q, strides, k, v, kv strides, dtype, forecast, f_dtype, f strides, protos, Df, top_k,
+    # route_scale, sel, n_sel, sel_cap, B, T, Hq, Hkv, D, bs, causal, scale, out, out strides, stream
+    routed = lambda f, sel, n_sel, cap, top_k, protos=P: (
+        P, 768, 768, 64, P, P, 256, 256, 64, 1, f, 1, 256, 256, 64, protos, 64, top_k, 0.125, sel, n_sel, cap,
+        1, 1024, 12, 4, 64, 64, 1, 0.125, P, 768, 768, None)
+    _expect(-1, "sparda_prefill_routed", *routed(None, None, None, 0, 8))        # no forecast
+    _expect(-1, "sparda_prefill_routed", *routed(P, P, None, 10, 8))            # sel without n_sel
+    _expect(-2, "sparda_prefill_routed", *routed(P, None, None, 0, 33))         # top_k > 32
+    _expect(-2, "sparda_prefill_routed", *routed(P, P, P, 9, 8))                # sel_cap < top_k + 2
+    _expect(-2, "sparda_prefill_routed", *routed(P, None, None, 0, 16))         # two launches need the lists
+    _expect(-5, "sparda_prefill_routed", *routed(P, None, None, 0, 8, P + 4))   # unaligned prototypes
     _expect(-4, "sparda_decode", P, 1, 1, P, P, 8, 8, 8, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,
             None, None, None, None, P, 1, None, 0, None)  # no workspace
     _expect(-4, "sparda_decode", P, 1, 1, P, P, 8, 8, 8, 1, None, 0, 0, 0, 1, 128, 12, 4, 64, 64, 8, 0, 0.125,

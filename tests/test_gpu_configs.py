@@ -42,35 +42,40 @@ def test_twelve_layer_forward_at_16k_against_the_oracle(monkeypatch):
     model = SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval()
     g = torch.Generator().manual_seed(1003)
     ids = torch.randint(0, cfg.vocab_size, (1, T), generator=g).to(DEV)
-    routes, prefills = [], []
-    real_route, real_prefill = sparda.route, sparda.prefill
+    prefills = []
+    real_prefill, real_routed = sparda.prefill, sparda.prefill_routed
 
-    def route_spy(forecast, protos, *a, **kw):
-        res = real_route(forecast, protos, *a, **kw)
-        routes.append(forecast.detach().float().cpu().numpy())
-        return res
+    def keep(q, kk, v, out, sel=None, n=None, f=None):
+        prefills.append({"q": q.detach().cpu(), "k": kk.detach().cpu(), "v": v.detach().cpu(),
+                         "sel": None if sel is None else sel.cpu().numpy(),
+                         "n": None if n is None else n.cpu().numpy(), "out": out.detach().cpu(),
+                         "f": None if f is None else f.detach().float().cpu().numpy()})
 
     def prefill_spy(q, kk, v, sel, n_sel, block_size, **kw):
         out = real_prefill(q, kk, v, sel, n_sel, block_size, **kw)
-        prefills.append({"q": q.detach().cpu(), "k": kk.detach().cpu(), "v": v.detach().cpu(),
-                         "sel": None if sel is None else sel.cpu().numpy(),
-                         "n": None if n_sel is None else n_sel.cpu().numpy(), "out": out.detach().cpu()})
+        keep(q, kk, v, out, sel, n_sel)
         return out
 
-    monkeypatch.setattr(sparda, "route", route_spy)
+    def routed_spy(q, kk, v, forecast, protos, block_size, top_k, **kw):
+        # the same launch, with the lists written out for the check
+        out, sel, n = real_routed(q, kk, v, forecast, protos, block_size, top_k, want_sel=True, **kw)
+        keep(q, kk, v, out, sel, n, forecast)
+        return out
+
     monkeypatch.setattr(sparda, "prefill", prefill_spy)
+    monkeypatch.setattr(sparda, "prefill_routed", routed_spy)
     with torch.no_grad():
         res = model(ids, return_forecasts=True)
     torch.cuda.synchronize()
     assert torch.isfinite(res["logits"]).all()
     assert len(prefills) == 12 and prefills[0]["sel"] is None  # layer 0: dense causal
-    assert len(routes) == 11
+    assert all(p["f"] is not None for p in prefills[1:])
     r = np.random.default_rng(16384)
     for L, p in enumerate(prefills):
         q, kk, v = np32(p["q"]), np32(p["k"]), np32(p["v"])
         if L > 0:
             # layer L routes with the forecast layer L-1 emitted
-            f = routes[L - 1]
+            f = p["f"]
             assert np.array_equal(f, np32(res["forecasts"][L - 1])), f"layer {L}: forecast hand-off"
             _, _, sel_o, n_o = O.route(f, O.compress(kk, bs), bs, k, True)
             assert np.array_equal(p["n"], n_o) and np.array_equal(p["sel"], sel_o), f"layer {L}: selection"

@@ -415,6 +415,88 @@ def test_prefill_scores_far_above_the_reference_maximum():
 
 
 # ---------------------------------------------------------------------------
+# routed prefill (router folded into the attention launch)
+# ---------------------------------------------------------------------------
+
+def _routed_case(B, T, Hq, Hkv, D, bs, k, seed, causal=True, fdtype=None, dtype=torch.bfloat16):
+    """prefill_routed against route + prefill on the same inputs: the lists
+    and the attention output equal bit for bit, with and without the lists
+    written out."""
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=dtype, seed=seed)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    f = d["forecast"] if fdtype is None else d["forecast"].to(fdtype)
+    protos = sparda.compress(d["k"], bs)
+    _, _, sel, n = sparda.route(f, protos, bs, k, causal=causal, want_topk=False, want_sel=True)
+    want = sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs, causal=causal)
+    got, sel2, n2 = sparda.prefill_routed(d["q"], d["k"], d["v"], f, protos, bs, k, causal=causal, want_sel=True)
+    got_plain = sparda.prefill_routed(d["q"], d["k"], d["v"], f, protos, bs, k, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(n2, n) and torch.equal(sel2, sel), "routed lists differ from the router's"
+    assert torch.equal(got, want), f"max diff {(got.float() - want.float()).abs().max().item()}"
+    assert torch.equal(got_plain, want)
+    return x, sel, n, got
+
+
+@pytest.mark.parametrize("R", [1, 2, 3, 4])
+@pytest.mark.parametrize("bs,k", [(64, 8), (32, 4)])
+def test_prefill_routed_equals_route_then_prefill(R, bs, k):
+    case(f"prefill_routed R={R} bs={bs} k={k} T=1000")
+    _routed_case(2, 1000, 4 * R, 4, 64, bs, k, seed=400 + R)
+    _routed_case(1, 777, 4 * R, 4, 64, bs, k, seed=410 + R, causal=False)
+
+
+def test_prefill_routed_full_size_against_the_oracle():
+    # prefill workload: B=4, T=4096, 12/4 heads, bs 64, top-8; lists against the
+    # oracle's router, sampled rows against the oracle's attention
+    case("prefill_routed B=4 T=4096")
+    x, sel, n, got = _routed_case(4, 4096, 12, 4, 64, 64, 8, seed=1001)
+    _, _, sel_o, n_o = O.route(np32(x["forecast"]), O.compress(np32(x["k"]), 64), 64, 8, True)
+    assert np.array_equal(sel.cpu().numpy(), sel_o) and np.array_equal(n.cpu().numpy(), n_o)
+    r = np.random.default_rng(11)
+    rows = sorted({(int(b), int(t)) for b, t in zip(r.integers(0, 4, 256), r.integers(0, 4096, 256))})
+    rows += [(b, t) for b in range(4) for t in (0, 63, 64, 4095)]
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, 64, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(got), want, torch.bfloat16, mask)
+
+
+def test_prefill_routed_long_context_and_block32():
+    case("prefill_routed B=1 T=16384 bs=64 k=8")
+    _routed_case(1, 16384, 12, 4, 64, 64, 8, seed=1005)
+    case("prefill_routed B=4 T=4096 bs=32 k=4")
+    _routed_case(4, 4096, 12, 4, 64, 32, 4, seed=1001)
+
+
+@pytest.mark.parametrize("bs", [64, 32])
+def test_prefill_routed_small_top_k_and_short_lengths(bs):
+    # top-k below the kernel's eight slots, top-k above the block count, single
+    # tokens, one and two blocks, ragged tails
+    for T, k in ((1, 8), (2, 1), (bs - 1, 3), (bs, 8), (bs + 1, 2), (2 * bs + 1, 8), (5 * bs - 1, 1), (300, 5)):
+        case(f"prefill_routed T={T} bs={bs} k={k}")
+        _routed_case(2, T, 12, 4, 64, bs, k, seed=500 + T + k)
+
+
+def test_prefill_routed_fp32_forecast():
+    case("prefill_routed fp32 forecast")
+    _routed_case(2, 1000, 12, 4, 64, 64, 8, seed=420, fdtype=torch.float32)
+    _routed_case(1, 600, 12, 4, 64, 32, 4, seed=421, fdtype=torch.float32, causal=False)
+
+
+def test_prefill_routed_two_launch_shapes():
+    # shapes outside the one-launch kernel: top-k above 8, 16-key blocks,
+    # D = 128, fp32 q/k/v, D = 32 (router then prefill through the hand-off
+    # lists)
+    case("prefill_routed two-launch shapes")
+    _routed_case(1, 1000, 12, 4, 64, 64, 16, seed=430)
+    _routed_case(1, 500, 12, 4, 64, 16, 4, seed=431)
+    _routed_case(1, 300, 4, 1, 128, 32, 3, seed=432)
+    _routed_case(1, 400, 12, 4, 64, 64, 8, seed=433, dtype=torch.float32)
+    _routed_case(2, 333, 8, 2, 32, 16, 2, seed=434)
+
+
+# ---------------------------------------------------------------------------
 # decode step
 # ---------------------------------------------------------------------------
 
