@@ -484,6 +484,26 @@ def test_prefill_routed_fp32_forecast():
     _routed_case(1, 600, 12, 4, 64, 32, 4, seed=421, fdtype=torch.float32, causal=False)
 
 
+def test_prefill_routed_strided_views():
+    # q / k / v as views of one packed projection output, the forecast a view
+    # of a wider buffer: the one-launch kernel reads them through their strides
+    case("prefill_routed strided views")
+    B, T, Hq, Hkv, D, bs, k = 2, 700, 12, 4, 64, 64, 8
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=torch.bfloat16, seed=440)
+    packed = torch.cat([x["q"], x["k"], x["v"]], dim=2).to(DEV)      # [B, T, Hq + 2 Hkv, D]
+    q, kk, v = packed[:, :, :Hq], packed[:, :, Hq:Hq + Hkv], packed[:, :, Hq + Hkv:]
+    wide = torch.zeros(B, T, Hkv, 2 * D, dtype=torch.bfloat16, device=DEV)
+    wide[..., :D] = x["forecast"].to(DEV)
+    f = wide[..., :D]
+    protos = sparda.compress(kk, bs)
+    got, sel, n = sparda.prefill_routed(q, kk, v, f, protos, bs, k, want_sel=True)
+    _, _, sel_w, n_w = sparda.route(f.contiguous(), protos, bs, k, want_topk=False, want_sel=True)
+    want = sparda.prefill(q.contiguous(), kk.contiguous(), v.contiguous(), sel_w, n_w, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(sel, sel_w) and torch.equal(n, n_w)
+    assert torch.equal(got, want)
+
+
 def test_prefill_routed_two_launch_shapes():
     # shapes outside the one-launch kernel: top-k above 8, 16-key blocks,
     # D = 128, fp32 q/k/v, D = 32 (router then prefill through the hand-off
