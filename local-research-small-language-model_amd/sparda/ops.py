@@ -235,14 +235,15 @@ def _routed_one_launch(q, k, v, forecast, protos, out, block_size: int, ke: int)
 def prefill_routed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, forecast: torch.Tensor,
                    protos: torch.Tensor, block_size: int, top_k: int, causal: bool = True,
                    scale: Optional[float] = None, route_scale: Optional[float] = None, want_sel: bool = False,
-                   out: Optional[torch.Tensor] = None):
+                   sel_cap: Optional[int] = None, out: Optional[torch.Tensor] = None):
     """Router + block-sparse prefill (model/forecast.py:89-130 then
     model/attention/sparse.py:231-281): ``route`` at positions 0.. and
     ``prefill`` on its lists, one launch where the shape allows.
 
     q [B,T,Hq,D], k/v [B,T,Hkv,D], forecast [B,T,Hkv,Df], protos [B,NB,Hkv,Df]
     fp32 (``compress`` of k). Returns out [B,T,Hq*D], or (out, sel, n_sel)
-    with want_sel (the lists ``route`` returns with want_sel).
+    with want_sel (the lists ``route`` returns with want_sel and the same
+    sel_cap, default min(top_k, NB) + 2).
     """
     dev = require_device(q, k, v, forecast, protos)
     _inference_only(q, k, v, forecast)
@@ -270,7 +271,7 @@ def prefill_routed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, forecast: 
     sel = n_sel = None
     cap = 0
     if want_sel or not _routed_one_launch(q, k, v, forecast, protos, out, block_size, ke):
-        cap = ke + 2
+        cap = sel_cap if sel_cap is not None else ke + 2
         sel = torch.empty((B, Hkv, T, cap), dtype=torch.int32, device=dev)
         n_sel = torch.empty((B, Hkv, T), dtype=torch.int32, device=dev)
     qsb, qst, qsh, _ = q.stride()

@@ -502,6 +502,11 @@ def test_prefill_routed_strided_views():
     torch.cuda.synchronize()
     assert torch.equal(sel, sel_w) and torch.equal(n, n_w)
     assert torch.equal(got, want)
+    # lists wider than the kernel's ten entries: -1 padding as the router writes it
+    got2, sel2, n2 = sparda.prefill_routed(q, kk, v, f, protos, bs, k, want_sel=True, sel_cap=13)
+    _, _, sel_w2, n_w2 = sparda.route(f.contiguous(), protos, bs, k, want_topk=False, want_sel=True, sel_cap=13)
+    torch.cuda.synchronize()
+    assert torch.equal(sel2, sel_w2) and torch.equal(n2, n_w2) and torch.equal(got2, want)
 
 
 def test_prefill_routed_two_launch_shapes():
