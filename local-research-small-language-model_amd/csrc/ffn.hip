@@ -13,21 +13,16 @@
 // residual sum); the norm is a per-row scale applied in fp32 after the
 // product instead of a rounded normalised activation.
 //
-// Both launches use the decode producer's layout: a 256-thread workgroup owns
-// 16 output columns, a 16-lane group per column keeps that column's weight
-// row(s) in registers (C/128 16-byte chunks per lane) and forms the dot
-// product with every x row, reduced across the group; the same lanes see the
-// whole x row, so the gate/up launch also forms sum(x^2) for 1/rms. The x
-// rows are staged in LDS first (rows.h).
+// Both launches use the decode producer's layout (rows.h): a workgroup owns 16
+// output columns, the x rows are the B operand of the matrix-core products, and
+// the gate/up launch also forms sum(x^2) for 1/rms from the same x slices.
 #include "common.h"
 #include "kernels.h"
 #include "rows.h"
 
 namespace sparda {
 
-constexpr int kFfnThreads = 256;
-constexpr int kFfnGuChunks = 8;     // gate/up: C <= 1024 (two weight rows per group)
-constexpr int kFfnDownChunks = 16;  // down: F <= 2048
+constexpr int kFfnThreads = kRowsWaves * kWave;
 
 __device__ __forceinline__ float bf16_round(float v) { return static_cast<float>(static_cast<__bf16>(v)); }
 
@@ -35,49 +30,25 @@ __device__ __forceinline__ float bf16_round(float v) { return static_cast<float>
 __global__ void __launch_bounds__(kFfnThreads)
 ffn_gate_up_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __restrict__ wgu, int M, int C,
                    int F, float eps, uint16_t* __restrict__ act) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][C]
-    __shared__ float alds[kRowsMaxM][16];
+    __shared__ RowsRed<2> red;
+    __shared__ float y[2][kRowsMaxM][16];
+    __shared__ float rs[16];
     const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-    const int li = lane % 16;
-    const int lc = 4 * (tid / kWave) + lane / 16;
-    const int f = blockIdx.x * 16 + lc;
-    const int nch = C / 128;
-    uint4 w[2][kFfnGuChunks];
-    const uint16_t* gr = wgu + static_cast<int64_t>(f) * C + li * 8;
-    const uint16_t* ur = wgu + static_cast<int64_t>(F + f) * C + li * 8;
-#pragma unroll
-    for (int i = 0; i < kFfnGuChunks; ++i) {
-        if (i < nch) {
-            w[0][i] = *reinterpret_cast<const uint4*>(gr + i * 128);
-            w[1][i] = *reinterpret_cast<const uint4*>(ur + i * 128);
-        }
-    }
-    stage_rows(x, x_st, M, C, xs);
-    float acc[2][kRowsMaxM], ss[kRowsMaxM];
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) acc[0][m] = acc[1][m] = ss[m] = 0.0f;
-    rows_dot<2, kFfnGuChunks, true>(xs, M, C, nch, li, w, acc, ss);
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) {
-        if (m < M) {
-            const float ag = row16_sum(acc[0][m]);
-            const float au = row16_sum(acc[1][m]);
-            const float s2 = row16_sum(ss[m]);
-            if (li == 0) {
-                const float inv = 1.0f / __builtin_sqrtf(s2 / static_cast<float>(C) + eps);
-                const float g = bf16_round(ag * inv);
-                const float u = bf16_round(au * inv);
-                const float s = bf16_round(g / (1.0f + expf(-g)));
-                alds[m][lc] = bf16_round(s * u);
-            }
-        }
-    }
-    __syncthreads();
-    for (int t = tid; t < M * 16; t += kFfnThreads) {
-        const int m = t / 16, c = t % 16;
-        act[static_cast<int64_t>(m) * F + blockIdx.x * 16 + c] =
-            __builtin_bit_cast(uint16_t, static_cast<__bf16>(alds[m][c]));
+    const int wave = tid / kWave;
+    const int r = tid % 16;
+    const int f0 = blockIdx.x * 16;
+    const uint16_t* wrow[2] = {wgu + static_cast<int64_t>(f0 + r) * C, wgu + static_cast<int64_t>(F + f0 + r) * C};
+    f32x4 acc[2];
+    float ss;
+    rows_mfma<2>(x, x_st, M, C, wrow, wave, acc, ss);
+    rows_reduce<2>(red, acc, ss, wave, true, y, rs);
+    if (tid < M * 16) {
+        const int m = tid / 16, c = tid % 16;
+        const float inv = 1.0f / __builtin_sqrtf(rs[m] / static_cast<float>(C) + eps);
+        const float g = bf16_round(y[0][m][c] * inv);
+        const float u = bf16_round(y[1][m][c] * inv);
+        const float sl = bf16_round(g / (1.0f + expf(-g)));
+        act[static_cast<int64_t>(m) * F + f0 + c] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(sl * u));
     }
 }
 
@@ -85,51 +56,33 @@ ffn_gate_up_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t*
 __global__ void __launch_bounds__(kFfnThreads)
 ffn_down_kernel(const uint16_t* __restrict__ a, int64_t a_st, const uint16_t* __restrict__ w, int M, int K, int N,
                 const uint16_t* __restrict__ res, int64_t res_st, uint16_t* __restrict__ out, int64_t out_st) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][K]
-    __shared__ float ylds[kRowsMaxM][16];
+    __shared__ RowsRed<1> red;
+    __shared__ float y[1][kRowsMaxM][16];
     const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-    const int li = lane % 16;
-    const int lc = 4 * (tid / kWave) + lane / 16;
-    const int n = blockIdx.x * 16 + lc;
-    const int nch = K / 128;
-    uint4 wr[1][kFfnDownChunks];
-    const uint16_t* wrow = w + static_cast<int64_t>(n) * K + li * 8;
-#pragma unroll
-    for (int i = 0; i < kFfnDownChunks; ++i)
-        if (i < nch) wr[0][i] = *reinterpret_cast<const uint4*>(wrow + i * 128);
-    stage_rows(a, a_st, M, K, xs);
-    float acc[1][kRowsMaxM], unused[kRowsMaxM];
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) acc[0][m] = 0.0f;
-    rows_dot<1, kFfnDownChunks, false>(xs, M, K, nch, li, wr, acc, unused);
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) {
-        if (m < M) {
-            const float y = row16_sum(acc[0][m]);
-            if (li == 0) ylds[m][lc] = y;
-        }
-    }
-    __syncthreads();
-    for (int t = tid; t < M * 16; t += kFfnThreads) {
-        const int m = t / 16, c = t % 16;
-        const int64_t col = static_cast<int64_t>(blockIdx.x) * 16 + c;
-        const float r = __builtin_bit_cast(float, static_cast<uint32_t>(res[m * res_st + col]) << 16);
-        out[m * out_st + col] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(r + bf16_round(ylds[m][c])));
+    const int wave = tid / kWave;
+    const int n0 = blockIdx.x * 16;
+    const uint16_t* wrow[1] = {w + static_cast<int64_t>(n0 + tid % 16) * K};
+    f32x4 acc[1];
+    float ss;
+    rows_mfma<1>(a, a_st, M, K, wrow, wave, acc, ss);
+    rows_reduce<1>(red, acc, ss, wave, false, y, nullptr);
+    if (tid < M * 16) {
+        const int m = tid / 16, c = tid % 16;
+        const int64_t col = n0 + c;
+        const float rv = __builtin_bit_cast(float, static_cast<uint32_t>(res[m * res_st + col]) << 16);
+        out[m * out_st + col] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(rv + bf16_round(y[0][m][c])));
     }
 }
 
 int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const void* w_down, int64_t M,
                       int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream) {
-    hipLaunchKernelGGL(ffn_gate_up_kernel, dim3(static_cast<unsigned>(F / 16)), dim3(kFfnThreads),
-                       static_cast<size_t>(M * C) * 2, stream,
+    hipLaunchKernelGGL(ffn_gate_up_kernel, dim3(static_cast<unsigned>(F / 16)), dim3(kFfnThreads), 0, stream,
                        static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w_gate_up),
                        static_cast<int>(M), static_cast<int>(C), static_cast<int>(F), eps,
                        static_cast<uint16_t*>(act));
     int rc = check_hip(hipGetLastError(), "ffn_gate_up_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(C / 16)), dim3(kFfnThreads),
-                       static_cast<size_t>(M * F) * 2, stream,
+    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(C / 16)), dim3(kFfnThreads), 0, stream,
                        static_cast<const uint16_t*>(act), F, static_cast<const uint16_t*>(w_down),
                        static_cast<int>(M), static_cast<int>(F), static_cast<int>(C),
                        static_cast<const uint16_t*>(x), x_st, static_cast<uint16_t*>(out), out_st);
@@ -142,44 +95,28 @@ int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const 
 __global__ void __launch_bounds__(kFfnThreads)
 norm_gemv_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __restrict__ w, int M, int C,
                  float eps, uint16_t* __restrict__ out, int64_t out_st) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][C]
-    __shared__ float ylds[kRowsMaxM][16];
+    __shared__ RowsRed<1> red;
+    __shared__ float y[1][kRowsMaxM][16];
+    __shared__ float rs[16];
     const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-    const int li = lane % 16;
-    const int lc = 4 * (tid / kWave) + lane / 16;
-    const int n = blockIdx.x * 16 + lc;
-    const int nch = C / 128;
-    uint4 wr[1][kFfnGuChunks];
-    const uint16_t* wrow = w + static_cast<int64_t>(n) * C + li * 8;
-#pragma unroll
-    for (int i = 0; i < kFfnGuChunks; ++i)
-        if (i < nch) wr[0][i] = *reinterpret_cast<const uint4*>(wrow + i * 128);
-    stage_rows(x, x_st, M, C, xs);
-    float acc[1][kRowsMaxM], ss[kRowsMaxM];
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) acc[0][m] = ss[m] = 0.0f;
-    rows_dot<1, kFfnGuChunks, true>(xs, M, C, nch, li, wr, acc, ss);
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) {
-        if (m < M) {
-            const float a = row16_sum(acc[0][m]);
-            const float s2 = row16_sum(ss[m]);
-            if (li == 0) ylds[m][lc] = a / __builtin_sqrtf(s2 / static_cast<float>(C) + eps);
-        }
-    }
-    __syncthreads();
-    for (int t = tid; t < M * 16; t += kFfnThreads) {
-        const int m = t / 16, c = t % 16;
-        out[m * out_st + static_cast<int64_t>(blockIdx.x) * 16 + c] =
-            __builtin_bit_cast(uint16_t, static_cast<__bf16>(ylds[m][c]));
+    const int wave = tid / kWave;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const uint16_t* wrow[1] = {w + (n0 + tid % 16) * C};
+    f32x4 acc[1];
+    float ss;
+    rows_mfma<1>(x, x_st, M, C, wrow, wave, acc, ss);
+    rows_reduce<1>(red, acc, ss, wave, true, y, rs);
+    if (tid < M * 16) {
+        const int m = tid / 16, c = tid % 16;
+        const float v = y[0][m][c] / __builtin_sqrtf(rs[m] / static_cast<float>(C) + eps);
+        out[m * out_st + n0 + c] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
     }
 }
 
 int launch_norm_gemv(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t N, float eps,
                      void* out, int64_t out_st, hipStream_t stream) {
-    hipLaunchKernelGGL(norm_gemv_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads),
-                       static_cast<size_t>(M * C) * 2, stream, static_cast<const uint16_t*>(x), x_st,
+    hipLaunchKernelGGL(norm_gemv_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads), 0, stream,
+                       static_cast<const uint16_t*>(x), x_st,
                        static_cast<const uint16_t*>(w), static_cast<int>(M), static_cast<int>(C), eps,
                        static_cast<uint16_t*>(out), out_st);
     return check_hip(hipGetLastError(), "norm_gemv_kernel");
@@ -187,8 +124,8 @@ int launch_norm_gemv(const void* x, int64_t x_st, const void* w, int64_t M, int6
 
 int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, int64_t K, int64_t N,
                          const void* res, int64_t res_st, void* out, int64_t out_st, hipStream_t stream) {
-    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads),
-                       static_cast<size_t>(M * K) * 2, stream, static_cast<const uint16_t*>(a), a_st,
+    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kFfnThreads), 0, stream,
+                       static_cast<const uint16_t*>(a), a_st,
                        static_cast<const uint16_t*>(w), static_cast<int>(M), static_cast<int>(K),
                        static_cast<int>(N), static_cast<const uint16_t*>(res), res_st, static_cast<uint16_t*>(out),
                        out_st);

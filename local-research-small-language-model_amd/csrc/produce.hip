@@ -187,15 +187,11 @@ produce_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __r
 // Decode shapes (M <= kRowsMaxM rows, a few tokens): the tiled kernel would
 // run N/128 workgroups and stream all of W' through a dozen CUs. Here a
 // workgroup owns 16 columns of one head (8 RoPE pairs: d0+p and d0+p+32,
-// p < 8), so N/16 workgroups share the weight read; the x rows are staged in
-// LDS, a 16-lane group per column holds the column's row of W' in registers
-// (C/128 16-byte chunks per lane) and takes the dot product with every x row,
-// reduced across the group. The same lanes see all of x's row, so each group
-// also forms sum(x^2) for 1/rms. Results go through LDS to the threads that
+// p < 8), so N/16 workgroups share the weight read; the 16 columns' rows of W'
+// are the A operand of matrix-core products with the x rows (rows.h), which
+// also yield sum(x^2) for 1/rms. Results go through LDS to the threads that
 // rotate and store the pairs.
 // ---------------------------------------------------------------------------
-constexpr int kRowsChunks = 16;     // C / 128 <= 16 (C <= 2048)
-
 template <int FDT>
 __global__ void __launch_bounds__(kPThreads)
 produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __restrict__ w, int M, int C,
@@ -204,34 +200,24 @@ produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t
                     uint16_t* __restrict__ k, uint16_t* __restrict__ v, void* __restrict__ f,
                     const int64_t* __restrict__ pos_dev, int64_t rope_len, uint16_t* __restrict__ kc,
                     uint16_t* __restrict__ vc, int64_t c_sb, int64_t c_st, int64_t c_sh, int64_t cap) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][C]
-    __shared__ float ylds[kRowsMaxM][16];
+    static_assert(kPThreads == kRowsWaves * kWave, "one rows_mfma workgroup");
+    __shared__ RowsRed<1> red;
+    __shared__ float ylds[1][kRowsMaxM][16];
+    __shared__ float rs[16];
     const int tid = threadIdx.x;
-    const int lane = tid % kWave;
     const int wave = tid / kWave;
-    const int li = lane % 16;
-    const int lc = 4 * wave + lane / 16;             // local column: pair lc/2, half lc%2
     const int nh = (blockIdx.x / 4) * 64;            // first column of the head
     const int d0 = (blockIdx.x % 4) * 8;
-    const int n = nh + d0 + lc / 2 + 32 * (lc % 2);  // row of W'
-    const int nch = C / 128;
-    uint4 wreg[1][kRowsChunks];
-    const uint16_t* wr = w + static_cast<int64_t>(n) * C + li * 8;
-#pragma unroll
-    for (int i = 0; i < kRowsChunks; ++i)
-        if (i < nch) wreg[0][i] = *reinterpret_cast<const uint4*>(wr + i * 128);
-    stage_rows(x, x_st, M, C, xs);
-    float acc[1][kRowsMaxM], ss[kRowsMaxM];
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) acc[0][m] = ss[m] = 0.0f;
-    rows_dot<1, kRowsChunks, true>(xs, M, C, nch, li, wreg, acc, ss);
-#pragma unroll
-    for (int m = 0; m < kRowsMaxM; ++m) {
-        if (m < M) {
-            const float a = row16_sum(acc[0][m]);
-            const float s2 = row16_sum(ss[m]);
-            if (li == 0) ylds[m][lc] = a / __builtin_sqrtf(s2 / static_cast<float>(C) + eps);
-        }
+    // local column lc = tile row: pair lc/2, half lc%2
+    const int lr = tid % 16;
+    const uint16_t* wrow[1] = {w + static_cast<int64_t>(nh + d0 + lr / 2 + 32 * (lr % 2)) * C};
+    f32x4 acc[1];
+    float ss;
+    rows_mfma<1>(x, x_st, M, C, wrow, wave, acc, ss);
+    rows_reduce<1>(red, acc, ss, wave, true, ylds, rs);
+    if (tid < M * 16) {
+        const int m = tid / 16, c = tid % 16;
+        ylds[0][m][c] = ylds[0][m][c] / __builtin_sqrtf(rs[m] / static_cast<float>(C) + eps);
     }
     __syncthreads();
 
@@ -246,7 +232,7 @@ produce_rows_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t
     const int64_t pos_hi = pos_dev != nullptr ? rope_len - 1 : INT64_MAX;
     for (int t = tid; t < M * 8; t += kPThreads) {
         const int m = t / 8, p = t % 8;
-        float y1 = ylds[m][2 * p], y2 = ylds[m][2 * p + 1];
+        float y1 = ylds[0][m][2 * p], y2 = ylds[0][m][2 * p + 1];
         const int d = d0 + p;
         if (region <= 1) {
             int64_t pos = pos_base + m % T;
@@ -280,8 +266,8 @@ int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_
                    const int64_t* pos_dev, int64_t rope_len, void* kc, void* vc, int64_t c_sb, int64_t c_st,
                    int64_t c_sh, int64_t cap) {
     const int64_t N = Nq + 2 * Nk + Nf;
-    if (M <= kRowsMaxM && C % 128 == 0 && C / 128 <= kRowsChunks) {
-        const size_t lds = static_cast<size_t>(M * C) * 2;
+    if (M <= kRowsMaxM && C % 128 == 0 && C / 128 <= kRowsWaves * kRowsMaxKB) {
+        const size_t lds = 0;
 #define SPARDA_PRODUCE_ROWS(FDT_)                                                                            \
     hipLaunchKernelGGL((produce_rows_kernel<FDT_>), dim3(static_cast<unsigned>(N / 16)), dim3(kPThreads), lds, \
                        stream, static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w),        \
