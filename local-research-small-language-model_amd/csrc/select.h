@@ -236,15 +236,17 @@ __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
     return T;
 }
 
-// wave_select with a candidate pre-filter. T0 = the k-th largest of the 64
-// lane maxima bounds the k-th largest key from below (the k lanes whose
-// maximum is >= T0 hold k keys >= T0; the keys fill lanes 0.. first, so at
-// least min(n, 64) >= k lanes hold one), hence the top-k lies among the keys
-// >= T0. When those fit in one register per lane they are compacted in index
-// order through ck_lds / ci_lds (64 entries each) and the 32-round threshold
-// search runs on that one register instead of CH: the ballot search costs
-// ~40 cycles per key register per round. Otherwise wave_select runs as is.
-// Same result as wave_select; called by a whole wavefront (wave-uniform flow).
+// wave_select with a candidate pre-filter. A lower bound T0 of the k-th
+// largest key (at least k keys are >= T0) confines the top-k to the keys
+// >= T0: the minimum of G >= k group maxima, or, when that admits more than
+// 64 keys, the k-th largest of the 64 lane maxima (the k lanes whose maximum
+// is >= T0 hold k keys >= T0; the keys fill lanes 0.. first, so at least
+// min(n, 64) >= k lanes hold one). When the keys >= T0 fit in one register
+// per lane they are compacted in index order through ck_lds / ci_lds (64
+// entries each) and ranked against each other (C lane reads instead of the
+// threshold search's 32 ballot rounds over CH key registers, ~40 cycles per
+// register per round). Otherwise wave_select runs as is. Same result as
+// wave_select; called by a whole wavefront (wave-uniform flow).
 template <int CH>
 __device__ __forceinline__ int wave_select_pre(const uint32_t (&kreg)[CH], int n, int k, int own,
                                                int32_t* sel_lds, uint32_t* ck_lds, int32_t* ci_lds) {
@@ -252,10 +254,32 @@ __device__ __forceinline__ int wave_select_pre(const uint32_t (&kreg)[CH], int n
     uint32_t lm = kreg[0];
 #pragma unroll
     for (int e = 1; e < CH; ++e) lm = kreg[e] > lm ? kreg[e] : lm;
-    const uint32_t T0 = wave_kth_largest(lm, k);
+    // First a cheaper bound: the lanes form G >= k groups (G a power of two),
+    // and the smallest of the G group maxima has at least G >= k keys at or
+    // above it (one per group). Six lane exchanges instead of a search.
+    int G = 1;
+    while (G < k && G < kWave) G <<= 1;
+    const int gs = kWave / G;
+    uint32_t gm = lm;
+    for (int o = 1; o < gs; o <<= 1) {
+        const uint32_t x = static_cast<uint32_t>(__shfl_xor(static_cast<int>(gm), o, kWave));
+        gm = x > gm ? x : gm;
+    }
+    for (int o = gs; o < kWave; o <<= 1) {
+        const uint32_t x = static_cast<uint32_t>(__shfl_xor(static_cast<int>(gm), o, kWave));
+        gm = x < gm ? x : gm;
+    }
+    uint32_t T0 = __builtin_amdgcn_readfirstlane(gm);
     int C = 0;
 #pragma unroll
     for (int e = 0; e < CH; ++e) C += ballot_count(kreg[e] >= T0);
+    if (C > kWave) {
+        // too many keys at or above it: the k-th largest lane maximum
+        T0 = wave_kth_largest(lm, k);
+        C = 0;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) C += ballot_count(kreg[e] >= T0);
+    }
     if (C > kWave) return wave_select<CH>(kreg, n, k, own, sel_lds);
     const uint64_t lanes_below = (1ull << lane) - 1ull;
     int base = 0;
@@ -272,18 +296,16 @@ __device__ __forceinline__ int wave_select_pre(const uint32_t (&kreg)[CH], int n
     __builtin_amdgcn_wave_barrier();  // LDS operations of one wavefront complete in order
     const uint32_t ck = lane < C ? ck_lds[lane] : 0u;
     const int ci = lane < C ? ci_lds[lane] : 0x7fffffff;
-    const uint32_t T = wave_kth_largest(ck, k);
-    int need_eq = k - ballot_count(ck > T);
-    uint64_t eq = __builtin_amdgcn_ballot_w64(ck == T);
-    uint64_t keep = 0;
-    for (; need_eq > 0 && eq != 0; --need_eq) {
-        const uint64_t low = eq & (~eq + 1ull);
-        keep |= low;
-        eq ^= low;
+    // the candidates' ranks (keys above, equal keys at lower index: lanes are
+    // in index order); the top k are the ranks below k
+    int rank = 0;
+    for (int j = 0; j < C; ++j) {
+        const uint32_t kj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ck), j));
+        rank += (kj > ck || (kj == ck && j < lane)) ? 1 : 0;
     }
     // candidates are in ascending index order, all <= own when taken: the
     // sink block 0 goes first and the own block last unless already taken
-    const uint64_t take = (__builtin_amdgcn_ballot_w64(ck > T) | keep) & __builtin_amdgcn_ballot_w64(ci <= own);
+    const uint64_t take = __builtin_amdgcn_ballot_w64(lane < C && rank < k) & __builtin_amdgcn_ballot_w64(ci <= own);
     const bool mine = (take >> lane) & 1ull;
     const bool has0 = __builtin_amdgcn_ballot_w64(mine && ci == 0) != 0;
     const bool has_own = __builtin_amdgcn_ballot_w64(mine && ci == own) != 0;
