@@ -3,7 +3,8 @@
  * forecast scorer, top-k selector and selection-set rules.
  *
  * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load this library, and only as the checker. The
+ * cpu_baseline leg may load this library, and only as the reference results
+ * are compared with. The
  * product (libsparda.so and the Python package) never links or calls it.
  *
  * Arithmetic contract (shared with the HIP kernels so that results are

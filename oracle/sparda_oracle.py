@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
-checker (or as the timed CPU baseline). The product path never imports it.
+reference results are compared with (or as the timed CPU baseline). The product path never imports it.
 
 What it restates (citations into tyborra/local-research-Small-Language-Model):
 

@@ -223,7 +223,7 @@ def test_prefill_full_size_sampled_rows():
 
 def test_prefill_long_context_16k_sampled_rows_and_selection_invariants():
     # T = 16384 (256 blocks): the reference switches to its chunked path above
-    # 8192 tokens; this build keeps the per-token rule, checked here against the
+    # 8192 tokens; this library keeps the per-token rule, checked here against the
     # oracle on sampled rows, plus the invariants of every selection list
     case("prefill B=1 T=16384 sampled")
     T, bs, k = 16384, 64, 8
