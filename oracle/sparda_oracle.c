@@ -4,8 +4,8 @@
  *
  * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load this library, and only as the reference results
- * are compared with. The
- * product (libsparda.so and the Python package) never links or calls it.
+ * are compared with. The product (libsparda.so and the Python package) never
+ * links or calls it.
  *
  * Arithmetic contract (shared with the HIP kernels so that results are
  * bit-comparable):
