@@ -118,7 +118,8 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
                                           int32_t (&picks)[KMAX]) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x % kWave;
-    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    // the wave within its group of kRouteWaves (a workgroup may route several sets at once)
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>((threadIdx.x / kWave) % kRouteWaves));
     const float* __restrict__ pbh = protos + (static_cast<int64_t>(b) * NB * H + h) * DF;
     const int64_t pstride = static_cast<int64_t>(H) * DF;
     const int64_t t = set * kWave + lane;
