@@ -128,8 +128,10 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
     const int64_t t_last = (set * kWave + kWave < Tq ? set * kWave + kWave : Tq) - 1;
     int64_t limit = causal ? (score_pos0 + tc) / bs : NB - 1;
     if (limit > NB - 1) limit = NB - 1;
-    int64_t jmax = causal ? (score_pos0 + t_last) / bs : NB - 1;  // uniform
-    if (jmax > NB - 1) jmax = NB - 1;
+    int64_t jmax64 = causal ? (score_pos0 + t_last) / bs : NB - 1;
+    if (jmax64 > NB - 1) jmax64 = NB - 1;
+    // uniform: the block loop and the prototype addresses stay on the scalar unit
+    const int jmax = __builtin_amdgcn_readfirstlane(static_cast<int>(jmax64));
 
     float fr[DF];
     {
@@ -144,34 +146,54 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
     best.init();
     constexpr int E = DF / 16;
     constexpr int C = 2;  // blocks scored side by side
-    const float* __restrict__ prow = pbh + (lane % 16) * E;
-    float pn[C][E];
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const int64_t jc = w + c * kRouteWaves;
-        load_f32<E>(prow + (jc < jmax ? jc : jmax) * pstride, pn[c]);
-    }
-    for (int64_t j = w; j <= jmax; j += C * kRouteWaves) {
-        float pc[E][C];
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) pc[e][c] = pn[c][e];
-            const int64_t jn = j + (C + c) * kRouteWaves;
-            load_f32<E>(prow + (jn < jmax ? jn : jmax) * pstride, pn[c]);
-        }
+    const int loff = (lane % 16) * E;  // this lane's elements of a prototype row
+    // prototype row of block min(jc, jmax) (a wave-uniform address), this lane's E elements
+    auto load_proto = [&](int jc, float (&o)[E]) __attribute__((always_inline)) {
+        const float* __restrict__ pb = pbh + static_cast<int64_t>(jc < jmax ? jc : jmax) * pstride;
+        load_f32<E>(pb + loff, o);
+    };
+    // scores blocks j, j + kRouteWaves, ... (C of them, prototypes in pc) and
+    // pushes their keys
+    auto score = [&](int j, const float (&pc)[E][C]) __attribute__((always_inline)) {
         float acc[C];
 #pragma unroll
         for (int c = 0; c < C; ++c) acc[c] = 0.0f;
         row_fma_chains<E, DF, C>(fr, pc, acc);
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            const int64_t jc = j + c * kRouteWaves;
+            const int jc = j + c * kRouteWaves;
             const float sc = acc[c] * scale;
             const bool ok = jc <= limit;  // limit <= jmax
             if (srow && ok) srow[jc] = sc;
             best.push(ok ? route_key(sc, static_cast<int32_t>(jc)) : 0.0);
         }
+    };
+    // two prototype buffers used in turn, each loaded one step ahead of its use
+    constexpr int kStep = C * kRouteWaves;
+    float pa[E][C], pz[E][C];
+    float tmp[E];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        load_proto(w + c * kRouteWaves, tmp);
+#pragma unroll
+        for (int e = 0; e < E; ++e) pa[e][c] = tmp[e];
+    }
+    for (int j = w; j <= jmax; j += 2 * kStep) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            load_proto(j + kStep + c * kRouteWaves, tmp);
+#pragma unroll
+            for (int e = 0; e < E; ++e) pz[e][c] = tmp[e];
+        }
+        score(j, pa);
+        if (j + kStep > jmax) break;  // uniform
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            load_proto(j + 2 * kStep + c * kRouteWaves, tmp);
+#pragma unroll
+            for (int e = 0; e < E; ++e) pa[e][c] = tmp[e];
+        }
+        score(j + kStep, pz);
     }
     if (srow) {
         for (int64_t j = w; j < NB; j += kRouteWaves)
