@@ -102,15 +102,14 @@ struct CompactSmem {
     // block -> union map and per-token facts.
     float4 acc[16 * kCols];
     uint16_t vstage[Win<W>::kWaves][32 * 64];   // half a V block per wave, swizzled
-    TokMask<W> umask[kMaxUnion];                // tokens selecting union block u
     uint32_t items[kMaxItems];                  // u | first tile << 16
     float mref[kCols];                          // log2 units
     float lsum[kCols];                          // row sums (exact-max pass: order keys)
     int32_t vers[kCols];                        // blocks added to the column so far
     uint16_t ulist[kMaxUnion];                  // block index of union entry u
-    uint16_t uofs[kMaxUnion + 1];               // rank records of u start here
-    uint8_t rankbuf[Win<W>::kMaxPairs];         // rank of block u in a token's list
-    uint8_t tokrank[Win<W>::kWaves][W];         // selecting token of each rank
+    uint16_t uofs[kMaxUnion + 1];               // records of union block u: uofs[u] .. uofs[u+1]-1
+    uint8_t rankbuf[Win<W>::kMaxPairs];         // per record: rank of the block in the token's list
+    uint8_t toklist[Win<W>::kMaxPairs];         // per record: the selecting token (ascending)
     int n_union, n_items, next_item, flag;
 };
 
@@ -288,7 +287,6 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 const int pos = nu + __popcll(bal & below);
                 const int item0 = ni + sc - chunks;
                 sm.ulist[pos] = static_cast<uint16_t>(j);
-                sm.umask[pos] = M;
                 sm.uofs[pos] = static_cast<uint16_t>(nrk + sr - rk);
                 jmap[j] = static_cast<uint16_t>(pos);
                 for (int cc = 0; cc < chunks; ++cc)
@@ -314,8 +312,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         for (int i = 0; i < kCMaxCap; ++i) {
             if (lst[i] != kSentinel) {
                 const int u = jmap[lst[i]];
-                const int p = mask_count_below(sm.umask[u], tok);
-                sm.rankbuf[sm.uofs[u] + p] = static_cast<uint8_t>(i);
+                const int e = sm.uofs[u] + mask_count_below(bitmap[lst[i]], tok);
+                sm.rankbuf[e] = static_cast<uint8_t>(i);
+                sm.toklist[e] = static_cast<uint8_t>(tok);
             }
         }
     }
@@ -383,7 +382,6 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     };
 
     uint16_t* vst = sm.vstage[wave];
-    uint8_t* trk = sm.tokrank[wave];
     const int rsub = 4 * grp + col16 / 4;
     const int csub = 4 * (col16 % 4);
 
@@ -394,14 +392,14 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         int qoff;   // element offset of the slot's q row (+ 8 grp) from qbase
         bool valid;
     };
-    auto slot = [&](int i, int ncol) __attribute__((always_inline)) -> Slot {
+    auto slot = [&](int i, int ncol, int rofs) __attribute__((always_inline)) -> Slot {
         const int e = 16 * i + col16;
         Slot s_;
         s_.valid = e < ncol;
         const int ei = s_.valid ? e : ncol - 1;  // padding slots repeat the last column, masked
         s_.tr = ei / R;
         const int h = ei - s_.tr * R;
-        const int tk = trk[s_.tr];
+        const int tk = sm.toklist[rofs + s_.tr];
         s_.c = tk * R + h;
         s_.qoff = tk * q_st32 + h * q_sh32 + 8 * grp;
         return s_;
@@ -421,20 +419,10 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         const int u = item & 0xffff;
         const int i0 = item >> 16;
         const int j = sm.ulist[u];
-        const Mask M = sm.umask[u];
-        const int ncol = R * mask_count(M);
+        const int rofs = sm.uofs[u];
+        const int ncol = R * (sm.uofs[u + 1] - rofs);
         const int tiles = (ncol + 15) / 16;
         const int nt = (i0 + kCChunk < tiles ? i0 + kCChunk : tiles) - i0;  // 1 .. kCChunk
-        const int rofs = sm.uofs[u];
-        {
-            int base = 0;
-#pragma unroll
-            for (int i = 0; i < W / 64; ++i) {
-                if ((M.w[i] >> lane) & 1ull) trk[base + __popcll(M.w[i] & below)] = static_cast<uint8_t>(64 * i + lane);
-                base += __popcll(M.w[i]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
         // causal: a block that ends past the window's first token holds keys
         // beyond some selecting tokens (key j*BS + i is allowed up to token t0 + tk)
         const bool diag = causal && (static_cast<int64_t>(j) + 1) * BS - 1 > t0;
@@ -448,7 +436,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
-                sl[t] = slot(i0 + t, ncol);
+                sl[t] = slot(i0 + t, ncol, rofs);
                 qa[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff);
                 qc[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff + 32);
                 rank[t] = sm.rankbuf[rofs + sl[t].tr];
