@@ -1,10 +1,10 @@
 // bf16 block-sparse GQA prefill over compacted tiles (D = 64, KV blocks of
 // BS = 64 or 32 keys, at most 10 selected blocks per token).
 //
-// One workgroup serves one (sequence b, KV head g, query window qb): W = 128
-// query tokens (8 wavefronts; 64 tokens and 4 wavefronts where the LDS of 128
-// does not fit: R = 4 or more than 512 KV blocks) x R = Hq/Hkv query heads =
-// W*R columns, column c = token * R + head. Every query token picks its own blocks, so a KV block
+// One workgroup of 12 wavefronts (one per CU, three per SIMD) serves one
+// (sequence b, KV head g, query window qb): W = 128 query tokens (64 for
+// R = 4, whose 128-token accumulators would not fit the LDS) x R = Hq/Hkv
+// query heads = W*R columns, column c = token * R + head. Every query token picks its own blocks, so a KV block
 // is attended by only some of the window's columns. For each block j in the
 // union of the window's selections, the columns that selected j are packed,
 // in token order, into tiles of 16 (the N side of v_mfma_f32_16x16x32_bf16):
@@ -44,15 +44,21 @@ namespace {
 constexpr int kCMaxCap = 10;                    // selection entries per token
 constexpr int kCChunk = 2;                      // tiles per work item
 
-// a query window of W tokens (64 or 128) per workgroup of W/16 wavefronts
+constexpr int kCMaxNB = 1024;                   // KV blocks
+// wavefronts per workgroup: one workgroup per CU, three wavefronts per SIMD
+constexpr int kCWaves = 12;
+constexpr int kCThreads = kCWaves * kWave;
+
+// a query window of W tokens (128; 64 for R = 4, whose accumulators for 128
+// tokens would not fit the LDS) per workgroup. Its 64-token sets are routed
+// by kSetWaves waves each, whose first wave then holds the set's tokens
+// (lane = token) through the set-up.
 template <int W>
 struct Win {
     static_assert(W == 64 || W == 128, "windows of 64 or 128 tokens");
-    static constexpr int kThreads = 4 * W;
-    static constexpr int kWaves = kThreads / kWave;
-    static constexpr int kMaxNB = W == 64 ? 1024 : 512;          // KV blocks (bitmap set-up)
     static constexpr int kMaxPairs = W * kCMaxCap;               // (token, block) pairs of a window
-    static constexpr int kMaxUnion = kMaxPairs < kMaxNB ? kMaxPairs : kMaxNB;  // distinct blocks
+    static constexpr int kMaxUnion = kMaxPairs < kCMaxNB ? kMaxPairs : kCMaxNB;  // distinct blocks
+    static constexpr int kSetWaves = kCWaves / (W / 64);
 };
 
 // the tokens of a window that selected a block: bit t of word t / 64
@@ -101,7 +107,7 @@ struct CompactSmem {
     // During the set-up the same bytes hold the per-block token bitmaps, the
     // block -> union map and per-token facts.
     float4 acc[16 * kCols];
-    uint16_t vstage[Win<W>::kWaves][32 * 64];   // half a V block per wave, swizzled
+    uint16_t vstage[kCWaves][32 * 64];          // half a V block per wave, swizzled
     uint32_t items[kMaxItems];                  // u | first tile << 16
     float mref[kCols];                          // log2 units
     float lsum[kCols];                          // row sums (exact-max pass: order keys)
@@ -125,16 +131,16 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 
 }  // namespace
 
-// W = 64: two workgroups per CU for R <= 3 (their LDS fits twice), one for
-// R = 4; W = 128 (R <= 3): one workgroup of 8 wavefronts per CU, whose tiles
-// are fuller when each token's selections are spread over many blocks.
+// W = 128 (R <= 3) or 64 (R = 4): one workgroup of 12 wavefronts per CU; the
+// wider window's tiles are fuller when each token's selections are spread
+// over many blocks.
 // BS: keys per KV block (64 or 32).
 // FDT < 0: the token lists come from sel / n_sel. FDT = the forecast's dtype:
 // the kernel routes its own window first (the router's per-set code, so the
 // lists are the router's bit for bit) and, with rt.sel set, also writes them
 // out as the router does.
 template <int R, int BS, int FDT, int W>
-__global__ void __launch_bounds__(Win<W>::kThreads, W == 64 && R <= 3 ? 2 : 1)
+__global__ void __launch_bounds__(kCThreads, 1)
 prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                        const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                        int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
@@ -144,8 +150,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     using Smem = CompactSmem<R, W>;
     using Mask = TokMask<W>;
     constexpr int kCols = Smem::kCols;
-    constexpr int kT = Win<W>::kThreads;
-    constexpr int kMaxNB = Win<W>::kMaxNB;
+    constexpr int kT = kCThreads;
+    constexpr int kSetWaves = Win<W>::kSetWaves;
+    constexpr int kMaxNB = kCMaxNB;
     __shared__ Smem sm;
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
@@ -153,9 +160,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     const int col16 = lane % 16;
     const int grp = lane / 16;
     const uint64_t below = (1ull << lane) - 1ull;
-    // token tok of the window is held by lane tok % 64 of wave 4 (tok / 64)
-    const bool owner = wave % 4 == 0;
-    const int tok = (wave / 4) * 64 + lane;
+    // token tok of the window is held by lane tok % 64 of wave kSetWaves * (tok / 64)
+    const bool owner = wave % kSetWaves == 0;
+    const int tok = (wave / kSetWaves) * 64 + lane;
 
     // heaviest query blocks first; consecutive ids cycle through (b, g)
     const int64_t BH = static_cast<int64_t>(gridDim.x) / NBq;
@@ -178,6 +185,8 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     // element offsets inside a window / a block fit in 32 bits (checked by the host)
     const int q_st32 = static_cast<int>(q_st), q_sh32 = static_cast<int>(q_sh), kv_st32 = static_cast<int>(kv_st);
 
+    static_assert(kMaxNB * (sizeof(Mask) + sizeof(uint16_t)) <= sizeof(sm.acc), "set-up aliases fit in acc");
+    static_assert(sizeof(Smem) <= 160 * 1024, "one workgroup's LDS");
     Mask* bitmap = reinterpret_cast<Mask*>(sm.acc);                   // [kMaxNB], set-up only
     uint16_t* jmap = reinterpret_cast<uint16_t*>(bitmap + kMaxNB);    // [kMaxNB], set-up only
 
@@ -188,15 +197,16 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     // blocks past the token's own (no key of theirs is allowed) are dropped
     const int tlim = static_cast<int>(causal ? (t0 + tok) / BS : NB - 1);
     if constexpr (FDT >= 0) {
-        // each group of four waves routes 64 of the window's tokens, every
-        // wave scoring a quarter of the candidate blocks; the group's first
-        // wave merges (through the group's V staging bytes, unused until the
-        // tiles) and holds token tok's picks
+        // each group of kSetWaves waves routes 64 of the window's tokens,
+        // every wave scoring its share of the candidate blocks; the group's
+        // first wave merges (through the group's V staging bytes, unused
+        // until the tiles: 4 KB per wave, one wave's key lists) and holds
+        // token tok's picks
         int32_t picks[kCRouteK];
-        if (route_set<FDT, kCRouteDf, kCRouteK>(rt.f, rt.fsb, rt.fst, rt.fsh, rt.protos, b, g, H,
-                                                qb * (W / 64) + wave / 4, T, NB, BS, rt.ke, causal, 0, rt.scale,
-                                                nullptr, 0, reinterpret_cast<double*>(&sm.vstage[4 * (wave / 4)][0]),
-                                                picks) &&
+        if (route_set<FDT, kCRouteDf, kCRouteK, kSetWaves>(
+                rt.f, rt.fsb, rt.fst, rt.fsh, rt.protos, b, g, H, qb * (W / 64) + wave / kSetWaves, T, NB, BS,
+                rt.ke, causal, 0, rt.scale, nullptr, 0,
+                reinterpret_cast<double*>(&sm.vstage[kSetWaves * (wave / kSetWaves)][0]), picks) &&
             tok < t_valid) {
             // {0, own} U picks, own = the token's block (prefill positions start at 0)
             const int own = static_cast<int>((t0 + tok) / BS);
@@ -407,15 +417,18 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 
     // one work item (packed word: union entry u | first tile i0 << 16): the
     // up to kCChunk tiles [i0, i1) of union block u, processed phase by phase
-    // so that their latencies overlap: q loads, S = K Q^T, references and P,
-    // O = V^T P^T, then one wait and one read-add-write of every column.
-    // kr holds the block's K operands and is reloaded with item word nxt's
-    // once the products are issued; vr holds its V rows and is reloaded with
-    // nxt's once staged.
+    // so that their latencies overlap: K, V and q loads, S = K Q^T, references
+    // and P, O = V^T P^T, then one wait and one read-add-write of every
+    // column. (The loads are not issued an item ahead: three waves per SIMD
+    // cover their latency, and the registers that would hold the next item's
+    // K and V are what lets the third wave fit.)
     // mode 0: P against the column's reference, which the column's first block
     //         sets to its own column maximum; 1: scores only, exact column
     //         maxima; 2: P against the exact maxima of mode 1
-    auto process = [&](int item, u32x4 (&kr)[kKR], u32x4 (&vr)[kVR], int nxt, int mode) __attribute__((always_inline)) {
+    auto process = [&](int item, int mode) __attribute__((always_inline)) {
+        u32x4 kr[kKR], vr[kVR];
+        load_k(item, kr);
+        load_v(item, vr);
         const int u = item & 0xffff;
         const int i0 = item >> 16;
         const int j = sm.ulist[u];
@@ -459,7 +472,6 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 }
             }
         }
-        load_k(nxt, kr);  // the next item's K operands, in flight from here
         // V^T operands: stage each half of the block, read it transposed
         bf16x8 va[4][kHalf];
 #pragma unroll
@@ -479,7 +491,6 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             }
         }
         __builtin_amdgcn_wave_barrier();
-        load_v(nxt, vr);  // unconditional (nxt repeats item at the end): the registers stay registers
 
         // masks, references, P
         bool own[kCChunk];
@@ -618,27 +629,13 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 __hip_atomic_store(&sm.vers[sl[t].c], rank[t] + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
 
-    // every wave takes items until none is left; each item's K and V are
-    // loaded while the item before it is computed
-    auto run = [&](int mode) {
+    // every wave takes items until none is left
+    auto run = [&](int mode) __attribute__((always_inline)) {
         const int n_items = sm.n_items;
-        // work item index -> packed item word; past the end: the current word
-        // again (loads stay in bounds)
-        auto word = [&](int idx, int fallback) -> int {
-            return idx < n_items ? static_cast<int>(sm.items[idx]) : fallback;
-        };
-        u32x4 kr[kKR], vr[kVR];
-        int cur_i = grab();
-        if (cur_i >= n_items) return;
-        int cur = word(cur_i, 0);
-        load_k(cur, kr);
-        load_v(cur, vr);
         while (true) {
-            const int nxt_i = grab();
-            const int nxt = word(nxt_i, cur);
-            process(cur, kr, vr, nxt, mode);
-            if (nxt_i >= n_items) break;
-            cur = nxt;
+            const int idx = grab();
+            if (idx >= n_items) break;
+            process(static_cast<int>(sm.items[idx]), mode);
         }
     };
 
@@ -704,22 +701,18 @@ static bool compact_layout_ok(int64_t R, int64_t q_sb, int64_t q_st, int64_t q_s
     return true;
 }
 
-// 128-token windows wherever their LDS fits (R <= 3, at most 512 KV blocks):
-// twice the tokens fill the tiles of each selected block, and one
-// workgroup of 8 wavefronts per CU keeps two per SIMD as two 64-token
-// workgroups did. Measured faster at every tested length (B=4 T=4096:
-// 140.9 against 149.5 us; B=1 T=16384: 195.2 against 239.7 us), with the same
-// output bit for bit (each column's sums do not depend on its tile mates).
-static int pick_window(int64_t T, int64_t bs, int64_t R) {
-    return (R <= 3 && cdiv(T, bs) <= Win<128>::kMaxNB) ? 128 : 64;
-}
+// 128-token windows wherever their LDS fits (R <= 3): twice the tokens of a
+// 64-token window fill the tiles of each selected block. Measured faster at
+// every tested length, with the same output bit for bit (each column's sums do
+// not depend on its tile mates).
+static int pick_window(int64_t R) { return R <= 3 ? 128 : 64; }
 
 bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs,
                                const int32_t* sel, int64_t cap, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st,
                                const void* q, const void* k, const void* v, const void* out) {
     if (dtype != SPARDA_BF16 || D != 64 || (bs != 64 && bs != 32) || sel == nullptr) return false;
-    if (cap < 1 || cap > kCMaxCap || cdiv(T, bs) > Win<64>::kMaxNB) return false;
+    if (cap < 1 || cap > kCMaxCap || cdiv(T, bs) > kCMaxNB) return false;
     if (Hq % Hkv != 0) return false;
     const int64_t R = Hq / Hkv;
     if (R < 1 || R > 4) return false;
@@ -732,7 +725,7 @@ bool prefill_routed_supported(int dtype, int f_dtype, int64_t T, int64_t Hq, int
                               const void* k, const void* v, const void* out, const float* protos) {
     if (dtype != SPARDA_BF16 || D != 64 || (bs != 64 && bs != 32)) return false;
     if (Df != kCRouteDf || ke < 1 || ke > kCRouteK || (f_dtype != SPARDA_BF16 && f_dtype != SPARDA_F32)) return false;
-    if (cdiv(T, bs) > Win<64>::kMaxNB || (reinterpret_cast<uintptr_t>(protos) & 15u) != 0) return false;
+    if (cdiv(T, bs) > kCMaxNB || (reinterpret_cast<uintptr_t>(protos) & 15u) != 0) return false;
     if (Hq % Hkv != 0) return false;
     const int64_t R = Hq / Hkv;
     if (R < 1 || R > 4) return false;
@@ -746,30 +739,22 @@ static int launch_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_s
                           int64_t bs, int causal, float scale, void* out, int64_t out_sb, int64_t out_st,
                           hipStream_t stream) {
     const int64_t R = Hq / Hkv;
-    const int W = pick_window(T, bs, R);
+    const int W = pick_window(R);  // 128, or 64 for R = 4
     const int64_t NBq = cdiv(T, W);  // query windows per (sequence, KV head)
     dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
     const float sl = scale * kCLog2e;
 #define SPARDA_PC(R_, W_)                                                                                    \
     if (bs == 32) SPARDA_PCB(R_, 32, W_); else SPARDA_PCB(R_, 64, W_)
 #define SPARDA_PCB(R_, BS_, W_)                                                                              \
-    hipLaunchKernelGGL((prefill_compact_kernel<R_, BS_, FDT, W_>), grid, dim3(Win<W_>::kThreads), 0, stream, \
+    hipLaunchKernelGGL((prefill_compact_kernel<R_, BS_, FDT, W_>), grid, dim3(kCThreads), 0, stream,          \
                        static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k),    \
                        static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, sel, n_sel, cap, T,              \
                        static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st, rt)
-    if (W == 128) {
-        switch (R) {
-            case 1: SPARDA_PC(1, 128); break;
-            case 2: SPARDA_PC(2, 128); break;
-            default: SPARDA_PC(3, 128); break;
-        }
-    } else {
-        switch (R) {
-            case 1: SPARDA_PC(1, 64); break;
-            case 2: SPARDA_PC(2, 64); break;
-            case 3: SPARDA_PC(3, 64); break;
-            default: SPARDA_PC(4, 64); break;
-        }
+    switch (R) {
+        case 1: SPARDA_PC(1, 128); break;
+        case 2: SPARDA_PC(2, 128); break;
+        case 3: SPARDA_PC(3, 128); break;
+        default: SPARDA_PC(4, 64); break;
     }
 #undef SPARDA_PCB
 #undef SPARDA_PC

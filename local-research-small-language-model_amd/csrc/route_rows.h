@@ -1,5 +1,5 @@
-// One set of 64 consecutive query rows routed by one workgroup of
-// kRouteWaves wavefronts (lane = row): forecast x prototype scores (the
+// One set of 64 consecutive query rows routed by a group of wavefronts of
+// one workgroup (lane = row): forecast x prototype scores (the
 // canonical fma chain), the per-row top-k of route keys, merged across the
 // waves. Shared by the stand-alone router and the prefill kernel that routes
 // its own query window, so both produce the same picks bit for bit.
@@ -98,19 +98,19 @@ __device__ __forceinline__ void load_forecast_row(const void* __restrict__ f, in
     }
 }
 
-// Routes rows set*64 + lane of (b, h). The waves split the candidate blocks
-// (wave w scores j = w, w + kRouteWaves, ...), so the block index is uniform
+// Routes rows set*64 + lane of (b, h) on NW wavefronts. The waves split the
+// candidate blocks (wave w scores j = w, w + NW, ...), so the block index is uniform
 // across a wavefront: every 16-lane row loads the block's prototype with one
 // coalesced load (lane i of the row holds elements E*i .. E*i+E-1, E = DF/16),
 // one block ahead of its use, and the fma chain takes element d from lane d/E
 // of the row through a DPP row broadcast. Each lane keeps its row's KMAX best
 // route keys; wave m merges the waves' lists through `lists` (LDS,
-// [kRouteWaves][KMAX][64] doubles) and returns true with the row's picks
+// [NW][KMAX][64] doubles) and returns true with the row's picks
 // (slots i >= ke: -1; slots no candidate filled: block i, the masked blocks
 // in ascending order); the other waves return false. With scores non-null,
 // every score of the row (-inf where masked) is written to scores[row * NB].
 // Called by every wavefront of the workgroup (two barriers inside).
-template <int FDT, int DF, int KMAX>
+template <int FDT, int DF, int KMAX, int NW = kRouteWaves>
 __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t fsh,
                                           const float* __restrict__ protos, int b, int h, int H, int64_t set,
                                           int64_t Tq, int64_t NB, int bs, int ke, int causal, int64_t score_pos0,
@@ -118,8 +118,8 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
                                           int32_t (&picks)[KMAX]) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x % kWave;
-    // the wave within its group of kRouteWaves (a workgroup may route several sets at once)
-    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>((threadIdx.x / kWave) % kRouteWaves));
+    // the wave within its group of NW (a workgroup may route several sets at once)
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>((threadIdx.x / kWave) % NW));
     const float* __restrict__ pbh = protos + (static_cast<int64_t>(b) * NB * H + h) * DF;
     const int64_t pstride = static_cast<int64_t>(H) * DF;
     const int64_t t = set * kWave + lane;
@@ -152,7 +152,7 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
         const float* __restrict__ pb = pbh + static_cast<int64_t>(jc < jmax ? jc : jmax) * pstride;
         load_f32<E>(pb + loff, o);
     };
-    // scores blocks j, j + kRouteWaves, ... (C of them, prototypes in pc) and
+    // scores blocks j, j + NW, ... (C of them, prototypes in pc) and
     // pushes their keys
     auto score = [&](int j, const float (&pc)[E][C]) __attribute__((always_inline)) {
         float acc[C];
@@ -161,7 +161,7 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
         row_fma_chains<E, DF, C>(fr, pc, acc);
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            const int jc = j + c * kRouteWaves;
+            const int jc = j + c * NW;
             const float sc = acc[c] * scale;
             const bool ok = jc <= limit;  // limit <= jmax
             if (srow && ok) srow[jc] = sc;
@@ -169,19 +169,19 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
         }
     };
     // two prototype buffers used in turn, each loaded one step ahead of its use
-    constexpr int kStep = C * kRouteWaves;
+    constexpr int kStep = C * NW;
     float pa[E][C], pz[E][C];
     float tmp[E];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        load_proto(w + c * kRouteWaves, tmp);
+        load_proto(w + c * NW, tmp);
 #pragma unroll
         for (int e = 0; e < E; ++e) pa[e][c] = tmp[e];
     }
     for (int j = w; j <= jmax; j += 2 * kStep) {
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            load_proto(j + kStep + c * kRouteWaves, tmp);
+            load_proto(j + kStep + c * NW, tmp);
 #pragma unroll
             for (int e = 0; e < E; ++e) pz[e][c] = tmp[e];
         }
@@ -189,14 +189,14 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
         if (j + kStep > jmax) break;  // uniform
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            load_proto(j + 2 * kStep + c * kRouteWaves, tmp);
+            load_proto(j + 2 * kStep + c * NW, tmp);
 #pragma unroll
             for (int e = 0; e < E; ++e) pa[e][c] = tmp[e];
         }
         score(j + kStep, pz);
     }
     if (srow) {
-        for (int64_t j = w; j < NB; j += kRouteWaves)
+        for (int64_t j = w; j < NB; j += NW)
             if (j > limit) srow[j] = -__builtin_inff();
     }
 
@@ -208,7 +208,7 @@ __device__ __forceinline__ bool route_set(const void* __restrict__ f, int64_t fs
     }
     __syncthreads();
     if (w != m) return false;
-    for (int o = 0; o < kRouteWaves; ++o) {
+    for (int o = 0; o < NW; ++o) {
         if (o == m) continue;
         double other[KMAX];
 #pragma unroll
