@@ -658,7 +658,13 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             sm.lsum[c] = 0.0f;
             sm.vers[c] = 0;
         }
-        for (int i = tid; i < 16 * kCols; i += kT) sm.acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        {
+            // an opaque copy of tid: the addresses are recomputed here rather
+            // than kept live (in scratch) from the first clearing
+            int i0 = tid;
+            asm volatile("" : "+v"(i0));
+            for (int i = i0; i < 16 * kCols; i += kT) sm.acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         if (tid == 0) {
             sm.next_item = 0;
             sm.flag &= ~1;
@@ -670,7 +676,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 
     // ---- epilogue: out[b, t, h*64 + d] = O / l, 16-byte stores ----
     const bool broken = (sm.flag & 2) != 0;  // a wait ran out (never expected): poison the window
-    for (int e = tid; e < kCols * 8; e += kT) {
+    int e0 = tid;
+    asm volatile("" : "+v"(e0));  // addresses computed here, not carried (in scratch) through the tiles
+    for (int e = e0; e < kCols * 8; e += kT) {
         const int c = e / 8, ch = e % 8;
         const int tk = c / R, h = c % R;
         if (tk >= t_valid) continue;
