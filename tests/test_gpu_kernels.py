@@ -469,6 +469,29 @@ def test_prefill_routed_long_context_and_block32():
     _routed_case(4, 4096, 12, 4, 64, 32, 4, seed=1001)
 
 
+def test_prefill_routed_block32_at_the_largest_block_count():
+    # 1024 blocks of 32 keys (T = 32768): 128-token windows with the most
+    # blocks the set-up holds; routed == route + prefill, sampled rows against
+    # the oracle
+    case("prefill_routed B=1 T=32768 bs=32 k=4")
+    T, bs, k = 32768, 32, 4
+    x, sel, n, got = _routed_case(1, T, 12, 4, 64, bs, k, seed=1011)
+    r = np.random.default_rng(11)
+    ts = sorted({int(t) for t in r.integers(0, T, 48)} | {0, 31, 32, 16384, T - 32, T - 1})
+    sel, n = sel.cpu().numpy(), n.cpu().numpy()
+    protos = O.compress(np32(x["k"]), bs)
+    f = np32(x["forecast"])
+    for t in ts:
+        _, _, s_o, n_o = O.route(f[:, t:t + 1], protos, bs, k, True, score_pos0=t, query_pos0=t)
+        assert np.array_equal(n[:, :, t], n_o[:, :, 0]) and np.array_equal(sel[:, :, t], s_o[:, :, 0]), f"row {t}"
+    rows = [(0, t) for t in ts]
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel, n, bs, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(got), want, torch.bfloat16, mask)
+
+
 @pytest.mark.parametrize("bs", [64, 32])
 def test_prefill_routed_small_top_k_and_short_lengths(bs):
     # top-k below the kernel's eight slots, top-k above the block count, single
