@@ -95,7 +95,30 @@ decode_score_kernel(const void* __restrict__ kc, int64_t kv_sb, int64_t kv_ss, i
         float s = -__builtin_inff();
         if (j <= limit) {
             float acc = 0.0f;
-            for (int d = 0; d < D; ++d) acc = __fmaf_rn(f_lds[h * D + d], p_lds[h * D + d], acc);
+            if (D == 64) {
+                // the same chain; the operands of each 16 steps read with 16-byte
+                // LDS loads ahead of their fmas (the chain, not the reads, is serial)
+                const float4* fr4 = reinterpret_cast<const float4*>(f_lds + h * 64);
+                const float4* pr4 = reinterpret_cast<const float4*>(p_lds + h * 64);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float4 fv[4], pv[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        fv[i] = fr4[4 * c + i];
+                        pv[i] = pr4[4 * c + i];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc = __fmaf_rn(fv[i].x, pv[i].x, acc);
+                        acc = __fmaf_rn(fv[i].y, pv[i].y, acc);
+                        acc = __fmaf_rn(fv[i].z, pv[i].z, acc);
+                        acc = __fmaf_rn(fv[i].w, pv[i].w, acc);
+                    }
+                }
+            } else {
+                for (int d = 0; d < D; ++d) acc = __fmaf_rn(f_lds[h * D + d], p_lds[h * D + d], acc);
+            }
             s = acc * scale;
         }
         ws_scores[(static_cast<int64_t>(b) * H + h) * NB + j] = s;
