@@ -469,6 +469,12 @@ def test_prefill_routed_long_context_and_block32():
     _routed_case(4, 4096, 12, 4, 64, 32, 4, seed=1001)
 
 
+def test_prefill_routed_four_heads_per_group_at_the_largest_block_count():
+    # R = 4 takes 64-token windows; 1024 blocks of 64 keys (T = 65536)
+    case("prefill_routed R=4 B=1 T=65536 bs=64 k=8")
+    _routed_case(1, 65536, 16, 4, 64, 64, 8, seed=1013)
+
+
 def test_prefill_routed_block32_at_the_largest_block_count():
     # 1024 blocks of 32 keys (T = 32768): 128-token windows with the most
     # blocks the set-up holds; routed == route + prefill, sampled rows against
