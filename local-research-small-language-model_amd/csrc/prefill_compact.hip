@@ -592,7 +592,12 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                                                                     ol[t], 0, 0, 0);
             }
         }
-        // add into every column after its earlier blocks (read-add-write, in block order)
+        // add into every column after its earlier blocks (read-add-write, in block
+        // order). The wave issues ahead of the SIMD's other waves until its
+        // columns are committed: later items of the same columns wait on them
+        // (1-3.5% faster than equal priority); its polls sleep, so a waiting
+        // wave does not hold back the one it waits for.
+        __builtin_amdgcn_s_setprio(2);
         for (uint32_t spins = 0;; ++spins) {
             bool ready = true;
 #pragma unroll
@@ -630,6 +635,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         for (int t = 0; t < kCChunk; ++t)
             if (t < nt && own[t])
                 __hip_atomic_store(&sm.vers[sl[t].c], rank[t] + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // every wave takes items until none is left
