@@ -813,19 +813,20 @@ def cpu_decode_baseline(args, torch, synth, info):
     on the host cores, at the decode workload (B=8, 16K cache, bf16), routed
     like the GPU leg (absolute-position causal mask; the reference's row-0 mask
     is the same operations on another mask row). N threads and 1 thread,
-    warm-up 3 / runs 10 of 8 steps each, median per step."""
+    warm-up 3 / runs 20 of 16 steps each, median per step, with the fastest
+    and slowest run beside it."""
     from oracle import reference_path as R
     x = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002)
     q = x["q"][:, :, None, :]
     k, v = x["k_cache"].transpose(1, 2), x["v_cache"].transpose(1, 2)
     f = x["forecast"][:, None]
-    steps = 8
+    steps = 16
     legs = {}
     with torch.no_grad():
         for n in _thread_counts(args, torch):
             torch.set_num_threads(n)
             med, lo, hi = cpu_timed(lambda: [R.sparse_decode(q, k, v, DS, f, BS, TOPK, routing="absolute")
-                                             for _ in range(steps)])
+                                             for _ in range(steps)], runs=20)
             legs[n] = (med / steps, lo / steps, hi / steps)
     torch.set_num_threads(max(legs))
     n = max(legs)
@@ -850,10 +851,11 @@ def cpu_baseline(args, torch, synth, info):
     q, k, v = (x[n].transpose(1, 2) for n in ("q", "k", "v"))
     f = x["forecast"]
     legs = {}
+    counts = _thread_counts(args, torch)  # once: it reads torch's thread count, which the loop changes
     with torch.no_grad():
-        for n in _thread_counts(args, torch):
+        for n in counts:
             torch.set_num_threads(n)
-            b = PB if n == max(_thread_counts(args, torch)) else 1
+            b = PB if n == max(counts) else 1
             med, lo, hi = cpu_timed(lambda: R.sparse_prefill(q[:b], k[:b], v[:b], f[:b], BS, TOPK))
             legs[n] = (b * PT / med, b, med, lo, hi)
     n = max(legs)

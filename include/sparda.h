@@ -10,8 +10,11 @@
  * No exception crosses the boundary. All tensor pointers are device pointers
  * owned by the caller unless stated otherwise. `stream` is a hipStream_t
  * (NULL = the legacy default stream); every call is stream-ordered and never
- * synchronises the device. Calls are re-entrant; the offload handle is the
- * only stateful object.
+ * synchronises the device, with one exception: sparda_offload_fetch with
+ * SPARDA_FETCH_DMA waits on the host for `stream` (the selection must reach
+ * the host to build the copies), so that form cannot be captured into a HIP
+ * graph; SPARDA_FETCH_KERNEL is the capturable form. Calls are re-entrant;
+ * the offload handle is the only stateful object.
  *
  * Layout vocabulary (the reference's own): B batch, S/T sequence length,
  * Hq query heads, Hkv key/value heads (== forecast heads), D head dim,
@@ -77,7 +80,9 @@ enum {
     SPARDA_FETCH_KERNEL = 0, /* gather kernel reading the arena through its device
                                 mapping; indices stay on the GPU */
     SPARDA_FETCH_DMA = 1,    /* hipMemcpyAsync per run of consecutive blocks; the
-                                selection is copied to the host first (one wait) */
+                                selection is copied to the host first: the call
+                                waits on the host for the stream (one
+                                hipStreamSynchronize), not capturable */
 };
 
 /* Host-resident KV cache of one layer (opaque; see sparda_offload_create). */
@@ -638,7 +643,12 @@ SPARDA_API int sparda_offload_rebuild_sums(sparda_offload_t h, int64_t len, int6
  * Replaces OffloadedKVCache.transfer_selected_blocks (offload.py:83-123) and
  * AsyncOffloadedKVCache.async_transfer_selected_blocks (async_offload.py:55-112):
  * no host gather, no per-call pinning. method: SPARDA_FETCH_KERNEL (never
- * waits) or SPARDA_FETCH_DMA (sel_cap <= 1024; waits once for `stream`).
+ * waits; graph-capturable) or SPARDA_FETCH_DMA (sel_cap <= 1024). The DMA
+ * form blocks the calling thread: it copies the selection to pinned host
+ * memory and calls hipStreamSynchronize(stream) before it can issue one
+ * hipMemcpyAsync per run of consecutive blocks, so it returns only after
+ * everything queued on `stream` before it has finished, and it must not be
+ * called under stream capture.
  */
 SPARDA_API int sparda_offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
                                     int64_t sel_cap, int64_t block_size, int64_t len, int method,

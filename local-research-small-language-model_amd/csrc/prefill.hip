@@ -138,6 +138,7 @@ prefill_weights_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_st, i
     __shared__ float p_lds[kPrefillWaves][kChunkKeys];
     __shared__ int32_t blocks[kWMaxList];
     __shared__ int n_blocks;
+    __shared__ int dead[kPrefillMaxGroup];  // query head of the group with no finite score in its row
 
     const int64_t t = blockIdx.x;
     const int g = blockIdx.y;
@@ -164,14 +165,6 @@ prefill_weights_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_st, i
         }
         n_blocks = n;
     }
-    // zero the rows of the weights; the allowed entries are written in pass 2
-    if (weights != nullptr) {
-        for (int64_t e = threadIdx.x; e < static_cast<int64_t>(R) * T; e += kPrefillThreads) {
-            const int hh = static_cast<int>(e / T);
-            const int64_t s = e % T;
-            store_elem<DT>(weights, b * w_sb + static_cast<int64_t>(g * R + hh) * w_sh + t * w_st + s, 0.0f);
-        }
-    }
     for (int e = threadIdx.x; e < R * DH; e += kPrefillThreads) {
         const int hh = e / DH, d = e % DH;
         q_lds[e] = load_elem<DT>(q, b * q_sb + t * q_st + static_cast<int64_t>(g * R + hh) * q_sh + d) * scale_log2;
@@ -195,6 +188,30 @@ prefill_weights_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_st, i
         for (int i = 0; i < HeadAcc<DH>::DPL; ++i) o_acc[r][i] = 0.0f;
     }
     for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1 && weights != nullptr) {
+            // the weights rows: zero outside the allowed set (its entries are
+            // written below), except a row with no finite score at all, which
+            // is NaN throughout, as the reference's F.softmax over an all -inf
+            // row gives it (sparse.py:266-268; 0/0); the output of such a row
+            // is then NaN too. Without weights the reference calls SDPA, which
+            // returns 0 for such a row, and so does this kernel.
+#pragma unroll
+            for (int r = 0; r < MAXR; ++r) {
+                const int hh = wave + r * kPrefillWaves;
+                if (hh < R && lane == 0) dead[hh] = l_row[r] == 0.0f;
+            }
+            __syncthreads();
+            for (int64_t e = threadIdx.x; e < static_cast<int64_t>(R) * T; e += kPrefillThreads) {
+                const int hh = static_cast<int>(e / T);
+                const int64_t s = e % T;
+                store_elem<DT>(weights, b * w_sb + static_cast<int64_t>(g * R + hh) * w_sh + t * w_st + s,
+                               dead[hh] ? __builtin_nanf("") : 0.0f);
+            }
+            __syncthreads();  // the fill is ordered before the allowed entries' stores
+#pragma unroll
+            for (int r = 0; r < MAXR; ++r)
+                if (l_row[r] == 0.0f) l_row[r] = __builtin_nanf("");  // p = x / NaN below: NaN
+        }
         for (int64_t bi = 0; bi < nblk; ++bi) {
             const int64_t s0 = (sel != nullptr ? static_cast<int64_t>(blocks[bi]) : bi) * bs;
             int64_t s1 = s0 + bs;
@@ -229,7 +246,10 @@ prefill_weights_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_st, i
                         l_row[r] = l_row[r] * __builtin_amdgcn_exp2f(m_row[r] - m_new) + wave_sum(p);
                         m_row[r] = m_new;
                     } else {
-                        const float p = sc == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sc - m_row[r]) / l_row[r];
+                        const float p = l_row[r] != l_row[r]
+                                            ? l_row[r]  // a row with no finite score, weights wanted: NaN
+                                            : (sc == -__builtin_inff() ? 0.0f
+                                                                       : __builtin_amdgcn_exp2f(sc - m_row[r]) / l_row[r]);
                         if (weights != nullptr && lane < nk)
                             store_elem<DT>(weights, b * w_sb + static_cast<int64_t>(h) * w_sh + t * w_st + c0 + lane, p);
                         p_lds[wave][lane] = p;
@@ -254,7 +274,9 @@ prefill_weights_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_st, i
 #pragma unroll
         for (int i = 0; i < HeadAcc<DH>::DPL; ++i) {
             const int d = lane + i * kWave;
-            if (d < DH) store_elem<DT>(out, b * out_sb + t * out_st + static_cast<int64_t>(h) * DH + d, o_acc[r][i]);
+            // NaN l: no finite score and weights wanted (also when no key was visited)
+            const float o = l_row[r] != l_row[r] ? l_row[r] : o_acc[r][i];
+            if (d < DH) store_elem<DT>(out, b * out_sb + t * out_st + static_cast<int64_t>(h) * DH + d, o);
         }
     }
 }

@@ -180,6 +180,14 @@ class HipSparseAttention(BaseAttention):
     def forward(self, x: torch.Tensor, rotary_emb: RotaryEmbedding, kv_cache: Optional[KVCache] = None,
                 mask: Optional[torch.Tensor] = None, is_causal: bool = True,
                 forecast_vector: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
+        if kwargs.get("use_chunked_gather"):
+            # the reference's per-query-block union routing (sparse.py:284-364,
+            # taken when this flag is set, sparse.py:420) has other semantics than
+            # the per-token rule this backend computes at every length
+            raise ValueError("HipSparseAttention: use_chunked_gather=True asks for the chunked-gather path "
+                             "(per-query-block union routing), which this backend does not implement; it "
+                             "applies the per-token masked-SDPA rule at every sequence length. Pass "
+                             "use_chunked_gather=False or leave it out.")
         B, T, _ = x.shape
         xq = self.wq(x).view(B, T, self.n_head, self.head_dim)
         xk = self.wk(x).view(B, T, self.n_kv_head, self.head_dim)

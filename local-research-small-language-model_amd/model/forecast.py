@@ -151,5 +151,5 @@ def compute_forecast_loss(pred_scores: torch.Tensor, target_distribution: torch.
         logits = torch.where(torch.isfinite(pred_scores), pred_scores, torch.full_like(pred_scores, -100.0))
         per = F.binary_cross_entropy_with_logits(logits, hot, reduction="none")
     else:
-        raise ValueError(f"Unknown forecast loss type: {loss_type}")
+        raise ValueError(f"compute_forecast_loss: loss_type must be 'kl' or 'bce', got {loss_type!r}")
     return torch.where(valid, per, torch.zeros_like(per)).sum() / n

@@ -229,7 +229,9 @@ def _routed_one_launch(q, k, v, forecast, protos, out, block_size: int, ke: int)
     ts = (q, k, v, out)
     if any(t.data_ptr() % 16 for t in ts + (protos,)) or any(st % 8 for t in ts for st in t.stride()[:-1]):
         return False
-    return 64 * q.stride(1) + (Hq // Hkv) * q.stride(2) + 64 < (1 << 30) and 64 * k.stride(1) + 64 < (1 << 30)
+    # the library's own bound on window-relative offsets (128-token windows)
+    return (128 * q.stride(1) + (Hq // Hkv) * q.stride(2) + 64 < (1 << 30)
+            and 64 * k.stride(1) + 64 < (1 << 30))
 
 
 def prefill_routed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, forecast: torch.Tensor,

@@ -277,7 +277,10 @@ def attention_prefill_masked(q, k, v, sel, n_sel, bs: int, causal: bool = True, 
     Selections have set semantics (repeated entries count once, entries
     outside [0, NB) attend nothing). mask: broadcastable to [B, Hq, T, T]
     (natural-log units, added to the allowed scores). Returns (out
-    [B,T,Hq*D], weights [B,Hq,T,T]); rows not evaluated are NaN.
+    [B,T,Hq*D], weights [B,Hq,T,T]); rows not evaluated are NaN. A row with
+    no finite score (the mask -inf on every allowed key, or no allowed key)
+    is NaN throughout, weights and output, as F.softmax over an all -inf
+    row gives it in the reference's weights path (sparse.py:266-268).
     """
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
@@ -306,6 +309,8 @@ def attention_prefill_masked(q, k, v, sel, n_sel, bs: int, causal: bool = True, 
                 s = (k[b, keys, g] @ q[b, t, h]) * scale
                 if m is not None:
                     s = s + m[b, h, t, keys]
+                if len(keys) == 0 or np.all(s == -np.inf):
+                    continue  # no finite score: the NaN row stays
                 mx = s.max()
                 p = np.exp(s - mx)
                 p = p / p.sum()

@@ -34,6 +34,27 @@ def test_oracle_teacher_closed_forms():
     assert np.allclose(m.sum(-1), 1.0)
 
 
+def test_oracle_dense_weights_gqa_against_sdpa():
+    # SDPA with identity values returns its own weight matrix (softmax(QK^T) @ I),
+    # and enable_gqa applies the library's query-head -> KV-head mapping, so
+    # this pins the oracle's h // R grouping, scale and causal mask with more
+    # than one KV head (a swapped mapping, h % Hkv, fails it)
+    g = np.random.default_rng(5)
+    B, T, Hq, Hkv, D = 2, 37, 6, 2, 16
+    q, k = g.standard_normal((B, T, Hq, D)), g.standard_normal((B, T, Hkv, D))
+    eye = torch.eye(T, dtype=torch.float64).expand(B, Hkv, T, T)
+    for causal in (True, False):
+        want = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(q).transpose(1, 2), torch.from_numpy(k).transpose(1, 2), eye,
+            is_causal=causal, enable_gqa=True).numpy()
+        got = O.dense_weights(q, k, causal)
+        assert got.shape == (B, Hq, T, T)
+        assert np.abs(got - want).max() < 1e-12
+    # the planted mistake a swapped head mapping would make is visible here
+    swapped = O.dense_weights(q[:, :, [0, 3, 1, 4, 2, 5]], k, True)
+    assert np.abs(swapped - O.dense_weights(q, k, True)).max() > 1e-3
+
+
 def test_teacher_selector_forward_matches_oracle():
     g = np.random.default_rng(2)
     q, k = g.standard_normal((2, 100, 6, 16)), g.standard_normal((2, 100, 2, 16))

@@ -59,6 +59,32 @@ def test_masked_prefill_per_kv_head_mask_and_dense_noncausal():
     _check(x, None, None, bs, False, torch.float32, mask=mq, mask_t=torch.from_numpy(m))
 
 
+def test_masked_prefill_fully_masked_row():
+    # a row whose mask is -inf on every allowed key: with the weights (the
+    # reference's F.softmax path) weights and output are NaN there, as the
+    # oracle has them; without (the reference's SDPA path) the output row is 0
+    case("prefill_masked fully masked row, with and without weights")
+    B, T, bs, k = 1, 192, 64, 2
+    x = synth.prefill_inputs(B, T, 12, 4, 64, dtype=torch.float32, seed=304)
+    _, _, sel, n = O.route(np32(x["forecast"]), O.compress(np32(x["k"]), bs), bs, k, True)
+    m = np.random.default_rng(304).standard_normal((B, 12, T, T)).astype(np.float32)
+    m[0, 5, 100, :] = -np.inf
+    d = {k_: t_.to(DEV) for k_, t_ in x.items()}
+    st, nt, mt = (torch.from_numpy(a).to(DEV) for a in (sel, n, m))
+    out, w = sparda.prefill_masked(d["q"], d["k"], d["v"], st, nt, bs, causal=True, mask=mt, want_weights=True)
+    plain = sparda.prefill_masked(d["q"], d["k"], d["v"], st, nt, bs, causal=True, mask=mt)
+    torch.cuda.synchronize()
+    want_o, want_w = O.attention_prefill_masked(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel, n, bs, True, mask=m)
+    go, gw, gp = np32(out), np32(w), np32(plain)
+    assert np.isnan(gw[0, 5, 100]).all() and np.isnan(go[0, 100, 5 * 64:6 * 64]).all()
+    assert (np.isnan(gw) == np.isnan(want_w)).all() and (np.isnan(go) == np.isnan(want_o)).all()
+    ok_w, ok_o = ~np.isnan(want_w), ~np.isnan(want_o)
+    assert_close_out(gw[ok_w], want_w[ok_w], torch.float32, what="weights")
+    assert_close_out(go[ok_o], want_o[ok_o], torch.float32)
+    assert (gp[0, 100, 5 * 64:6 * 64] == 0).all()
+    assert_close_out(gp[ok_o], want_o[ok_o], torch.float32, what="output without weights")
+
+
 def test_masked_prefill_static_noncausal_window():
     case("prefill_masked static non-causal window")
     B, T, bs, k = 1, 256, 32, 2

@@ -438,6 +438,26 @@ def test_masked_prefill_dense_equals_sdpa_with_attn_mask():
     assert np.allclose(out, ref.permute(0, 2, 1, 3).reshape(1, 96, 64).numpy(), atol=1e-10)
 
 
+def test_masked_prefill_fully_masked_row_is_softmax_nan():
+    # library pin: the reference's weights path is F.softmax(scores + mask),
+    # which is NaN throughout a row whose scores are all -inf, and the output
+    # (weights @ V) is NaN there too; every other row is unaffected
+    q, k, v = _small(6)
+    T = 96
+    m = np.random.default_rng(6).standard_normal((1, 4, T, T))
+    m[0, 1, 40, :] = -np.inf
+    out, w = O.attention_prefill_masked(q, k, v, None, None, 16, True, mask=m)
+    tq, tk = (torch.from_numpy(x).permute(0, 2, 1, 3) for x in (q, k))
+    tk = torch.repeat_interleave(tk, 2, dim=1)
+    causal = torch.triu(torch.full((T, T), float("-inf"), dtype=torch.float64), 1)
+    ref_w = F.softmax(tq @ tk.transpose(-1, -2) / np.sqrt(q.shape[-1]) + causal + torch.from_numpy(m), dim=-1)
+    assert torch.isnan(ref_w[0, 1, 40]).all() and np.isnan(w[0, 1, 40]).all()
+    assert np.isnan(out[0, 40, 16:32]).all()
+    ok = ~np.isnan(ref_w.numpy())
+    assert np.allclose(w[ok], ref_w.numpy()[ok], atol=1e-12)
+    assert np.isfinite(np.delete(out[0, 40], np.s_[16:32])).all() and np.isfinite(np.delete(out, 40, 1)).all()
+
+
 def test_masked_prefill_minus_inf_block_equals_dropping_it():
     # -inf over one listed block is the list without it; a constant shift of the
     # mask changes nothing (softmax shift invariance)
