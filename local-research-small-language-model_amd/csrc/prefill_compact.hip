@@ -15,19 +15,19 @@
 // diagonal block).
 //
 // Accumulation. P is taken against a fixed per-column reference m_ref: the
-// column maximum of the column's first selected block (its smallest block,
-// the sink for router lists), set by the tile that processes that block. It is
-// a score of an allowed key, so it never exceeds the row maximum and the row
-// keeps a term P = 1. Contributions are then plain sums (no rescaling): each
-// tile's O^T and row sums are formed from zero and added into fp32
-// accumulators acc[col][d], lsum[col] in LDS. Work items (a block and up to
-// two of its tiles) are taken by the waves from a shared counter in block
-// order; a column's contributions are added in ascending block order, each
-// tile waiting until the column's earlier blocks have been added (vers[col] =
-// blocks added so far), so the result does not depend on timing. A block
-// whose row sum passes 2^64 (a score more than 64 log2-units above the
-// reference) trips a flag; the workgroup then takes the exact row maxima in a
-// scores-only pass and redoes the window against them.
+// score of the first key of the column's first listed block (key 0, the sink,
+// for router lists), computed in the set-up. It is the score of an allowed
+// key, so it never exceeds the row maximum and the row keeps a term P ~ 1.
+// Contributions are then plain sums (no rescaling): each tile's O^T and row
+// sums are formed from zero and added into fp32 accumulators acc[col][d],
+// lsum[col] in LDS. Work items (a block and up to three of its tiles) are
+// taken by the waves from a shared counter in block order; a column's
+// contributions are added in ascending block order, each tile waiting until
+// the column's earlier blocks have been added (vers[col] = blocks added so
+// far), so the result does not depend on timing. A block whose row sum passes
+// 2^64 (a score more than 64 log2-units above the reference) trips a flag;
+// the workgroup then takes the exact row maxima in a scores-only pass and
+// redoes the window against them.
 //
 // K A operands are read straight from memory; V is staged per wavefront in
 // LDS, half a block at a time (XOR-swizzled 16-byte chunks), and read
@@ -266,6 +266,10 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             }
         }
     }
+    // the first key of the token's first listed block (always an allowed key),
+    // or -1: its score is the column's reference (set-up 2). Held in the row
+    // sums' bytes until set-up 3 clears them.
+    if (owner) reinterpret_cast<int*>(sm.lsum)[tok] = (has_tok && lst[0] != kSentinel) ? lst[0] * BS : -1;
     for (int i = tid; i <= jmax; i += kT) bitmap[i] = Mask{};
     __syncthreads();
     if (has_tok) {
@@ -316,6 +320,39 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             sm.next_item = 0;
             sm.flag = 0;
         }
+    } else {
+        // meanwhile the other waves take each column's reference: the score
+        // (log2 units) of the first key of the column's first listed block.
+        // Any allowed score serves (the row keeps a term near 1, so the sums
+        // neither underflow nor, short of a score 64 log2-units above it,
+        // overflow); fixing it before the tiles leaves no tile waiting for
+        // another tile's maximum.
+        for (int c = tid - kWave; c < kCols; c += kT - kWave) {
+            const int tk = c / R, h = c - (c / R) * R;
+            const int s0 = reinterpret_cast<const int*>(sm.lsum)[tk];
+            float ref = 0.0f;
+            if (s0 >= 0) {
+                const uint16_t* qr = qbase + tk * q_st32 + h * q_sh32;
+                const uint16_t* kr = kbase + static_cast<int64_t>(s0) * kv_st;
+                u32x4 qv[8], kv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    qv[i] = *reinterpret_cast<const u32x4*>(qr + 8 * i);
+                    kv[i] = *reinterpret_cast<const u32x4*>(kr + 8 * i);
+                }
+                float a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        a = __builtin_fmaf(__uint_as_float(qv[i][e] << 16), __uint_as_float(kv[i][e] << 16), a);
+                        a = __builtin_fmaf(__uint_as_float(qv[i][e] & 0xffff0000u),
+                                           __uint_as_float(kv[i][e] & 0xffff0000u), a);
+                    }
+                ref = a * scale_log2;
+            }
+            sm.mref[c] = ref;
+        }
     }
     __syncthreads();
 
@@ -332,7 +369,6 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         }
     }
     for (int c = tid; c < kCols; c += kT) {
-        sm.mref[c] = 0.0f;
         sm.lsum[c] = 0.0f;
         sm.vers[c] = 0;
     }
@@ -420,14 +456,13 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
 
     // one work item (packed word: union entry u | first tile i0 << 16): the
     // up to kCChunk tiles [i0, i1) of union block u, processed phase by phase
-    // so that their latencies overlap: K, V and q loads, S = K Q^T, references
-    // and P, O = V^T P^T, then one wait and one read-add-write of every
-    // column. (The loads are not issued an item ahead: three waves per SIMD
+    // so that their latencies overlap: K, V and q loads with the columns'
+    // references, S = K Q^T, P, O = V^T P^T, then one wait and one
+    // read-add-write of every column. (The loads are not issued an item ahead: three waves per SIMD
     // cover their latency, and the registers that would hold the next item's
     // K and V are what lets the third wave fit.)
-    // mode 0: P against the column's reference, which the column's first block
-    //         sets to its own column maximum; 1: scores only, exact column
-    //         maxima; 2: P against the exact maxima of mode 1
+    // mode 0: P against the columns' references; 1: scores only, the exact
+    // column maxima (into the row sums' bytes)
     auto process = [&](int item, int mode) __attribute__((always_inline)) {
         u32x4 kr[kKR], vr[kVR];
         load_k(item, kr);
@@ -449,6 +484,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         Slot sl[kCChunk];
         u32x4 qa[kCChunk], qc[kCChunk];
         int rank[kCChunk];
+        float ref[kCChunk];
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
@@ -456,6 +492,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                 qa[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff);
                 qc[t] = *reinterpret_cast<const u32x4*>(qbase + sl[t].qoff + 32);
                 rank[t] = sm.rankbuf[rofs + sl[t].tr];
+                ref[t] = sm.mref[sl[t].c];
             }
         }
         // S^T = K Q^T for every tile (every key sub-tile: on the causal
@@ -495,10 +532,9 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
         }
         __builtin_amdgcn_wave_barrier();
 
-        // masks, references, P
+        // masks: keys past a column's token on the causal diagonal, keys past T
+        // in a ragged last block
         bool own[kCChunk];
-        uint4 pw[kCChunk][kHalf];
-        bool any_first = false, any_later = false;
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
@@ -511,51 +547,25 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                         for (int ii = 0; ii < 4; ++ii)
                             if (16 * n + 4 * grp + ii > lim) s[t][n][ii] = -__builtin_inff();
                 }
-                any_first = any_first || (sl[t].valid && rank[t] == 0);
-                any_later = any_later || (own[t] && rank[t] > 0);
-            }
-        }
-        float cm[kCChunk];
-        if (mode == 1 || __ballot(any_first) != 0ull) {
-#pragma unroll
-            for (int t = 0; t < kCChunk; ++t) {
-                if (t < nt) {
-                    const float x = max_sub_nn(s[t]);
-                    cm[t] = pair32_max(pair16_max(x)) * scale_log2;
-                }
             }
         }
         if (mode == 1) {
+            // exact column maxima (order keys of the maxima, in the row sums' bytes)
 #pragma unroll
-            for (int t = 0; t < kCChunk; ++t)
-                if (t < nt && own[t]) atomicMax(reinterpret_cast<uint32_t*>(sm.lsum) + sl[t].c, order_key(cm[t]));
+            for (int t = 0; t < kCChunk; ++t) {
+                if (t < nt) {
+                    const float cm = pair32_max(pair16_max(max_sub_nn(s[t]))) * scale_log2;
+                    if (own[t]) atomicMax(reinterpret_cast<uint32_t*>(sm.lsum) + sl[t].c, order_key(cm));
+                }
+            }
             return;
         }
-        if (mode == 0 && __ballot(any_later) != 0ull) {
-            // later blocks: their columns' first blocks have set the references
-            for (uint32_t spins = 0;; ++spins) {
-                bool ready = true;
-#pragma unroll
-                for (int t = 0; t < kCChunk; ++t)
-                    if (t < nt && own[t] && rank[t] > 0)
-                        ready = ready && __hip_atomic_load(&sm.vers[sl[t].c], __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_WORKGROUP) >= 1;
-                if (__ballot(!ready) == 0ull) break;
-                if (spins >= kCSpinLimit) {
-                    if (lane == 0) atomicOr(&sm.flag, 2);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        }
+        // P = exp2(S * scale log2 e - reference), bf16
+        uint4 pw[kCChunk][kHalf];
 #pragma unroll
         for (int t = 0; t < kCChunk; ++t) {
             if (t < nt) {
-                const bool first = mode == 0 && sl[t].valid && rank[t] == 0;
-                const float m = first ? cm[t] : sm.mref[sl[t].c];
-                if (first && own[t]) sm.mref[sl[t].c] = m;
-                const float neg = sl[t].valid ? -m : -__builtin_inff();
+                const float neg = sl[t].valid ? -ref[t] : -__builtin_inff();
 #pragma unroll
                 for (int mm = 0; mm < kHalf; ++mm) {
                     bf16x8 pb;
@@ -676,7 +686,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
             sm.flag &= ~1;
         }
         __syncthreads();
-        run(2);
+        run(0);  // the references are now the exact maxima: every P <= 1
         __syncthreads();
     }
 
