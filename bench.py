@@ -185,6 +185,14 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         pairs = int(keys.sum().item()) * (HQ // HKV)
         ms_step = graphed(routed, out)
         ms_two = graphed(two_launch, out2)
+        # the dense causal step of the same layer (the reference's dense
+        # fallback: layer 0 of every forward), kernel time by events
+        dense = {}
+        if T == MT:
+            ms_dense = events_ms(lambda: sparda.prefill(q, k, v, None, None, BS, out=out2), args.steps, torch)
+            dflop = 4 * D * HQ * B * T * (T + 1) // 2
+            dense = {"dense_attn_us": ms_dense * 1e3, "dense_attn_tflops": dflop / (ms_dense * 1e-3) / 1e12,
+                     "dense_attn_frac": dflop / (ms_dense * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
     flops = 4 * D * pairs
     tflops = flops / (ms_attn * 1e-3) / 1e12
     # compressor: read K, write the fp32 prototypes; router: read the forecast
@@ -211,6 +219,7 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         "attn_from_lists_us": ms_attn_lists * 1e3,
         "attn_from_lists_tflops": flops / (ms_attn_lists * 1e-3) / 1e12,
         "dense_causal_flop": 4 * D * HQ * B * T * (T + 1) // 2,
+        **dense,
     }
 
 

@@ -36,6 +36,15 @@ int launch_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_s
                           int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale,
                           void* out, int64_t out_sb, int64_t out_st, hipStream_t stream);
 
+// dense (no selection lists) bf16 prefill, D = 64 (prefill_dense.hip)
+bool prefill_dense_supported(int dtype, int64_t Hq, int64_t Hkv, int64_t D, int64_t q_sb, int64_t q_st,
+                             int64_t q_sh, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb,
+                             int64_t out_st, const void* q, const void* k, const void* v, const void* out);
+int launch_prefill_dense(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                         int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t B, int64_t T, int64_t Hq,
+                         int64_t Hkv, int causal, float scale, void* out, int64_t out_sb, int64_t out_st,
+                         hipStream_t stream);
+
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,
                    void* q, void* k, void* v, void* f, int f_dtype, hipStream_t stream,

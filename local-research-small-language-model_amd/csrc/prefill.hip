@@ -327,12 +327,18 @@ int launch_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, cons
                    const int32_t* sel, const int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
                    int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int causal, float scale,
                    void* out, int64_t out_sb, int64_t out_st, hipStream_t stream) {
-    // per-token selections: columns compacted per block; dense (no selection
-    // lists) and wider selections: the union-of-blocks matrix-core kernel.
+    // per-token selections: columns compacted per block; dense steps (no
+    // selection lists): the dense kernel; wider selections: the
+    // union-of-blocks matrix-core kernel.
     // Without lists every key up to the query (or every key) is attended, so
     // the block size does not enter the result and the 64-key kernel serves
     // any block size.
     if (sel == nullptr) bs = 64;
+    // no lists: every key up to the token (or every key), the dense kernel
+    if (sel == nullptr && prefill_dense_supported(dtype, Hq, Hkv, D, q_sb, q_st, q_sh, kv_sb, kv_st, kv_sh, out_sb,
+                                                  out_st, q, k, v, out))
+        return launch_prefill_dense(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, B, T, Hq, Hkv, causal, scale,
+                                    out, out_sb, out_st, stream);
     if (prefill_compact_supported(dtype, T, Hq, Hkv, D, bs, sel, cap, q_sb, q_st, q_sh, kv_sb, kv_st, kv_sh,
                                   out_sb, out_st, q, k, v, out))
         return launch_prefill_compact(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, sel, n_sel, cap, B, T, Hq,

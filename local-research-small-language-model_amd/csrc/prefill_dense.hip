@@ -1,0 +1,273 @@
+// bf16 dense GQA prefill on the gfx950 matrix cores (D = 64), causal or not:
+// the reference's dense fallback (model/attention/sparse.py:201-224: layer 0,
+// no forecast, or at most two KV blocks) without selection lists.
+//
+// One workgroup of 8 wavefronts serves one (sequence b, KV head g, window of
+// 128 query tokens); wavefront w owns tokens [16w, 16w+16) of the window for
+// all R = Hq/Hkv query heads of the group: 16R columns (column c -> token
+// 16w + c / R, head c % R), R tiles of 16 columns whose Q operands stay in
+// registers. The workgroup walks the KV blocks of 64 keys in ascending order
+// up to its last token's block; each block's K and V are staged once in LDS
+// (double-buffered; the next block is loaded into registers while the
+// current one is computed) and shared by all 128 tokens and R heads. Per tile
+// and block, with v_mfma_f32_16x16x32_bf16:
+//     S^T[key, col] = K[key, :] . Q[col, :]           (8 MFMA)
+//     online softmax per column (fp32, log2 domain; the running maximum is
+//     raised only when a block's maximum exceeds it by more than 2^8, so the
+//     accumulators are rarely rescaled and P stays <= 2^8)
+//     O^T[d, col]  += V^T[d, key] . P^T[key, col]      (8 MFMA)
+//     l[col]       += 1^T P^T                           (2 MFMA, a ones A operand)
+// A wavefront whose tokens all lie before a block skips it (the causal
+// triangle is not computed); the diagonal block masks the keys past each
+// column's token. No per-token membership logic: every key up to the token
+// (or every key) is attended.
+#include "common.h"
+#include "kernels.h"
+#include "mfma.h"
+
+namespace sparda {
+
+namespace {
+
+constexpr int kDBs = 64;                 // keys per KV block
+constexpr int kDD = 64;                  // head dim
+constexpr int kDWaves = 8;               // wavefronts per workgroup
+constexpr int kDThreads = kDWaves * kWave;
+constexpr int kDWin = 16 * kDWaves;      // query tokens per workgroup
+constexpr int kDKRow = kDD + 8;          // K row in LDS, bf16 elements (144 B)
+constexpr int kDVRow = kDD + 16;         // V row in LDS, bf16 elements (160 B)
+constexpr float kDLog2e = 1.4426950408889634f;
+constexpr float kDLazy = 8.0f;           // raise the running max only past 2^8
+
+struct DenseSmem {
+    uint16_t k[2][kDBs * kDKRow];
+    uint16_t v[2][kDBs * kDVRow];
+};
+
+}  // namespace
+
+template <int R>
+__global__ void __launch_bounds__(kDThreads, 2)
+prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t kv_sb, int64_t kv_st,
+                     int64_t kv_sh, int64_t T, int H, int64_t NBq, int causal, float scale_log2,
+                     uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st) {
+    __shared__ DenseSmem sm;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    const int col16 = lane % 16;
+    const int grp = lane / 16;
+
+    // heaviest windows first; consecutive ids cycle through (b, g)
+    const int64_t BH = static_cast<int64_t>(gridDim.x) / NBq;
+    const int64_t bg = blockIdx.x % BH;
+    const int64_t qw = NBq - 1 - blockIdx.x / BH;
+    const int b = static_cast<int>(bg / H);
+    const int g = static_cast<int>(bg % H);
+    const int64_t t0 = qw * kDWin;
+    const int64_t NB = cdiv(T, kDBs);
+    const int t_valid = static_cast<int>(T - t0 < kDWin ? T - t0 : kDWin);
+    // blocks of the workgroup and of this wavefront (causal: up to the last token's block)
+    const int64_t last_tok = t0 + t_valid - 1;
+    const int nblk = static_cast<int>(causal ? last_tok / kDBs + 1 : NB);
+    const int64_t w_first = t0 + 16 * wave;  // this wavefront's first token
+    int64_t w_last = w_first + 15;
+    w_last = w_last < T - 1 ? w_last : T - 1;
+    const bool w_live = w_first < T;
+    const int w_nblk = !w_live ? 0 : static_cast<int>(causal ? w_last / kDBs + 1 : NB);
+
+    // Q operands of this wavefront's tiles (column col16 of tile tt; rows past T read row T-1)
+    int tok[R];
+    bf16x8 qreg[R][2];
+#pragma unroll
+    for (int tt = 0; tt < R; ++tt) {
+        const int c = 16 * tt + col16;
+        tok[tt] = 16 * wave + c / R;
+        int64_t t = t0 + tok[tt];
+        t = t < T ? t : T - 1;
+        const uint16_t* qp = q + b * q_sb + t * q_st + static_cast<int64_t>(g * R + c % R) * q_sh + 8 * grp;
+        qreg[tt][0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp));
+        qreg[tt][1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + 32));
+    }
+
+    f32x4 o[R][4], ol[R];
+    float m_run[R];
+    bf16x8 ones_a;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
+#pragma unroll
+    for (int tt = 0; tt < R; ++tt) {
+        m_run[tt] = -__builtin_inff();
+        ol[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // staging: thread -> 16-byte chunk (row tid / 8, column tid % 8) of K and of V;
+    // rows past T (a ragged last block) read row T-1 (finite values, masked)
+    const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
+    const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
+    const int srow = tid / 8, scol = (tid % 8) * 8;
+    const int lds_k = srow * kDKRow + scol, lds_v = srow * kDVRow + scol;
+    auto fetch = [&](int j, uint4& kv_k, uint4& kv_v) __attribute__((always_inline)) {
+        int64_t s = static_cast<int64_t>(j) * kDBs + srow;
+        s = s < T ? s : T - 1;
+        kv_k = *reinterpret_cast<const uint4*>(kbase + s * kv_st + scol);
+        kv_v = *reinterpret_cast<const uint4*>(vbase + s * kv_st + scol);
+    };
+
+    auto compute = [&](int buf, int j) __attribute__((always_inline)) {
+        // K A operands: key 16n + col16, dims 32kk + 8grp .. +7
+        bf16x8 ka[4][2];
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+                ka[n][kk] = lds_read8(&sm.k[buf][(16 * n + col16) * kDKRow + 32 * kk + 8 * grp]);
+        // V^T A operands, read transposed from the row-major tile
+        bf16x8 va[4][2];
+        {
+            const int rsub = 4 * grp + col16 / 4;
+            const int csub = 4 * (col16 % 4);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const uint16_t* base = &sm.v[buf][(32 * m + rsub) * kDVRow + 16 * dt + csub];
+                    const i16x4 lo = lds_read_tr(base);
+                    const i16x4 hi = lds_read_tr(base + 16 * kDVRow);
+                    va[dt][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                }
+        }
+        // keys past a column's token (causal diagonal) or past T (ragged tail) are masked
+        const int64_t key0 = static_cast<int64_t>(j) * kDBs;
+        const bool edge = causal ? key0 + kDBs - 1 > w_first : key0 + kDBs > T;
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt) {
+            f32x4 s[4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][0], qreg[tt][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[n][1], qreg[tt][1], s[n], 0, 0, 0);
+            }
+            if (edge) {
+                const int64_t lim64 = causal ? t0 + tok[tt] - key0 : T - 1 - key0;  // keys <= lim are allowed
+                const int lim = static_cast<int>(lim64 < kDBs ? lim64 : kDBs);
+#pragma unroll
+                for (int n = 0; n < 4; ++n)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (16 * n + 4 * grp + i > lim) s[n][i] = -__builtin_inff();
+            }
+            const float cand = pair32_max(pair16_max(max16_nn(s))) * scale_log2;  // block's column max, log2 units
+            // -inf (a column whose keys here are all masked: it has none allowed
+            // yet) leaves the running state alone
+            const float m_new = cand > m_run[tt] + kDLazy ? cand : m_run[tt];
+            const float alpha = m_new != m_run[tt] ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
+            m_run[tt] = m_new;
+            const float neg = m_new == -__builtin_inff() ? -__builtin_inff() : -m_new;
+            uint4 pw[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                bf16x8 pb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pb[i] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m][i], scale_log2, neg)));
+                    pb[4 + i] =
+                        static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m + 1][i], scale_log2, neg)));
+                }
+                pw[m] = __builtin_bit_cast(uint4, pb);
+            }
+            if (__ballot(alpha != 1.0f) != 0ull) {
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[tt][dt] *= alpha;
+                ol[tt] *= alpha;
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][0], __builtin_bit_cast(bf16x8, pw[0]),
+                                                                    o[tt][dt], 0, 0, 0);
+                o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][1], __builtin_bit_cast(bf16x8, pw[1]),
+                                                                    o[tt][dt], 0, 0, 0);
+            }
+            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[0]), ol[tt], 0, 0, 0);
+            ol[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_a, __builtin_bit_cast(bf16x8, pw[1]), ol[tt], 0, 0, 0);
+        }
+    };
+
+    // block u is computed from buffer u & 1 while block u + 1 is in registers;
+    // one barrier per block orders its stash before the reads of the next
+    uint4 nk, nv;
+    fetch(0, nk, nv);
+    *reinterpret_cast<uint4*>(&sm.k[0][lds_k]) = nk;
+    *reinterpret_cast<uint4*>(&sm.v[0][lds_v]) = nv;
+    if (nblk > 1) fetch(1, nk, nv);
+    __syncthreads();
+    for (int u = 0; u < nblk; ++u) {
+        const int buf = u & 1;
+        if (u < w_nblk) compute(buf, u);  // wave-uniform: blocks past this wavefront's tokens are skipped
+        if (u + 1 < nblk) {
+            *reinterpret_cast<uint4*>(&sm.k[buf ^ 1][lds_k]) = nk;
+            *reinterpret_cast<uint4*>(&sm.v[buf ^ 1][lds_v]) = nv;
+            if (u + 2 < nblk) fetch(u + 2, nk, nv);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: out[b, t, h*64 + d] = O / l ----
+#pragma unroll
+    for (int tt = 0; tt < R; ++tt) {
+        // the row sum of column col16 sits in lane col16 (lane group 0), element 0
+        const float lsum = __shfl(ol[tt][0], col16, kWave);
+        if (tok[tt] >= t_valid) continue;
+        const int c = 16 * tt + col16;
+        const float inv = 1.0f / lsum;
+        uint16_t* orow = out + b * out_sb + (t0 + tok[tt]) * out_st + static_cast<int64_t>(g * R + c % R) * kDD;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            bf16x4 w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = static_cast<__bf16>(o[tt][dt][i] * inv);
+            *reinterpret_cast<bf16x4*>(orow + 16 * dt + 4 * grp) = w;
+        }
+    }
+}
+
+bool prefill_dense_supported(int dtype, int64_t Hq, int64_t Hkv, int64_t D, int64_t q_sb, int64_t q_st,
+                             int64_t q_sh, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb,
+                             int64_t out_st, const void* q, const void* k, const void* v, const void* out) {
+    if (dtype != SPARDA_BF16 || D != kDD || Hq % Hkv != 0) return false;
+    const int64_t R = Hq / Hkv;
+    if (R < 1 || R > 4) return false;
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!al16(q) || !al16(k) || !al16(v) || (reinterpret_cast<uintptr_t>(out) & 7u)) return false;
+    if ((q_sb % 8) || (q_st % 8) || (q_sh % 8) || (kv_sb % 8) || (kv_st % 8) || (kv_sh % 8)) return false;
+    if ((out_sb % 4) || (out_st % 4)) return false;
+    return true;
+}
+
+int launch_prefill_dense(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                         int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t B, int64_t T, int64_t Hq,
+                         int64_t Hkv, int causal, float scale, void* out, int64_t out_sb, int64_t out_st,
+                         hipStream_t stream) {
+    const int64_t NBq = cdiv(T, kDWin);
+    const int64_t R = Hq / Hkv;
+    dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
+    const float sl = scale * kDLog2e;
+#define SPARDA_DN(R_)                                                                                      \
+    hipLaunchKernelGGL((prefill_dense_kernel<R_>), grid, dim3(kDThreads), 0, stream,                       \
+                       static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k), \
+                       static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, T, static_cast<int>(Hkv), NBq, \
+                       causal, sl, static_cast<uint16_t*>(out), out_sb, out_st)
+    switch (R) {
+        case 1: SPARDA_DN(1); break;
+        case 2: SPARDA_DN(2); break;
+        case 3: SPARDA_DN(3); break;
+        default: SPARDA_DN(4); break;
+    }
+#undef SPARDA_DN
+    return check_hip(hipGetLastError(), "prefill_dense_kernel");
+}
+
+}  // namespace sparda

@@ -204,6 +204,24 @@ def test_prefill_mfma_dense_and_noncausal():
     _prefill_case(1, 300, 12, 4, 64, 64, 8, torch.bfloat16, seed=63, causal=False, dense=True)
 
 
+@pytest.mark.parametrize("R", [1, 2, 3, 4])
+def test_prefill_dense_kernel_group_sizes_and_ragged_lengths(R):
+    # steps without lists (the reference's dense fallback, sparse.py:201-224):
+    # 128-token windows, ragged last windows and blocks, causal and not
+    for B, T, causal in ((2, 1000, True), (1, 129, True), (1, 1, True), (1, 65, False), (1, 200, False),
+                         (1, 256, True)):
+        case(f"prefill dense R={R} B={B} T={T} causal={causal}")
+        _prefill_case(B, T, 4 * R, 4, 64, 64, 8, torch.bfloat16, seed=90 + R + T, causal=causal, dense=True)
+
+
+def test_prefill_dense_kernel_16k_sampled_rows():
+    # the dense causal layer of the 12-layer forward's shape (B=1, T=16384)
+    case("prefill dense B=1 T=16384")
+    r = np.random.default_rng(12)
+    rows = sorted({(0, int(t)) for t in r.integers(0, 16384, 48)} | {(0, 0), (0, 127), (0, 128), (0, 16383)})
+    _prefill_case(1, 16384, 12, 4, 64, 64, 8, torch.bfloat16, seed=1003, dense=True, rows=rows)
+
+
 def test_prefill_general_kernel_shapes():
     # reference test geometry: 8 q heads / 2 kv heads, D=32, bs=16, k=2
     case("prefill general D=32 bs=16")
