@@ -101,6 +101,25 @@ SPARDA_API int sparda_version(void);
 /* Message describing the last non-zero status returned on this thread. */
 SPARDA_API const char* sparda_last_error(void);
 
+/* Bits of the per-device status word (sparda_status). */
+enum {
+    /* A compacted prefill workgroup gave up an ordering wait after its poll
+     * limit (never expected: waits end when earlier tiles commit). Its query
+     * window's output rows were written as NaN. */
+    SPARDA_STATUS_PREFILL_WAIT_TIMEOUT = 1,
+};
+
+/*
+ * Status word of the current device: the SPARDA_STATUS_* conditions raised by
+ * kernels since it was last cleared. Writes it to `out` (one uint32, device
+ * memory), clearing it when `clear` != 0; stream-ordered like every other
+ * call (the word reflects the launches queued on `stream` before it), with no
+ * host wait, so it can be captured into a HIP graph. No counterpart in the
+ * reference, which has no kernels that can abandon work; the caller reads
+ * `out` when the stream has reached it.
+ */
+SPARDA_API int sparda_status(uint32_t* out, int clear, void* stream);
+
 /*
  * KV block compressor.
  * Replaces KVBlockCompressor.forward (model/forecast.py:57-78).

@@ -68,6 +68,11 @@ SPARDA_API int sparda_version(void) { return 100; }
 
 SPARDA_API const char* sparda_last_error(void) { return g_last_error; }
 
+SPARDA_API int sparda_status(uint32_t* out, int clear, void* stream) {
+    SPARDA_REQUIRE(out, SPARDA_ERR_NULL, "status: null out");
+    return launch_read_status(out, clear != 0, static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
                                int64_t stride_b, int64_t stride_s, int64_t stride_h,
                                int64_t block_size, float* protos, void* stream) {

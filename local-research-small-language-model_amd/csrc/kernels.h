@@ -36,6 +36,9 @@ int launch_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_s
                           int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t bs, int causal, float scale,
                           void* out, int64_t out_sb, int64_t out_st, hipStream_t stream);
 
+// copy the device's status word (SPARDA_STATUS_* bits) to out, clearing it when asked
+int launch_read_status(uint32_t* out, int clear, hipStream_t stream);
+
 // dense (no selection lists) bf16 prefill, D = 64 (prefill_dense.hip)
 bool prefill_dense_supported(int dtype, int64_t Hq, int64_t Hkv, int64_t D, int64_t q_sb, int64_t q_st,
                              int64_t q_sh, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb,

@@ -39,6 +39,10 @@
 
 namespace sparda {
 
+// Per-device status word: SPARDA_STATUS_* bits set by kernels that had to
+// abandon work (read and cleared by sparda_status). Each GPU holds its own copy.
+__device__ uint32_t g_sparda_status;
+
 namespace {
 
 constexpr int kCMaxCap = 10;                    // selection entries per token
@@ -92,7 +96,7 @@ __device__ __forceinline__ int mask_count_below(const TokMask<W>& m, int t) {
 }
 constexpr float kCLog2e = 1.4426950408889634f;
 constexpr float kCGuard = 18446744073709551616.0f;  // 2^64
-constexpr uint32_t kCSpinLimit = 1u << 20;
+constexpr uint32_t kCSpinLimit = 1u << 20;  // polls of one ordering wait before it is abandoned
 constexpr int kSentinel = 0x7fffffff;
 constexpr int kCRouteK = kCMaxCap - 2;         // router picks per token when the kernel routes
 constexpr int kCRouteDf = 64;                   // forecast dimension when the kernel routes
@@ -145,7 +149,8 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                        int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
                        const int32_t* __restrict__ sel, const int32_t* __restrict__ n_sel, int64_t cap,
                        int64_t T, int H, int64_t NBq, int causal, float scale_log2,
-                       uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st, CompactRoute rt) {
+                       uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st, CompactRoute rt,
+                       uint32_t spin_limit) {
     using Smem = CompactSmem<R, W>;
     using Mask = TokMask<W>;
     constexpr int kCols = Smem::kCols;
@@ -616,7 +621,7 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
                     ready = ready && __hip_atomic_load(&sm.vers[sl[t].c], __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_WORKGROUP) >= rank[t];
             if (__ballot(!ready) == 0ull) break;
-            if (spins >= kCSpinLimit) {
+            if (spins >= spin_limit) {
                 if (lane == 0) atomicOr(&sm.flag, 2);
                 break;
             }
@@ -691,7 +696,10 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     }
 
     // ---- epilogue: out[b, t, h*64 + d] = O / l, 16-byte stores ----
-    const bool broken = (sm.flag & 2) != 0;  // a wait ran out (never expected): poison the window
+    // a wait ran out (never expected): the window is poisoned with NaN and
+    // the device's status word records it for the host (sparda_status)
+    const bool broken = (sm.flag & 2) != 0;
+    if (broken && tid == 0) atomicOr(&g_sparda_status, static_cast<uint32_t>(SPARDA_STATUS_PREFILL_WAIT_TIMEOUT));
     int e0 = tid;
     asm volatile("" : "+v"(e0));  // addresses computed here, not carried (in scratch) through the tiles
     for (int e = e0; e < kCols * 8; e += kT) {
@@ -734,6 +742,19 @@ static bool compact_layout_ok(int64_t R, int64_t q_sb, int64_t q_st, int64_t q_s
 // not depend on its tile mates).
 static int pick_window(int64_t R) { return R <= 3 ? 128 : 64; }
 
+// Polls an ordering wait makes before the workgroup abandons it (the window
+// is then NaN and the status word flags it). SPARDA_PREFILL_WAIT_LIMIT
+// overrides the default, read once per process: failure-handling tests set
+// it to 0 so that any wait not ready at its first poll is abandoned, with
+// every wave still finishing its work normally.
+static uint32_t wait_limit() {
+    static const uint32_t lim = [] {
+        const char* e = getenv("SPARDA_PREFILL_WAIT_LIMIT");
+        return e != nullptr ? static_cast<uint32_t>(strtoul(e, nullptr, 10)) : kCSpinLimit;
+    }();
+    return lim;
+}
+
 bool prefill_compact_supported(int dtype, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t bs,
                                const int32_t* sel, int64_t cap, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t out_sb, int64_t out_st,
@@ -770,13 +791,15 @@ static int launch_compact(const void* q, int64_t q_sb, int64_t q_st, int64_t q_s
     const int64_t NBq = cdiv(T, W);  // query windows per (sequence, KV head)
     dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
     const float sl = scale * kCLog2e;
+    const uint32_t spin = wait_limit();
 #define SPARDA_PC(R_, W_)                                                                                    \
     if (bs == 32) SPARDA_PCB(R_, 32, W_); else SPARDA_PCB(R_, 64, W_)
 #define SPARDA_PCB(R_, BS_, W_)                                                                              \
     hipLaunchKernelGGL((prefill_compact_kernel<R_, BS_, FDT, W_>), grid, dim3(kCThreads), 0, stream,          \
                        static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k),    \
                        static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, sel, n_sel, cap, T,              \
-                       static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st, rt)
+                       static_cast<int>(Hkv), NBq, causal, sl, static_cast<uint16_t*>(out), out_sb, out_st, rt, \
+                       spin)
     switch (R) {
         case 1: SPARDA_PC(1, 128); break;
         case 2: SPARDA_PC(2, 128); break;
@@ -807,6 +830,17 @@ int launch_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, int64_t q_s
                                           B, T, Hq, Hkv, bs, causal, scale, out, out_sb, out_st, stream);
     return launch_compact<SPARDA_BF16>(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, nullptr, nullptr, 0, rt, B,
                                        T, Hq, Hkv, bs, causal, scale, out, out_sb, out_st, stream);
+}
+
+__global__ void read_status_kernel(uint32_t* __restrict__ out, int clear) {
+    if (threadIdx.x == 0) {
+        *out = clear ? atomicExch(&g_sparda_status, 0u) : atomicOr(&g_sparda_status, 0u);
+    }
+}
+
+int launch_read_status(uint32_t* out, int clear, hipStream_t stream) {
+    hipLaunchKernelGGL(read_status_kernel, dim3(1), dim3(kWave), 0, stream, out, clear);
+    return check_hip(hipGetLastError(), "read_status_kernel");
 }
 
 }  // namespace sparda

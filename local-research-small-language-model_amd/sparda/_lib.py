@@ -46,6 +46,7 @@ _size = ctypes.c_size_t
 SIGNATURES = {
     "sparda_version": (_int, []),
     "sparda_last_error": (ctypes.c_char_p, []),
+    "sparda_status": (_int, [_p, _int, _p]),
     "sparda_compress": (_int, [_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
     "sparda_route": (_int, [_p, _int, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _int, _i64, _i64, _f32, _p, _p, _p, _p, _i64, _p]),

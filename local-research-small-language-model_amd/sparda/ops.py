@@ -360,6 +360,19 @@ class DecodeWorkspace:
         return self.buf
 
 
+STATUS_PREFILL_WAIT_TIMEOUT = 1
+
+
+def status(device=None, clear: bool = True) -> int:
+    """The device's status word (STATUS_* bits raised by kernels since it was
+    last cleared), read on the current stream; clears it unless clear=False.
+    Waits for the stream to reach the read (one .item())."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    word = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("sparda_status", word.data_ptr(), 1 if clear else 0, _stream(dev))
+    return int(word.item()) & 0xffffffff
+
+
 def decode_workspace_bytes(B: int, S: int, Hq: int, Hkv: int, D: int, block_size: int, top_k: int) -> int:
     return int(_lib.load().sparda_decode_workspace_bytes(B, S, Hq, Hkv, D, block_size, top_k))
 
