@@ -739,9 +739,10 @@ def bench_teacher(args, torch, sparda, synth):
 def pmc_workload(args, torch, sparda, synth):
     """Short eager run for hardware-counter passes: at B=4 T=4096, then at B=1
     T=16384, three prefill steps (compress + routed prefill) and one step of
-    the three-launch form (compress, router, prefill from its lists); decode
-    steps and a plain device copy of COPY_BYTES (the calibration of
-    FETCH_SIZE / WRITE_SIZE). Counter values are per dispatch, in this order."""
+    the three-launch form (compress, router, prefill from its lists); then one
+    dense causal prefill at B=1 T=16384 (no lists); decode steps and a plain
+    device copy of COPY_BYTES (the calibration of FETCH_SIZE / WRITE_SIZE).
+    Counter values are per dispatch, in this order."""
     x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
     x16 = synth.prefill_inputs(1, MT, HQ, HKV, D, dtype=torch.bfloat16, seed=1003, device="cuda")
     c = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002, device="cuda")
@@ -756,6 +757,7 @@ def pmc_workload(args, torch, sparda, synth):
             protos = sparda.compress(xs["k"], BS)
             _, _, sel, n_sel = sparda.route(xs["forecast"], protos, BS, TOPK, want_topk=False, want_sel=True)
             sparda.prefill(xs["q"], xs["k"], xs["v"], sel, n_sel, BS)
+        sparda.prefill(x16["q"], x16["k"], x16["v"], None, None, BS)
         for _ in range(3):
             sparda.decode(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], BS, TOPK, routing="absolute",
                           workspace=ws)
