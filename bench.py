@@ -844,7 +844,7 @@ def cpu_decode_baseline(args, torch, synth, info):
     out = {"value": round(legs[n][0] * 1e6, 1), "unit": "us/step", "cores": n, "kind": "port",
            "sample": f"the decode workload (B=8, 16K cache, bf16) through the reference's decode step restated "
                      f"op for op in PyTorch (whole-cache recompression, absolute-position routing as the GPU "
-                     f"leg, topk compaction, gather, masked SDPA); warm-up 3, median of 10 runs of {steps} "
+                     f"leg, topk compaction, gather, masked SDPA); warm-up 3, median of 20 runs of {steps} "
                      f"steps; torch threads={n}",
            "min_us": round(legs[n][1] * 1e6, 1), "max_us": round(legs[n][2] * 1e6, 1), "cpu": info}
     if 1 in legs and n != 1:
