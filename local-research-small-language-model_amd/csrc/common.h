@@ -135,6 +135,28 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Query window of workgroup `id` in a grid of BH (sequence, KV head) pairs x
+// NBq windows, heaviest (latest) windows first. Workgroups go to the chip's 8
+// XCDs in turn (XCD id % 8), each XCD with its own L2. With fewer pairs than
+// XCDs, a pair's windows are cut into 2S chunks (S = 8 / BH XCDs per pair) and
+// XCD slot s takes chunk s, then its mirror 2S-1-s, each heaviest first: the
+// XCD reads the K/V blocks of two window ranges of one pair instead of the
+// whole sequence, and the slots get about equal work when a window's cost
+// grows with its position. Otherwise consecutive ids cycle through the pairs.
+__device__ __forceinline__ void window_order(int64_t id, int64_t BH, int64_t NBq, int64_t& bg, int64_t& qw) {
+    constexpr int64_t kXcd = 8;
+    if (BH < kXcd && kXcd % BH == 0 && NBq % (2 * (kXcd / BH)) == 0) {
+        const int64_t x = id % kXcd, j = id / kXcd;
+        const int64_t S = kXcd / BH, s = x / BH, c = NBq / (2 * S);
+        bg = x % BH;
+        const int64_t chunk = j < c ? s : 2 * S - 1 - s;
+        qw = NBq - 1 - (chunk * c + (j < c ? j : j - c));
+    } else {
+        bg = id % BH;
+        qw = NBq - 1 - id / BH;
+    }
+}
+
 // VEC consecutive elements widened to fp32 (the index must be VEC-aligned).
 template <int DT, int VEC>
 __device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&o)[VEC]) {

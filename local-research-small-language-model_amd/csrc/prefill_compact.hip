@@ -168,10 +168,10 @@ prefill_compact_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_s
     const bool owner = wave % kSetWaves == 0;
     const int tok = (wave / kSetWaves) * 64 + lane;
 
-    // heaviest query blocks first; consecutive ids cycle through (b, g)
+    // heaviest query windows first, XCD-aware when there are few (b, g) pairs
     const int64_t BH = static_cast<int64_t>(gridDim.x) / NBq;
-    const int64_t bg = blockIdx.x % BH;
-    const int64_t qb = NBq - 1 - blockIdx.x / BH;
+    int64_t bg, qb;
+    window_order(blockIdx.x, BH, NBq, bg, qb);
     const int b = static_cast<int>(bg / H);
     const int g = static_cast<int>(bg % H);
     static_assert(BS == 64 || BS == 32, "KV blocks of 64 or 32 keys");

@@ -59,10 +59,10 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
     const int col16 = lane % 16;
     const int grp = lane / 16;
 
-    // heaviest windows first; consecutive ids cycle through (b, g)
+    // heaviest windows first, XCD-aware when there are few (b, g) pairs
     const int64_t BH = static_cast<int64_t>(gridDim.x) / NBq;
-    const int64_t bg = blockIdx.x % BH;
-    const int64_t qw = NBq - 1 - blockIdx.x / BH;
+    int64_t bg, qw;
+    window_order(blockIdx.x, BH, NBq, bg, qw);
     const int b = static_cast<int>(bg / H);
     const int g = static_cast<int>(bg % H);
     const int64_t t0 = qw * kDWin;
