@@ -334,9 +334,12 @@ def bench_decode(args, torch, sparda, synth):
 
 def bench_offload(args, torch, sparda, synth):
     """12-layer decode at a 32K context with every layer but layer 0 holding its
-    KV in a pinned host arena: forecast-routed blocks prefetched on a side
-    stream while the previous layer's attention + FFN run. Also times the
-    synchronous offload step and the fully GPU-resident sparse step."""
+    KV in a pinned host arena: forecast-routed blocks prefetched while the
+    previous layer runs (eagerly on a side stream; replayed from a graph,
+    carried by the previous layer's attention launch, on a side stream, or
+    serially). Also times the synchronous offload step, the fully GPU-resident
+    sparse step, and one layer's attention launch with and without the next
+    layer's prefetch inside it."""
     from model.attention import AsyncOffloadedKVCache, KVCache, OffloadedKVCache, PrototypeKVCache
     from model.config import ModelConfig
     from model.model import SparDAResearchModel
@@ -364,7 +367,7 @@ def bench_offload(args, torch, sparda, synth):
             res_caches[li].update(kd, vd)
     torch.cuda.synchronize()
     g = torch.Generator().manual_seed(1006)
-    ids = torch.randint(0, cfg.vocab_size, (8 * (W + K), 1, 1), generator=g).to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (12 * (W + K), 1, 1), generator=g).to(dev)
     it = iter(range(ids.shape[0]))
 
     def run(m, caches, n):
@@ -458,28 +461,76 @@ def bench_offload(args, torch, sparda, synth):
     del proto_caches
 
     # the offloaded step replayed from a HIP graph (GraphDecoder over the same
-    # host arenas, positions in device memory): the prefetch of layer L+1 on a
-    # side stream under layer L's attention + FFN, and the same step with the
-    # prefetches on the compute stream (no overlap)
+    # host arenas, positions in device memory): the prefetch of layer L+1
+    # carried by layer L's attention launch (the default), on a side stream
+    # under layer L's attention + FFN, and on the compute stream (no overlap)
     from model.decode_graph import GraphDecoder
 
-    def offload_graph_us(overlap):
-        gd = GraphDecoder(model, 1, cap, caches=off_caches, overlap=overlap)
-        with torch.no_grad():
+    # the three decoders are recorded first, then timed in alternating rounds
+    # of S steps (median over the rounds), so that a drift of the host link
+    # or clocks during the run affects the three alike
+    R, S = 8, max(1, K // 8)
+    decs = {name: GraphDecoder(model, 1, cap, caches=off_caches, overlap=m)
+            for name, m in (("fused", "fused"), ("side", True), ("serial", False))}
+    rounds = {name: [] for name in decs}
+    with torch.no_grad():
+        for gd in decs.values():
             for _ in range(W):
                 gd.step(ids[next(it)])
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(K // 2):
-                gd.step(ids[next(it)])
-            e1.record()
-            e1.synchronize()
-        del gd
-        return e0.elapsed_time(e1) * 1e3 / (K // 2)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(R):
+            for name, gd in decs.items():
+                e0.record()
+                for _ in range(S):
+                    gd.step(ids[next(it)])
+                e1.record()
+                e1.synchronize()
+                rounds[name].append(e0.elapsed_time(e1) * 1e3 / S)
+    del decs
+    med = {name: sorted(v)[len(v) // 2] for name, v in rounds.items()}
+    us_off_graph, us_off_graph_side, us_off_graph_serial = med["fused"], med["side"], med["serial"]
 
-    us_off_graph = offload_graph_us(overlap=True)
-    us_off_graph_serial = offload_graph_us(overlap=False)
+    # one layer's launches at this context (HIP events on the launch stream):
+    # layer 1's attention over its fetched blocks alone, layer 2's prefetch
+    # (selection + host-link copy) as launches of their own, and layer 1's
+    # attention launch carrying layer 2's prefetch
+    c1, c2 = off_caches[1], off_caches[2]
+    L = c1.current_len
+    pos = torch.full((1,), L, dtype=torch.int64, device=dev)
+    gq = torch.Generator().manual_seed(1007)
+    q1 = torch.randn(1, HQ, D, generator=gq).to(dev, torch.bfloat16)
+    kn1 = torch.randn(1, HKV, D, generator=gq).to(dev, torch.bfloat16)
+    vn1 = torch.randn(1, HKV, D, generator=gq).to(dev, torch.bfloat16)
+    f1 = torch.randn(1, HKV, D, generator=gq).to(dev, torch.bfloat16)
+    bufs = [dict(sel=torch.empty((1, HKV, TOPK + 2), dtype=torch.int32, device=dev),
+                 n=torch.empty((1, HKV), dtype=torch.int32, device=dev),
+                 k=torch.empty((1, HKV, TOPK + 2, BS, D), dtype=torch.bfloat16, device=dev),
+                 v=torch.empty((1, HKV, TOPK + 2, BS, D), dtype=torch.bfloat16, device=dev)) for _ in range(2)]
+
+    def prefetch_into(c, bq):
+        sparda.select_decode_at(f1, c.block_sums(BS), pos, cap, BS, TOPK, routing="absolute", sel=bq["sel"],
+                                n_sel=bq["n"], lookahead=True)
+        c.arena.fetch_at(bq["sel"], bq["n"], BS, pos, bq["k"], bq["v"])
+
+    prefetch_into(c1, bufs[0])
+    spec = dict(arena=c2.arena, forecast=f1, block_sums=c2.block_sums(BS), top_k=TOPK, routing="absolute",
+                sel=bufs[1]["sel"], n_sel=bufs[1]["n"], k_dst=bufs[1]["k"], v_dst=bufs[1]["v"])
+
+    def attend(carry=None):
+        sparda.decode_at(q1, bufs[0]["k"], bufs[0]["v"], pos, BS, bufs[0]["sel"], bufs[0]["n"], max_len=cap,
+                         compact=True, k_new=kn1, v_new=vn1, prefetch=carry)
+
+    t_attn = events_ms(attend, 50, torch) * 1e3
+    t_pf = events_ms(lambda: prefetch_into(c2, bufs[1]), 50, torch) * 1e3
+    t_carry = events_ms(lambda: attend(spec), 50, torch) * 1e3
+    carried = {
+        "attention_us": round(t_attn, 2),
+        "prefetch_separate_us": round(t_pf, 2),
+        "attention_carrying_prefetch_us": round(t_carry, 2),
+        "hidden_us": round(t_attn + t_pf - t_carry, 2),
+        "overlap": round(min(1.0, max(0.0, 1.0 - (t_carry - t_attn) / t_pf)), 4) if t_pf > 0 else None,
+    }
     # host link: one 256 MiB pinned host -> device copy
     hb = torch.empty(256 << 20, dtype=torch.uint8).pin_memory()
     db = torch.empty_like(hb, device=dev)
@@ -491,8 +542,9 @@ def bench_offload(args, torch, sparda, synth):
     return {
         "workload": f"decode with offloaded KV: {OB_LAYERS} layers, B=1, context {OB_CTX} (512 blocks of 64), "
                     f"bf16 KV [32768,4,64] per layer in pinned host memory for layers 1..{OB_LAYERS - 1} "
-                    "(layer 0 GPU-resident), top-8 + sink + current blocks prefetched per layer on a side "
-                    "stream; step = one token through the 12-layer model incl. LM head",
+                    "(layer 0 GPU-resident), top-8 + sink + current blocks prefetched per layer (eager: on a side "
+                    "stream; replayed: carried by the previous layer's attention launch, or on a side stream, or "
+                    "serial); step = one token through the 12-layer model incl. LM head",
         "us_per_step_async": round(us_async, 1),
         "us_per_step_sync": round(us_sync, 1),
         "us_per_step_async_dma": round(us_async_dma, 1),
@@ -502,7 +554,10 @@ def bench_offload(args, torch, sparda, synth):
         "us_per_step_cached_prototypes": round(us_proto_eager, 1),
         "us_per_step_cached_prototypes_graph": round(us_proto_graph, 1),
         "us_per_step_async_graph": round(us_off_graph, 1),
+        "us_per_step_async_graph_side_stream": round(us_off_graph_side, 1),
         "us_per_step_async_graph_serial_prefetch": round(us_off_graph_serial, 1),
+        "async_graph_rounds_us": {name: [round(x, 1) for x in v] for name, v in rounds.items()},
+        "carried_prefetch_one_layer": carried,
         "steps": K,
         "overlap": round(1.0 - ex / tr, 4) if tr > 0 else None,
         "transfer_us_per_layer": round(tr * 1e3, 2),
@@ -900,7 +955,8 @@ def main():
               "model": bench_model, "producer": bench_producer, "teacher": bench_teacher,
               "generate": bench_generate, "pmc": pmc_workload}[args.only]
         r = fn(args, torch, sparda, synth)
-        print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}), flush=True)
+        print(json.dumps({args.only: {k: v for k, v in r.items() if isinstance(v, (int, float, str, list, dict))}}),
+              flush=True)
         return
     log("prefill workload")
     pre = bench_prefill(args, torch, sparda, synth)

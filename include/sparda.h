@@ -620,6 +620,61 @@ SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const
 SPARDA_API int sparda_offload_fetch_at(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
                                        int64_t sel_cap, int64_t block_size, const int64_t* len_dev, void* k_dst,
                                        void* v_dst, void* stream);
+
+/*
+ * The next layer's prefetch carried by a decode attention launch.
+ * The reference issues the prefetch of layer L+1 on a transfer stream before
+ * layer L's attention (AsyncForecastOffloadAttention.prefetch,
+ * model/attention/async_offload.py:170-294, called from
+ * model/transformer.py:110-115) so that the copy runs under layer L's
+ * attention and FFN. Here the same selection and copy run as extra
+ * workgroups of layer L's sparda_decode_at launch, one per (sequence, KV
+ * head), beside its attention workgroups: one stream, no cross-stream
+ * join, capturable. The results equal sparda_select_decode_at (lookahead)
+ * followed by sparda_offload_fetch_at (len_dev = pos_dev) bit for bit.
+ *   arena: the next layer's arena; its batch, KV heads, head dim and dtype
+ *     must be those of the attended layer
+ *   forecast: [B,Hkv,D] (strides f_sb, f_sh, 1), the forecast that routes
+ *     the next layer
+ *   block_sums: the next layer's [B,nb_stride,Hkv,D] fp32 sums (16-byte
+ *     aligned) covering the tokens before p
+ *   top_k, routing, scale: as sparda_select_decode_at (scale: the routing
+ *     scale)
+ *   sel / n_sel: [B,Hkv,sel_cap] / [B,Hkv] int32 receiving the selection
+ *   k_dst / v_dst: [B,Hkv,sel_cap,block_size,D] compact buffers (16-byte
+ *     aligned) receiving the blocks
+ */
+typedef struct sparda_prefetch_args {
+    sparda_offload_t arena;
+    const void* forecast;
+    int f_dtype;
+    int64_t f_sb, f_sh;
+    const float* block_sums;
+    int64_t nb_stride;
+    int64_t top_k;
+    int routing;
+    float scale;
+    int32_t* sel;
+    int32_t* n_sel;
+    int64_t sel_cap;
+    void* k_dst;
+    void* v_dst;
+} sparda_prefetch_args;
+
+/*
+ * sparda_decode_at (same arguments, same result) whose launch also carries
+ * `next`'s prefetch at the same position p = *pos_dev (the selection before
+ * token p is appended to the next layer). Needs the matrix-core attention:
+ * bf16, D = 64, blocks of 64 or 32 keys, 16-byte aligned q rows.
+ */
+SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                         int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                                         const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
+                                         int64_t window_k, const void* k_new, const void* v_new, int64_t new_sb,
+                                         int64_t new_sh, int64_t B, int64_t max_len, const int64_t* pos_dev,
+                                         int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, float scale,
+                                         void* out, int64_t out_sb, const sparda_prefetch_args* next,
+                                         void* stream);
 SPARDA_API int sparda_offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
                                         int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
                                         float* block_sums, void* stream);

@@ -381,12 +381,13 @@ SPARDA_API int sparda_select_decode_at(const void* forecast, int f_dtype, int64_
                                 static_cast<hipStream_t>(stream), pos_dev, lookahead != 0);
 }
 
-SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
-                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
-                                const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
-                                const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
-                                int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
-                                int64_t block_size, float scale, void* out, int64_t out_sb, void* stream) {
+static int decode_at_checked(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                             int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                             const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
+                             const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
+                             int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
+                             int64_t block_size, float scale, void* out, int64_t out_sb, void* stream,
+                             const sparda::PrefetchDev* pf) {
     SPARDA_REQUIRE(q && k && v && out && pos_dev, SPARDA_ERR_NULL, "decode_at: null q/k/v/out/pos_dev");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
                    "decode_at: pos_dev must be 8-byte aligned");
@@ -412,7 +413,75 @@ SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const
                    SPARDA_ERR_STRIDE, "decode_at: k_new/v_new rows must be 16-byte aligned");
     return launch_decode_at(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
                             k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
-                            out_sb, static_cast<hipStream_t>(stream));
+                            out_sb, static_cast<hipStream_t>(stream), pf);
+}
+
+SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                                const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
+                                const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
+                                int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
+                                int64_t block_size, float scale, void* out, int64_t out_sb, void* stream) {
+    return decode_at_checked(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
+                             k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
+                             out_sb, stream, nullptr);
+}
+
+SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                         int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
+                                         const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
+                                         int64_t window_k, const void* k_new, const void* v_new, int64_t new_sb,
+                                         int64_t new_sh, int64_t B, int64_t max_len, const int64_t* pos_dev,
+                                         int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, float scale,
+                                         void* out, int64_t out_sb, const sparda_prefetch_args* next,
+                                         void* stream) {
+    SPARDA_REQUIRE(next, SPARDA_ERR_NULL, "decode_at_prefetch: null prefetch arguments");
+    const sparda_prefetch_args& n = *next;
+    SPARDA_REQUIRE(n.arena, SPARDA_ERR_HANDLE, "decode_at_prefetch: null arena handle");
+    SPARDA_REQUIRE(n.forecast && n.block_sums && n.sel && n.n_sel && n.k_dst && n.v_dst, SPARDA_ERR_NULL,
+                   "decode_at_prefetch: null prefetch pointer");
+    SPARDA_REQUIRE(decode_at_matrix_core(dtype, D, block_size, q_sb, q_sh, q), SPARDA_ERR_MODE,
+                   "decode_at_prefetch: needs the matrix-core attention (bf16, D=64, blocks of 64 or 32 keys, "
+                   "16-byte aligned q rows)");
+    SPARDA_REQUIRE(offload_batch(n.arena) == B && offload_heads(n.arena) == Hkv && offload_head_dim(n.arena) == D &&
+                       offload_dtype(n.arena) == dtype,
+                   SPARDA_ERR_SHAPE, "decode_at_prefetch: the arena's batch, KV heads, head dim and dtype must be "
+                   "the attended layer's");
+    SPARDA_REQUIRE(dtype_ok(n.f_dtype), SPARDA_ERR_DTYPE, "decode_at_prefetch: forecast dtype %d", n.f_dtype);
+    SPARDA_REQUIRE(n.routing == SPARDA_ROUTE_REFERENCE || n.routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
+                   "decode_at_prefetch: unknown routing %d", n.routing);
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(n.block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
+                   "decode_at_prefetch: block_sums must be 16-byte aligned");
+    SPARDA_REQUIRE(n.top_k >= 1 && n.top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "decode_at_prefetch: top_k out of range");
+    SPARDA_REQUIRE(n.sel_cap >= n.top_k + 2 && n.sel_cap <= kMaxSelCap, SPARDA_ERR_SHAPE,
+                   "decode_at_prefetch: sel_cap must be in [top_k+2, %d]", kMaxSelCap);
+    SPARDA_REQUIRE(max_len >= 1 && n.nb_stride >= cdiv(max_len, block_size), SPARDA_ERR_SHAPE,
+                   "decode_at_prefetch: nb_stride too small");
+    SPARDA_REQUIRE(cdiv(max_len, block_size) <= 4096, SPARDA_ERR_SHAPE, "decode_at_prefetch: more than 4096 blocks");
+    SPARDA_REQUIRE(aligned16(n.k_dst) && aligned16(n.v_dst), SPARDA_ERR_STRIDE,
+                   "decode_at_prefetch: destinations must be 16-byte aligned");
+    PrefetchDev pf{};
+    pf.f = n.forecast;
+    pf.f_sb = n.f_sb;
+    pf.f_sh = n.f_sh;
+    pf.f_bf16 = n.f_dtype == SPARDA_BF16 ? 1 : 0;
+    pf.sums = n.block_sums;
+    pf.nb_stride = n.nb_stride;
+    pf.pos_max = max_len - 1;
+    pf.bs = static_cast<int>(block_size);
+    pf.k = static_cast<int>(n.top_k);
+    pf.cap = static_cast<int>(n.sel_cap);
+    pf.absolute = n.routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0;
+    pf.pow2 = (block_size & (block_size - 1)) == 0 ? 1 : 0;
+    pf.scale = n.scale;
+    pf.sel = n.sel;
+    pf.n_sel = n.n_sel;
+    pf.dk = static_cast<char*>(n.k_dst);
+    pf.dv = static_cast<char*>(n.v_dst);
+    offload_prefetch_dev(n.arena, &pf);
+    return decode_at_checked(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
+                             k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
+                             out_sb, stream, &pf);
 }
 
 SPARDA_API int sparda_offload_create(int64_t B, int64_t max_seq, int64_t Hkv, int64_t D, int dtype,

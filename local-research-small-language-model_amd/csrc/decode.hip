@@ -22,6 +22,7 @@
 #include "kernels.h"
 #include "attend.h"
 #include "mfma.h"
+#include "prefetch.h"
 #include "select.h"
 
 namespace sparda {
@@ -180,7 +181,8 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      int32_t* __restrict__ sel_out, int32_t* __restrict__ n_sel_out,
                      void* __restrict__ out, int64_t out_sb, const int64_t* __restrict__ pos_dev,
                      float* sums, int64_t nb_stride, int update_sums, const void* __restrict__ fsel,
-                     int fsel_bf16, int64_t fs_sb, int64_t fs_sh, int absolute, float fscale, int pow2) {
+                     int fsel_bf16, int64_t fs_sb, int64_t fs_sh, int absolute, float fscale, int pow2,
+                     PrefetchDev pf) {
     using E = typename KvElem<DT>::T;
     constexpr int VR = v_row_elems<DT, DH>();
     constexpr int KW = DT == SPARDA_BF16 ? DH / 2 : DH;  // K row words per lane
@@ -195,6 +197,16 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
 
     const int g = blockIdx.x;
     const int b = blockIdx.y;
+    if constexpr (MF) {
+        // blockIdx.z = 1: the next layer's prefetch for (b, g), carried by this
+        // launch so that its selection and host-link copy run beside the
+        // attention workgroups (the host sets z = 2 only with pf filled in)
+        if (blockIdx.z != 0) {
+            prefetch_workgroup<CH, DH>(pf, g, b, pos_dev, fsel_lds, reinterpret_cast<uint32_t*>(dyn), sel_lds, ck_lds,
+                                       ci_lds, &n_lds);
+            return;
+        }
+    }
     const int R = Hq / H;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
@@ -707,7 +719,13 @@ struct AttendArgs {
     float* sums = nullptr; int64_t nb_stride = 0; int update_sums = 0;
     const void* fsel = nullptr; int fsel_bf16 = 0; int64_t fs_sb = 0, fs_sh = 0;
     int absolute = 0; float fscale = 0.0f;
+    const PrefetchDev* pf = nullptr;  // the next layer's prefetch carried by the launch (matrix-core path)
 };
+
+bool decode_at_matrix_core(int dtype, int64_t D, int64_t bs, int64_t q_sb, int64_t q_sh, const void* q) {
+    return dtype == SPARDA_BF16 && D == 64 && (bs == 64 || bs == 32) && (q_sb % 8) == 0 && (q_sh % 8) == 0 &&
+           (reinterpret_cast<uintptr_t>(q) & 15u) == 0;
+}
 
 static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     const int64_t NB = cdiv(a.S, a.bs);
@@ -717,11 +735,13 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     // most blocks one workgroup can attend: the selection capacity, or every block when dense
     const int64_t max_blocks = a.sel_mode == 1 ? NB : a.cap;
     // matrix-core block attention: bf16, D = 64, bs = 64, 16-byte aligned q rows
-    const bool mf = a.dtype == SPARDA_BF16 && a.D == 64 && (a.bs == 64 || a.bs == 32) && (a.q_sb % 8) == 0 &&
-                    (a.q_sh % 8) == 0 && (reinterpret_cast<uintptr_t>(a.q) & 15u) == 0;
+    const bool mf = decode_at_matrix_core(a.dtype, a.D, a.bs, a.q_sb, a.q_sh, a.q);
+    if (a.pf != nullptr && !mf)
+        return set_error(SPARDA_ERR_MODE, "decode: a carried prefetch needs the bf16 D=64 matrix-core attention");
+    const PrefetchDev pf = a.pf != nullptr ? *a.pf : PrefetchDev{};
     constexpr size_t kLdsBudget = 150 * 1024;
     const int pow2 = (a.bs & (a.bs - 1)) == 0 ? 1 : 0;
-    dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
+    dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B), a.pf != nullptr ? 2u : 1u);
 #define SPARDA_ATT(DT_, DH_, CH_)                                                                        \
     do {                                                                                                 \
         if constexpr (DT_ == SPARDA_BF16 && DH_ == 64) {                                                 \
@@ -740,14 +760,15 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
         int waves = max_blocks < kAttendMaxWaves ? static_cast<int>(max_blocks) : kAttendMaxWaves;       \
         while (waves > 1 && ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb > kLdsBudget) --waves; \
         size_t lds = ((waves * pb + 15) & ~static_cast<size_t>(15)) + waves * wb;                        \
-        if (a.sel_mode == 4 && lds < static_cast<size_t>(NB) * 4) lds = static_cast<size_t>(NB) * 4;       \
+        if ((a.sel_mode == 4 || a.pf != nullptr) && lds < static_cast<size_t>(NB) * 4)                  \
+            lds = static_cast<size_t>(NB) * 4;                                                           \
         hipLaunchKernelGGL((decode_attend_kernel<DT_, DH_, CH_, MF_, MBS_>), grid2, dim3(waves * kWave), lds, stream, \
                            a.q, a.q_sb, a.q_sh, a.kc, a.vc, a.kv_sb, a.kv_ss, a.kv_sh, a.S, Hq_i, Hkv_i,  \
                            static_cast<int>(a.bs), NB, static_cast<int>(a.k), a.sel_mode, a.cap,         \
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
                            a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb, a.pos_dev, a.sums, \
                            a.nb_stride, a.update_sums, a.fsel, a.fsel_bf16, a.fs_sb, a.fs_sh, a.absolute,       \
-                           a.fscale, pow2);                                                                    \
+                           a.fscale, pow2, pf);                                                                \
     } while (0)
 #define SPARDA_ATT_C(DT_, DH_)                            \
     if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
@@ -871,7 +892,7 @@ int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, c
                      const int32_t* n_sel, int64_t cap, int64_t window_k, const void* k_new, const void* v_new,
                      int64_t new_sb, int64_t new_sh, int64_t B, int64_t S_max, const int64_t* pos_dev,
                      int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
-                     hipStream_t stream) {
+                     hipStream_t stream, const PrefetchDev* pf) {
     int mode, cap_i;
     int64_t kk;
     if (sel != nullptr) {
@@ -884,6 +905,7 @@ int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, c
     AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S_max, Hq, Hkv, D, bs, kk, mode, cap_i, scale,
                  nullptr, sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb,
                  pos_dev};
+    a.pf = pf;
     return launch_attend(a, stream);
 }
 

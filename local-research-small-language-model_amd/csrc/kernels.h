@@ -129,14 +129,48 @@ int launch_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
                        int routing, float scale, float fscale, int32_t* sel_out, int32_t* n_sel_out, void* out,
                        int64_t out_sb, hipStream_t stream);
 
+// The prefetch of the next layer's blocks carried by a decode attention launch
+// as extra workgroups, one per (sequence, KV head): the selection of
+// launch_select_decode with pos_dev and lookahead (blocks of [0, p) scored from
+// the block sums; p = *pos_dev clamped into [0, pos_max]), then the copy of
+// offload_fetch's gather kernel from the arena into the compact buffers
+// (arena length p, clamped into [0, Smax]).
+struct PrefetchDev {
+    const void* f;          // forecast [B, H, D], element strides (f_sb, f_sh, 1)
+    int64_t f_sb, f_sh;
+    int f_bf16;
+    const float* sums;      // [B, nb_stride, H, D] fp32, 16-byte aligned
+    int64_t nb_stride;
+    int64_t pos_max;
+    int bs, k, cap, absolute, pow2;
+    float scale;
+    int32_t* sel;           // [B, H, cap]
+    int32_t* n_sel;         // [B, H]
+    const char* ak;         // arena device mappings, [B][H][Smax][row_bytes] each
+    const char* av;
+    int64_t H, Smax, row_bytes;
+    char* dk;               // compact buffers [B][H][cap][bs][row_bytes] each
+    char* dv;
+};
+// the arena fields of a PrefetchDev (ak, av, H, Smax, row_bytes)
+void offload_prefetch_dev(sparda_offload_t h, PrefetchDev* pf);
+int64_t offload_batch(sparda_offload_t h);
+int64_t offload_heads(sparda_offload_t h);
+int64_t offload_head_dim(sparda_offload_t h);
+int offload_dtype(sparda_offload_t h);
+
 // attention at a device-held position: S = *pos_dev + 1 (clamped to S_max);
-// the caller's list (sel), the window of window_k blocks, or every block
+// the caller's list (sel), the window of window_k blocks, or every block.
+// pf (optional, bf16 D = 64 matrix-core attention only): the next layer's
+// prefetch in the same launch.
 int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
                      int64_t kv_ss, int64_t kv_sh, int dtype, int compact, const int32_t* sel,
                      const int32_t* n_sel, int64_t cap, int64_t window_k, const void* k_new, const void* v_new,
                      int64_t new_sb, int64_t new_sh, int64_t B, int64_t S_max, const int64_t* pos_dev,
                      int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
-                     hipStream_t stream);
+                     hipStream_t stream, const PrefetchDev* pf = nullptr);
+// whether launch_decode_at takes the matrix-core attention (which can carry a prefetch)
+bool decode_at_matrix_core(int dtype, int64_t D, int64_t bs, int64_t q_sb, int64_t q_sh, const void* q);
 
 // host-resident KV arena (offload.hip)
 constexpr int64_t kMaxFetchSlots = 1024;  // selection capacity of a DMA fetch

@@ -28,6 +28,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "prefetch.h"
 #include "select.h"
 
 struct sparda_offload {
@@ -104,6 +105,18 @@ int offload_destroy(sparda_offload_t h) {
 }
 
 int64_t offload_max_seq(sparda_offload_t h) { return h->Smax; }
+int64_t offload_batch(sparda_offload_t h) { return h->B; }
+int64_t offload_heads(sparda_offload_t h) { return h->H; }
+int64_t offload_head_dim(sparda_offload_t h) { return h->D; }
+int offload_dtype(sparda_offload_t h) { return h->dtype; }
+
+void offload_prefetch_dev(sparda_offload_t h, PrefetchDev* pf) {
+    pf->ak = h->dev;
+    pf->av = h->dev + arena_bytes(h);
+    pf->H = h->H;
+    pf->Smax = h->Smax;
+    pf->row_bytes = h->D * h->esz;
+}
 
 void offload_host(sparda_offload_t h, void** k, void** v) {
     *k = h->host;
@@ -154,15 +167,15 @@ block_sums_kernel(const void* __restrict__ k, int64_t sb, int64_t st, int64_t sh
         float* out = sums + ((b * nb_stride + j) * H + g) * D + d;
         const int64_t base = b * sb + g * sh + d;
         float acc = s_lo == j * bs ? 0.0f : *out;
-        int64_t s = s_lo;
-        for (; s + U <= s_hi; s += U) {
+        // a partial last batch reads its last token again and skips the repeats
+        for (int64_t s = s_lo; s < s_hi; s += U) {
             float x[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + (s + u - pos) * st);
+            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(k, base + ((s + u < s_hi ? s + u : s_hi - 1) - pos) * st);
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc = acc + x[u];
+            for (int u = 0; u < U; ++u)
+                if (s + u < s_hi) acc = acc + x[u];
         }
-        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(k, base + (s - pos) * st);
         *out = acc;
     }
 }
@@ -207,16 +220,17 @@ append_at_kernel(void* __restrict__ kc, void* __restrict__ vc, int64_t sb, int64
     for (int64_t e = threadIdx.x; e < H * D; e += blockDim.x) {
         const int64_t g = e / D, d = e % D;
         const int64_t base = b * sb + g * sh + d;
+        // rows in batches of U loads in flight (a partial last batch reads its
+        // last row again and skips the repeats), added in row order
         float acc = 0.0f;
-        int64_t s = j * bs;
-        for (; s + U <= s_hi; s += U) {
+        for (int64_t s = j * bs; s < s_hi; s += U) {
             float x[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(kc, base + (s + u) * st);
+            for (int u = 0; u < U; ++u) x[u] = load_elem<DT>(kc, base + (s + u < s_hi ? s + u : s_hi - 1) * st);
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc = acc + x[u];
+            for (int u = 0; u < U; ++u)
+                if (s + u < s_hi) acc = acc + x[u];
         }
-        for (; s < s_hi; ++s) acc = acc + load_elem<DT>(kc, base + s * st);
         if (k_new != nullptr) {
             const int64_t ni = b * n_sb + g * n_sh + d;
             const E kv = static_cast<const E*>(k_new)[ni];
@@ -310,7 +324,6 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
     const int g = blockIdx.x;
     const int b = blockIdx.y;
     const int tid = threadIdx.x;
-    const int lane = tid % kWave;
     const int64_t bg = static_cast<int64_t>(b) * H + g;
     // with pos_dev: a decode step at token p = *pos_dev (clamped into [0, pos_arg]),
     // len = p + 1, or with lookahead the prefetch before token p is appended,
@@ -323,41 +336,10 @@ select_decode_kernel(const void* __restrict__ f, int64_t f_sb, int64_t f_sh, con
         score_pos = absolute ? pos : 0;
     }
     const int own = static_cast<int>(pos / bs);
-    for (int d = tid; d < DH; d += kSelThreads) f_lds[d] = load_elem<FDT>(f, b * f_sb + g * f_sh + d);
-    __syncthreads();
-    const bool dense = own + 1 <= k + 2;
-    if (!dense) {
-        // every thread scores blocks tid, tid + 256, ...: p = sum / bs, canonical
-        // fma chain; all DH/4 loads of a block are issued before the chain. For
-        // a power-of-two bs, sum * (1/bs) is the same correctly rounded value as
-        // sum / bs (the reciprocal is exact), at the cost of one multiply.
-        const float den = static_cast<float>(bs);
-        const float inv = 1.0f / den;
-        const int64_t limit = score_pos / bs;
-        for (int64_t j = tid; j < n_present; j += kSelThreads) {
-            const float s = j <= limit ? score_from_sum<DH, POW2>(sums + ((b * nb_stride + j) * H + g) * DH, f_lds,
-                                                                 den, inv, scale)
-                                       : -__builtin_inff();
-            key_lds[j] = order_key(s);
-        }
-    }
-    __syncthreads();
-    if (tid < kWave) {
-        int m;
-        if (dense) {
-            m = own + 1;
-            if (lane < m) sel_lds[lane] = lane;
-        } else {
-            m = select_keys_upto<CH>(key_lds, static_cast<int>(n_present), k, own, sel_lds, lane, ck_lds, ci_lds);
-            if (own >= n_present) {  // the own block holds no token yet: it has no score but is attended
-                if (lane == 0) sel_lds[m] = own;
-                m += 1;
-            }
-        }
-        if (lane == 0) m_lds = m;
-    }
-    __syncthreads();
-    const int m = m_lds;
+    const int m = select_from_sums<CH, DH, POW2>(f, FDT == SPARDA_BF16, b * f_sb + g * f_sh,
+                                                 sums + (b * nb_stride * H + g) * DH, H * DH, n_present,
+                                                 score_pos / bs, own, k, static_cast<int>(bs), scale, f_lds,
+                                                 key_lds, sel_lds, ck_lds, ci_lds, &m_lds);
     for (int i = tid; i < cap; i += kSelThreads) sel[bg * cap + i] = i < m ? sel_lds[i] : -1;
     if (tid == 0) n_sel[bg] = m;
 }

@@ -27,11 +27,15 @@ densely, as the eager path does). Layer L's block issues the prefetch of
 layer L+1 right after its producer has formed F_L (transformer.py:110-115):
 the selection from layer L+1's block sums (the lookahead before token *pos
 is appended, async_offload.py:196-260) and the gather of the selected blocks
-from the arena into device buffers, then an event that layer L+1 waits for;
-with overlap=True on a side stream, so that the copy over the host link runs
-under layer L's attention and FFN inside the graph. Layer L+1 then appends
-its token into the arena and attends over the fetched blocks with the new
-token supplied separately.
+from the arena into device buffers, then an event that layer L+1 waits for.
+With overlap="fused" (the default) the selection and the copy over the host
+link run as extra workgroups of layer L's attention launch
+(sparda_decode_at_prefetch), beside its attention workgroups: the overlap the
+reference gets from its transfer stream, without a cross-stream dependency
+in the graph. overlap=False issues them as launches of their own on the
+compute stream, overlap=True on a side stream joined by an event. Layer L+1
+then appends its token into the arena and attends over the fetched blocks
+with the new token supplied separately.
 
 The kernels and their launch shapes are those of the eager decode with the
 fused producer (HipSparseAttention with PrototypeKVCache, or
@@ -71,12 +75,12 @@ class GraphDecoder:
     caches: None (a PrototypeKVCache per sparse layer; for offload layers a
     GPU KVCache at layer 0 and an AsyncOffloadedKVCache elsewhere), or one
     cache per layer of those types, all holding the same number of tokens
-    (their contents are decoded on from there). overlap=True issues the
-    offload prefetches on a side stream joined by an event before the layer
-    that needs them; the default issues them on the compute stream, which a
-    replayed graph runs faster here (each cross-stream dependency inside the
-    graph costs more than the ~20 us per layer of selection and host-link
-    copy it would hide).
+    (their contents are decoded on from there). overlap selects where the
+    offload prefetch of layer L+1 runs: "fused" (default) inside layer L's
+    attention launch; False as launches of its own on the compute stream;
+    True on a side stream joined by an event before the layer that needs it
+    (each cross-stream dependency inside a replayed graph costs more than the
+    selection and host-link copy it would hide).
 
     taps: layers whose attention inputs and output the recorded step keeps in
     ``tapped[i]`` (q [B,Hq,D], the routing forecast or None, the attention
@@ -84,7 +88,7 @@ class GraphDecoder:
     buffers that every replay rewrites, for checking a replayed step."""
 
     def __init__(self, model, batch_size: int, max_seq_len: int, caches: Optional[Sequence] = None,
-                 overlap: bool = False, taps: Sequence[int] = ()):
+                 overlap="fused", taps: Sequence[int] = ()):
         cfg = model.config
         p = next(model.parameters())
         self.device = p.device
@@ -109,6 +113,8 @@ class GraphDecoder:
         self.B = batch_size
         self.max_len = max_seq_len
         self.block_size = cfg.block_size
+        if overlap not in (False, True, "fused"):
+            raise ValueError(f"GraphDecoder: overlap must be False, True or 'fused', got {overlap!r}")
         self.overlap = overlap
         bs, H, D = cfg.block_size, cfg.n_kv_head, cfg.head_dim
         if caches is None:
@@ -171,26 +177,42 @@ class GraphDecoder:
         return self.kinds[i] == _SPARSE and a.mode not in ("dense", "static") and f is not None
 
     def _attend(self, i: int, a, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                f: Optional[torch.Tensor]) -> torch.Tensor:
+                f: Optional[torch.Tensor], carry=None) -> torch.Tensor:
+        """Layer i's append and attention; carry = (j, f_i): layer j's prefetch
+        for this step, carried by the attention launch."""
         bs = self.block_size
         cache = self.caches[i]
         kind = self.kinds[i]
+        nxt = self._prefetch_spec(*carry) if carry is not None else None
         if kind == _OFFLOAD:
             pf = self._pf[i]
             torch.cuda.current_stream().wait_event(pf["ev"])
             cache.arena.append_at(k, v, self.pos, bs, cache.block_sums(bs))
             return sparda.decode_at(q, pf["k"], pf["v"], self.pos, bs, pf["sel"], pf["n"], max_len=self.max_len,
-                                    compact=True, k_new=k[:, 0], v_new=v[:, 0])
+                                    compact=True, k_new=k[:, 0], v_new=v[:, 0], prefetch=nxt)
         if kind == _RESIDENT_DENSE:
             sparda.append_at(cache.k, cache.v, self.pos, bs, None, k, v)
-            return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len)
+            return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len,
+                                    prefetch=nxt)
         if self._producer_appends(i, a, f):
+            if carry is not None:  # this launch carries no prefetch: issue it first
+                self._prefetch(*carry)
             return sparda.decode_sums(q, cache.k, cache.v, self.max_len, f, cache.block_sums, bs, a.top_k_blocks,
                                       routing=a.decode_routing, pos_dev=self.pos, update_current=True)
         # dense / static-window layers: the append keeps the block sums current
         sparda.append_at(cache.k, cache.v, self.pos, bs, cache.block_sums, k, v)
         window = 0 if a.mode == "dense" else a.top_k_blocks
-        return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=window, max_len=self.max_len)
+        return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=window, max_len=self.max_len,
+                                prefetch=nxt)
+
+    def _prefetch_spec(self, i: int, f: torch.Tensor) -> dict:
+        """Layer i's prefetch for this step (from layer i-1's forecast), as a
+        decode launch carries it."""
+        a = self.model.layers[i].attention
+        cache, pf = self.caches[i], self._pf[i]
+        return dict(arena=cache.arena, forecast=f.reshape(self.B, a.n_kv_head, -1),
+                    block_sums=cache.block_sums(self.block_size), top_k=a.top_k_blocks, routing=a.decode_routing,
+                    sel=pf["sel"], n_sel=pf["n"], k_dst=pf["k"], v_dst=pf["v"])
 
     def _prefetch(self, i: int, f: torch.Tensor):
         """Selection + gather of layer i's blocks for this step, from layer i-1's forecast."""
@@ -216,9 +238,12 @@ class GraphDecoder:
             q, k, v, f = sparda.produce(x, layer._fused_weight(), a.n_head * a.head_dim, a.n_kv_head * a.head_dim,
                                         fc.forecast_heads * fc.forecast_dim, layer.attn_norm.eps, self.cos,
                                         self.sin, f_dtype=x.dtype, pos_dev=self.pos, k_cache=kc, v_cache=vc)
+            carry = None
             if i + 1 < n and self.kinds[i + 1] == _OFFLOAD:
                 ev = self._pf[i + 1]["ev"]
-                if self.overlap:
+                if self.overlap == "fused":
+                    carry = (i + 1, f)
+                elif self.overlap:
                     self._side.wait_stream(main)
                     with torch.cuda.stream(self._side):
                         self._prefetch(i + 1, f)
@@ -226,7 +251,9 @@ class GraphDecoder:
                 else:
                     self._prefetch(i + 1, f)
                     ev.record(main)
-            out = self._attend(i, a, q[:, 0], k, v, prev_f)
+            out = self._attend(i, a, q[:, 0], k, v, prev_f, carry)
+            if carry is not None:
+                self._pf[i + 1]["ev"].record(main)
             if i in self._taps:
                 t = dict(q=q[:, 0], f=prev_f, out=out)
                 if self.kinds[i] == _OFFLOAD:

@@ -42,6 +42,14 @@ _f32 = ctypes.c_float
 _p = ctypes.c_void_p
 _size = ctypes.c_size_t
 
+
+class PrefetchArgs(ctypes.Structure):
+    """sparda_prefetch_args: the next layer's prefetch carried by
+    sparda_decode_at_prefetch (field order and types as in the header)."""
+    _fields_ = [("arena", _p), ("forecast", _p), ("f_dtype", _int), ("f_sb", _i64), ("f_sh", _i64),
+                ("block_sums", _p), ("nb_stride", _i64), ("top_k", _i64), ("routing", _int), ("scale", _f32),
+                ("sel", _p), ("n_sel", _p), ("sel_cap", _i64), ("k_dst", _p), ("v_dst", _p)]
+
 # name -> (restype, argtypes); mirrors include/sparda.h
 SIGNATURES = {
     "sparda_version": (_int, []),
@@ -92,6 +100,9 @@ SIGNATURES = {
                                        _int, _f32, _p, _p, _i64, _int, _p]),
     "sparda_decode_at": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _i64, _p, _p,
                                 _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
+    "sparda_decode_at_prefetch": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _i64,
+                                         _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64,
+                                         ctypes.POINTER(PrefetchArgs), _p]),
     "sparda_decode_sums": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _p, _i64,
                                   _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f32, _p, _p, _p,
                                   _i64, _p]),

@@ -7,6 +7,7 @@ tensor raises instead of falling back to another implementation.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Tuple
 
@@ -817,7 +818,7 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
               sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None, window: int = 0,
               max_len: Optional[int] = None, scale: Optional[float] = None,
               out: Optional[torch.Tensor] = None, compact: bool = False, k_new: Optional[torch.Tensor] = None,
-              v_new: Optional[torch.Tensor] = None) -> torch.Tensor:
+              v_new: Optional[torch.Tensor] = None, prefetch: Optional[dict] = None) -> torch.Tensor:
     """Decode attention of q [B,Hq,D] at token p = pos_dev (a one-element int64
     device tensor, read when the kernel runs) over the caches [B,Smax,Hkv,D]
     holding p + 1 tokens: the blocks sel[b,g,:n_sel], or with sel None the
@@ -825,7 +826,14 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
     at most window + 2), or every block (window 0). compact: k / v are fetched
     block buffers [B,Hkv,cap,bs,D] (slot i = block sel[b,g,i]); k_new / v_new
     [B,Hkv,D]: the key and value of position p. p is clamped below max_len
-    (default: the cache capacity; required with compact)."""
+    (default: the cache capacity; required with compact).
+
+    prefetch: the next layer's prefetch carried by the same launch
+    (sparda_decode_at_prefetch; bf16, D = 64): a dict with ``arena`` (the next
+    layer's OffloadArena), ``forecast`` [B,Hkv,Df], ``block_sums`` (its sums),
+    ``top_k``, ``routing``, optional ``scale``, and the outputs ``sel`` /
+    ``n_sel`` / ``k_dst`` / ``v_dst`` — what select_decode_at(lookahead=True)
+    and OffloadArena.fetch_at would write, bit for bit."""
     dev = require_device(q, k, v, pos_dev, sel, n_sel, k_new, v_new)
     _inference_only(q, k, v, k_new, v_new)
     if not (q.dtype == k.dtype == v.dtype):
@@ -868,13 +876,56 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
     if out is None:
         out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
     qsb, qsh, _ = q.stride()
-    call("sparda_decode_at", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
-         _dtype_code(q), int(bool(compact)), sel.data_ptr() if sel is not None else None,
-         n_sel.data_ptr() if n_sel is not None else None, cap, int(window),
-         k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
-         nsb, nsh, B, max_len, _pos_ptr(pos_dev), Hq, Hkv, D, block_size, float(scale), out.data_ptr(),
-         out.stride(0), _stream(dev))
+    args = (q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
+            _dtype_code(q), int(bool(compact)), sel.data_ptr() if sel is not None else None,
+            n_sel.data_ptr() if n_sel is not None else None, cap, int(window),
+            k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
+            nsb, nsh, B, max_len, _pos_ptr(pos_dev), Hq, Hkv, D, block_size, float(scale), out.data_ptr(),
+            out.stride(0))
+    if prefetch is None:
+        call("sparda_decode_at", *args, _stream(dev))
+    else:
+        pf, keep = _prefetch_args(prefetch, B, Hkv, D, block_size, dev)
+        call("sparda_decode_at_prefetch", *args, ctypes.byref(pf), _stream(dev))
+        del keep
     return out
+
+
+def _prefetch_args(spec: dict, B: int, Hkv: int, D: int, block_size: int, dev):
+    """The sparda_prefetch_args of a decode_at prefetch spec (checked as
+    select_decode_at and OffloadArena.fetch_at check theirs), with the
+    tensors it points into."""
+    arena = spec["arena"]
+    f, sums = spec["forecast"], spec["block_sums"]
+    sel, n_sel, k_dst, v_dst = spec["sel"], spec["n_sel"], spec["k_dst"], spec["v_dst"]
+    require_device(f, sums, sel, n_sel, k_dst, v_dst)
+    if (arena.B, arena.Hkv, arena.D) != (B, Hkv, D):
+        raise ValueError("sparda: the prefetched arena must have the attended layer's batch, KV heads and head dim")
+    if sums.dtype != torch.float32 or not sums.is_contiguous() or tuple(sums.shape[:1]) + tuple(sums.shape[2:]) \
+            != (B, Hkv, D):
+        raise TypeError("sparda: prefetch block_sums must be contiguous float32 [B,nb,Hkv,D]")
+    f = _rowmajor(f.reshape(B, Hkv, -1) if f.dim() != 3 else f)
+    routing = spec.get("routing", "reference")
+    if routing not in ("reference", "absolute"):
+        raise ValueError(f"sparda: routing must be 'reference' or 'absolute', got {routing!r}")
+    scale = spec.get("scale")
+    if scale is None:
+        scale = default_scale(f.shape[-1])
+    if sel.dtype != torch.int32 or n_sel.dtype != torch.int32 or not (sel.is_contiguous() and n_sel.is_contiguous()):
+        raise TypeError("sparda: prefetch sel / n_sel must be contiguous int32 tensors")
+    cap = sel.shape[-1]
+    if tuple(sel.shape) != (B, Hkv, cap) or tuple(n_sel.shape) != (B, Hkv):
+        raise ValueError("sparda: prefetch sel / n_sel must be [B,Hkv,cap] / [B,Hkv]")
+    if not (k_dst.is_contiguous() and v_dst.is_contiguous()) or tuple(k_dst.shape) != (B, Hkv, cap, block_size, D) \
+            or k_dst.shape != v_dst.shape:
+        raise ValueError("sparda: prefetch destinations must be contiguous [B,Hkv,sel_cap,block_size,D]")
+    if k_dst.dtype != arena.dtype or v_dst.dtype != arena.dtype:
+        raise TypeError("sparda: prefetch destinations must have the arena dtype")
+    fsb, fsh, _ = f.stride()
+    pf = _lib.PrefetchArgs(arena.handle.value, f.data_ptr(), _dtype_code(f), fsb, fsh, sums.data_ptr(), sums.shape[1],
+                           int(spec["top_k"]), _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE,
+                           float(scale), sel.data_ptr(), n_sel.data_ptr(), cap, k_dst.data_ptr(), v_dst.data_ptr())
+    return pf, (f, sums, sel, n_sel, k_dst, v_dst)
 
 
 def block_sums(k: torch.Tensor, pos: int, n: int, block_size: int, sums: torch.Tensor) -> torch.Tensor:
@@ -935,7 +986,6 @@ class OffloadArena:
     """
 
     def __init__(self, B: int, max_seq: int, Hkv: int, D: int, dtype: torch.dtype, device=None):
-        import ctypes
         self.B, self.max_seq, self.Hkv, self.D, self.dtype = B, max_seq, Hkv, D, dtype
         self.device = torch.device(device) if device is not None else torch.device("cuda")
         with torch.cuda.device(self.device):

@@ -93,6 +93,68 @@ def test_device_position_ops_equal_host_length_ops(dtype, routing):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+@pytest.mark.parametrize("bs", [64, 32])
+def test_decode_at_carrying_a_prefetch_equals_separate_launches(routing, bs):
+    # the attention launch that carries the next layer's prefetch (selection
+    # with lookahead + copy from the arena) must leave the attention output,
+    # the selection and the compact buffers exactly as decode_at,
+    # select_decode_at(lookahead) and fetch_at do as separate launches
+    case(f"decode_at carrying the next layer's prefetch, bs={bs} {routing}")
+    B, Smax, Hq, Hkv, D, k = 2, 2048, 12, 4, 64, 8
+    cap, bf = k + 2, torch.bfloat16
+    g = torch.Generator().manual_seed(13)
+    kc = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    vc = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    q = torch.randn(B, Hq, D, generator=g).to(bf).to(DEV)
+    f = torch.randn(B, Hkv, 64, generator=g).to(bf if bs == 64 else torch.float32).to(DEV)
+    kn = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    vn = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    arena = sparda.OffloadArena(B, Smax, Hkv, D, bf)
+    arena.append(kn, vn, 0)
+    nb = Smax // bs
+    own_sums = torch.zeros((B, nb, Hkv, D), device=DEV)
+    sparda.block_sums(kc, 0, Smax, bs, own_sums)
+
+    def outputs():
+        return (torch.full((B, Hkv, cap), 7, dtype=torch.int32, device=DEV),
+                torch.full((B, Hkv), 7, dtype=torch.int32, device=DEV),
+                torch.full((B, Hkv, cap, bs, D), 3.0, dtype=bf, device=DEV),
+                torch.full((B, Hkv, cap, bs, D), 3.0, dtype=bf, device=DEV))
+
+    for p in (0, 1, bs - 1, bs, bs + 1, 639, 640, 641, 1535, 2047):
+        case(f"  position {p}")
+        pos = _pos(p)
+        sums = torch.zeros((B, nb, Hkv, D), device=DEV)
+        if p > 0:
+            sparda.block_sums(kn, 0, p, bs, sums)
+        s1, n1, k1, v1 = outputs()
+        sparda.select_decode_at(f, sums, pos, Smax, bs, k, routing=routing, sel=s1, n_sel=n1, lookahead=True)
+        arena.fetch_at(s1, n1, bs, pos, k1, v1)
+        sa, na = sparda.select_decode_at(f, own_sums, pos, Smax, bs, k, routing=routing)
+        for mode in ("list", "every block"):
+            s2, n2, k2, v2 = outputs()
+            spec = dict(arena=arena, forecast=f, block_sums=sums, top_k=k, routing=routing, sel=s2, n_sel=n2,
+                        k_dst=k2, v_dst=v2)
+            if mode == "list":
+                o_plain = sparda.decode_at(q, kc, vc, pos, bs, sa, na)
+                o_carry = sparda.decode_at(q, kc, vc, pos, bs, sa, na, prefetch=spec)
+            else:
+                o_plain = sparda.decode_at(q, kc, vc, pos, bs, window=0)
+                o_carry = sparda.decode_at(q, kc, vc, pos, bs, window=0, prefetch=spec)
+            assert torch.equal(o_carry, o_plain), f"attention output, {mode}, p={p}"
+            assert torch.equal(n2, n1) and torch.equal(s2, s1), f"selection, {mode}, p={p}"
+            assert torch.equal(k2, k1) and torch.equal(v2, v1), f"fetched blocks, {mode}, p={p}"
+    # only the matrix-core attention carries a prefetch: fp32 is refused before any launch
+    s2, n2, k2, v2 = outputs()
+    spec = dict(arena=arena, forecast=f, block_sums=own_sums, top_k=k, routing=routing, sel=s2, n_sel=n2,
+                k_dst=k2, v_dst=v2)
+    with pytest.raises(ValueError):
+        sparda.decode_at(q.float(), kc.float(), vc.float(), _pos(100), bs, window=0, prefetch=spec)
+    torch.cuda.synchronize()
+    arena.close()
+
+
 def test_device_positions_are_clamped_into_range():
     case("device-position clamping")
     B, Smax, Hq, Hkv, D, bs, k = 1, 1000, 12, 4, 64, 64, 8
@@ -211,25 +273,31 @@ def test_graph_replayed_offload_steps_equal_eager_async_offload(routing):
         for _ in range(cfg.n_layer - 1)]
     gd = GraphDecoder(model, B, cap, overlap=True)
     serial = GraphDecoder(model, B, cap, overlap=False)
+    fused = GraphDecoder(model, B, cap)  # the prefetch carried by the previous layer's attention launch
+    assert fused.overlap == "fused"
     with torch.no_grad():
         want = [model(ids[:, :T0], kv_caches=caches)["logits"][:, -1]]
         for t in range(T0, T0 + n):
             want.append(model(ids[:, t:t + 1], kv_caches=caches)["logits"][:, -1])
         got = [gd.prefill(ids[:, :T0])]
         got_s = [serial.prefill(ids[:, :T0])]
+        got_f = [fused.prefill(ids[:, :T0])]
         for t in range(T0, T0 + n):
             got.append(gd.step(ids[:, t:t + 1]).clone())
             got_s.append(serial.step(ids[:, t:t + 1]).clone())
+            got_f.append(fused.step(ids[:, t:t + 1]).clone())
     torch.cuda.synchronize()
-    for i, (a, b, c) in enumerate(zip(got, got_s, want)):
+    for i, (a, b, d, c) in enumerate(zip(got, got_s, got_f, want)):
         assert torch.equal(a, c), f"step {i}: max diff {(a.float() - c.float()).abs().max().item()}"
         assert torch.equal(b, c), f"serial step {i}"
+        assert torch.equal(d, c), f"fused-prefetch step {i}"
     L = T0 + n
-    assert torch.equal(gd.caches[0].k[:, :L], caches[0].k[:, :L])
-    for c, e in zip(gd.caches[1:], caches[1:]):
-        assert c.current_len == e.current_len == L
-        assert torch.equal(c.cpu_k[:, :L], e.cpu_k[:, :L]) and torch.equal(c.cpu_v[:, :L], e.cpu_v[:, :L])
-        assert torch.equal(c.block_sums(64), e.block_sums(64))
+    for dec in (gd, fused):
+        assert torch.equal(dec.caches[0].k[:, :L], caches[0].k[:, :L])
+        for c, e in zip(dec.caches[1:], caches[1:]):
+            assert c.current_len == e.current_len == L
+            assert torch.equal(c.cpu_k[:, :L], e.cpu_k[:, :L]) and torch.equal(c.cpu_v[:, :L], e.cpu_v[:, :L])
+            assert torch.equal(c.block_sums(64), e.block_sums(64))
 
 
 def test_graph_decoder_sixteen_sequences_and_capacity_limit():
