@@ -10,7 +10,9 @@
   (the 257-512-block selection tier), exact block fetches by both transfer
   methods, the offloaded decode step against the oracle, and the 12-layer
   async-prefetch model equal to the synchronous offload model over 3 steps
-  with no stale prefetch.
+  with no stale prefetch; the same model replayed from a HIP graph with each
+  prefetch carried by the previous layer's attention launch, every offloaded
+  layer's selection and attention checked against the oracle at each step.
 """
 
 import numpy as np
@@ -204,3 +206,48 @@ def test_twelve_layer_async_prefetch_model_at_32k_equals_sync_offload():
     assert all(c.current_len == CTX - 8 + steps for c in ca)
     assert sum(layer.attention.stale_prefetches for layer in ma.layers[1:]) == 0
     assert all(layer.attention.prefetched_bytes > 0 for layer in ma.layers[1:])
+
+
+def test_twelve_layer_replayed_offload_steps_at_32k_against_the_oracle():
+    # the 12-layer offloaded model at a 32K context decoded by GraphDecoder,
+    # each layer's prefetch carried by the previous layer's attention launch:
+    # at every replayed step, every offloaded layer's prefetched selection
+    # (bit for bit) and attention output (bf16 bar) against the oracle, from
+    # the q, routing forecast and output the replay left in its buffers and the
+    # arena contents
+    from model.decode_graph import GraphDecoder
+    case("12-layer replayed offload steps at 32K vs the oracle (carried prefetch)")
+    bs, k, steps = 64, 8, 2
+    cap = CTX + 64
+    cfg = ModelConfig(n_layer=12, context_length=cap, block_size=bs, top_k_blocks=k, decode_routing="absolute",
+                      attention_backend="async_offload", norm_eps=1e-5)
+    torch.manual_seed(1005)
+    model = SparDAResearchModel(cfg).to(DEV, torch.bfloat16).eval()
+    caches = [KVCache(1, cap, 4, 64, DEV, torch.bfloat16)] + [
+        AsyncOffloadedKVCache(1, cap, 4, 64, DEV, torch.bfloat16, block_size=bs) for _ in range(11)]
+    for li in range(12):
+        for _, kk, vv in synth.kv_chunks(1, CTX - 8, 4, 64, seed=2200 + li):
+            caches[li].update(kk.to(DEV, torch.bfloat16), vv.to(DEV, torch.bfloat16))
+    torch.cuda.synchronize()
+    gd = GraphDecoder(model, 1, cap, caches=caches, taps=tuple(range(1, 12)))
+    assert gd.overlap == "fused"
+    g = torch.Generator().manual_seed(1007)
+    ids = torch.randint(0, cfg.vocab_size, (steps, 1, 1), generator=g).to(DEV)
+    with torch.no_grad():
+        for s in range(steps):
+            logits = gd.step(ids[s])
+            torch.cuda.synchronize()
+            assert torch.isfinite(logits).all()
+            S = gd.length
+            for i in range(1, 12):
+                case(f"  step {s}, position {S - 1}, layer {i}")
+                c, tap = gd.caches[i], gd.tapped[i]
+                kc, vc = c.cpu_k[:, :S].float().numpy(), c.cpu_v[:, :S].float().numpy()
+                # the prefetch selected before the token at S - 1 was appended
+                sel_o, n_o = O.prefetch_selection(kc, S - 1, S - 1, np32(tap["f"].reshape(1, 4, -1)), bs, k,
+                                                  "absolute")
+                assert np.array_equal(tap["n_sel"].cpu().numpy(), n_o)
+                assert np.array_equal(tap["sel"].cpu().numpy(), sel_o)
+                want = O.attention_decode(np32(tap["q"]), kc, vc, S, sel_o, n_o, bs)
+                assert_close_out(np32(tap["out"]), want, torch.bfloat16, what=f"layer {i} at {S - 1}")
+    assert gd.length == CTX - 8 + steps
