@@ -12,11 +12,15 @@
 // current one is computed) and shared by all 128 tokens and R heads. Per tile
 // and block, with v_mfma_f32_16x16x32_bf16:
 //     S^T[key, col] = K[key, :] . Q[col, :]           (8 MFMA)
-//     online softmax per column (fp32, log2 domain; the running maximum is
-//     raised only when a block's maximum exceeds it by more than 2^8, so the
-//     accumulators are rarely rescaled and P stays <= 2^8)
+//     P = exp2(S * scale log2 e - ref[col]), bf16      (fp32 exponent)
 //     O^T[d, col]  += V^T[d, key] . P^T[key, col]      (8 MFMA)
 //     l[col]       += 1^T P^T                           (2 MFMA, a ones A operand)
+// ref[col] is the column's maximum over block 0 (which every column attends,
+// key 0 being allowed to every token), taken when block 0 is computed; later
+// blocks take no maxima and never rescale. A score more than 64 log2-units
+// above the reference shows as a row sum past 2^64 at the end; the window is
+// then walked once for the exact column maxima and again against them (every
+// P <= 1).
 // A wavefront whose tokens all lie before a block skips it (the causal
 // triangle is not computed); the diagonal block masks the keys past each
 // column's token. No per-token membership logic: every key up to the token
@@ -37,11 +41,12 @@ constexpr int kDWin = 16 * kDWaves;      // query tokens per workgroup
 constexpr int kDKRow = kDD + 8;          // K row in LDS, bf16 elements (144 B)
 constexpr int kDVRow = kDD + 16;         // V row in LDS, bf16 elements (160 B)
 constexpr float kDLog2e = 1.4426950408889634f;
-constexpr float kDLazy = 8.0f;           // raise the running max only past 2^8
+constexpr float kDGuard = 18446744073709551616.0f;  // 2^64: a row sum past it means a score far above ref
 
 struct DenseSmem {
     uint16_t k[2][kDBs * kDKRow];
     uint16_t v[2][kDBs * kDVRow];
+    int flag;                             // some column's row sum passed kDGuard
 };
 
 }  // namespace
@@ -92,17 +97,22 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
     }
 
     f32x4 o[R][4], ol[R];
-    float m_run[R];
+    float ref[R];  // the columns' references, log2 units
     bf16x8 ones_a;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones_a[e] = static_cast<__bf16>(col16 == 0 ? 1.0f : 0.0f);
+    auto clear = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int tt = 0; tt < R; ++tt) {
-        m_run[tt] = -__builtin_inff();
-        ol[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tt = 0; tt < R; ++tt) {
+            ol[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+            for (int dt = 0; dt < 4; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    clear();
+#pragma unroll
+    for (int tt = 0; tt < R; ++tt) ref[tt] = -__builtin_inff();
+    if (tid == 0) sm.flag = 0;  // ordered before its uses by the staging barrier
 
     // staging: thread -> 16-byte chunk (row tid / 8, column tid % 8) of K and of V;
     // rows past T (a ragged last block) read row T-1 (finite values, masked)
@@ -117,7 +127,9 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
         kv_v = *reinterpret_cast<const uint4*>(vbase + s * kv_st + scol);
     };
 
-    auto compute = [&](int buf, int j) __attribute__((always_inline)) {
+    // mode 0: P against the references (block 0 sets them unless `keep`);
+    // mode 1: scores only, the exact column maxima into ref
+    auto compute = [&](int buf, int j, int mode, bool keep) __attribute__((always_inline)) {
         // K A operands: key 16n + col16, dims 32kk + 8grp .. +7
         bf16x8 ka[4][2];
 #pragma unroll
@@ -127,7 +139,7 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
                 ka[n][kk] = lds_read8(&sm.k[buf][(16 * n + col16) * kDKRow + 32 * kk + 8 * grp]);
         // V^T A operands, read transposed from the row-major tile
         bf16x8 va[4][2];
-        {
+        if (mode == 0) {
             const int rsub = 4 * grp + col16 / 4;
             const int csub = 4 * (col16 % 4);
 #pragma unroll
@@ -160,13 +172,13 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
                     for (int i = 0; i < 4; ++i)
                         if (16 * n + 4 * grp + i > lim) s[n][i] = -__builtin_inff();
             }
-            const float cand = pair32_max(pair16_max(max16_nn(s))) * scale_log2;  // block's column max, log2 units
-            // -inf (a column whose keys here are all masked: it has none allowed
-            // yet) leaves the running state alone
-            const float m_new = cand > m_run[tt] + kDLazy ? cand : m_run[tt];
-            const float alpha = m_new != m_run[tt] ? __builtin_amdgcn_exp2f(m_run[tt] - m_new) : 1.0f;
-            m_run[tt] = m_new;
-            const float neg = m_new == -__builtin_inff() ? -__builtin_inff() : -m_new;
+            if (mode == 1 || (j == 0 && !keep)) {  // wave-uniform
+                const float cand = pair32_max(pair16_max(max16_nn(s))) * scale_log2;  // block's column max, log2 units
+                ref[tt] = mode == 1 ? fmaxf(ref[tt], cand) : cand;
+                if (mode == 1) continue;
+            }
+            // a column with no allowed key (ref -inf) gets P = 0 throughout
+            const float neg = ref[tt] == -__builtin_inff() ? -__builtin_inff() : -ref[tt];
             uint4 pw[2];
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
@@ -178,11 +190,6 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
                         static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * m + 1][i], scale_log2, neg)));
                 }
                 pw[m] = __builtin_bit_cast(uint4, pb);
-            }
-            if (__ballot(alpha != 1.0f) != 0ull) {
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) o[tt][dt] *= alpha;
-                ol[tt] *= alpha;
             }
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
@@ -198,21 +205,40 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
 
     // block u is computed from buffer u & 1 while block u + 1 is in registers;
     // one barrier per block orders its stash before the reads of the next
-    uint4 nk, nv;
-    fetch(0, nk, nv);
-    *reinterpret_cast<uint4*>(&sm.k[0][lds_k]) = nk;
-    *reinterpret_cast<uint4*>(&sm.v[0][lds_v]) = nv;
-    if (nblk > 1) fetch(1, nk, nv);
-    __syncthreads();
-    for (int u = 0; u < nblk; ++u) {
-        const int buf = u & 1;
-        if (u < w_nblk) compute(buf, u);  // wave-uniform: blocks past this wavefront's tokens are skipped
-        if (u + 1 < nblk) {
-            *reinterpret_cast<uint4*>(&sm.k[buf ^ 1][lds_k]) = nk;
-            *reinterpret_cast<uint4*>(&sm.v[buf ^ 1][lds_v]) = nv;
-            if (u + 2 < nblk) fetch(u + 2, nk, nv);
-        }
+    auto walk = [&](int mode, bool keep) __attribute__((always_inline)) {
+        uint4 nk, nv;
+        fetch(0, nk, nv);
+        *reinterpret_cast<uint4*>(&sm.k[0][lds_k]) = nk;
+        *reinterpret_cast<uint4*>(&sm.v[0][lds_v]) = nv;
+        if (nblk > 1) fetch(1, nk, nv);
         __syncthreads();
+        for (int u = 0; u < nblk; ++u) {
+            const int buf = u & 1;
+            if (u < w_nblk) compute(buf, u, mode, keep);  // wave-uniform: blocks past this wavefront's tokens are skipped
+            if (u + 1 < nblk) {
+                *reinterpret_cast<uint4*>(&sm.k[buf ^ 1][lds_k]) = nk;
+                *reinterpret_cast<uint4*>(&sm.v[buf ^ 1][lds_v]) = nv;
+                if (u + 2 < nblk) fetch(u + 2, nk, nv);
+            }
+            __syncthreads();
+        }
+    };
+    walk(0, false);
+    // a row sum past 2^64 (or not finite): a score more than 64 log2-units above
+    // its column's reference somewhere; the row sums sit in lanes 0..15, element 0
+    {
+        bool bad = false;
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt) bad = bad || (w_live && lane < 16 && !(ol[tt][0] <= kDGuard));
+        if (__ballot(bad) != 0ull && lane == 0) atomicOr(&sm.flag, 1);
+    }
+    __syncthreads();
+    if (sm.flag != 0) {  // workgroup-uniform: every wave walks again
+#pragma unroll
+        for (int tt = 0; tt < R; ++tt) ref[tt] = -__builtin_inff();
+        walk(1, true);   // the exact column maxima
+        clear();
+        walk(0, true);   // against them: every P <= 1
     }
 
     // ---- epilogue: out[b, t, h*64 + d] = O / l ----

@@ -432,6 +432,31 @@ def test_prefill_scores_far_above_the_reference_maximum():
     assert np.abs(hot - np32(v)[0, s_hot, 0][None, :]).max() <= 2e-2
 
 
+@pytest.mark.parametrize("hot", [True, False])
+def test_prefill_dense_kernel_scores_far_above_block_zero(hot):
+    # the dense kernel's references are block 0's column maxima; a key ~72
+    # log2-units above them trips the row-sum guard and the window is walked
+    # again for the exact maxima (hot); 40 log2-units above stays on the
+    # first walk (P up to 2^40, not hot)
+    case(f"prefill dense, a key far above block 0 (hot={hot})")
+    B, T, Hq, Hkv, bs = 1, 256, 12, 4, 64
+    x = synth.prefill_inputs(B, T, Hq, Hkv, 64, dtype=torch.float32, seed=94)
+    q, k, v = x["q"].clone(), x["k"].clone(), x["v"].clone()
+    e1 = torch.zeros(64)
+    e1[0] = 20.0 if hot else 15.0
+    t_hot, s_hot = 200, 70      # token 200 (block 3) and a key of block 1
+    q[0, t_hot, :, :] = e1
+    k[0, t_hot, :] = -e1
+    k[0, 0, :] = -e1
+    k[0, s_hot, :] = e1         # dot 400 (225): 72 (40) log2-units above 0
+    q, k, v = (t_.to(torch.bfloat16) for t_ in (q, k, v))
+    out = sparda.prefill(q.to(DEV), k.to(DEV), v.to(DEV), None, None, bs)
+    want = O.attention_prefill(np32(q), np32(k), np32(v), None, None, bs, True)
+    assert_close_out(np32(out), want, torch.bfloat16)
+    hot_row = np32(out)[0, t_hot].reshape(Hq, 64)
+    assert np.abs(hot_row - np32(v)[0, s_hot].repeat(Hq // Hkv, axis=0)).max() <= 2e-2
+
+
 # ---------------------------------------------------------------------------
 # routed prefill (router folded into the attention launch)
 # ---------------------------------------------------------------------------
