@@ -905,6 +905,8 @@ def _prefetch_args(spec: dict, B: int, Hkv: int, D: int, block_size: int, dev):
             != (B, Hkv, D):
         raise TypeError("sparda: prefetch block_sums must be contiguous float32 [B,nb,Hkv,D]")
     f = _rowmajor(f.reshape(B, Hkv, -1) if f.dim() != 3 else f)
+    if tuple(f.shape) != (B, Hkv, D):
+        raise ValueError(f"sparda: the prefetch forecast must be [B,Hkv,{D}], got {tuple(f.shape)}")
     routing = spec.get("routing", "reference")
     if routing not in ("reference", "absolute"):
         raise ValueError(f"sparda: routing must be 'reference' or 'absolute', got {routing!r}")
