@@ -659,6 +659,9 @@ typedef struct sparda_prefetch_args {
     int64_t sel_cap;
     void* k_dst;
     void* v_dst;
+    int stage;   /* 0: selection and copy; 1: the selection only (into sel / n_sel);
+                    2: the copy only, of the selection in sel / n_sel (left there by a
+                    stage-1 launch earlier on the stream; forecast and block_sums unused) */
 } sparda_prefetch_args;
 
 /*
@@ -667,6 +670,18 @@ typedef struct sparda_prefetch_args {
  * token p is appended to the next layer). Needs the matrix-core attention:
  * bf16, D = 64, blocks of 64 or 32 keys, 16-byte aligned q rows.
  */
+/*
+ * sparda_offload_append_at (same arguments, same result) whose launch also
+ * carries `next`'s prefetch stage (normally 1, the selection, so that the
+ * attention launch that follows carries only the copy, stage 2). max_len:
+ * the positions' bound, as sparda_decode_at's (the selection clamps p into
+ * [0, max_len - 1]). Needs bf16, D = 64.
+ */
+SPARDA_API int sparda_offload_append_at_prefetch(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
+                                                 int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
+                                                 float* block_sums, int64_t max_len,
+                                                 const sparda_prefetch_args* next, void* stream);
+
 SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
                                          int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
                                          const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,

@@ -427,6 +427,60 @@ SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const
                              out_sb, stream, nullptr);
 }
 
+// The device form of a prefetch carried by another launch, after the checks
+// both carrying entries make (the next layer's arena: batch B, Hkv KV heads,
+// head dim 64, dtype bf16 like the carrying layer).
+static int prefetch_dev(const sparda_prefetch_args* next, int64_t B, int64_t Hkv, int64_t D, int dtype,
+                        int64_t max_len, int64_t block_size, const char* who, PrefetchDev* pf) {
+    SPARDA_REQUIRE(next, SPARDA_ERR_NULL, "%s: null prefetch arguments", who);
+    const sparda_prefetch_args& n = *next;
+    SPARDA_REQUIRE(n.arena, SPARDA_ERR_HANDLE, "%s: null arena handle", who);
+    SPARDA_REQUIRE(n.stage >= 0 && n.stage <= 2, SPARDA_ERR_MODE, "%s: stage %d not in {0, 1, 2}", who, n.stage);
+    SPARDA_REQUIRE(n.sel && n.n_sel, SPARDA_ERR_NULL, "%s: null sel / n_sel", who);
+    SPARDA_REQUIRE(n.stage == 2 || (n.forecast && n.block_sums), SPARDA_ERR_NULL, "%s: null forecast / block_sums",
+                   who);
+    SPARDA_REQUIRE(n.stage == 1 || (n.k_dst && n.v_dst), SPARDA_ERR_NULL, "%s: null destinations", who);
+    SPARDA_REQUIRE(D == 64 && dtype == SPARDA_BF16, SPARDA_ERR_MODE, "%s: a carried prefetch needs bf16, D=64", who);
+    SPARDA_REQUIRE(offload_batch(n.arena) == B && offload_heads(n.arena) == Hkv && offload_head_dim(n.arena) == D &&
+                       offload_dtype(n.arena) == dtype,
+                   SPARDA_ERR_SHAPE, "%s: the arena's batch, KV heads, head dim and dtype must be the carrying "
+                   "layer's", who);
+    SPARDA_REQUIRE(n.stage == 2 || dtype_ok(n.f_dtype), SPARDA_ERR_DTYPE, "%s: forecast dtype %d", who, n.f_dtype);
+    SPARDA_REQUIRE(n.routing == SPARDA_ROUTE_REFERENCE || n.routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
+                   "%s: unknown routing %d", who, n.routing);
+    SPARDA_REQUIRE(n.stage == 2 || (reinterpret_cast<uintptr_t>(n.block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
+                   "%s: block_sums must be 16-byte aligned", who);
+    SPARDA_REQUIRE(n.top_k >= 1 && n.top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "%s: top_k out of range", who);
+    SPARDA_REQUIRE(n.sel_cap >= n.top_k + 2 && n.sel_cap <= kMaxSelCap, SPARDA_ERR_SHAPE,
+                   "%s: sel_cap must be in [top_k+2, %d]", who, kMaxSelCap);
+    SPARDA_REQUIRE(block_size > 0 && max_len >= 1 && (n.stage == 2 || n.nb_stride >= cdiv(max_len, block_size)),
+                   SPARDA_ERR_SHAPE, "%s: nb_stride too small", who);
+    SPARDA_REQUIRE(cdiv(max_len, block_size) <= 4096, SPARDA_ERR_SHAPE, "%s: more than 4096 blocks", who);
+    SPARDA_REQUIRE(n.stage == 1 || (aligned16(n.k_dst) && aligned16(n.v_dst)), SPARDA_ERR_STRIDE,
+                   "%s: destinations must be 16-byte aligned", who);
+    *pf = PrefetchDev{};
+    pf->f = n.forecast;
+    pf->f_sb = n.f_sb;
+    pf->f_sh = n.f_sh;
+    pf->f_bf16 = n.f_dtype == SPARDA_BF16 ? 1 : 0;
+    pf->sums = n.block_sums;
+    pf->nb_stride = n.nb_stride;
+    pf->pos_max = max_len - 1;
+    pf->bs = static_cast<int>(block_size);
+    pf->k = static_cast<int>(n.top_k);
+    pf->cap = static_cast<int>(n.sel_cap);
+    pf->absolute = n.routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0;
+    pf->pow2 = (block_size & (block_size - 1)) == 0 ? 1 : 0;
+    pf->scale = n.scale;
+    pf->sel = n.sel;
+    pf->n_sel = n.n_sel;
+    pf->dk = static_cast<char*>(n.k_dst);
+    pf->dv = static_cast<char*>(n.v_dst);
+    pf->stage = n.stage;
+    offload_prefetch_dev(n.arena, pf);
+    return 0;
+}
+
 SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
                                          int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int dtype, int compact,
                                          const int32_t* sel, const int32_t* n_sel, int64_t sel_cap,
@@ -435,50 +489,12 @@ SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_
                                          int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, float scale,
                                          void* out, int64_t out_sb, const sparda_prefetch_args* next,
                                          void* stream) {
-    SPARDA_REQUIRE(next, SPARDA_ERR_NULL, "decode_at_prefetch: null prefetch arguments");
-    const sparda_prefetch_args& n = *next;
-    SPARDA_REQUIRE(n.arena, SPARDA_ERR_HANDLE, "decode_at_prefetch: null arena handle");
-    SPARDA_REQUIRE(n.forecast && n.block_sums && n.sel && n.n_sel && n.k_dst && n.v_dst, SPARDA_ERR_NULL,
-                   "decode_at_prefetch: null prefetch pointer");
     SPARDA_REQUIRE(decode_at_matrix_core(dtype, D, block_size, q_sb, q_sh, q), SPARDA_ERR_MODE,
                    "decode_at_prefetch: needs the matrix-core attention (bf16, D=64, blocks of 64 or 32 keys, "
                    "16-byte aligned q rows)");
-    SPARDA_REQUIRE(offload_batch(n.arena) == B && offload_heads(n.arena) == Hkv && offload_head_dim(n.arena) == D &&
-                       offload_dtype(n.arena) == dtype,
-                   SPARDA_ERR_SHAPE, "decode_at_prefetch: the arena's batch, KV heads, head dim and dtype must be "
-                   "the attended layer's");
-    SPARDA_REQUIRE(dtype_ok(n.f_dtype), SPARDA_ERR_DTYPE, "decode_at_prefetch: forecast dtype %d", n.f_dtype);
-    SPARDA_REQUIRE(n.routing == SPARDA_ROUTE_REFERENCE || n.routing == SPARDA_ROUTE_ABSOLUTE, SPARDA_ERR_MODE,
-                   "decode_at_prefetch: unknown routing %d", n.routing);
-    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(n.block_sums) & 15u) == 0, SPARDA_ERR_STRIDE,
-                   "decode_at_prefetch: block_sums must be 16-byte aligned");
-    SPARDA_REQUIRE(n.top_k >= 1 && n.top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "decode_at_prefetch: top_k out of range");
-    SPARDA_REQUIRE(n.sel_cap >= n.top_k + 2 && n.sel_cap <= kMaxSelCap, SPARDA_ERR_SHAPE,
-                   "decode_at_prefetch: sel_cap must be in [top_k+2, %d]", kMaxSelCap);
-    SPARDA_REQUIRE(max_len >= 1 && n.nb_stride >= cdiv(max_len, block_size), SPARDA_ERR_SHAPE,
-                   "decode_at_prefetch: nb_stride too small");
-    SPARDA_REQUIRE(cdiv(max_len, block_size) <= 4096, SPARDA_ERR_SHAPE, "decode_at_prefetch: more than 4096 blocks");
-    SPARDA_REQUIRE(aligned16(n.k_dst) && aligned16(n.v_dst), SPARDA_ERR_STRIDE,
-                   "decode_at_prefetch: destinations must be 16-byte aligned");
-    PrefetchDev pf{};
-    pf.f = n.forecast;
-    pf.f_sb = n.f_sb;
-    pf.f_sh = n.f_sh;
-    pf.f_bf16 = n.f_dtype == SPARDA_BF16 ? 1 : 0;
-    pf.sums = n.block_sums;
-    pf.nb_stride = n.nb_stride;
-    pf.pos_max = max_len - 1;
-    pf.bs = static_cast<int>(block_size);
-    pf.k = static_cast<int>(n.top_k);
-    pf.cap = static_cast<int>(n.sel_cap);
-    pf.absolute = n.routing == SPARDA_ROUTE_ABSOLUTE ? 1 : 0;
-    pf.pow2 = (block_size & (block_size - 1)) == 0 ? 1 : 0;
-    pf.scale = n.scale;
-    pf.sel = n.sel;
-    pf.n_sel = n.n_sel;
-    pf.dk = static_cast<char*>(n.k_dst);
-    pf.dv = static_cast<char*>(n.v_dst);
-    offload_prefetch_dev(n.arena, &pf);
+    PrefetchDev pf;
+    const int rc = prefetch_dev(next, B, Hkv, D, dtype, max_len, block_size, "decode_at_prefetch", &pf);
+    if (rc) return rc;
     return decode_at_checked(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
                              k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
                              out_sb, stream, &pf);
@@ -782,6 +798,24 @@ SPARDA_API int sparda_offload_append_at(sparda_offload_t h, const void* k, const
     SPARDA_REQUIRE(!block_sums || block_size > 0, SPARDA_ERR_SHAPE, "offload_append_at: block_size must be > 0");
     return offload_append_at(h, k, v, new_sb, new_sh, pos_dev, block_sums ? block_size : 1, block_sums,
                              static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_offload_append_at_prefetch(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
+                                                 int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
+                                                 float* block_sums, int64_t max_len,
+                                                 const sparda_prefetch_args* next, void* stream) {
+    SPARDA_REQUIRE(h, SPARDA_ERR_HANDLE, "offload_append_at_prefetch: null handle");
+    SPARDA_REQUIRE(k && v && pos_dev, SPARDA_ERR_NULL, "offload_append_at_prefetch: null k/v/pos_dev");
+    SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
+                   "offload_append_at_prefetch: pos_dev must be 8-byte aligned");
+    SPARDA_REQUIRE(new_sb >= 0 && new_sh >= 0, SPARDA_ERR_STRIDE, "offload_append_at_prefetch: negative stride");
+    SPARDA_REQUIRE(block_size > 0, SPARDA_ERR_SHAPE, "offload_append_at_prefetch: block_size must be > 0");
+    PrefetchDev pf;
+    const int rc = prefetch_dev(next, offload_batch(h), offload_heads(h), offload_head_dim(h), offload_dtype(h),
+                                max_len, block_size, "offload_append_at_prefetch", &pf);
+    if (rc) return rc;
+    return offload_append_at(h, k, v, new_sb, new_sh, pos_dev, block_size, block_sums,
+                             static_cast<hipStream_t>(stream), &pf);
 }
 
 }  // extern "C"

@@ -129,12 +129,13 @@ int launch_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
                        int routing, float scale, float fscale, int32_t* sel_out, int32_t* n_sel_out, void* out,
                        int64_t out_sb, hipStream_t stream);
 
-// The prefetch of the next layer's blocks carried by a decode attention launch
-// as extra workgroups, one per (sequence, KV head): the selection of
+// The prefetch of the next layer's blocks carried by another launch as extra
+// workgroups, one per (sequence, KV head): the selection of
 // launch_select_decode with pos_dev and lookahead (blocks of [0, p) scored from
 // the block sums; p = *pos_dev clamped into [0, pos_max]), then the copy of
 // offload_fetch's gather kernel from the arena into the compact buffers
-// (arena length p, clamped into [0, Smax]).
+// (arena length p, clamped into [0, Smax]). stage: 0 both, 1 the selection
+// only, 2 the copy only (of the selection a stage-1 launch left in sel/n_sel).
 struct PrefetchDev {
     const void* f;          // forecast [B, H, D], element strides (f_sb, f_sh, 1)
     int64_t f_sb, f_sh;
@@ -151,6 +152,7 @@ struct PrefetchDev {
     int64_t H, Smax, row_bytes;
     char* dk;               // compact buffers [B][H][cap][bs][row_bytes] each
     char* dv;
+    int stage;
 };
 // the arena fields of a PrefetchDev (ak, av, H, Smax, row_bytes)
 void offload_prefetch_dev(sparda_offload_t h, PrefetchDev* pf);
@@ -196,7 +198,8 @@ int offload_fetch(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel, 
                   const int64_t* len_dev = nullptr);
 // decode-step append of one token at row *pos_dev of the arena (device mapping) + its block's sums
 int offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t n_sb, int64_t n_sh,
-                      const int64_t* pos_dev, int64_t bs, float* sums, hipStream_t stream);
+                      const int64_t* pos_dev, int64_t bs, float* sums, hipStream_t stream,
+                      const PrefetchDev* pf = nullptr);
 
 int launch_prefill(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
                    const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,

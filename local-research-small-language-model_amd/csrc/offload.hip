@@ -44,6 +44,9 @@ struct sparda_offload {
 
 namespace sparda {
 
+constexpr int kSelThreads = 256;
+constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
+
 static size_t arena_bytes(const sparda_offload* h) {
     return static_cast<size_t>(h->B * h->H * h->Smax * h->D * h->esz);
 }
@@ -201,15 +204,29 @@ int launch_block_sums(const void* k, int dtype, int64_t sb, int64_t st, int64_t 
 // rows are written into the caches at row p; the fp32 sums of the block
 // holding p are recomputed over [p - p % bs, p] in token order (the sums
 // block_sums_kernel gives), row p taken from k_new, so that no thread reads a
-// row another thread writes.
+// row another thread writes. Workgroups past the first n_append carry the
+// selection stage of the next layer's prefetch (pf, D = 64), one per
+// (sequence, KV head) of that layer.
 template <int DT>
 __global__ void __launch_bounds__(256)
 append_at_kernel(void* __restrict__ kc, void* __restrict__ vc, int64_t sb, int64_t st, int64_t sh,
                  const void* __restrict__ k_new, const void* __restrict__ v_new, int64_t n_sb, int64_t n_sh,
                  int64_t H, int64_t D, int64_t bs, int64_t max_len, int64_t nb_stride,
-                 const int64_t* __restrict__ pos_dev, float* __restrict__ sums) {
+                 const int64_t* __restrict__ pos_dev, float* __restrict__ sums, int n_append, PrefetchDev pf) {
     using E = typename std::conditional<DT == SPARDA_BF16, uint16_t, float>::type;
     constexpr int U = 32;
+    if (static_cast<int>(blockIdx.x) >= n_append) {
+        __shared__ float f_lds[kMaxHeadDim];
+        __shared__ uint32_t key_lds[kSelMaxBlocks];
+        __shared__ int32_t sel_lds[kMaxSelCap + 2];
+        __shared__ uint32_t ck_lds[kWave];
+        __shared__ int32_t ci_lds[kWave];
+        __shared__ int m_lds;
+        const int idx = static_cast<int>(blockIdx.x) - n_append;
+        prefetch_workgroup<64, 64>(pf, idx % static_cast<int>(pf.H), idx / static_cast<int>(pf.H), pos_dev, f_lds,
+                                   key_lds, sel_lds, ck_lds, ci_lds, &m_lds);
+        return;
+    }
     const int64_t b = blockIdx.x;
     int64_t p = *pos_dev;
     p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
@@ -242,19 +259,31 @@ append_at_kernel(void* __restrict__ kc, void* __restrict__ vc, int64_t sb, int64
     }
 }
 
+static int launch_append_at_pf(void* kc, void* vc, int dtype, int64_t sb, int64_t st, int64_t sh,
+                               const void* k_new, const void* v_new, int64_t n_sb, int64_t n_sh, int64_t B,
+                               int64_t H, int64_t D, int64_t bs, int64_t max_len, int64_t nb_stride,
+                               const int64_t* pos_dev, float* sums, hipStream_t stream, const PrefetchDev* pf) {
+    int threads = static_cast<int>(H * D < 256 ? H * D : 256);
+    threads = ((threads + kWave - 1) / kWave) * kWave;
+    // a carried selection takes workgroups of kSelThreads (the append's own need fewer at small H*D)
+    if (pf != nullptr) threads = kSelThreads;
+    const int64_t n_pf = pf != nullptr ? B * pf->H : 0;  // the next layer's batch is B too
+    dim3 grid(static_cast<unsigned>(B + n_pf));
+    const PrefetchDev pfv = pf != nullptr ? *pf : PrefetchDev{};
+    if (dtype == SPARDA_BF16)
+        hipLaunchKernelGGL(append_at_kernel<SPARDA_BF16>, grid, dim3(threads), 0, stream, kc, vc, sb, st, sh, k_new,
+                           v_new, n_sb, n_sh, H, D, bs, max_len, nb_stride, pos_dev, sums, static_cast<int>(B), pfv);
+    else
+        hipLaunchKernelGGL(append_at_kernel<SPARDA_F32>, grid, dim3(threads), 0, stream, kc, vc, sb, st, sh, k_new,
+                           v_new, n_sb, n_sh, H, D, bs, max_len, nb_stride, pos_dev, sums, static_cast<int>(B), pfv);
+    return check_hip(hipGetLastError(), "append_at_kernel");
+}
+
 int launch_append_at(void* kc, void* vc, int dtype, int64_t sb, int64_t st, int64_t sh, const void* k_new,
                      const void* v_new, int64_t n_sb, int64_t n_sh, int64_t B, int64_t H, int64_t D, int64_t bs,
                      int64_t max_len, int64_t nb_stride, const int64_t* pos_dev, float* sums, hipStream_t stream) {
-    int threads = static_cast<int>(H * D < 256 ? H * D : 256);
-    threads = ((threads + kWave - 1) / kWave) * kWave;
-    dim3 grid(static_cast<unsigned>(B));
-    if (dtype == SPARDA_BF16)
-        hipLaunchKernelGGL(append_at_kernel<SPARDA_BF16>, grid, dim3(threads), 0, stream, kc, vc, sb, st, sh, k_new,
-                           v_new, n_sb, n_sh, H, D, bs, max_len, nb_stride, pos_dev, sums);
-    else
-        hipLaunchKernelGGL(append_at_kernel<SPARDA_F32>, grid, dim3(threads), 0, stream, kc, vc, sb, st, sh, k_new,
-                           v_new, n_sb, n_sh, H, D, bs, max_len, nb_stride, pos_dev, sums);
-    return check_hip(hipGetLastError(), "append_at_kernel");
+    return launch_append_at_pf(kc, vc, dtype, sb, st, sh, k_new, v_new, n_sb, n_sh, B, H, D, bs, max_len, nb_stride,
+                               pos_dev, sums, stream, nullptr);
 }
 
 int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb, int64_t st, int64_t sh,
@@ -286,11 +315,11 @@ int offload_append(sparda_offload_t h, const void* k, const void* v, int64_t sb,
 }
 
 int offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t n_sb, int64_t n_sh,
-                      const int64_t* pos_dev, int64_t bs, float* sums, hipStream_t stream) {
+                      const int64_t* pos_dev, int64_t bs, float* sums, hipStream_t stream, const PrefetchDev* pf) {
     // the arena through its device mapping: [B][H][Smax][D] -> strides (H*Smax*D, D, Smax*D)
-    return launch_append_at(h->dev, h->dev + arena_bytes(h), h->dtype, h->H * h->Smax * h->D, h->D, h->Smax * h->D,
-                            k, v, n_sb, n_sh, h->B, h->H, h->D, bs, h->Smax, cdiv(h->Smax, bs), pos_dev, sums,
-                            stream);
+    return launch_append_at_pf(h->dev, h->dev + arena_bytes(h), h->dtype, h->H * h->Smax * h->D, h->D,
+                               h->Smax * h->D, k, v, n_sb, n_sh, h->B, h->H, h->D, bs, h->Smax, cdiv(h->Smax, bs),
+                               pos_dev, sums, stream, pf);
 }
 
 int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sums, hipStream_t stream) {
@@ -306,8 +335,6 @@ int offload_rebuild_sums(sparda_offload_t h, int64_t len, int64_t bs, float* sum
 // own = pos/bs. If own+1 <= k+2 every block 0..own is selected (the dense
 // fallback); otherwise sel = ascending {0, own} U top-k (ties by lower index).
 // ---------------------------------------------------------------------------
-constexpr int kSelThreads = 256;
-constexpr int kSelMaxBlocks = 4096;  // blocks a selection can score (LDS key array)
 
 template <int FDT, int CH, int DH, bool POW2>
 __global__ void __launch_bounds__(kSelThreads)

@@ -70,7 +70,8 @@ __device__ __forceinline__ int select_from_sums(const void* f, bool f_bf16, int6
 // list written to pf.sel / pf.n_sel, then the selected blocks (rows below p)
 // copied from the arena into the compact slots. Wavefront w copies slots
 // w, w + nwaves, ...: 2 x 8 sixteen-byte loads in flight per lane for a
-// 64 x 128-byte block of K and of V.
+// 64 x 128-byte block of K and of V. Stage 1 stops after the selection;
+// stage 2 copies the selection found in pf.sel / pf.n_sel.
 template <int CHMAX, int DH>
 __device__ __forceinline__ void prefetch_workgroup(const PrefetchDev& pf, int g, int b, const int64_t* pos_dev,
                                                    float* f_lds, uint32_t* key_lds, int32_t* sel_lds,
@@ -81,20 +82,31 @@ __device__ __forceinline__ void prefetch_workgroup(const PrefetchDev& pf, int g,
     const int nwaves = static_cast<int>(blockDim.x) / kWave;
     const int64_t bg = static_cast<int64_t>(b) * pf.H + g;
     const int64_t p = *pos_dev;
-    const int64_t pos = p < 0 ? 0 : (p > pf.pos_max ? pf.pos_max : p);
-    const int64_t n_present = (pos + pf.bs - 1) / pf.bs;
-    const int64_t score_limit = (pf.absolute ? pos : 0) / pf.bs;
-    const int own = static_cast<int>(pos / pf.bs);
-    const float* sums = pf.sums + (static_cast<int64_t>(b) * pf.nb_stride * pf.H + g) * DH;
-    const int64_t f_off = b * pf.f_sb + g * pf.f_sh;
-    const int m = pf.pow2 ? select_from_sums<CHMAX, DH, true>(pf.f, pf.f_bf16 != 0, f_off, sums, pf.H * DH, n_present,
-                                                              score_limit, own, pf.k, pf.bs, pf.scale, f_lds,
-                                                              key_lds, sel_lds, ck_lds, ci_lds, m_lds)
-                          : select_from_sums<CHMAX, DH, false>(pf.f, pf.f_bf16 != 0, f_off, sums, pf.H * DH,
-                                                               n_present, score_limit, own, pf.k, pf.bs, pf.scale,
-                                                               f_lds, key_lds, sel_lds, ck_lds, ci_lds, m_lds);
-    for (int i = tid; i < pf.cap; i += static_cast<int>(blockDim.x)) pf.sel[bg * pf.cap + i] = i < m ? sel_lds[i] : -1;
-    if (tid == 0) pf.n_sel[bg] = m;
+    int m;
+    if (pf.stage != 2) {
+        const int64_t pos = p < 0 ? 0 : (p > pf.pos_max ? pf.pos_max : p);
+        const int64_t n_present = (pos + pf.bs - 1) / pf.bs;
+        const int64_t score_limit = (pf.absolute ? pos : 0) / pf.bs;
+        const int own = static_cast<int>(pos / pf.bs);
+        const float* sums = pf.sums + (static_cast<int64_t>(b) * pf.nb_stride * pf.H + g) * DH;
+        const int64_t f_off = b * pf.f_sb + g * pf.f_sh;
+        m = pf.pow2 ? select_from_sums<CHMAX, DH, true>(pf.f, pf.f_bf16 != 0, f_off, sums, pf.H * DH, n_present,
+                                                        score_limit, own, pf.k, pf.bs, pf.scale, f_lds, key_lds,
+                                                        sel_lds, ck_lds, ci_lds, m_lds)
+                    : select_from_sums<CHMAX, DH, false>(pf.f, pf.f_bf16 != 0, f_off, sums, pf.H * DH, n_present,
+                                                         score_limit, own, pf.k, pf.bs, pf.scale, f_lds, key_lds,
+                                                         sel_lds, ck_lds, ci_lds, m_lds);
+        for (int i = tid; i < pf.cap; i += static_cast<int>(blockDim.x))
+            pf.sel[bg * pf.cap + i] = i < m ? sel_lds[i] : -1;
+        if (tid == 0) pf.n_sel[bg] = m;
+        if (pf.stage == 1) return;
+    } else {
+        // the selection an earlier launch of the stream wrote
+        m = pf.n_sel[bg];
+        m = m < 0 ? 0 : (m > pf.cap ? pf.cap : m);
+        for (int i = tid; i < m; i += static_cast<int>(blockDim.x)) sel_lds[i] = pf.sel[bg * pf.cap + i];
+        __syncthreads();
+    }
 
     // the copy: arena length p, clamped into [0, Smax] (the gather kernel's rule)
     const int64_t len = p < 0 ? 0 : (p > pf.Smax ? pf.Smax : p);

@@ -32,7 +32,8 @@ With overlap="fused" (the default) the selection and the copy over the host
 link run as extra workgroups of layer L's attention launch
 (sparda_decode_at_prefetch), beside its attention workgroups: the overlap the
 reference gets from its transfer stream, without a cross-stream dependency
-in the graph. overlap=False issues them as launches of their own on the
+in the graph. When layer L is offloaded too, the selection rides on layer L's
+arena-append launch and only the copy on its attention launch. overlap=False issues them as launches of their own on the
 compute stream, overlap=True on a side stream joined by an event. Layer L+1
 then appends its token into the arena and attends over the fetched blocks
 with the new token supplied separately.
@@ -187,9 +188,13 @@ class GraphDecoder:
         if kind == _OFFLOAD:
             pf = self._pf[i]
             torch.cuda.current_stream().wait_event(pf["ev"])
-            cache.arena.append_at(k, v, self.pos, bs, cache.block_sums(bs))
+            # a carried prefetch: its selection rides on the append launch, its
+            # host-link copy on the attention launch
+            cache.arena.append_at(k, v, self.pos, bs, cache.block_sums(bs),
+                                  prefetch=None if nxt is None else {**nxt, "stage": 1}, max_len=self.max_len)
             return sparda.decode_at(q, pf["k"], pf["v"], self.pos, bs, pf["sel"], pf["n"], max_len=self.max_len,
-                                    compact=True, k_new=k[:, 0], v_new=v[:, 0], prefetch=nxt)
+                                    compact=True, k_new=k[:, 0], v_new=v[:, 0],
+                                    prefetch=None if nxt is None else {**nxt, "stage": 2})
         if kind == _RESIDENT_DENSE:
             sparda.append_at(cache.k, cache.v, self.pos, bs, None, k, v)
             return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len,

@@ -833,7 +833,9 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
     layer's OffloadArena), ``forecast`` [B,Hkv,Df], ``block_sums`` (its sums),
     ``top_k``, ``routing``, optional ``scale``, and the outputs ``sel`` /
     ``n_sel`` / ``k_dst`` / ``v_dst`` — what select_decode_at(lookahead=True)
-    and OffloadArena.fetch_at would write, bit for bit."""
+    and OffloadArena.fetch_at would write, bit for bit. Optional ``stage``: 0
+    (default) selection and copy, 1 the selection only, 2 the copy only of
+    the selection already in sel / n_sel."""
     dev = require_device(q, k, v, pos_dev, sel, n_sel, k_new, v_new)
     _inference_only(q, k, v, k_new, v_new)
     if not (q.dtype == k.dtype == v.dtype):
@@ -892,12 +894,15 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
 
 
 def _prefetch_args(spec: dict, B: int, Hkv: int, D: int, block_size: int, dev):
-    """The sparda_prefetch_args of a decode_at prefetch spec (checked as
-    select_decode_at and OffloadArena.fetch_at check theirs), with the
-    tensors it points into."""
+    """The sparda_prefetch_args of a prefetch spec carried by another launch
+    (checked as select_decode_at and OffloadArena.fetch_at check theirs), with
+    the tensors it points into."""
     arena = spec["arena"]
     f, sums = spec["forecast"], spec["block_sums"]
     sel, n_sel, k_dst, v_dst = spec["sel"], spec["n_sel"], spec["k_dst"], spec["v_dst"]
+    stage = int(spec.get("stage", 0))
+    if stage not in (0, 1, 2):
+        raise ValueError(f"sparda: prefetch stage must be 0, 1 or 2, got {stage}")
     require_device(f, sums, sel, n_sel, k_dst, v_dst)
     if (arena.B, arena.Hkv, arena.D) != (B, Hkv, D):
         raise ValueError("sparda: the prefetched arena must have the attended layer's batch, KV heads and head dim")
@@ -926,7 +931,8 @@ def _prefetch_args(spec: dict, B: int, Hkv: int, D: int, block_size: int, dev):
     fsb, fsh, _ = f.stride()
     pf = _lib.PrefetchArgs(arena.handle.value, f.data_ptr(), _dtype_code(f), fsb, fsh, sums.data_ptr(), sums.shape[1],
                            int(spec["top_k"]), _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE,
-                           float(scale), sel.data_ptr(), n_sel.data_ptr(), cap, k_dst.data_ptr(), v_dst.data_ptr())
+                           float(scale), sel.data_ptr(), n_sel.data_ptr(), cap, k_dst.data_ptr(), v_dst.data_ptr(),
+                           stage)
     return pf, (f, sums, sel, n_sel, k_dst, v_dst)
 
 
@@ -1077,10 +1083,14 @@ class OffloadArena:
              _pos_ptr(len_dev), k_dst.data_ptr(), v_dst.data_ptr(), _stream(dev))
 
     def append_at(self, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.Tensor, block_size: int = 0,
-                  block_sums: Optional[torch.Tensor] = None) -> None:
+                  block_sums: Optional[torch.Tensor] = None, prefetch: Optional[dict] = None,
+                  max_len: Optional[int] = None) -> None:
         """One token k, v ([B,1,Hkv,D] or [B,Hkv,D], device) into the arena at row
         pos_dev (a one-element int64 GPU tensor, read when the kernel runs),
-        with its block's sums recomputed from the arena when block_sums is given."""
+        with its block's sums recomputed from the arena when block_sums is given.
+        prefetch (with max_len, the positions' bound): the next layer's prefetch
+        stage carried by the same launch, a decode_at prefetch dict (normally
+        stage 1, the selection; sparda_offload_append_at_prefetch)."""
         dev = require_device(k, v, block_sums, pos_dev)
         if k.dtype != self.dtype or v.dtype != self.dtype:
             raise TypeError(f"sparda: arena holds {self.dtype}, got {k.dtype}/{v.dtype}")
@@ -1091,5 +1101,14 @@ class OffloadArena:
         if block_sums is not None and (block_sums.dtype != torch.float32 or not block_sums.is_contiguous()):
             raise TypeError("sparda: block sums must be contiguous float32")
         nsb, nsh, _ = k.stride()
-        call("sparda_offload_append_at", self.handle, k.data_ptr(), v.data_ptr(), nsb, nsh, _pos_ptr(pos_dev),
-             block_size, block_sums.data_ptr() if block_sums is not None else None, _stream(dev))
+        if prefetch is None:
+            call("sparda_offload_append_at", self.handle, k.data_ptr(), v.data_ptr(), nsb, nsh, _pos_ptr(pos_dev),
+                 block_size, block_sums.data_ptr() if block_sums is not None else None, _stream(dev))
+            return
+        if max_len is None or block_size <= 0:
+            raise ValueError("sparda: a carried prefetch needs max_len and the block size")
+        pf, keep = _prefetch_args(prefetch, self.B, self.Hkv, self.D, block_size, dev)
+        call("sparda_offload_append_at_prefetch", self.handle, k.data_ptr(), v.data_ptr(), nsb, nsh, _pos_ptr(pos_dev),
+             block_size, block_sums.data_ptr() if block_sums is not None else None, int(max_len), ctypes.byref(pf),
+             _stream(dev))
+        del keep

@@ -155,6 +155,71 @@ def test_decode_at_carrying_a_prefetch_equals_separate_launches(routing, bs):
     arena.close()
 
 
+@pytest.mark.parametrize("routing", ["reference", "absolute"])
+def test_prefetch_split_over_the_append_and_attention_launches(routing):
+    # the next layer's selection carried by this layer's arena append (stage 1)
+    # and its copy by this layer's attention launch (stage 2): the selection,
+    # the fetched blocks, the append (arena rows and block sums) and the
+    # attention output equal the separate launches'
+    case(f"prefetch stages over the append and attention launches, {routing}")
+    B, Smax, Hq, Hkv, D, bs, k = 2, 2048, 12, 4, 64, 64, 8
+    cap, bf = k + 2, torch.bfloat16
+    g = torch.Generator().manual_seed(14)
+    f = torch.randn(B, Hkv, 64, generator=g).to(bf).to(DEV)
+    q = torch.randn(B, Hq, D, generator=g).to(bf).to(DEV)
+    kn = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    vn = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    kc = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    vc = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
+    nxt = sparda.OffloadArena(B, Smax, Hkv, D, bf)
+    nxt.append(kn, vn, 0)
+    cur_a = sparda.OffloadArena(B, Smax, Hkv, D, bf)   # appended to plainly
+    cur_b = sparda.OffloadArena(B, Smax, Hkv, D, bf)   # appended to by the launch carrying the selection
+    cur_a.append(kc[:, :1500], vc[:, :1500], 0)
+    cur_b.append(kc[:, :1500], vc[:, :1500], 0)
+    nb = Smax // bs
+
+    def outputs():
+        return (torch.full((B, Hkv, cap), 7, dtype=torch.int32, device=DEV),
+                torch.full((B, Hkv), 7, dtype=torch.int32, device=DEV),
+                torch.full((B, Hkv, cap, bs, D), 3.0, dtype=bf, device=DEV),
+                torch.full((B, Hkv, cap, bs, D), 3.0, dtype=bf, device=DEV))
+
+    sums_a = torch.zeros((B, nb, Hkv, D), device=DEV)
+    sums_b = torch.zeros((B, nb, Hkv, D), device=DEV)
+    cur_a.rebuild_sums(1500, bs, sums_a)
+    cur_b.rebuild_sums(1500, bs, sums_b)
+    for p in (1500, 1535, 1536, 1537, 2047):
+        case(f"  position {p}")
+        pos = _pos(p)
+        sums = torch.zeros((B, nb, Hkv, D), device=DEV)
+        sparda.block_sums(kn, 0, p, bs, sums)
+        s1, n1, k1, v1 = outputs()
+        sparda.select_decode_at(f, sums, pos, Smax, bs, k, routing=routing, sel=s1, n_sel=n1, lookahead=True)
+        nxt.fetch_at(s1, n1, bs, pos, k1, v1)
+        s2, n2, k2, v2 = outputs()
+        spec = dict(arena=nxt, forecast=f, block_sums=sums, top_k=k, routing=routing, sel=s2, n_sel=n2,
+                    k_dst=k2, v_dst=v2)
+        row_k, row_v = kc[:, p:p + 1], vc[:, p:p + 1]
+        cur_a.append_at(row_k, row_v, pos, bs, sums_a)
+        cur_b.append_at(row_k, row_v, pos, bs, sums_b, prefetch={**spec, "stage": 1}, max_len=Smax)
+        torch.cuda.synchronize()
+        assert torch.equal(n2, n1) and torch.equal(s2, s1), f"selection at {p}"
+        assert (k2 == 3.0).all() and (v2 == 3.0).all(), "stage 1 copies nothing"
+        assert torch.equal(sums_b, sums_a), f"block sums at {p}"
+        # the carrying layer attends densely over its own (resident) cache here
+        o_plain = sparda.decode_at(q, kc, vc, pos, bs, window=0)
+        o_carry = sparda.decode_at(q, kc, vc, pos, bs, window=0, prefetch={**spec, "stage": 2})
+        assert torch.equal(o_carry, o_plain), f"attention output at {p}"
+        assert torch.equal(k2, k1) and torch.equal(v2, v1), f"fetched blocks at {p}"
+        assert torch.equal(s2, s1) and torch.equal(n2, n1), "stage 2 leaves the selection"
+    L = 2048
+    assert torch.equal(cur_a.k_host[:, :L], cur_b.k_host[:, :L]) and torch.equal(cur_a.v_host[:, :L],
+                                                                                  cur_b.v_host[:, :L])
+    for a in (nxt, cur_a, cur_b):
+        a.close()
+
+
 def test_device_positions_are_clamped_into_range():
     case("device-position clamping")
     B, Smax, Hq, Hkv, D, bs, k = 1, 1000, 12, 4, 64, 64, 8
