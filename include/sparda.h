@@ -375,6 +375,15 @@ SPARDA_API int sparda_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
  *   k_new/v_new: optional [B,Hkv,D] (strides new_sb, new_sh, 1): the key and
  *     value of position S-1, used instead of what k/v hold there.
  *   q: [B,Hq,D]; out: [B,Hq*D] stride out_sb. 16-byte aligned rows.
+ *   workspace (optional, 16-byte aligned, may be NULL): with sel == NULL on
+ *     the matrix-core attention (bf16, D = 64, blocks of 64 or 32 keys) the
+ *     blocks are split over workgroups, four per workgroup (more when
+ *     workspace_bytes / (B*Hkv*(Hq/Hkv)*(D+2)*4) splits do not cover them),
+ *     whose partials a second launch merges (flash-decoding); NULL or too
+ *     small for two splits: one workgroup per (sequence, KV head). The split
+ *     changes no selection, only the order in which partial softmax sums are
+ *     combined. sparda_decode_dense_workspace_bytes gives the size of the
+ *     full split for a length.
  */
 SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                                       const void* k, const void* v,
@@ -385,7 +394,21 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                                       int64_t new_sb, int64_t new_sh,
                                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
                                       int64_t block_size, float scale,
-                                      void* out, int64_t out_sb, void* stream);
+                                      void* out, int64_t out_sb,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes for which a dense decode (sparda_decode_selected with sel
+ * NULL, sparda_decode_at / sparda_decode_at_prefetch with sel NULL and
+ * window_k 0) of up to max_len tokens takes its full split: four blocks
+ * per workgroup (more only past 4096 workgroups per (sequence, KV head)),
+ * so that which split holds a block, and with it the result, depends on the
+ * length and not on max_len; 0 when it would not split. No counterpart in the reference: the
+ * reference attends densely with SDPA (model/attention/offload.py:180-200,
+ * model/attention/async_offload.py:399-417).
+ */
+SPARDA_API size_t sparda_decode_dense_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                                      int64_t max_len, int64_t block_size);
 
 /*
  * Teacher block mass for routing-quality evaluation: the dense attention
@@ -583,7 +606,8 @@ SPARDA_API int sparda_decode_sums(const void* q, int64_t q_sb, int64_t q_sh, con
  *   or, with sel NULL and window_k > 0, the static window
  *   {0} U [cb - window_k + 1, cb] (cb = p / bs; every block while cb + 1 <=
  *   window_k + 2) that sparda_decode uses without a forecast, or every block
- *   (sel NULL, window_k 0).
+ *   (sel NULL, window_k 0; split over the workgroups a workspace allows, as
+ *   in sparda_decode_selected).
  * sparda_offload_fetch_at: sparda_offload_fetch (gather kernel) with
  *   len = *len_dev, clamped into [0, max_seq].
  * sparda_offload_append_at: appends one token (k / v [B,Hkv,D], strides
@@ -616,7 +640,8 @@ SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const
                                 const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
                                 const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
-                                int64_t block_size, float scale, void* out, int64_t out_sb, void* stream);
+                                int64_t block_size, float scale, void* out, int64_t out_sb, void* workspace,
+                                size_t workspace_bytes, void* stream);
 SPARDA_API int sparda_offload_fetch_at(sparda_offload_t h, const int32_t* sel, const int32_t* n_sel,
                                        int64_t sel_cap, int64_t block_size, const int64_t* len_dev, void* k_dst,
                                        void* v_dst, void* stream);
@@ -689,7 +714,7 @@ SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_
                                          int64_t new_sh, int64_t B, int64_t max_len, const int64_t* pos_dev,
                                          int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, float scale,
                                          void* out, int64_t out_sb, const sparda_prefetch_args* next,
-                                         void* stream);
+                                         void* workspace, size_t workspace_bytes, void* stream);
 SPARDA_API int sparda_offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
                                         int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
                                         float* block_sums, void* stream);

@@ -301,8 +301,10 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                                       const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh,
                                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
                                       int64_t block_size, float scale, void* out, int64_t out_sb,
-                                      void* stream) {
+                                      void* workspace, size_t workspace_bytes, void* stream) {
     SPARDA_REQUIRE(q && k && v && out, SPARDA_ERR_NULL, "decode_selected: null q/k/v/out");
+    SPARDA_REQUIRE(!workspace || aligned16(workspace), SPARDA_ERR_WORKSPACE,
+                   "decode_selected: workspace must be 16-byte aligned");
     SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "decode_selected: sel and n_sel go together");
     SPARDA_REQUIRE(!k_new == !v_new, SPARDA_ERR_NULL, "decode_selected: k_new and v_new go together");
     SPARDA_REQUIRE(!compact || sel, SPARDA_ERR_MODE, "decode_selected: compact buffers need a selection");
@@ -323,7 +325,13 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
                    SPARDA_ERR_STRIDE, "decode_selected: k_new/v_new rows must be 16-byte aligned");
     return launch_decode_selected(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap,
                                   k_new, v_new, new_sb, new_sh, B, S, Hq, Hkv, D, block_size, scale, out,
-                                  out_sb, static_cast<hipStream_t>(stream));
+                                  out_sb, static_cast<hipStream_t>(stream), workspace,
+                                  workspace ? workspace_bytes : 0);
+}
+
+SPARDA_API size_t sparda_decode_dense_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                                      int64_t max_len, int64_t block_size) {
+    return decode_dense_workspace_bytes(B, Hq, Hkv, D, max_len, block_size);
 }
 
 SPARDA_API int sparda_select_decode(const void* forecast, int f_dtype, int64_t f_sb, int64_t f_sh,
@@ -386,9 +394,11 @@ static int decode_at_checked(const void* q, int64_t q_sb, int64_t q_sh, const vo
                              const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
                              const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                              int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
-                             int64_t block_size, float scale, void* out, int64_t out_sb, void* stream,
-                             const sparda::PrefetchDev* pf) {
+                             int64_t block_size, float scale, void* out, int64_t out_sb, void* workspace,
+                             size_t workspace_bytes, void* stream, const sparda::PrefetchDev* pf) {
     SPARDA_REQUIRE(q && k && v && out && pos_dev, SPARDA_ERR_NULL, "decode_at: null q/k/v/out/pos_dev");
+    SPARDA_REQUIRE(!workspace || aligned16(workspace), SPARDA_ERR_WORKSPACE,
+                   "decode_at: workspace must be 16-byte aligned");
     SPARDA_REQUIRE((reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_STRIDE,
                    "decode_at: pos_dev must be 8-byte aligned");
     SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "decode_at: sel and n_sel go together");
@@ -413,7 +423,8 @@ static int decode_at_checked(const void* q, int64_t q_sb, int64_t q_sh, const vo
                    SPARDA_ERR_STRIDE, "decode_at: k_new/v_new rows must be 16-byte aligned");
     return launch_decode_at(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
                             k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
-                            out_sb, static_cast<hipStream_t>(stream), pf);
+                            out_sb, static_cast<hipStream_t>(stream), pf, workspace,
+                            workspace ? workspace_bytes : 0);
 }
 
 SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
@@ -421,10 +432,11 @@ SPARDA_API int sparda_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const
                                 const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t window_k,
                                 const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B,
                                 int64_t max_len, const int64_t* pos_dev, int64_t Hq, int64_t Hkv, int64_t D,
-                                int64_t block_size, float scale, void* out, int64_t out_sb, void* stream) {
+                                int64_t block_size, float scale, void* out, int64_t out_sb, void* workspace,
+                                size_t workspace_bytes, void* stream) {
     return decode_at_checked(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
                              k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
-                             out_sb, stream, nullptr);
+                             out_sb, workspace, workspace_bytes, stream, nullptr);
 }
 
 // The device form of a prefetch carried by another launch, after the checks
@@ -488,7 +500,7 @@ SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_
                                          int64_t new_sh, int64_t B, int64_t max_len, const int64_t* pos_dev,
                                          int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, float scale,
                                          void* out, int64_t out_sb, const sparda_prefetch_args* next,
-                                         void* stream) {
+                                         void* workspace, size_t workspace_bytes, void* stream) {
     SPARDA_REQUIRE(decode_at_matrix_core(dtype, D, block_size, q_sb, q_sh, q), SPARDA_ERR_MODE,
                    "decode_at_prefetch: needs the matrix-core attention (bf16, D=64, blocks of 64 or 32 keys, "
                    "16-byte aligned q rows)");
@@ -497,7 +509,7 @@ SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_
     if (rc) return rc;
     return decode_at_checked(q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
                              k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, block_size, scale, out,
-                             out_sb, stream, &pf);
+                             out_sb, workspace, workspace_bytes, stream, &pf);
 }
 
 SPARDA_API int sparda_offload_create(int64_t B, int64_t max_seq, int64_t Hkv, int64_t D, int dtype,

@@ -182,7 +182,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
                      void* __restrict__ out, int64_t out_sb, const int64_t* __restrict__ pos_dev,
                      float* sums, int64_t nb_stride, int update_sums, const void* __restrict__ fsel,
                      int fsel_bf16, int64_t fs_sb, int64_t fs_sh, int absolute, float fscale, int pow2,
-                     PrefetchDev pf) {
+                     PrefetchDev pf, int nsplit, int split_blocks, float* __restrict__ ws_part) {
     using E = typename KvElem<DT>::T;
     constexpr int VR = v_row_elems<DT, DH>();
     constexpr int KW = DT == SPARDA_BF16 ? DH / 2 : DH;  // K row words per lane
@@ -197,11 +197,15 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
 
     const int g = blockIdx.x;
     const int b = blockIdx.y;
+    // blockIdx.z < nsplit: split z of the (sequence, KV head)'s slots, slots
+    // [z * split_blocks, (z + 1) * split_blocks) (nsplit > 1 only for the
+    // matrix-core dense mode with a workspace)
+    const int split = static_cast<int>(blockIdx.z);
     if constexpr (MF) {
-        // blockIdx.z = 1: the next layer's prefetch for (b, g), carried by this
-        // launch so that its selection and host-link copy run beside the
-        // attention workgroups (the host sets z = 2 only with pf filled in)
-        if (blockIdx.z != 0) {
+        // blockIdx.z = nsplit: the next layer's prefetch for (b, g), carried by
+        // this launch so that its selection and host-link copy run beside the
+        // attention workgroups (the host adds that z only with pf filled in)
+        if (split >= nsplit) {
             prefetch_workgroup<CH, DH>(pf, g, b, pos_dev, fsel_lds, reinterpret_cast<uint32_t*>(dyn), sel_lds, ck_lds,
                                        ci_lds, &n_lds);
             return;
@@ -341,7 +345,11 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     }
     __syncthreads();
     const int n = n_lds;
-    if (threadIdx.x < cap) {
+    // this workgroup's slots [s_lo, s_hi): all of them, or those of split `split`
+    const int s_per = nsplit > 1 ? split_blocks : n;
+    const int s_lo = split * s_per < n ? split * s_per : n;
+    const int s_hi = s_lo + s_per < n ? s_lo + s_per : n;
+    if (split == 0 && threadIdx.x < cap) {
         const int i = threadIdx.x;
         if (sel_out != nullptr) sel_out[bg * cap + i] = i < n ? (sel_mode == 1 ? i : sel_lds[i]) : -1;
         if (i == 0 && n_sel_out != nullptr) n_sel_out[bg] = n;
@@ -384,7 +392,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
         for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
         float m_run = -__builtin_inff();
         const int64_t nbase = b * new_sb + g * new_sh;
-        for (int w = wave; w < n; w += nwaves) {
+        for (int w = s_lo + wave; w < s_hi; w += nwaves) {
             const int64_t j = sel_mode == 1 ? w : sel_lds[w];
             if (j < 0 || j > cb) continue;  // not a block of [0, S): nothing to attend
             const int64_t s0 = j * kBs;
@@ -535,7 +543,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     }
     __builtin_amdgcn_wave_barrier();
 
-    for (int w = wave; w < n; w += nwaves) {
+    for (int w = s_lo + wave; w < s_hi; w += nwaves) {
         const int64_t j = sel_mode == 1 ? w : sel_lds[w];
         if (j < 0 || j > cb) continue;  // not a block of [0, S): nothing to attend
         const int64_t s0 = j * bs;
@@ -685,7 +693,7 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
     __syncthreads();
 
     // merge the wave partials in wave order (waves without a block hold m = -inf, l = 0)
-    const int nw = n < nwaves ? n : nwaves;
+    const int nw = s_hi - s_lo < nwaves ? s_hi - s_lo : nwaves;
     for (int e = threadIdx.x; e < R * DH; e += blockDim.x) {
         const int hh = e / DH, d = e % DH;
         float M = -__builtin_inff();
@@ -697,9 +705,99 @@ decode_attend_kernel(const void* __restrict__ q, int64_t q_sb, int64_t q_sh,
             den = den + wt * ps[1];
             num = num + wt * ps[2 + d];
         }
-        store_elem<DT>(out, b * out_sb + static_cast<int64_t>(g * R + hh) * DH + d, num / den);
+        if (nsplit == 1) {
+            store_elem<DT>(out, b * out_sb + static_cast<int64_t>(g * R + hh) * DH + d, num / den);
+        } else {
+            // the split's partial (m, l, o[DH]) of head hh, unnormalised (an
+            // empty split: m = -inf, l = 0, o = 0), merged by decode_merge_kernel
+            float* pw = ws_part + ((bg * nsplit + split) * R + hh) * (DH + 2);
+            if (d == 0) {
+                pw[0] = M;
+                pw[1] = den;
+            }
+            pw[2 + d] = num;
+        }
     }
     __syncthreads();
+}
+
+// The splits of a dense decode (decode_attend_kernel with nsplit > 1): one
+// workgroup per (sequence, KV head) folds the nsplit partials of each of its
+// R heads. Thread (q, e) of Q groups takes the splits q, q + Q, q + 2Q, ...
+// of element e = (head, dim) in split order (32 loads in flight), keeping a
+// running (m, l, o) that is rescaled when a split's maximum exceeds it; the
+// groups are then combined in group order. A split's group depends on its
+// index alone and an empty split (m = -inf, l = 0, o = 0) adds exact zeros,
+// so the splits past the last block (a launch sized for a longer cache)
+// change nothing.
+constexpr int kMergeThreads = 768;
+
+template <int DT, int DH>
+__global__ void __launch_bounds__(kMergeThreads)
+decode_merge_kernel(const float* __restrict__ ws_part, int nsplit, int R, int H, int Q, void* __restrict__ out,
+                    int64_t out_sb) {
+    __shared__ float m_q[kMergeThreads], l_q[kMergeThreads], o_q[kMergeThreads];
+    constexpr int U = 32;
+    const int g = blockIdx.x;
+    const int b = blockIdx.y;
+    const int64_t bg = static_cast<int64_t>(b) * H + g;
+    const int RD = R * DH;
+    const int per = static_cast<int>(blockDim.x) / Q;  // elements per round
+    const int t = static_cast<int>(threadIdx.x);
+    const int q = t / per;
+    const int step = R * (DH + 2);
+    for (int e0 = 0; e0 < RD; e0 += per) {  // the same trip count in every thread
+        const int e = e0 + t % per;
+        const bool live = q < Q && e < RD;
+        const int hh = live ? e / DH : 0, d = live ? e % DH : 0;
+        const float* p0 = ws_part + (bg * nsplit * R + hh) * (DH + 2);
+        // this group's splits q + Q j; indices past the last re-read split q
+        // (in bounds) and are not added
+        const int nj = live && q < nsplit ? (nsplit - q + Q - 1) / Q : 0;
+        float M = -__builtin_inff(), num = 0.0f, den = 0.0f;
+        for (int j0 = 0; j0 < nj; j0 += U) {
+            float mv[U], lv[U], ov[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int off = (q + Q * (j0 + u < nj ? j0 + u : 0)) * step;
+                mv[u] = p0[off];
+                lv[u] = p0[off + 1];
+                ov[u] = p0[off + 2 + d];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (j0 + u < nj && mv[u] != -__builtin_inff()) {
+                    if (mv[u] > M) {
+                        const float sc = __builtin_amdgcn_exp2f(M - mv[u]);
+                        num = num * sc;
+                        den = den * sc;
+                        M = mv[u];
+                    }
+                    const float wt = __builtin_amdgcn_exp2f(mv[u] - M);
+                    den = den + wt * lv[u];
+                    num = num + wt * ov[u];
+                }
+            }
+        }
+        m_q[t] = M;
+        l_q[t] = den;
+        o_q[t] = num;
+        __syncthreads();
+        if (live && q == 0) {
+            float Mall = -__builtin_inff();
+            for (int r = 0; r < Q; ++r) Mall = fmaxf(Mall, m_q[r * per + t]);
+            float n_all = 0.0f, d_all = 0.0f;
+            for (int r = 0; r < Q; ++r) {
+                const float mr = m_q[r * per + t];
+                if (mr == -__builtin_inff()) continue;  // a group without a block
+                const float wt = __builtin_amdgcn_exp2f(mr - Mall);
+                n_all = n_all + wt * o_q[r * per + t];
+                d_all = d_all + wt * l_q[r * per + t];
+            }
+            store_elem<DT>(out, b * out_sb + static_cast<int64_t>(g * R + hh) * DH + d, n_all / d_all);
+        }
+        __syncthreads();  // m_q, l_q, o_q are rewritten by the next round
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -720,7 +818,42 @@ struct AttendArgs {
     const void* fsel = nullptr; int fsel_bf16 = 0; int64_t fs_sb = 0, fs_sh = 0;
     int absolute = 0; float fscale = 0.0f;
     const PrefetchDev* pf = nullptr;  // the next layer's prefetch carried by the launch (matrix-core path)
+    // dense mode on the matrix cores: a workspace for split partials (nullptr: one workgroup per (b, g))
+    float* ws_part = nullptr; size_t ws_bytes = 0;
 };
+
+// Splits of a dense decode: kSplitBlocks blocks per workgroup (more when the
+// workspace holds fewer splits, or past kMaxSplits), so that the split of a
+// block, and with it the result, depends on the length alone, not on the
+// capacity a launch is sized for; no split below two.
+constexpr int64_t kSplitBlocks = 4;
+constexpr int64_t kMaxSplits = 4096;
+
+struct DenseSplit {
+    int n = 1;       // splits per (sequence, KV head)
+    int blocks = 0;  // blocks per split
+};
+
+static int64_t dense_split_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
+    return B * Hkv * (Hq / Hkv) * (D + 2) * static_cast<int64_t>(sizeof(float));
+}
+
+static DenseSplit dense_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t NB, size_t ws_bytes) {
+    int64_t fit = static_cast<int64_t>(ws_bytes) / dense_split_bytes(B, Hq, Hkv, D);
+    fit = fit < kMaxSplits ? fit : kMaxSplits;
+    if (fit < 2) return DenseSplit{};
+    int64_t per = kSplitBlocks;
+    if (cdiv(NB, per) > fit) per = cdiv(NB, fit);
+    const int64_t n = cdiv(NB, per);
+    if (n < 2) return DenseSplit{};
+    return DenseSplit{static_cast<int>(n), static_cast<int>(per)};
+}
+
+size_t decode_dense_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t S, int64_t bs) {
+    if (B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || S <= 0 || bs <= 0) return 0;
+    const DenseSplit sp = dense_split(B, Hq, Hkv, D, cdiv(S, bs), static_cast<size_t>(-1) / 2);
+    return sp.n >= 2 ? static_cast<size_t>(sp.n * dense_split_bytes(B, Hq, Hkv, D)) : 0;
+}
 
 bool decode_at_matrix_core(int dtype, int64_t D, int64_t bs, int64_t q_sb, int64_t q_sh, const void* q) {
     return dtype == SPARDA_BF16 && D == 64 && (bs == 64 || bs == 32) && (q_sb % 8) == 0 && (q_sh % 8) == 0 &&
@@ -732,16 +865,23 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
     const float scale_log2 = a.scale * kLog2e;
     const int Hq_i = static_cast<int>(a.Hq), Hkv_i = static_cast<int>(a.Hkv);
     const int64_t R = a.Hq / a.Hkv;
-    // most blocks one workgroup can attend: the selection capacity, or every block when dense
-    const int64_t max_blocks = a.sel_mode == 1 ? NB : a.cap;
     // matrix-core block attention: bf16, D = 64, bs = 64, 16-byte aligned q rows
     const bool mf = decode_at_matrix_core(a.dtype, a.D, a.bs, a.q_sb, a.q_sh, a.q);
+    // dense on the matrix cores with a workspace: the blocks split over nsplit
+    // workgroups per (sequence, KV head), then decode_merge_kernel
+    const DenseSplit split = (mf && a.sel_mode == 1 && a.ws_part != nullptr)
+                                 ? dense_split(a.B, a.Hq, a.Hkv, a.D, NB, a.ws_bytes)
+                                 : DenseSplit{};
+    const int nsplit = split.n;
+    // most blocks one workgroup can attend: the selection capacity, or its share of every block when dense
+    const int64_t max_blocks = a.sel_mode == 1 ? (nsplit > 1 ? split.blocks : NB) : a.cap;
     if (a.pf != nullptr && !mf)
         return set_error(SPARDA_ERR_MODE, "decode: a carried prefetch needs the bf16 D=64 matrix-core attention");
     const PrefetchDev pf = a.pf != nullptr ? *a.pf : PrefetchDev{};
     constexpr size_t kLdsBudget = 150 * 1024;
     const int pow2 = (a.bs & (a.bs - 1)) == 0 ? 1 : 0;
-    dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B), a.pf != nullptr ? 2u : 1u);
+    dim3 grid2(static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B),
+               static_cast<unsigned>(nsplit) + (a.pf != nullptr ? 1u : 0u));
 #define SPARDA_ATT(DT_, DH_, CH_)                                                                        \
     do {                                                                                                 \
         if constexpr (DT_ == SPARDA_BF16 && DH_ == 64) {                                                 \
@@ -768,7 +908,15 @@ static int launch_attend(const AttendArgs& a, hipStream_t stream) {
                            scale_log2, a.scores, a.sel_in, a.n_sel_in, a.compact, a.k_new, a.v_new,     \
                            a.new_sb, a.new_sh, a.sel_out, a.n_sel_out, a.out, a.out_sb, a.pos_dev, a.sums, \
                            a.nb_stride, a.update_sums, a.fsel, a.fsel_bf16, a.fs_sb, a.fs_sh, a.absolute,       \
-                           a.fscale, pow2, pf);                                                                \
+                           a.fscale, pow2, pf, nsplit, split.blocks, a.ws_part);                               \
+        if (nsplit > 1) {                                                                                \
+            const int rd = static_cast<int>(R) * DH_;                                                    \
+            const int qg = rd >= kMergeThreads ? 1 : (kMergeThreads / rd < 4 ? kMergeThreads / rd : 4);  \
+            const int thr = rd >= kMergeThreads ? kMergeThreads : rd * qg;                               \
+            hipLaunchKernelGGL((decode_merge_kernel<DT_, DH_>), dim3(static_cast<unsigned>(a.Hkv),       \
+                               static_cast<unsigned>(a.B)), dim3(thr), 0, stream, a.ws_part, nsplit,     \
+                               static_cast<int>(R), Hkv_i, qg, a.out, a.out_sb);                         \
+        }                                                                                                \
     } while (0)
 #define SPARDA_ATT_C(DT_, DH_)                            \
     if (NB <= 256) SPARDA_ATT(DT_, DH_, 4);               \
@@ -859,10 +1007,12 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
                            const int32_t* sel, const int32_t* n_sel, int64_t cap, const void* k_new,
                            const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B, int64_t S,
                            int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out,
-                           int64_t out_sb, hipStream_t stream) {
+                           int64_t out_sb, hipStream_t stream, void* ws, size_t ws_bytes) {
     AttendArgs a{q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, B, S, Hq, Hkv, D, bs, cap > 2 ? cap - 2 : 0,
                  sel == nullptr ? 1 : 3, static_cast<int>(sel == nullptr ? 0 : cap), scale, nullptr,
                  sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb};
+    a.ws_part = static_cast<float*>(ws);
+    a.ws_bytes = ws_bytes;
     return launch_attend(a, stream);
 }
 
@@ -892,7 +1042,7 @@ int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, c
                      const int32_t* n_sel, int64_t cap, int64_t window_k, const void* k_new, const void* v_new,
                      int64_t new_sb, int64_t new_sh, int64_t B, int64_t S_max, const int64_t* pos_dev,
                      int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
-                     hipStream_t stream, const PrefetchDev* pf) {
+                     hipStream_t stream, const PrefetchDev* pf, void* ws, size_t ws_bytes) {
     int mode, cap_i;
     int64_t kk;
     if (sel != nullptr) {
@@ -906,6 +1056,8 @@ int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, c
                  nullptr, sel, n_sel, compact, k_new, v_new, new_sb, new_sh, nullptr, nullptr, out, out_sb,
                  pos_dev};
     a.pf = pf;
+    a.ws_part = static_cast<float*>(ws);
+    a.ws_bytes = ws_bytes;
     return launch_attend(a, stream);
 }
 

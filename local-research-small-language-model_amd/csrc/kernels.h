@@ -113,7 +113,9 @@ int launch_decode_selected(const void* q, int64_t q_sb, int64_t q_sh, const void
                            const int32_t* sel, const int32_t* n_sel, int64_t cap, const void* k_new,
                            const void* v_new, int64_t new_sb, int64_t new_sh, int64_t B, int64_t S,
                            int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out,
-                           int64_t out_sb, hipStream_t stream);
+                           int64_t out_sb, hipStream_t stream, void* ws = nullptr, size_t ws_bytes = 0);
+// bytes of the split partials a dense decode of S tokens uses (0: it does not split)
+size_t decode_dense_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t S, int64_t bs);
 
 int launch_select_decode(const void* f, int fdtype, int64_t f_sb, int64_t f_sh, const float* sums, int64_t B,
                          int64_t H, int64_t D, int64_t nb_stride, int64_t len, int64_t pos, int64_t bs,
@@ -164,13 +166,14 @@ int offload_dtype(sparda_offload_t h);
 // attention at a device-held position: S = *pos_dev + 1 (clamped to S_max);
 // the caller's list (sel), the window of window_k blocks, or every block.
 // pf (optional, bf16 D = 64 matrix-core attention only): the next layer's
-// prefetch in the same launch.
+// prefetch in the same launch. ws (optional): the dense mode's split partials.
 int launch_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v, int64_t kv_sb,
                      int64_t kv_ss, int64_t kv_sh, int dtype, int compact, const int32_t* sel,
                      const int32_t* n_sel, int64_t cap, int64_t window_k, const void* k_new, const void* v_new,
                      int64_t new_sb, int64_t new_sh, int64_t B, int64_t S_max, const int64_t* pos_dev,
                      int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, float scale, void* out, int64_t out_sb,
-                     hipStream_t stream, const PrefetchDev* pf = nullptr);
+                     hipStream_t stream, const PrefetchDev* pf = nullptr, void* ws = nullptr,
+                     size_t ws_bytes = 0);
 // whether launch_decode_at takes the matrix-core attention (which can carry a prefetch)
 bool decode_at_matrix_core(int dtype, int64_t D, int64_t bs, int64_t q_sb, int64_t q_sh, const void* q);
 

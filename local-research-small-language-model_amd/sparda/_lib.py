@@ -78,7 +78,9 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _i64, _i64, _i64, _int, _f32, _p, _p, _p, _p, _p, _i64,
                                      _p]),
     "sparda_decode_selected": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _p, _p,
-                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p, _size,
+                                      _p]),
+    "sparda_decode_dense_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "sparda_select_decode": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                     _int, _f32, _p, _p, _i64, _p]),
     "sparda_offload_create": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_p)]),
@@ -99,10 +101,10 @@ SIGNATURES = {
     "sparda_select_decode_at": (_int, [_p, _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                                        _int, _f32, _p, _p, _i64, _int, _p]),
     "sparda_decode_at": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _i64, _p, _p,
-                                _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p]),
+                                _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p, _size, _p]),
     "sparda_decode_at_prefetch": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _int, _p, _p, _i64, _i64,
                                          _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64,
-                                         ctypes.POINTER(PrefetchArgs), _p]),
+                                         ctypes.POINTER(PrefetchArgs), _p, _size, _p]),
     "sparda_decode_sums": (_int, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64, _p, _i64,
                                   _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f32, _p, _p, _p,
                                   _i64, _p]),

@@ -378,6 +378,19 @@ def decode_workspace_bytes(B: int, S: int, Hq: int, Hkv: int, D: int, block_size
     return int(_lib.load().sparda_decode_workspace_bytes(B, S, Hq, Hkv, D, block_size, top_k))
 
 
+def _dense_split_ws(B: int, Hq: int, Hkv: int, D: int, S: int, block_size: int, dev):
+    """(pointer, bytes, tensor) of the split partials of a dense decode of up
+    to S tokens (sparda_decode_dense_workspace_bytes; (None, 0, None) when it
+    does not split). The tensor comes from torch's allocator, so a call under
+    graph capture takes it from the graph's pool; the caller keeps it alive
+    until the launch is enqueued."""
+    nbytes = int(_lib.load().sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, S, block_size))
+    if nbytes == 0:
+        return None, 0, None
+    ws = torch.empty(nbytes // 4 + 4, dtype=torch.float32, device=dev)
+    return ws.data_ptr(), nbytes, ws
+
+
 def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, S: int,
            forecast: Optional[torch.Tensor], block_size: int, top_k: int, routing: str = "reference",
            scale: Optional[float] = None, workspace: Optional[DecodeWorkspace] = None,
@@ -489,11 +502,15 @@ def decode_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, b
     if out is None:
         out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
     qsb, qsh, _ = q.stride()
+    # dense (no selection): the blocks split over workgroups, partials in a workspace
+    ws_ptr, ws_bytes, ws = _dense_split_ws(B, Hq, Hkv, D, S, block_size, dev) if sel is None else (None, 0, None)
     call("sparda_decode_selected", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
          _dtype_code(q), int(compact), sel.data_ptr() if sel is not None else None,
          n_sel.data_ptr() if n_sel is not None else None, cap,
          k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
-         nsb, nsh, B, S, Hq, Hkv, D, block_size, float(scale), out.data_ptr(), out.stride(0), _stream(dev))
+         nsb, nsh, B, S, Hq, Hkv, D, block_size, float(scale), out.data_ptr(), out.stride(0), ws_ptr, ws_bytes,
+         _stream(dev))
+    del ws
     return out
 
 
@@ -884,12 +901,16 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
             k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
             nsb, nsh, B, max_len, _pos_ptr(pos_dev), Hq, Hkv, D, block_size, float(scale), out.data_ptr(),
             out.stride(0))
+    # every block (no selection, no window): split over workgroups, partials in a workspace
+    dense = sel is None and int(window) == 0
+    ws_ptr, ws_bytes, ws = _dense_split_ws(B, Hq, Hkv, D, max_len, block_size, dev) if dense else (None, 0, None)
     if prefetch is None:
-        call("sparda_decode_at", *args, _stream(dev))
+        call("sparda_decode_at", *args, ws_ptr, ws_bytes, _stream(dev))
     else:
         pf, keep = _prefetch_args(prefetch, B, Hkv, D, block_size, dev)
-        call("sparda_decode_at_prefetch", *args, ctypes.byref(pf), _stream(dev))
+        call("sparda_decode_at_prefetch", *args, ctypes.byref(pf), ws_ptr, ws_bytes, _stream(dev))
         del keep
+    del ws
     return out
 
 

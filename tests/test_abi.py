@@ -124,6 +124,19 @@ def test_decode_workspace_size_formula():
     assert sparda.decode_workspace_bytes(B, S, Hq, Hkv, D, bs, k) == want
 
 
+def test_dense_decode_split_workspace_size():
+    # four blocks per split (more past 4096 splits per (sequence, KV head));
+    # each split's partial is (m, l, o[D]) fp32 for each of the R heads
+    lib = sparda.load()
+    B, Hq, Hkv, D, bs = 1, 12, 4, 64, 64
+    per_split = B * Hkv * (Hq // Hkv) * (D + 2) * 4
+    assert lib.sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, 32768, bs) == 128 * per_split  # 512 blocks
+    assert lib.sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, 8 * 64 + 1, bs) == 3 * per_split  # 9 blocks
+    assert lib.sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, 4 * 64, bs) == 0  # one split: none
+    assert lib.sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, 1 << 20, bs) == 4096 * per_split  # 16384 blocks
+    assert lib.sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, 1 << 21, bs) == 4096 * per_split  # the cap
+
+
 def test_offload_and_selected_decode_argument_errors():
     import ctypes
     P = 4096
@@ -135,13 +148,15 @@ def test_offload_and_selected_decode_argument_errors():
     _expect(-7, "sparda_offload_append", None, P, P, 1, 1, 1, 0, 1, 64, None, None)
     _expect(-7, "sparda_offload_fetch", None, P, P, 10, 64, 100, 0, P, P, None)
     _expect(-1, "sparda_decode_selected", None, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, None, None, 0, 0,
-            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None, 0, None)
     _expect(-6, "sparda_decode_selected", P, 1, 1, P, P, 8, 8, 8, 1, 1, None, None, 0, None, None, 0, 0,
-            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)  # compact without a selection
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None, 0, None)  # compact without a selection
     _expect(-2, "sparda_decode_selected", P, 1, 1, P, P, 8, 8, 8, 1, 0, P, P, 40, None, None, 0, 0,
-            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)  # sel_cap > 34
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None, 0, None)  # sel_cap > 34
     _expect(-5, "sparda_decode_selected", P, 1, 1, P + 2, P, 8, 8, 8, 1, 0, None, None, 0, None, None, 0, 0,
-            1, 100, 12, 4, 64, 64, 0.125, P, 1, None)  # misaligned K
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, None, 0, None)  # misaligned K
+    _expect(-4, "sparda_decode_selected", P, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, None, None, 0, 0,
+            1, 100, 12, 4, 64, 64, 0.125, P, 1, P + 4, 4096, None)  # misaligned workspace
     _expect(-2, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 50, 64, 8, 1, 0.125, P, P, 10,
             None)  # pos < len - 1
     _expect(-2, "sparda_select_decode", P, 1, 1, 1, P, 1, 4, 64, 64, 100, 100, 64, 8, 1, 0.125, P, P, 9,
@@ -198,17 +213,17 @@ def test_device_position_entry_argument_errors():
     # decode_at: q, q_sb, q_sh, k, v, kv_sb, kv_ss, kv_sh, dtype, compact, sel, n_sel, sel_cap, window_k,
     #            k_new, v_new, new_sb, new_sh, B, max_len, pos_dev, Hq, Hkv, D, bs, scale, out, out_sb, stream
     _expect(-1, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, 8, None, None, 0, 0, 1, 100, None,
-            12, 4, 64, 64, 0.125, P, 1, None)
+            12, 4, 64, 64, 0.125, P, 1, None, 0, None)
     _expect(-6, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, P, P, 10, 8, None, None, 0, 0, 1, 100, Q, 12, 4,
-            64, 64, 0.125, P, 1, None)  # a list and a window
+            64, 64, 0.125, P, 1, None, 0, None)  # a list and a window
     _expect(-6, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 1, None, None, 0, 8, None, None, 0, 0, 1, 100, Q,
-            12, 4, 64, 64, 0.125, P, 1, None)  # compact buffers without a selection
+            12, 4, 64, 64, 0.125, P, 1, None, 0, None)  # compact buffers without a selection
     _expect(-1, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, P, P, 10, 0, P, None, 8, 8, 1, 100, Q, 12, 4,
-            64, 64, 0.125, P, 1, None)  # k_new without v_new
+            64, 64, 0.125, P, 1, None, 0, None)  # k_new without v_new
     _expect(-2, "sparda_decode_at", P, 1, 1, P, P, 8, 8, 8, 1, 0, None, None, 0, 33, None, None, 0, 0, 1, 100, Q,
-            12, 4, 64, 64, 0.125, P, 1, None)  # window > 32
+            12, 4, 64, 64, 0.125, P, 1, None, 0, None)  # window > 32
     _expect(-5, "sparda_decode_at", P, 1, 1, P + 2, P, 8, 8, 8, 1, 0, None, None, 0, 8, None, None, 0, 0, 1, 100,
-            Q, 12, 4, 64, 64, 0.125, P, 1, None)  # misaligned K
+            Q, 12, 4, 64, 64, 0.125, P, 1, None, 0, None)  # misaligned K
     # offload entries at a device position (handle checks come first)
     _expect(-7, "sparda_offload_fetch_at", None, P, P, 10, 64, Q, P, P, None)
     _expect(-7, "sparda_offload_append_at", None, P, P, 256, 64, Q, 64, P, None)

@@ -63,6 +63,53 @@ def test_decode_selected_dense_any_length(S):
     assert_close_out(np32(out), want, torch.bfloat16)
 
 
+@pytest.mark.parametrize("bs", [64, 32])
+def test_dense_decode_split_over_workgroups(bs):
+    """The dense decode split over workgroups (flash-decoding partials in a
+    workspace, merged by a second launch) against the one-workgroup form
+    through the C ABI and against the oracle; then decode_at at short
+    positions of a long cache, where most splits hold no block."""
+    from sparda._lib import call
+    B, S, Hq, Hkv, D = 2, 9000, 12, 4, 64
+    case(f"dense decode split bs={bs} B={B} S={S}")
+    x = synth.decode_inputs(B, S, Hq, Hkv, D, dtype=torch.bfloat16, seed=24 + bs)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    q, kc, vc = d["q"], d["k_cache"], d["v_cache"]
+    nbytes = sparda.load().sparda_decode_dense_workspace_bytes(B, Hq, Hkv, D, S, bs)
+    assert nbytes > 0
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=DEV)
+    outs = {}
+    for name, (wp, wb) in {"one": (None, 0), "split": (ws.data_ptr(), nbytes)}.items():
+        o = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=DEV)
+        kv_sb, kv_ss, kv_sh, _ = kc.stride()
+        call("sparda_decode_selected", q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
+                    kv_sb, kv_ss, kv_sh, 1, 0, None, None, 0, None, None, 0, 0, B, S, Hq, Hkv, D, bs,
+                    D ** -0.5, o.data_ptr(), o.stride(0), wp, wb, torch.cuda.current_stream().cuda_stream)
+        outs[name] = o
+    torch.cuda.synchronize()
+    NB = (S + bs - 1) // bs
+    sel = np.arange(NB, dtype=np.int32).reshape(1, 1, NB).repeat(Hkv, axis=1).repeat(B, axis=0)
+    n = np.full((B, Hkv), NB, np.int32)
+    want = O.attention_decode(np32(x["q"]), np32(x["k_cache"]), np32(x["v_cache"]), S, sel, n, bs)
+    for o in outs.values():
+        assert_close_out(np32(o), want, torch.bfloat16)
+    # the two forms differ only in the order partial sums are combined
+    diff = (outs["one"].float() - outs["split"].float()).abs().max().item()
+    assert diff <= 4e-3, diff
+    # positions of a cache of 9000 rows: the split count follows max_len, the
+    # blocks the position (splits past the last block hold none)
+    for p in (0, 5, bs - 1, bs, 3 * bs + 7, 700, S - 1):
+        case(f"dense decode_at split bs={bs} p={p}")
+        pos = torch.tensor([p], dtype=torch.int64, device=DEV)
+        o = sparda.decode_at(q, kc, vc, pos, bs, window=0)
+        torch.cuda.synchronize()
+        nb = p // bs + 1
+        sel_p = np.arange(nb, dtype=np.int32).reshape(1, 1, nb).repeat(Hkv, axis=1).repeat(B, axis=0)
+        want_p = O.attention_decode(np32(x["q"]), np32(x["k_cache"]), np32(x["v_cache"]), p + 1, sel_p,
+                                    np.full((B, Hkv), nb, np.int32), bs)
+        assert_close_out(np32(o), want_p, torch.bfloat16)
+
+
 def test_decode_selected_new_token_override_and_invalid_slots():
     case("decode_selected k_new override, skipped blocks")
     B, S, Hq, Hkv, D, bs = 2, 700, 12, 4, 64, 64
