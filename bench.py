@@ -346,8 +346,10 @@ def bench_offload(args, torch, sparda, synth):
     dev = torch.device("cuda")
     W, K = 4, args.offload_steps
     cap = OB_CTX + 8 * (W + K) + 64
+    # the fused producer and decode FFN, as the generation leg uses them
     cfg = ModelConfig(n_layer=OB_LAYERS, context_length=cap, block_size=BS, top_k_blocks=TOPK,
-                      decode_routing="absolute", attention_backend="async_offload", norm_eps=1e-5)
+                      decode_routing="absolute", attention_backend="async_offload", norm_eps=1e-5,
+                      fused_producer=True, fused_ffn=True)
     torch.manual_seed(1004)
     model = SparDAResearchModel(cfg).to(dev, torch.bfloat16).eval()
     res_cfg = ModelConfig(**{**cfg.__dict__, "attention_backend": "hip_sparse"})
@@ -543,8 +545,9 @@ def bench_offload(args, torch, sparda, synth):
         "workload": f"decode with offloaded KV: {OB_LAYERS} layers, B=1, context {OB_CTX} (512 blocks of 64), "
                     f"bf16 KV [32768,4,64] per layer in pinned host memory for layers 1..{OB_LAYERS - 1} "
                     "(layer 0 GPU-resident), top-8 + sink + current blocks prefetched per layer (eager: on a side "
-                    "stream; replayed: carried by the previous layer's attention launch, or on a side stream, or "
-                    "serial); step = one token through the 12-layer model incl. LM head",
+                    "stream; replayed: carried by the previous layer's append and attention launches, or on a side "
+                    "stream, or serial); fused producer and decode FFN; step = one token through the 12-layer model "
+                    "incl. LM head",
         "us_per_step_async": round(us_async, 1),
         "us_per_step_sync": round(us_sync, 1),
         "us_per_step_async_dma": round(us_async_dma, 1),

@@ -687,6 +687,9 @@ typedef struct sparda_prefetch_args {
     int stage;   /* 0: selection and copy; 1: the selection only (into sel / n_sel);
                     2: the copy only, of the selection in sel / n_sel (left there by a
                     stage-1 launch earlier on the stream; forecast and block_sums unused) */
+    int parts;   /* stage 2: the copy in `parts` shares (0 or 1: all of it), of which
+                    this launch copies share `part`: the slots s with s % parts == part */
+    int part;
 } sparda_prefetch_args;
 
 /*
@@ -715,6 +718,23 @@ SPARDA_API int sparda_decode_at_prefetch(const void* q, int64_t q_sb, int64_t q_
                                          int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, float scale,
                                          void* out, int64_t out_sb, const sparda_prefetch_args* next,
                                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * sparda_ffn_decode (same arguments, same result) whose two launches also
+ * carry a share of the next layer's prefetch copy: gate_up_next and
+ * down_next (either may be NULL) are stage-2 prefetch arguments (the copy of
+ * the selection a stage-1 launch left in sel / n_sel) with `parts` / `part`
+ * naming the share, at position p = *pos_dev (the arena length p, as in
+ * sparda_decode_at_prefetch); block_size: the arena's blocks. The arenas'
+ * batch must be M (one row per sequence). No counterpart in the reference:
+ * it spreads the copy that transformer.py:110-115 issues on a transfer
+ * stream over the attention and feed-forward launches of the same layer.
+ */
+SPARDA_API int sparda_ffn_decode_prefetch(const void* x, int64_t x_stride_row, const void* w_gate_up,
+                                          const void* w_down, int64_t M, int64_t C, int64_t F, float eps, void* act,
+                                          void* out, int64_t out_stride_row, const sparda_prefetch_args* gate_up_next,
+                                          const sparda_prefetch_args* down_next, const int64_t* pos_dev,
+                                          int64_t block_size, void* stream);
 SPARDA_API int sparda_offload_append_at(sparda_offload_t h, const void* k, const void* v, int64_t new_sb,
                                         int64_t new_sh, const int64_t* pos_dev, int64_t block_size,
                                         float* block_sums, void* stream);

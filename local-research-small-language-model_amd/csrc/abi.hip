@@ -452,6 +452,9 @@ static int prefetch_dev(const sparda_prefetch_args* next, int64_t B, int64_t Hkv
     SPARDA_REQUIRE(n.stage == 2 || (n.forecast && n.block_sums), SPARDA_ERR_NULL, "%s: null forecast / block_sums",
                    who);
     SPARDA_REQUIRE(n.stage == 1 || (n.k_dst && n.v_dst), SPARDA_ERR_NULL, "%s: null destinations", who);
+    SPARDA_REQUIRE(n.parts >= 0 && n.parts <= kMaxSelCap && (n.parts <= 1 ? n.part == 0 : n.part >= 0 && n.part < n.parts),
+                   SPARDA_ERR_SHAPE, "%s: copy share %d of %d", who, n.part, n.parts);
+    SPARDA_REQUIRE(n.parts <= 1 || n.stage == 2, SPARDA_ERR_MODE, "%s: a share of the copy needs stage 2", who);
     SPARDA_REQUIRE(D == 64 && dtype == SPARDA_BF16, SPARDA_ERR_MODE, "%s: a carried prefetch needs bf16, D=64", who);
     SPARDA_REQUIRE(offload_batch(n.arena) == B && offload_heads(n.arena) == Hkv && offload_head_dim(n.arena) == D &&
                        offload_dtype(n.arena) == dtype,
@@ -489,6 +492,8 @@ static int prefetch_dev(const sparda_prefetch_args* next, int64_t B, int64_t Hkv
     pf->dk = static_cast<char*>(n.k_dst);
     pf->dv = static_cast<char*>(n.v_dst);
     pf->stage = n.stage;
+    pf->parts = n.parts >= 1 ? n.parts : 1;
+    pf->part = n.parts >= 1 ? n.part : 0;
     offload_prefetch_dev(n.arena, pf);
     return 0;
 }
@@ -691,6 +696,44 @@ SPARDA_API int sparda_ffn_decode(const void* x, int64_t x_stride_row, const void
                    SPARDA_ERR_STRIDE, "ffn_decode: rows and weights must be 16-byte aligned");
     return launch_ffn_decode(x, x_stride_row, w_gate_up, w_down, M, C, F, eps, act, out, out_stride_row,
                              static_cast<hipStream_t>(stream));
+}
+
+SPARDA_API int sparda_ffn_decode_prefetch(const void* x, int64_t x_stride_row, const void* w_gate_up,
+                                          const void* w_down, int64_t M, int64_t C, int64_t F, float eps, void* act,
+                                          void* out, int64_t out_stride_row, const sparda_prefetch_args* gate_up_next,
+                                          const sparda_prefetch_args* down_next, const int64_t* pos_dev,
+                                          int64_t block_size, void* stream) {
+    SPARDA_REQUIRE(gate_up_next || down_next, SPARDA_ERR_NULL, "ffn_decode_prefetch: no prefetch arguments");
+    SPARDA_REQUIRE(pos_dev && (reinterpret_cast<uintptr_t>(pos_dev) & 7u) == 0, SPARDA_ERR_NULL,
+                   "ffn_decode_prefetch: pos_dev must be a non-null, 8-byte aligned int64");
+    SPARDA_REQUIRE(x && w_gate_up && w_down && act && out, SPARDA_ERR_NULL, "ffn_decode_prefetch: null pointer");
+    SPARDA_REQUIRE(M >= 1 && M <= 16, SPARDA_ERR_SHAPE, "ffn_decode_prefetch: %lld rows (decode batches of 1..16)",
+                   (long long)M);
+    SPARDA_REQUIRE(C >= 128 && C % 128 == 0 && C <= 1024, SPARDA_ERR_SHAPE,
+                   "ffn_decode_prefetch: model width %lld must be a multiple of 128 up to 1024", (long long)C);
+    SPARDA_REQUIRE(F >= 128 && F % 128 == 0 && F <= 2048, SPARDA_ERR_SHAPE,
+                   "ffn_decode_prefetch: hidden width %lld must be a multiple of 128 up to 2048", (long long)F);
+    SPARDA_REQUIRE(x_stride_row >= C && x_stride_row % 8 == 0 && out_stride_row >= C && out_stride_row % 8 == 0 &&
+                       aligned16(x) && aligned16(w_gate_up) && aligned16(w_down) && aligned16(act) && aligned16(out),
+                   SPARDA_ERR_STRIDE, "ffn_decode_prefetch: rows and weights must be 16-byte aligned");
+    // the copy (stage 2) uses no position bound: max_len 1 passes the selection's checks
+    PrefetchDev pg, pd;
+    int64_t heads = 0;
+    for (int i = 0; i < 2; ++i) {
+        const sparda_prefetch_args* n = i == 0 ? gate_up_next : down_next;
+        if (!n) continue;
+        SPARDA_REQUIRE(n->stage == 2, SPARDA_ERR_MODE, "ffn_decode_prefetch: the carried prefetch must be stage 2");
+        SPARDA_REQUIRE(n->arena, SPARDA_ERR_HANDLE, "ffn_decode_prefetch: null arena handle");
+        const int64_t h = offload_heads(n->arena);
+        SPARDA_REQUIRE(heads == 0 || h == heads, SPARDA_ERR_SHAPE, "ffn_decode_prefetch: the two arenas' heads differ");
+        heads = h;
+        const int rc = prefetch_dev(n, M, h, 64, SPARDA_BF16, 1, block_size, "ffn_decode_prefetch",
+                                    i == 0 ? &pg : &pd);
+        if (rc) return rc;
+    }
+    return launch_ffn_decode(x, x_stride_row, w_gate_up, w_down, M, C, F, eps, act, out, out_stride_row,
+                             static_cast<hipStream_t>(stream), gate_up_next ? &pg : nullptr,
+                             down_next ? &pd : nullptr, M * heads, pos_dev);
 }
 
 SPARDA_API int sparda_norm_gemv(const void* x, int64_t x_stride_row, const void* w, int64_t M, int64_t C,

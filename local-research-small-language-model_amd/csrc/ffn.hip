@@ -18,6 +18,7 @@
 // the gate/up launch also forms sum(x^2) for 1/rms from the same x slices.
 #include "common.h"
 #include "kernels.h"
+#include "prefetch.h"
 #include "rows.h"
 
 namespace sparda {
@@ -26,10 +27,26 @@ constexpr int kFfnThreads = kRowsWaves * kWave;
 
 __device__ __forceinline__ float bf16_round(float v) { return static_cast<float>(static_cast<__bf16>(v)); }
 
+// Both launches may carry a share of the next layer's prefetch copy (stage 2):
+// workgroups n_out, n_out + 1, ... copy it for (sequence, KV head) = the
+// index past n_out, beside the product workgroups.
+#define SPARDA_CARRIED_COPY()                                                                          \
+    do {                                                                                               \
+        if (static_cast<int>(blockIdx.x) >= n_out) {                                                  \
+            __shared__ int32_t pf_sel[kMaxSelCap];                                                     \
+            const int idx = static_cast<int>(blockIdx.x) - n_out;                                      \
+            prefetch_copy_workgroup(pf, static_cast<int>(idx % pf.H), static_cast<int>(idx / pf.H), pos_dev, \
+                                    pf_sel);                                                           \
+            return;                                                                                    \
+        }                                                                                              \
+    } while (0)
+
 // grid F/16: act[m, f] for 16 columns f per workgroup
 __global__ void __launch_bounds__(kFfnThreads)
 ffn_gate_up_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t* __restrict__ wgu, int M, int C,
-                   int F, float eps, uint16_t* __restrict__ act) {
+                   int F, float eps, uint16_t* __restrict__ act, int n_out, PrefetchDev pf,
+                   const int64_t* __restrict__ pos_dev) {
+    SPARDA_CARRIED_COPY();
     __shared__ RowsRed<2> red;
     __shared__ float y[2][kRowsMaxM][16];
     __shared__ float rs[16];
@@ -55,7 +72,9 @@ ffn_gate_up_kernel(const uint16_t* __restrict__ x, int64_t x_st, const uint16_t*
 // grid N/16: out[m, n] = bf16(res[m, n] + bf16(a[m, :] . W[n, :])), W [N, K]
 __global__ void __launch_bounds__(kFfnThreads)
 ffn_down_kernel(const uint16_t* __restrict__ a, int64_t a_st, const uint16_t* __restrict__ w, int M, int K, int N,
-                const uint16_t* __restrict__ res, int64_t res_st, uint16_t* __restrict__ out, int64_t out_st) {
+                const uint16_t* __restrict__ res, int64_t res_st, uint16_t* __restrict__ out, int64_t out_st,
+                int n_out, PrefetchDev pf, const int64_t* __restrict__ pos_dev) {
+    SPARDA_CARRIED_COPY();
     __shared__ RowsRed<1> red;
     __shared__ float y[1][kRowsMaxM][16];
     const int tid = threadIdx.x;
@@ -75,17 +94,24 @@ ffn_down_kernel(const uint16_t* __restrict__ a, int64_t a_st, const uint16_t* __
 }
 
 int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const void* w_down, int64_t M,
-                      int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream) {
-    hipLaunchKernelGGL(ffn_gate_up_kernel, dim3(static_cast<unsigned>(F / 16)), dim3(kFfnThreads), 0, stream,
-                       static_cast<const uint16_t*>(x), x_st, static_cast<const uint16_t*>(w_gate_up),
-                       static_cast<int>(M), static_cast<int>(C), static_cast<int>(F), eps,
-                       static_cast<uint16_t*>(act));
+                      int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream,
+                      const PrefetchDev* pf_gate_up, const PrefetchDev* pf_down, int64_t pf_groups,
+                      const int64_t* pos_dev) {
+    const int n_gu = static_cast<int>(F / 16), n_dn = static_cast<int>(C / 16);
+    const PrefetchDev none{};
+    hipLaunchKernelGGL(ffn_gate_up_kernel,
+                       dim3(static_cast<unsigned>(n_gu + (pf_gate_up != nullptr ? pf_groups : 0))),
+                       dim3(kFfnThreads), 0, stream, static_cast<const uint16_t*>(x), x_st,
+                       static_cast<const uint16_t*>(w_gate_up), static_cast<int>(M), static_cast<int>(C),
+                       static_cast<int>(F), eps, static_cast<uint16_t*>(act), n_gu,
+                       pf_gate_up != nullptr ? *pf_gate_up : none, pos_dev);
     int rc = check_hip(hipGetLastError(), "ffn_gate_up_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(C / 16)), dim3(kFfnThreads), 0, stream,
-                       static_cast<const uint16_t*>(act), F, static_cast<const uint16_t*>(w_down),
-                       static_cast<int>(M), static_cast<int>(F), static_cast<int>(C),
-                       static_cast<const uint16_t*>(x), x_st, static_cast<uint16_t*>(out), out_st);
+    hipLaunchKernelGGL(ffn_down_kernel, dim3(static_cast<unsigned>(n_dn + (pf_down != nullptr ? pf_groups : 0))),
+                       dim3(kFfnThreads), 0, stream, static_cast<const uint16_t*>(act), F,
+                       static_cast<const uint16_t*>(w_down), static_cast<int>(M), static_cast<int>(F),
+                       static_cast<int>(C), static_cast<const uint16_t*>(x), x_st, static_cast<uint16_t*>(out),
+                       out_st, n_dn, pf_down != nullptr ? *pf_down : none, pos_dev);
     return check_hip(hipGetLastError(), "ffn_down_kernel");
 }
 
@@ -128,7 +154,7 @@ int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, 
                        static_cast<const uint16_t*>(a), a_st,
                        static_cast<const uint16_t*>(w), static_cast<int>(M), static_cast<int>(K),
                        static_cast<int>(N), static_cast<const uint16_t*>(res), res_st, static_cast<uint16_t*>(out),
-                       out_st);
+                       out_st, static_cast<int>(N / 16), PrefetchDev{}, nullptr);
     return check_hip(hipGetLastError(), "ffn_down_kernel");
 }
 

@@ -61,8 +61,14 @@ int launch_norm_gemv(const void* x, int64_t x_st, const void* w, int64_t M, int6
 // out[m] = bf16(res[m] + bf16(a[m] . W^T)) for M <= 16 rows: W [N, K] bf16, K <= 2048
 int launch_rows_residual(const void* a, int64_t a_st, const void* w, int64_t M, int64_t K, int64_t N,
                          const void* res, int64_t res_st, void* out, int64_t out_st, hipStream_t stream);
+struct PrefetchDev;
+// pf_gate_up / pf_down (optional): a share of the next layer's prefetch copy
+// (stage 2) carried by the gate/up and the down launch, pf_groups = B * Hkv
+// workgroups each after the product workgroups
 int launch_ffn_decode(const void* x, int64_t x_st, const void* w_gate_up, const void* w_down, int64_t M,
-                      int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream);
+                      int64_t C, int64_t F, float eps, void* act, void* out, int64_t out_st, hipStream_t stream,
+                      const PrefetchDev* pf_gate_up = nullptr, const PrefetchDev* pf_down = nullptr,
+                      int64_t pf_groups = 0, const int64_t* pos_dev = nullptr);
 
 int launch_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb,
                         int64_t k_st, int64_t k_sh, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int causal,
@@ -155,6 +161,7 @@ struct PrefetchDev {
     char* dk;               // compact buffers [B][H][cap][bs][row_bytes] each
     char* dv;
     int stage;
+    int parts, part;        // the copy of the slots s with s % parts == part (parts >= 1)
 };
 // the arena fields of a PrefetchDev (ak, av, H, Smax, row_bytes)
 void offload_prefetch_dev(sparda_offload_t h, PrefetchDev* pf);

@@ -65,21 +65,74 @@ __device__ __forceinline__ int select_from_sums(const void* f, bool f_bf16, int6
     return *m_lds;
 }
 
+// The copy of (b, g)'s selected blocks (m slots of sel_lds, rows below the
+// arena length p = *pos_dev clamped into [0, Smax]) from the arena into the
+// compact slots: share pf.part of pf.parts, the slots s with s % parts ==
+// part. Wavefront w copies the share's slots w, w + nwaves, ...: 2 x 8
+// sixteen-byte loads in flight per lane for a 64 x 128-byte block of K and of V.
+__device__ __forceinline__ void prefetch_copy(const PrefetchDev& pf, int64_t bg, int64_t p, const int32_t* sel_lds,
+                                             int m) {
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int nwaves = static_cast<int>(blockDim.x) / kWave;
+    const int64_t len = p < 0 ? 0 : (p > pf.Smax ? pf.Smax : p);
+    constexpr int kIn = 8;  // 16-byte chunks of K (and of V) in flight per lane
+    const int parts = pf.parts >= 1 ? pf.parts : 1;  // (the host passes parts >= 1, part < parts)
+    const int part = pf.part >= 0 && pf.part < parts ? pf.part : 0;
+    for (int i = wave;; i += nwaves) {
+        const int slot = part + parts * i;
+        if (slot >= m || slot >= pf.cap) break;
+        const int64_t j = sel_lds[slot];
+        if (j < 0 || j * pf.bs >= len) continue;
+        const int64_t rows = (j + 1) * pf.bs < len ? pf.bs : len - j * pf.bs;
+        const int64_t chunks = rows * pf.row_bytes / 16;
+        const pf_u32x4* sk = reinterpret_cast<const pf_u32x4*>(pf.ak + (bg * pf.Smax + j * pf.bs) * pf.row_bytes);
+        const pf_u32x4* sv = reinterpret_cast<const pf_u32x4*>(pf.av + (bg * pf.Smax + j * pf.bs) * pf.row_bytes);
+        pf_u32x4* tk = reinterpret_cast<pf_u32x4*>(pf.dk + (bg * pf.cap + slot) * pf.bs * pf.row_bytes);
+        pf_u32x4* tv = reinterpret_cast<pf_u32x4*>(pf.dv + (bg * pf.cap + slot) * pf.bs * pf.row_bytes);
+        for (int c0 = lane; c0 < chunks; c0 += kIn * kWave) {
+            // chunks past the block's rows re-read its last chunk (in bounds) and are not stored
+            pf_u32x4 kr[kIn], vr[kIn];
+#pragma unroll
+            for (int i2 = 0; i2 < kIn; ++i2) {
+                const int c = c0 + i2 * kWave < chunks ? c0 + i2 * kWave : static_cast<int>(chunks) - 1;
+                kr[i2] = sk[c];
+                vr[i2] = sv[c];
+            }
+#pragma unroll
+            for (int i2 = 0; i2 < kIn; ++i2) {
+                const int c = c0 + i2 * kWave;
+                if (c < chunks) {
+                    tk[c] = kr[i2];
+                    tv[c] = vr[i2];
+                }
+            }
+        }
+    }
+}
+
+// The selection an earlier launch of the stream wrote for (b, g), into
+// sel_lds (every thread calls it; it synchronises the workgroup); returns its
+// length, clamped into [0, cap].
+__device__ __forceinline__ int prefetch_read_selection(const PrefetchDev& pf, int64_t bg, int32_t* sel_lds) {
+    int m = pf.n_sel[bg];
+    m = m < 0 ? 0 : (m > pf.cap ? pf.cap : m);
+    for (int i = static_cast<int>(threadIdx.x); i < m; i += static_cast<int>(blockDim.x))
+        sel_lds[i] = pf.sel[bg * pf.cap + i];
+    __syncthreads();
+    return m;
+}
+
 // The prefetch of (b, g) by one workgroup: the selection with lookahead at
 // token p = *pos_dev (len = p: the blocks before the token is appended), its
-// list written to pf.sel / pf.n_sel, then the selected blocks (rows below p)
-// copied from the arena into the compact slots. Wavefront w copies slots
-// w, w + nwaves, ...: 2 x 8 sixteen-byte loads in flight per lane for a
-// 64 x 128-byte block of K and of V. Stage 1 stops after the selection;
-// stage 2 copies the selection found in pf.sel / pf.n_sel.
+// list written to pf.sel / pf.n_sel, then the selected blocks copied
+// (prefetch_copy). Stage 1 stops after the selection; stage 2 copies the
+// selection found in pf.sel / pf.n_sel.
 template <int CHMAX, int DH>
 __device__ __forceinline__ void prefetch_workgroup(const PrefetchDev& pf, int g, int b, const int64_t* pos_dev,
                                                    float* f_lds, uint32_t* key_lds, int32_t* sel_lds,
                                                    uint32_t* ck_lds, int32_t* ci_lds, int* m_lds) {
     const int tid = static_cast<int>(threadIdx.x);
-    const int lane = tid % kWave;
-    const int wave = tid / kWave;
-    const int nwaves = static_cast<int>(blockDim.x) / kWave;
     const int64_t bg = static_cast<int64_t>(b) * pf.H + g;
     const int64_t p = *pos_dev;
     int m;
@@ -101,44 +154,18 @@ __device__ __forceinline__ void prefetch_workgroup(const PrefetchDev& pf, int g,
         if (tid == 0) pf.n_sel[bg] = m;
         if (pf.stage == 1) return;
     } else {
-        // the selection an earlier launch of the stream wrote
-        m = pf.n_sel[bg];
-        m = m < 0 ? 0 : (m > pf.cap ? pf.cap : m);
-        for (int i = tid; i < m; i += static_cast<int>(blockDim.x)) sel_lds[i] = pf.sel[bg * pf.cap + i];
-        __syncthreads();
+        m = prefetch_read_selection(pf, bg, sel_lds);
     }
+    prefetch_copy(pf, bg, p, sel_lds, m);
+}
 
-    // the copy: arena length p, clamped into [0, Smax] (the gather kernel's rule)
-    const int64_t len = p < 0 ? 0 : (p > pf.Smax ? pf.Smax : p);
-    constexpr int kIn = 8;  // 16-byte chunks of K (and of V) in flight per lane
-    for (int slot = wave; slot < m && slot < pf.cap; slot += nwaves) {
-        const int64_t j = sel_lds[slot];
-        if (j < 0 || j * pf.bs >= len) continue;
-        const int64_t rows = (j + 1) * pf.bs < len ? pf.bs : len - j * pf.bs;
-        const int64_t chunks = rows * pf.row_bytes / 16;
-        const pf_u32x4* sk = reinterpret_cast<const pf_u32x4*>(pf.ak + (bg * pf.Smax + j * pf.bs) * pf.row_bytes);
-        const pf_u32x4* sv = reinterpret_cast<const pf_u32x4*>(pf.av + (bg * pf.Smax + j * pf.bs) * pf.row_bytes);
-        pf_u32x4* tk = reinterpret_cast<pf_u32x4*>(pf.dk + (bg * pf.cap + slot) * pf.bs * pf.row_bytes);
-        pf_u32x4* tv = reinterpret_cast<pf_u32x4*>(pf.dv + (bg * pf.cap + slot) * pf.bs * pf.row_bytes);
-        for (int c0 = lane; c0 < chunks; c0 += kIn * kWave) {
-            // chunks past the block's rows re-read its last chunk (in bounds) and are not stored
-            pf_u32x4 kr[kIn], vr[kIn];
-#pragma unroll
-            for (int i = 0; i < kIn; ++i) {
-                const int c = c0 + i * kWave < chunks ? c0 + i * kWave : static_cast<int>(chunks) - 1;
-                kr[i] = sk[c];
-                vr[i] = sv[c];
-            }
-#pragma unroll
-            for (int i = 0; i < kIn; ++i) {
-                const int c = c0 + i * kWave;
-                if (c < chunks) {
-                    tk[c] = kr[i];
-                    tv[c] = vr[i];
-                }
-            }
-        }
-    }
+// A launch that carries only a share of the copy (stage 2): (b, g)'s selection
+// from pf.sel / pf.n_sel, then its share of the blocks. Needs kMaxSelCap ints of LDS.
+__device__ __forceinline__ void prefetch_copy_workgroup(const PrefetchDev& pf, int g, int b, const int64_t* pos_dev,
+                                                        int32_t* sel_lds) {
+    const int64_t bg = static_cast<int64_t>(b) * pf.H + g;
+    const int m = prefetch_read_selection(pf, bg, sel_lds);
+    prefetch_copy(pf, bg, *pos_dev, sel_lds, m);
 }
 
 }  // namespace sparda

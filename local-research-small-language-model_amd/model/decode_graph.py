@@ -178,9 +178,11 @@ class GraphDecoder:
         return self.kinds[i] == _SPARSE and a.mode not in ("dense", "static") and f is not None
 
     def _attend(self, i: int, a, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                f: Optional[torch.Tensor], carry=None) -> torch.Tensor:
+                f: Optional[torch.Tensor], carry=None, parts: int = 1) -> torch.Tensor:
         """Layer i's append and attention; carry = (j, f_i): layer j's prefetch
-        for this step, carried by the attention launch."""
+        for this step, carried by the attention launch (on an offloaded layer:
+        its selection by the append launch, share 0 of `parts` of its copy by
+        the attention launch)."""
         bs = self.block_size
         cache = self.caches[i]
         kind = self.kinds[i]
@@ -194,7 +196,7 @@ class GraphDecoder:
                                   prefetch=None if nxt is None else {**nxt, "stage": 1}, max_len=self.max_len)
             return sparda.decode_at(q, pf["k"], pf["v"], self.pos, bs, pf["sel"], pf["n"], max_len=self.max_len,
                                     compact=True, k_new=k[:, 0], v_new=v[:, 0],
-                                    prefetch=None if nxt is None else {**nxt, "stage": 2})
+                                    prefetch=None if nxt is None else {**nxt, "stage": 2, "parts": parts, "part": 0})
         if kind == _RESIDENT_DENSE:
             sparda.append_at(cache.k, cache.v, self.pos, bs, None, k, v)
             return sparda.decode_at(q, cache.k, cache.v, self.pos, bs, window=0, max_len=self.max_len,
@@ -256,9 +258,10 @@ class GraphDecoder:
                 else:
                     self._prefetch(i + 1, f)
                     ev.record(main)
-            out = self._attend(i, a, q[:, 0], k, v, prev_f, carry)
-            if carry is not None:
-                self._pf[i + 1]["ev"].record(main)
+            # an offloaded layer with the fused feed-forward spreads the carried
+            # copy over its attention and both feed-forward launches
+            parts = 3 if (carry is not None and self.kinds[i] == _OFFLOAD and layer._use_fused_ffn(x)) else 1
+            out = self._attend(i, a, q[:, 0], k, v, prev_f, carry, parts)
             if i in self._taps:
                 t = dict(q=q[:, 0], f=prev_f, out=out)
                 if self.kinds[i] == _OFFLOAD:
@@ -268,7 +271,16 @@ class GraphDecoder:
                 x = sparda.rows_residual(out.view(B, 1, a.n_head * a.head_dim), a.wo.weight, x)
             else:
                 x = x + a.wo(out.view(B, 1, a.n_head * a.head_dim))
-            x = layer.ffn_residual(x)
+            if parts > 1:
+                nxt = self._prefetch_spec(*carry)
+                x = sparda.ffn_decode(x, layer._fused_ffn_weight(), layer.ffn.w_down.weight, layer.ffn_norm.eps,
+                                      prefetch=tuple({**nxt, "stage": 2, "parts": parts, "part": p}
+                                                     for p in (1, 2)),
+                                      pos_dev=self.pos, block_size=self.block_size)
+            else:
+                x = layer.ffn_residual(x)
+            if carry is not None:
+                self._pf[i + 1]["ev"].record(main)
             prev_f = f
         self.logits = m.logits(x)[:, -1, :]
         self.pos.add_(1)

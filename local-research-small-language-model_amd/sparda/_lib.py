@@ -48,7 +48,8 @@ class PrefetchArgs(ctypes.Structure):
     sparda_decode_at_prefetch (field order and types as in the header)."""
     _fields_ = [("arena", _p), ("forecast", _p), ("f_dtype", _int), ("f_sb", _i64), ("f_sh", _i64),
                 ("block_sums", _p), ("nb_stride", _i64), ("top_k", _i64), ("routing", _int), ("scale", _f32),
-                ("sel", _p), ("n_sel", _p), ("sel_cap", _i64), ("k_dst", _p), ("v_dst", _p), ("stage", _int)]
+                ("sel", _p), ("n_sel", _p), ("sel_cap", _i64), ("k_dst", _p), ("v_dst", _p), ("stage", _int),
+                ("parts", _int), ("part", _int)]
 
 # name -> (restype, argtypes); mirrors include/sparda.h
 SIGNATURES = {
@@ -109,6 +110,9 @@ SIGNATURES = {
                                   _int, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f32, _p, _p, _p,
                                   _i64, _p]),
     "sparda_ffn_decode": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _i64, _p]),
+    "sparda_ffn_decode_prefetch": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _i64,
+                                          ctypes.POINTER(PrefetchArgs), ctypes.POINTER(PrefetchArgs), _p, _i64,
+                                          _p]),
     "sparda_rows_residual": (_int, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p]),
     "sparda_norm_gemv": (_int, [_p, _i64, _p, _i64, _i64, _i64, _f32, _p, _i64, _p]),
     "sparda_offload_fetch_at": (_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p]),

@@ -665,11 +665,17 @@ def decode_sums(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, forec
 
 
 def ffn_decode(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor, eps: float,
-               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+               out: Optional[torch.Tensor] = None, prefetch: Optional[tuple] = None,
+               pos_dev: Optional[torch.Tensor] = None, block_size: int = 64) -> torch.Tensor:
     """x + SwiGLU(RMSNorm(x)) for decode-sized batches (model/transformer.py:18-31,
     126-129; model/norm.py:15-21): x [B,T,C] bf16 with B*T <= 16, w_gate_up
     [2F, C] = [w_gate; w_up] * norm_weight (folded into the columns), w_down
-    [C, F], all bf16. Returns [B,T,C] bf16."""
+    [C, F], all bf16. Returns [B,T,C] bf16.
+
+    prefetch: (gate_up_spec, down_spec), either None: shares of the next
+    layer's prefetch copy carried by the two launches (sparda_ffn_decode_prefetch),
+    each a decode_at prefetch spec with ``stage`` 2 and ``parts`` / ``part``,
+    at position pos_dev over arenas of block_size-key blocks."""
     dev = require_device(x, w_gate_up, w_down, out)
     _inference_only(x, w_gate_up, w_down)
     if not (x.dtype == w_gate_up.dtype == w_down.dtype == torch.bfloat16):
@@ -687,8 +693,26 @@ def ffn_decode(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor, e
     if out is None:
         out = torch.empty((B, T, C), dtype=torch.bfloat16, device=dev)
     o2 = out.view(B * T, C)
-    call("sparda_ffn_decode", x2.data_ptr(), x2.stride(0), w_gate_up.data_ptr(), w_down.data_ptr(), B * T, C, F,
-         float(eps), act.data_ptr(), o2.data_ptr(), o2.stride(0), _stream(dev))
+    if prefetch is None:
+        call("sparda_ffn_decode", x2.data_ptr(), x2.stride(0), w_gate_up.data_ptr(), w_down.data_ptr(), B * T, C, F,
+             float(eps), act.data_ptr(), o2.data_ptr(), o2.stride(0), _stream(dev))
+        return out
+    if pos_dev is None or T != 1:
+        raise ValueError("sparda: a carried prefetch needs pos_dev and one token per sequence")
+    args, keep = [], []
+    for spec in prefetch:
+        if spec is None:
+            args.append(None)
+            continue
+        if int(spec.get("stage", 0)) != 2:
+            raise ValueError("sparda: the feed-forward launches carry only the copy (stage 2)")
+        pf, k = _prefetch_args(spec, B, spec["arena"].Hkv, spec["arena"].D, block_size, dev)
+        args.append(ctypes.byref(pf))
+        keep.append((pf, k))
+    call("sparda_ffn_decode_prefetch", x2.data_ptr(), x2.stride(0), w_gate_up.data_ptr(), w_down.data_ptr(), B * T,
+         C, F, float(eps), act.data_ptr(), o2.data_ptr(), o2.stride(0), args[0], args[1], _pos_ptr(pos_dev),
+         block_size, _stream(dev))
+    del keep
     return out
 
 
@@ -924,6 +948,9 @@ def _prefetch_args(spec: dict, B: int, Hkv: int, D: int, block_size: int, dev):
     stage = int(spec.get("stage", 0))
     if stage not in (0, 1, 2):
         raise ValueError(f"sparda: prefetch stage must be 0, 1 or 2, got {stage}")
+    parts, part = int(spec.get("parts", 1)), int(spec.get("part", 0))
+    if not (1 <= parts and 0 <= part < parts) or (parts > 1 and stage != 2):
+        raise ValueError(f"sparda: prefetch share {part} of {parts} (shares need stage 2)")
     require_device(f, sums, sel, n_sel, k_dst, v_dst)
     if (arena.B, arena.Hkv, arena.D) != (B, Hkv, D):
         raise ValueError("sparda: the prefetched arena must have the attended layer's batch, KV heads and head dim")
@@ -953,7 +980,7 @@ def _prefetch_args(spec: dict, B: int, Hkv: int, D: int, block_size: int, dev):
     pf = _lib.PrefetchArgs(arena.handle.value, f.data_ptr(), _dtype_code(f), fsb, fsh, sums.data_ptr(), sums.shape[1],
                            int(spec["top_k"]), _lib.ROUTE_ABSOLUTE if routing == "absolute" else _lib.ROUTE_REFERENCE,
                            float(scale), sel.data_ptr(), n_sel.data_ptr(), cap, k_dst.data_ptr(), v_dst.data_ptr(),
-                           stage)
+                           stage, parts, part)
     return pf, (f, sums, sel, n_sel, k_dst, v_dst)
 
 

@@ -173,6 +173,10 @@ def test_prefetch_split_over_the_append_and_attention_launches(routing):
     vc = torch.randn(B, Smax, Hkv, D, generator=g).to(bf).to(DEV)
     nxt = sparda.OffloadArena(B, Smax, Hkv, D, bf)
     nxt.append(kn, vn, 0)
+    C, Fh = 256, 512  # a small feed-forward to carry shares of the copy
+    xf = torch.randn(B, 1, C, generator=g).to(bf).to(DEV)
+    wgu = (torch.randn(2 * Fh, C, generator=g) * 0.05).to(bf).to(DEV)
+    wdn = (torch.randn(C, Fh, generator=g) * 0.05).to(bf).to(DEV)
     cur_a = sparda.OffloadArena(B, Smax, Hkv, D, bf)   # appended to plainly
     cur_b = sparda.OffloadArena(B, Smax, Hkv, D, bf)   # appended to by the launch carrying the selection
     cur_a.append(kc[:, :1500], vc[:, :1500], 0)
@@ -213,6 +217,22 @@ def test_prefetch_split_over_the_append_and_attention_launches(routing):
         assert torch.equal(o_carry, o_plain), f"attention output at {p}"
         assert torch.equal(k2, k1) and torch.equal(v2, v1), f"fetched blocks at {p}"
         assert torch.equal(s2, s1) and torch.equal(n2, n1), "stage 2 leaves the selection"
+        # the copy in three shares: share 0 by the attention launch, shares 1
+        # and 2 by the two feed-forward launches; each copies its slots only
+        _, _, k3, v3 = outputs()
+        spec3 = {**spec, "k_dst": k3, "v_dst": v3, "stage": 2, "parts": 3}
+        o3 = sparda.decode_at(q, kc, vc, pos, bs, window=0, prefetch={**spec3, "part": 0})
+        torch.cuda.synchronize()
+        assert torch.equal(o3, o_plain)
+        mine = torch.zeros(cap, dtype=torch.bool)
+        mine[0::3] = True
+        assert torch.equal(k3[:, :, mine], k1[:, :, mine]) and (k3[:, :, ~mine] == 3.0).all(), "share 0"
+        y_plain = sparda.ffn_decode(xf, wgu, wdn, 1e-5)
+        y = sparda.ffn_decode(xf, wgu, wdn, 1e-5, prefetch=({**spec3, "part": 1}, {**spec3, "part": 2}),
+                              pos_dev=pos, block_size=bs)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_plain), f"feed-forward output at {p}"
+        assert torch.equal(k3, k1) and torch.equal(v3, v1), f"blocks fetched in three shares at {p}"
     L = 2048
     assert torch.equal(cur_a.k_host[:, :L], cur_b.k_host[:, :L]) and torch.equal(cur_a.v_host[:, :L],
                                                                                   cur_b.v_host[:, :L])
