@@ -403,7 +403,9 @@ SPARDA_API int sparda_decode_selected(const void* q, int64_t q_sb, int64_t q_sh,
  * window_k 0) of up to max_len tokens takes its full split: four blocks
  * per workgroup (more only past 4096 workgroups per (sequence, KV head)),
  * so that which split holds a block, and with it the result, depends on the
- * length and not on max_len; 0 when it would not split. No counterpart in the reference: the
+ * length and not on max_len; 0 when it would not split. Only the
+ * matrix-core attention (bf16, D = 64, blocks of 64 or 32 keys) splits;
+ * other calls ignore a workspace. No counterpart in the reference: the
  * reference attends densely with SDPA (model/attention/offload.py:180-200,
  * model/attention/async_offload.py:399-417).
  */

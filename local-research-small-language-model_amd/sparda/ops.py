@@ -502,8 +502,9 @@ def decode_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, S: int, b
     if out is None:
         out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
     qsb, qsh, _ = q.stride()
-    # dense (no selection): the blocks split over workgroups, partials in a workspace
-    ws_ptr, ws_bytes, ws = _dense_split_ws(B, Hq, Hkv, D, S, block_size, dev) if sel is None else (None, 0, None)
+    # dense (no selection) on the matrix cores: the blocks split over workgroups, partials in a workspace
+    split = sel is None and q.dtype == torch.bfloat16 and D == 64 and block_size in (32, 64)
+    ws_ptr, ws_bytes, ws = _dense_split_ws(B, Hq, Hkv, D, S, block_size, dev) if split else (None, 0, None)
     call("sparda_decode_selected", q.data_ptr(), qsb, qsh, k.data_ptr(), v.data_ptr(), kv_sb, kv_ss, kv_sh,
          _dtype_code(q), int(compact), sel.data_ptr() if sel is not None else None,
          n_sel.data_ptr() if n_sel is not None else None, cap,
@@ -925,8 +926,8 @@ def decode_at(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos_dev: torch.
             k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
             nsb, nsh, B, max_len, _pos_ptr(pos_dev), Hq, Hkv, D, block_size, float(scale), out.data_ptr(),
             out.stride(0))
-    # every block (no selection, no window): split over workgroups, partials in a workspace
-    dense = sel is None and int(window) == 0
+    # every block (no selection, no window) on the matrix cores: split over workgroups, partials in a workspace
+    dense = sel is None and int(window) == 0 and q.dtype == torch.bfloat16 and D == 64 and block_size in (32, 64)
     ws_ptr, ws_bytes, ws = _dense_split_ws(B, Hq, Hkv, D, max_len, block_size, dev) if dense else (None, 0, None)
     if prefetch is None:
         call("sparda_decode_at", *args, ws_ptr, ws_bytes, _stream(dev))
