@@ -175,6 +175,25 @@ SPARDA_API int sparda_topk_scores(const float* scores, int64_t rows, int64_t NB,
                                   void* stream);
 
 /*
+ * Per-query-block lists of the chunked-gather prefill. Replaces the
+ * selection of SparseAttention._forward_chunked_gather
+ * (model/attention/sparse.py:303-333): for query block bq (rows
+ * bq*bs .. min(T, (bq+1)*bs) - 1) the set {0, bq} U the union of those rows'
+ * top-k picks (topk [B,H,T,top_k_width] int32: sparda_route's non-causal
+ * top-k, used for bq > 0) or, with topk NULL or at bq = 0, U the static
+ * window [max(0, bq-top_k+1), bq]; blocks past bq dropped; then its lowest
+ * min(NB, top_k+2) indices (the reference cuts with torch.topk over a 0/1
+ * mask, whose order among the equal entries is unspecified; the lowest
+ * indices are the library's tie rule). Every row of the block gets the
+ * block's list: sel/n_sel [B,H,T,sel_cap] / [B,H,T] int32, ascending, -1
+ * padded, min(NB, top_k+2) <= sel_cap <= 34, NB = ceil(T/bs) <= 4096.
+ * sparda_prefill over these lists is the chunked path's attention.
+ */
+SPARDA_API int sparda_select_chunked(const int32_t* topk, int64_t top_k_width, int64_t B, int64_t H, int64_t T,
+                                     int64_t block_size, int64_t top_k, int32_t* sel, int32_t* n_sel,
+                                     int64_t sel_cap, void* stream);
+
+/*
  * Forecast-free selection lists: dense causal fallback and the static
  * sink + sliding-window modes.
  * Replaces model/attention/sparse.py:113-123 (decode dense fallback),

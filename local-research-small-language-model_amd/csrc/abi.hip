@@ -132,6 +132,19 @@ SPARDA_API int sparda_topk_scores(const float* scores, int64_t rows, int64_t NB,
                               static_cast<hipStream_t>(stream));
 }
 
+SPARDA_API int sparda_select_chunked(const int32_t* topk, int64_t top_k_width, int64_t B, int64_t H, int64_t T,
+                                     int64_t block_size, int64_t top_k, int32_t* sel, int32_t* n_sel,
+                                     int64_t sel_cap, void* stream) {
+    SPARDA_REQUIRE(sel && n_sel, SPARDA_ERR_NULL, "select_chunked: null sel / n_sel");
+    SPARDA_REQUIRE(B > 0 && H > 0 && T > 0 && block_size > 0 && top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE,
+                   "select_chunked: bad sizes");
+    SPARDA_REQUIRE(!topk || (top_k_width >= 1 && top_k_width <= top_k), SPARDA_ERR_SHAPE,
+                   "select_chunked: top-k width %lld not in [1, top_k]", (long long)top_k_width);
+    SPARDA_REQUIRE(B <= 65535 && H <= 65535, SPARDA_ERR_SHAPE, "select_chunked: grid too large");
+    return launch_chunk_select(topk, top_k_width, B, H, T, block_size, top_k, sel, n_sel, sel_cap,
+                               static_cast<hipStream_t>(stream));
+}
+
 SPARDA_API int sparda_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H, int64_t NB,
                                    int64_t block_size, int64_t top_k, int64_t query_pos0, int32_t* sel,
                                    int32_t* n_sel, int64_t sel_cap, void* stream) {

@@ -77,6 +77,11 @@ int launch_teacher_mass(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
 int launch_topk_scores(const float* scores, int64_t rows, int64_t NB, int ke, int algo,
                        int32_t* topk, hipStream_t stream);
 
+// chunked-gather lists: per query block of bs rows, {0, bq} U the rows' top-k
+// picks (topk [B,H,T,ke]; NULL: the static window of k blocks) up to bq, the
+// lowest cap of them; NB = ceil(T / bs) <= 4096
+int launch_chunk_select(const int32_t* topk, int64_t ke, int64_t B, int64_t H, int64_t T, int64_t bs, int64_t k,
+                        int32_t* sel, int32_t* n_sel, int64_t cap, hipStream_t stream);
 int launch_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H, int64_t NB, int64_t bs,
                         int64_t k, int64_t query_pos0, int32_t* sel, int32_t* n_sel, int cap,
                         hipStream_t stream);

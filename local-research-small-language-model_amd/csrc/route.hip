@@ -266,6 +266,83 @@ int launch_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H, int64_t NB, 
 }
 
 // ---------------------------------------------------------------------------
+// chunked-gather lists (model/attention/sparse.py:303-333): one workgroup per
+// (query block bq, head h, sequence b). The block's set {0, bq} U (the union of
+// its rows' top-k picks, when given and bq > 0; else the static window
+// [bq-k+1, bq]), picks past bq dropped, is a bitmap in LDS; its lowest
+// cut = min(NB, k + 2) entries, ascending, become every row's list (rows of
+// cap entries, -1 padded).
+// ---------------------------------------------------------------------------
+constexpr int kChunkMaxNB = 4096;
+
+__global__ void __launch_bounds__(256)
+chunk_select_kernel(const int32_t* __restrict__ topk, int ke, int64_t T, int H, int bs, int64_t NB, int k, int cut,
+                    int cap, int32_t* __restrict__ sel, int32_t* __restrict__ n_sel) {
+    __shared__ uint32_t bits[kChunkMaxNB / 32];
+    __shared__ int32_t lst[kMaxSelCap];
+    __shared__ int m_lds;
+    const int bq = blockIdx.x;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int nw = static_cast<int>((NB + 31) / 32);
+    for (int i = tid; i < nw; i += blockDim.x) bits[i] = 0u;
+    __syncthreads();
+    const int64_t r0 = static_cast<int64_t>(bq) * bs;
+    const int64_t r1 = r0 + bs < T ? r0 + bs : T;
+    const int64_t rowbase = (static_cast<int64_t>(b) * H + h) * T;
+    if (tid == 0) {
+        atomicOr(&bits[0], 1u);
+        atomicOr(&bits[bq / 32], 1u << (bq % 32));
+    }
+    if (topk != nullptr && bq > 0) {
+        const int64_t n = (r1 - r0) * ke;
+        for (int64_t e = tid; e < n; e += blockDim.x) {
+            const int j = topk[(rowbase + r0) * ke + e];
+            if (j >= 0 && j <= bq) atomicOr(&bits[j / 32], 1u << (j % 32));
+        }
+    } else {
+        const int lo = bq - k + 1 > 0 ? bq - k + 1 : 0;
+        for (int j = lo + tid; j <= bq; j += blockDim.x) atomicOr(&bits[j / 32], 1u << (j % 32));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int m = 0;
+        for (int w = 0; w < nw && m < cut; ++w) {
+            uint32_t x = bits[w];
+            while (x != 0u && m < cut) {
+                lst[m++] = 32 * w + __builtin_ctz(x);
+                x &= x - 1u;
+            }
+        }
+        m_lds = m;
+    }
+    __syncthreads();
+    const int m = m_lds;
+    for (int64_t e = tid; e < (r1 - r0) * cap; e += blockDim.x) {
+        const int64_t t = r0 + e / cap;
+        const int i = static_cast<int>(e % cap);
+        sel[(rowbase + t) * cap + i] = i < m ? lst[i] : -1;
+    }
+    for (int64_t t = r0 + tid; t < r1; t += blockDim.x) n_sel[rowbase + t] = m;
+}
+
+int launch_chunk_select(const int32_t* topk, int64_t ke, int64_t B, int64_t H, int64_t T, int64_t bs, int64_t k,
+                        int32_t* sel, int32_t* n_sel, int64_t cap, hipStream_t stream) {
+    const int64_t NB = cdiv(T, bs);
+    if (NB > kChunkMaxNB) return set_error(SPARDA_ERR_SHAPE, "select_chunked: more than %d blocks", kChunkMaxNB);
+    const int64_t cut = NB < k + 2 ? NB : k + 2;
+    if (cut > cap || cap > kMaxSelCap)
+        return set_error(SPARDA_ERR_SHAPE, "select_chunked: sel_cap %lld outside [%lld, %d]", (long long)cap,
+                         (long long)cut, kMaxSelCap);
+    hipLaunchKernelGGL(chunk_select_kernel, dim3(static_cast<unsigned>(NB), static_cast<unsigned>(H),
+                       static_cast<unsigned>(B)), dim3(256), 0, stream, topk, static_cast<int>(ke), T,
+                       static_cast<int>(H), static_cast<int>(bs), NB, static_cast<int>(k), static_cast<int>(cut),
+                       static_cast<int>(cap), sel, n_sel);
+    return check_hip(hipGetLastError(), "chunk_select_kernel");
+}
+
+// ---------------------------------------------------------------------------
 // gather: grid (n, H, B); each workgroup copies one block of K and of V
 // ---------------------------------------------------------------------------
 template <int DT>

@@ -158,7 +158,26 @@ class HipSparseAttention(BaseAttention):
         return sparda.select_fixed(sparda.SEL_WINDOW_PREFILL, B, T, self.n_kv_head, nb, self.block_size,
                                    self.top_k_blocks, 0, device=xq.device)
 
-    def _prefill(self, xq, xk, xv, forecast_vector, is_causal, mask=None, return_attn_weights=False):
+    def _chunked_prefill(self, xq, xk, xv, forecast_vector):
+        """The chunked-gather prefill (sparse.py:284-364): per query block of
+        block_size rows one list, {0, own} U the union of its rows' non-causal
+        top-k (forecast mode with a forecast, from the second block on) or the
+        static window, cut to min(NB, k+2) (lowest block indices), then the
+        causal attention over it. Like the reference's chunked path it takes no
+        mask, causality flag or weights."""
+        B, T = xq.shape[:2]
+        topk = None
+        if self.mode == "forecast" and forecast_vector is not None:
+            protos = sparda.compress(xk, self.block_size)
+            topk = sparda.route(forecast_vector, protos, self.block_size, self.top_k_blocks, causal=False)[0]
+        sel, n_sel = sparda.select_chunked(topk, B, self.n_kv_head, T, self.block_size, self.top_k_blocks,
+                                           device=xq.device)
+        return self.wo(sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=True))
+
+    def _prefill(self, xq, xk, xv, forecast_vector, is_causal, mask=None, return_attn_weights=False,
+                 use_chunked_gather=False):
+        if use_chunked_gather and self.mode != "dense":
+            return self._chunked_prefill(xq, xk, xv, forecast_vector)
         if (mask is None and not return_attn_weights and self.mode == "forecast"
                 and not self._dense_prefill(xq.shape[1], forecast_vector)):
             # compressor, then router and attention in one call (one launch
@@ -180,29 +199,26 @@ class HipSparseAttention(BaseAttention):
     def forward(self, x: torch.Tensor, rotary_emb: RotaryEmbedding, kv_cache: Optional[KVCache] = None,
                 mask: Optional[torch.Tensor] = None, is_causal: bool = True,
                 forecast_vector: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
-        if kwargs.get("use_chunked_gather"):
-            # the reference's per-query-block union routing (sparse.py:284-364,
-            # taken when this flag is set, sparse.py:420) has other semantics than
-            # the per-token rule this backend computes at every length
-            raise ValueError("HipSparseAttention: use_chunked_gather=True asks for the chunked-gather path "
-                             "(per-query-block union routing), which this backend does not implement; it "
-                             "applies the per-token masked-SDPA rule at every sequence length. Pass "
-                             "use_chunked_gather=False or leave it out.")
         B, T, _ = x.shape
         xq = self.wq(x).view(B, T, self.n_head, self.head_dim)
         xk = self.wk(x).view(B, T, self.n_kv_head, self.head_dim)
         xv = self.wv(x).view(B, T, self.n_kv_head, self.head_dim)
         offset = kv_cache.current_len if kv_cache is not None else 0
         xq, xk = rotary_emb(xq, xk, offset=offset)
+        # use_chunked_gather: the reference's per-query-block routing
+        # (sparse.py:284-364) when asked for; without the flag the per-token
+        # rule applies at every length (the reference switches to the chunked
+        # path by itself past 8192 tokens, sparse.py:420)
         return self.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
                                       forecast_vector=forecast_vector, mask=mask,
-                                      return_attn_weights=kwargs.get("return_attn_weights", False))
+                                      return_attn_weights=kwargs.get("return_attn_weights", False),
+                                      use_chunked_gather=bool(kwargs.get("use_chunked_gather", False)))
 
     def forward_projected(self, xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
                           kv_cache: Optional[KVCache] = None, is_causal: bool = True,
                           forecast_vector: Optional[torch.Tensor] = None,
                           residual: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
-                          return_attn_weights: bool = False):
+                          return_attn_weights: bool = False, use_chunked_gather: bool = False):
         """The attention after the projections and RoPE: xq [B,T,Hq,D], xk / xv
         [B,T,Hkv,D] (already rotated at the cache's current position). Entered
         from forward, or directly by a block whose fused producer computed them.
@@ -221,4 +237,4 @@ class HipSparseAttention(BaseAttention):
             if kv_cache.current_len != 0:
                 raise NotImplementedError("prefill into a non-empty cache is not supported")
             kv_cache.update(xk, xv)
-        return self._prefill(xq, xk, xv, forecast_vector, is_causal, mask, return_attn_weights)
+        return self._prefill(xq, xk, xv, forecast_vector, is_causal, mask, return_attn_weights, use_chunked_gather)

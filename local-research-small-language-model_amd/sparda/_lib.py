@@ -60,6 +60,7 @@ SIGNATURES = {
     "sparda_route": (_int, [_p, _int, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _int, _i64, _i64, _f32, _p, _p, _p, _p, _i64, _p]),
     "sparda_topk_scores": (_int, [_p, _i64, _i64, _i64, _int, _p, _p]),
+    "sparda_select_chunked": (_int, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p]),
     "sparda_select_fixed": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p]),
     "sparda_gather_blocks": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _p, _p, _p]),

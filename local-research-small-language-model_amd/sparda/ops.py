@@ -152,6 +152,32 @@ def select_fixed(mode: int, B: int, Tq: int, H: int, NB: int, block_size: int, t
     return sel, n_sel
 
 
+def select_chunked(topk: Optional[torch.Tensor], B: int, H: int, T: int, block_size: int, top_k: int,
+                   device=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Lists of the chunked-gather prefill (model/attention/sparse.py:303-333):
+    per query block of block_size rows, {0, own} U the union of its rows'
+    top-k picks (topk int32 [B,H,T,ke], route(..., causal=False)'s; None: the
+    static window of top_k blocks), blocks past the own one dropped, cut to the
+    lowest min(NB, top_k+2). Returns sel [B,H,T,cap], n_sel [B,H,T]."""
+    if topk is not None:
+        dev = require_device(topk)
+        if topk.dtype != torch.int32 or tuple(topk.shape[:3]) != (B, H, T):
+            raise ValueError("sparda: select_chunked takes int32 top-k picks [B,H,T,ke]")
+        topk = topk.contiguous()
+    else:
+        dev = torch.device(device) if device is not None else torch.device("cuda")
+        if dev.type != "cuda":
+            raise RuntimeError("sparda: select_chunked needs a GPU device")
+    NB = (T + block_size - 1) // block_size
+    cap = min(NB, top_k + 2)
+    sel = torch.empty((B, H, T, cap), dtype=torch.int32, device=dev)
+    n_sel = torch.empty((B, H, T), dtype=torch.int32, device=dev)
+    call("sparda_select_chunked", topk.data_ptr() if topk is not None else None,
+         topk.shape[-1] if topk is not None else 0, B, H, T, block_size, top_k, sel.data_ptr(), n_sel.data_ptr(),
+         cap, _stream(dev))
+    return sel, n_sel
+
+
 def gather_blocks(k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
                   block_size: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """k, v [B,H,S,D]; block_indices [B,H,n] -> [B,H,n*bs,D] (model/attention/sparse.py:19-62)."""

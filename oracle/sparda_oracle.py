@@ -16,6 +16,11 @@ What it restates (citations into tyborra/local-research-Small-Language-Model):
                    selection (model/attention/sparse.py:126-154)
 * ``sel_fixed``  — dense fallback and the static windows
                    (model/attention/sparse.py:113-123, 142-147, 250-251)
+* ``chunked_selection`` — the per-query-block lists of the chunked-gather
+                   prefill (model/attention/sparse.py:303-333): sink + own
+                   block + the union of the block's rows' non-causal top-k
+                   (or the static window), future blocks dropped, cut to
+                   min(NB, k+2) by the lowest block indices
 * ``gather_blocks`` — gather_kv_blocks, model/attention/sparse.py:19-62
 * ``attention_prefill`` — masked SDPA over the allowed set,
                    model/attention/sparse.py:255-281, computed per query row in
@@ -191,6 +196,39 @@ def sel_fixed(mode: int, B: int, Tq: int, H: int, NB: int, bs: int, k: int,
         n[t] = len(blocks)
     sel = np.broadcast_to(sel, (B, H, Tq, cap)).copy()
     n = np.broadcast_to(n, (B, H, Tq)).copy()
+    return sel, n
+
+
+def chunked_selection(tk, B: int, H: int, T: int, bs: int, k: int):
+    """Lists of the chunked-gather prefill (model/attention/sparse.py:303-333).
+
+    For query block bq (rows bq*bs .. min(T, (bq+1)*bs) - 1): {0, bq} U the
+    union of those rows' top-k picks (tk [B,H,T,ke], the non-causal per-row
+    top-k of sparse.py:321-323) when tk is given and bq > 0, else U the
+    static window [max(0, bq-k+1), bq] (sparse.py:324-328); blocks past bq
+    dropped (sparse.py:330-331); then cut to min(NB, k+2) entries. The cut is
+    torch.topk over a 0/1 mask (sparse.py:333), whose order among equal
+    values is unspecified; here the lowest block indices are kept (the
+    library's tie rule). Every row of the block gets the block's list.
+    Returns sel [B,H,T,cap] (ascending, -1 padded), n [B,H,T], cap = min(NB, k+2).
+    """
+    NB = num_blocks(T, bs)
+    cap = min(NB, k + 2)
+    sel = np.full((B, H, T, cap), -1, np.int32)
+    n = np.zeros((B, H, T), np.int32)
+    for b in range(B):
+        for h in range(H):
+            for bq in range(NB):
+                rows = range(bq * bs, min(T, (bq + 1) * bs))
+                blocks = {0, bq}
+                if tk is not None and bq > 0:
+                    blocks |= {int(j) for t in rows for j in np.asarray(tk[b, h, t]).ravel()}
+                else:
+                    blocks |= set(range(max(0, bq - k + 1), bq + 1))
+                lst = sorted(j for j in blocks if 0 <= j <= bq)[:cap]
+                for t in rows:
+                    sel[b, h, t, :len(lst)] = lst
+                    n[b, h, t] = len(lst)
     return sel, n
 
 

@@ -1,0 +1,100 @@
+"""GPU parity of the chunked-gather prefill (model/attention/sparse.py:284-364):
+the per-query-block lists (sparda_select_chunked) bit-exact against the
+oracle's, and the whole path (compress, non-causal route, lists, prefill) and
+HipSparseAttention with use_chunked_gather=True against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import sparda
+from sparda import synth
+from model.attention import HipSparseAttention
+from model.config import ModelConfig
+from model.rope import RotaryEmbedding
+from oracle import sparda_oracle as O
+from helpers import assert_close_out, np32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("T,bs,k,spread", [(1000, 64, 8, None), (1000, 64, 4, 16), (777, 32, 4, 6),
+                                           (64, 64, 8, None), (16384, 64, 8, None), (5000, 16, 2, 40)])
+def test_select_chunked_equals_the_oracle(T, bs, k, spread):
+    case(f"select_chunked T={T} bs={bs} k={k} spread={spread}")
+    B, H = 2, 3
+    NB = (T + bs - 1) // bs
+    ke = min(k, NB)
+    rng = np.random.default_rng(T + k)
+    tk = rng.integers(0, spread or NB, size=(B, H, T, ke)).astype(np.int32) % NB
+    sel, n = sparda.select_chunked(torch.from_numpy(tk).to(DEV), B, H, T, bs, k)
+    sel_o, n_o = O.chunked_selection(tk, B, H, T, bs, k)
+    torch.cuda.synchronize()
+    assert np.array_equal(n.cpu().numpy(), n_o)
+    assert np.array_equal(sel.cpu().numpy(), sel_o)
+    # the static window (no forecast)
+    sel, n = sparda.select_chunked(None, B, H, T, bs, k, device=DEV)
+    sel_o, n_o = O.chunked_selection(None, B, H, T, bs, k)
+    torch.cuda.synchronize()
+    assert np.array_equal(n.cpu().numpy(), n_o) and np.array_equal(sel.cpu().numpy(), sel_o)
+
+
+@pytest.mark.parametrize("B,T,bs,k", [(2, 1500, 64, 8), (1, 16384, 64, 8), (1, 2000, 32, 4)])
+def test_chunked_prefill_against_the_oracle(B, T, bs, k):
+    case(f"chunked prefill B={B} T={T} bs={bs} k={k}")
+    Hq, Hkv, D = 12, 4, 64
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=torch.bfloat16, seed=700 + T)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    protos = sparda.compress(d["k"], bs)
+    topk = sparda.route(d["forecast"], protos, bs, k, causal=False)[0]
+    sel, n = sparda.select_chunked(topk, B, Hkv, T, bs, k)
+    out = sparda.prefill(d["q"], d["k"], d["v"], sel, n, bs, causal=True)
+    torch.cuda.synchronize()
+    _, tk_o, _, _ = O.route(np32(x["forecast"]), O.compress(np32(x["k"]), bs), bs, k, False)
+    assert np.array_equal(topk.cpu().numpy(), tk_o)
+    sel_o, n_o = O.chunked_selection(tk_o, B, Hkv, T, bs, k)
+    assert np.array_equal(sel.cpu().numpy(), sel_o) and np.array_equal(n.cpu().numpy(), n_o)
+    r = np.random.default_rng(3)
+    rows = sorted({(int(b), int(t)) for b, t in zip(r.integers(0, B, 64), r.integers(0, T, 64))})
+    rows += [(0, 0), (0, bs - 1), (0, bs), (B - 1, T - 1)]
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, bs, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(out), want, torch.bfloat16, mask)
+
+
+@pytest.mark.parametrize("with_forecast", [True, False])
+def test_backend_use_chunked_gather(with_forecast):
+    # HipSparseAttention with use_chunked_gather=True: the chunked lists and the
+    # prefill over them, then wo (layer 1 with a forecast; without one the
+    # static window, as the reference's chunked path takes for layer 0)
+    case(f"HipSparseAttention use_chunked_gather forecast={with_forecast}")
+    cfg = ModelConfig(block_size=64, top_k_blocks=8, context_length=2048)
+    attn = HipSparseAttention(cfg, layer_idx=1).to(DEV, torch.bfloat16).eval()
+    rot = RotaryEmbedding(cfg.head_dim, cfg.context_length).to(DEV)
+    g = torch.Generator().manual_seed(12)
+    B, T = 1, 1200
+    x = torch.randn(B, T, cfg.n_embd, generator=g).to(DEV, torch.bfloat16)
+    f = (torch.randn(B, T, cfg.n_kv_head, cfg.forecast_dim, generator=g).to(DEV, torch.bfloat16)
+         if with_forecast else None)
+    with torch.no_grad():
+        got = attn(x, rot, forecast_vector=f, use_chunked_gather=True)
+        xq = attn.wq(x).view(B, T, attn.n_head, attn.head_dim)
+        xk = attn.wk(x).view(B, T, attn.n_kv_head, attn.head_dim)
+        xv = attn.wv(x).view(B, T, attn.n_kv_head, attn.head_dim)
+        xq, xk = rot(xq, xk, offset=0)
+        topk = None
+        if with_forecast:
+            topk = sparda.route(f, sparda.compress(xk, 64), 64, 8, causal=False)[0]
+        sel, n = sparda.select_chunked(topk, B, attn.n_kv_head, T, 64, 8, device=DEV)
+        want = attn.wo(sparda.prefill(xq, xk, xv, sel, n, 64, causal=True))
+        per_token = attn(x, rot, forecast_vector=f)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert not torch.equal(got, per_token)  # the per-token rule is another selection
