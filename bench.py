@@ -104,6 +104,7 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
     q, k, v, f = x["q"], x["k"], x["v"], x["forecast"]
     out = torch.empty((B, T, HQ * D), dtype=torch.bfloat16, device="cuda")
     out2 = torch.empty_like(out)
+    out3 = torch.empty_like(out) if T > 8192 else None
     state = {}
 
     def routed(ev=None):
@@ -131,6 +132,26 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         if ev is not None:
             ev[3].record()
         state["sel"], state["n"] = sel, n
+
+    def chunked(ev=None):
+        # the reference's path past 8192 tokens (sparse.py:284-364): every
+        # row's non-causal top-k, one list per query block, causal attention
+        # over the lists; ev: 5 events bracketing the four launches
+        if ev is not None:
+            ev[0].record()
+        protos = sparda.compress(k, BS)
+        if ev is not None:
+            ev[1].record()
+        topk = sparda.route(f, protos, BS, TOPK, causal=False)[0]
+        if ev is not None:
+            ev[2].record()
+        sel, n = sparda.select_chunked(topk, B, HKV, T, BS, TOPK)
+        if ev is not None:
+            ev[3].record()
+        sparda.prefill(q, k, v, sel, n, BS, causal=True, out=out3)
+        if ev is not None:
+            ev[4].record()
+        state["csel"], state["cn"] = sel, n
 
     def eager(step, n_ev):
         for _ in range(args.warmup):
@@ -177,14 +198,30 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         ms_two_eager, (_, ms_route, ms_attn_lists) = eager(two_launch, 4)
         assert torch.isfinite(out.float()).all(), "non-finite prefill output"
         assert torch.equal(out, out2), "routed prefill differs from route + prefill"
-        sel, n = state["sel"], state["n"]
-        # useful work: for each (b, g, t) the allowed keys are full blocks
-        # below the own block plus t%bs+1 keys of the own block
         t = torch.arange(T, device="cuda")
-        keys = (n.to(torch.int64) - 1) * BS + (t % BS + 1)
-        pairs = int(keys.sum().item()) * (HQ // HKV)
+
+        def useful_pairs(sel, n):
+            # for each (b, g, t) the allowed keys: every listed block below the
+            # own one in full, t%bs+1 keys of the own block when it is listed
+            last = torch.gather(sel, -1, (n.to(torch.int64) - 1).clamp(min=0)[..., None])[..., 0]
+            own_listed = (last == t // BS).to(torch.int64)
+            keys = n.to(torch.int64) * BS - own_listed * (BS - (t % BS + 1))
+            return int(keys.sum().item()) * (HQ // HKV)
+
+        pairs = useful_pairs(state["sel"], state["n"])
         ms_step = graphed(routed, out)
         ms_two = graphed(two_launch, out2)
+        chunk = {}
+        if out3 is not None:
+            ms_ch_eager, (_, ms_ch_route, ms_ch_select, ms_ch_attn) = eager(chunked, 5)
+            assert torch.isfinite(out3.float()).all(), "non-finite chunked prefill output"
+            cflop = 4 * D * useful_pairs(state["csel"], state["cn"])
+            ms_ch = graphed(chunked, out3)
+            chunk = {"chunked": {
+                "ms_per_step": ms_ch, "tok_s": B * T / (ms_ch * 1e-3), "ms_per_step_eager": ms_ch_eager,
+                "route_us": ms_ch_route * 1e3, "select_us": ms_ch_select * 1e3, "attn_us": ms_ch_attn * 1e3,
+                "attn_useful_flop": cflop, "attn_tflops": cflop / (ms_ch_attn * 1e-3) / 1e12,
+                "attn_frac": cflop / (ms_ch_attn * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
         # the dense causal step of the same layer (the reference's dense
         # fallback: layer 0 of every forward), kernel time by events
         dense = {}
@@ -220,6 +257,7 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         "attn_from_lists_tflops": flops / (ms_attn_lists * 1e-3) / 1e12,
         "dense_causal_flop": 4 * D * HQ * B * T * (T + 1) // 2,
         **dense,
+        **chunk,
     }
 
 
@@ -649,8 +687,9 @@ def bench_generate(args, torch, sparda, synth, batch=1):
 def bench_model(args, torch, sparda, synth, fused=False):
     """12-layer forward of the model at B=1, T=16384 (bf16 weights from the
     model's N(0, 0.02) init, vocab 32000 tied, d 768, 12/4 heads, SwiGLU 2048;
-    layer 0 dense causal, layers 1..11 forecast-routed sparse with layer L's
-    forecast routing layer L+1), token ids uniform in [0, 32000). Reports
+    at this length the chunked path in every layer: layer 0 the static
+    window, layers 1..11 routed per query block with layer L's forecast
+    routing layer L+1), token ids uniform in [0, 32000). Reports
     tok/s of the whole forward (embeddings to logits) and the time of each
     layer's attention (projections + RoPE + compress + routed attention +
     output projection), from HIP events recorded around the attention modules."""
@@ -698,8 +737,9 @@ def bench_model(args, torch, sparda, synth, fused=False):
         fz = bench_model(args, torch, sparda, synth, fused=True)
     return {
         "workload": f"12-layer forward, B=1, T={MT}, bf16 (d 768, 12/4 heads, head dim 64, SwiGLU 2048, "
-                    "vocab 32000 tied, block 64, top-8); layer 0 dense causal, layers 1-11 forecast-routed "
-                    "sparse; embeddings to logits",
+                    "vocab 32000 tied, block 64, top-8); past 8192 tokens every layer takes the chunked "
+                    "path (one list per 64-token query block, cut to 10 blocks): layer 0 the static window, "
+                    "layers 1-11 routed by the previous layer's forecast; embeddings to logits",
         "ms_per_forward": round(ms, 3),
         "tok_s": round(MT / (ms * 1e-3), 1),
         "attention_ms_per_layer": [round(x, 3) for x in attn],
@@ -968,7 +1008,9 @@ def main():
     log(f"prefill at T={MT} (one layer of the 12-layer forward's shape)")
     p16 = bench_prefill(args, torch, sparda, synth, B=1, T=MT, seed=1003)
     log(f"prefill 16K: {p16['ms_per_step']:.3f} ms/step, attention {p16['attn_ms']*1e3:.1f} us "
-        f"({p16['attn_tflops']:.1f} TFLOP/s useful)")
+        f"({p16['attn_tflops']:.1f} TFLOP/s useful); chunked path {p16['chunked']['ms_per_step']:.3f} ms/step "
+        f"(route {p16['chunked']['route_us']:.1f} us, lists {p16['chunked']['select_us']:.1f} us, attention "
+        f"{p16['chunked']['attn_us']:.1f} us)")
     log("prefill with the reference's default block configuration (32-key blocks, top-4)")
     p32 = bench_prefill(args, torch, sparda, synth, BS=32, TOPK=4)
     log(f"prefill bs=32 k=4: {p32['ms_per_step']:.3f} ms/step, attention {p32['attn_ms']*1e3:.1f} us")
@@ -988,7 +1030,7 @@ def main():
     log("12-layer forward workload")
     mdl = bench_model(args, torch, sparda, synth)
     log(f"model: {mdl['ms_per_forward']:.2f} ms per {MT}-token forward ({mdl['tok_s']:.0f} tok/s), "
-        f"attention {100 * mdl['attention_fraction']:.1f}% (layer 0 dense {mdl['attention_ms_per_layer'][0]:.2f} ms, "
+        f"attention {100 * mdl['attention_fraction']:.1f}% (layer 0 window {mdl['attention_ms_per_layer'][0]:.2f} ms, "
         f"sparse layers {sum(mdl['attention_ms_per_layer'][1:]) / 11:.2f} ms each); fused producer "
         f"{mdl['ms_per_forward_fused_producer']:.2f} ms ({mdl['tok_s_fused_producer']:.0f} tok/s)")
     log("graph-replayed generation")
@@ -1042,14 +1084,20 @@ def main():
         "prefill_16k": {
             "workload": f"the same layer at B=1, T={MT} (256 blocks, top-8 + sink + own), the attention shape of "
                         "one layer of the 12-layer forward; step = compress + routed block-sparse MFMA "
-                        "prefill, HIP graph replay",
+                        "prefill (the per-token rule), HIP graph replay; the reference's chunked path at "
+                        "this length under chunked",
             "ms_per_step": round(p16["ms_per_step"], 4),
             "tok_s": round(p16["tok_s"], 1),
             "roofline": {"bound": "mfma", "achieved": round(p16["attn_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(p16["attn_tflops"] / PEAK_BF16_TFLOPS, 4),
                          "traffic": traffic.get("prefill_attention_16k")},
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16.items()
-               if k not in ("ms_per_step", "tok_s")},
+               if k not in ("ms_per_step", "tok_s", "chunked")},
+            "chunked": {"workload": "the reference's path at this length (the backend's default past 8192 "
+                                    "tokens): compress + every row's non-causal top-k + one list per 64-token "
+                                    "query block (cut to 10 blocks) + causal block-sparse MFMA prefill over the "
+                                    "lists, HIP graph replay",
+                        **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16["chunked"].items()}},
         },
         "prefill_block32": {
             "workload": f"the prefill layer at B={PB}, T={PT} with the reference's default block configuration "

@@ -5,10 +5,13 @@ gather_kv_blocks (model/attention/sparse.py:19-62).
 
 Prefill: compressor, then the router and the block-sparse attention in one
 launch (bf16 MFMA kernel that routes its own query windows, for D = 64 and
-blocks of 32 or 64 keys), or router then prefill kernel for other shapes. The per-token allowed
-set is the reference's masked-SDPA rule (sparse.py:226-281) at every length;
-the reference's chunked path for T > 8192 (sparse.py:284-364, different
-routing semantics) is not reproduced.
+blocks of 32 or 64 keys), or router then prefill kernel for other shapes. Up
+to 8192 tokens the per-token allowed set is the reference's masked-SDPA rule
+(sparse.py:226-281); past that length, or when the caller passes
+use_chunked_gather=True, the chunked path (sparse.py:284-364, 420): one list
+per query block of block_size rows (the union of its rows' non-causal picks,
+cut to k+2 blocks) and causal attention over it; use_chunked_gather=False
+keeps the per-token rule at any length.
 
 Decode (T == 1 with a KVCache): one libsparda call — whole-cache
 compression, routing, split-K attention over the selected blocks, combine.
@@ -23,6 +26,10 @@ from model.attention.base import BaseAttention, KVCache
 from model.config import ModelConfig
 from model.forecast import ForecastBlockSelector, KVBlockCompressor
 from model.rope import RotaryEmbedding
+
+# prefill lengths above this take the chunked path unless the caller says
+# otherwise (model/attention/sparse.py:420)
+CHUNKED_GATHER_MIN_T = 8192
 
 
 def gather_kv_blocks(k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
@@ -175,7 +182,11 @@ class HipSparseAttention(BaseAttention):
         return self.wo(sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=True))
 
     def _prefill(self, xq, xk, xv, forecast_vector, is_causal, mask=None, return_attn_weights=False,
-                 use_chunked_gather=False):
+                 use_chunked_gather=None):
+        if use_chunked_gather is None:
+            # the reference's default: the chunked path past 8192 tokens
+            # (sparse.py:420), whatever mask, causality or weights are asked for
+            use_chunked_gather = xq.shape[1] > CHUNKED_GATHER_MIN_T
         if use_chunked_gather and self.mode != "dense":
             return self._chunked_prefill(xq, xk, xv, forecast_vector)
         if (mask is None and not return_attn_weights and self.mode == "forecast"
@@ -205,20 +216,19 @@ class HipSparseAttention(BaseAttention):
         xv = self.wv(x).view(B, T, self.n_kv_head, self.head_dim)
         offset = kv_cache.current_len if kv_cache is not None else 0
         xq, xk = rotary_emb(xq, xk, offset=offset)
-        # use_chunked_gather: the reference's per-query-block routing
-        # (sparse.py:284-364) when asked for; without the flag the per-token
-        # rule applies at every length (the reference switches to the chunked
-        # path by itself past 8192 tokens, sparse.py:420)
+        # use_chunked_gather: the per-query-block routing (sparse.py:284-364);
+        # absent, it follows the length (past 8192 tokens, sparse.py:420)
+        chunked = kwargs.get("use_chunked_gather")
         return self.forward_projected(xq, xk, xv, kv_cache=kv_cache, is_causal=is_causal,
                                       forecast_vector=forecast_vector, mask=mask,
                                       return_attn_weights=kwargs.get("return_attn_weights", False),
-                                      use_chunked_gather=bool(kwargs.get("use_chunked_gather", False)))
+                                      use_chunked_gather=None if chunked is None else bool(chunked))
 
     def forward_projected(self, xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
                           kv_cache: Optional[KVCache] = None, is_causal: bool = True,
                           forecast_vector: Optional[torch.Tensor] = None,
                           residual: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
-                          return_attn_weights: bool = False, use_chunked_gather: bool = False):
+                          return_attn_weights: bool = False, use_chunked_gather: Optional[bool] = None):
         """The attention after the projections and RoPE: xq [B,T,Hq,D], xk / xv
         [B,T,Hkv,D] (already rotated at the cache's current position). Entered
         from forward, or directly by a block whose fused producer computed them.
@@ -226,7 +236,9 @@ class HipSparseAttention(BaseAttention):
         attention, the projection and the sum in one kernel. A prefill with an
         additive mask or return_attn_weights returns (out, weights) as the
         reference does; a decode step ignores both, as the reference's does
-        (sparse.py:398-410)."""
+        (sparse.py:398-410). use_chunked_gather (None: T > 8192) picks the
+        chunked prefill, which like the reference's takes no mask, causality
+        flag or weights (sparse.py:420-428)."""
         T = xq.shape[1]
         if kv_cache is not None and T == 1:
             kv_cache.update(xk, xv)

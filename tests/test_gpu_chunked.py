@@ -98,3 +98,28 @@ def test_backend_use_chunked_gather(with_forecast):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert not torch.equal(got, per_token)  # the per-token rule is another selection
+
+
+def test_backend_default_follows_the_length():
+    # without the flag the backend takes the chunked path past 8192 tokens and
+    # the per-token rule up to it (sparse.py:420); the flag overrides either
+    # way, and the chunked path answers a weights request with the output
+    # alone, as the reference's does
+    case("HipSparseAttention default at T=8192 / 8193")
+    cfg = ModelConfig(block_size=64, top_k_blocks=8, context_length=8256)
+    attn = HipSparseAttention(cfg, layer_idx=1).to(DEV, torch.bfloat16).eval()
+    rot = RotaryEmbedding(cfg.head_dim, cfg.context_length).to(DEV)
+    g = torch.Generator().manual_seed(13)
+    for T, chunked in ((8192, False), (8193, True)):
+        x = torch.randn(1, T, cfg.n_embd, generator=g).to(DEV, torch.bfloat16)
+        f = torch.randn(1, T, cfg.n_kv_head, cfg.forecast_dim, generator=g).to(DEV, torch.bfloat16)
+        with torch.no_grad():
+            default = attn(x, rot, forecast_vector=f)
+            as_chunked = attn(x, rot, forecast_vector=f, use_chunked_gather=True)
+            per_token = attn(x, rot, forecast_vector=f, use_chunked_gather=False)
+            weights_asked = attn(x, rot, forecast_vector=f, return_attn_weights=True) if chunked else None
+        torch.cuda.synchronize()
+        assert torch.equal(default, as_chunked if chunked else per_token), T
+        assert not torch.equal(as_chunked, per_token), T
+        if chunked:
+            assert isinstance(weights_asked, torch.Tensor) and torch.equal(weights_asked, as_chunked)

@@ -2,9 +2,12 @@
 
 * The 12-layer forward at T=16384 (B=1, bf16, N(0, 0.02) weights, RMSNorm eps
   1e-5, block 64, top-8), layer L's forecast routing layer L+1
-  (model/model.py:97-139): every layer's selection lists bit-exact against the
-  oracle's routing of the forecast and keys the layer used, sampled attention
-  rows of every layer within the bf16 bar, finite logits.
+  (model/model.py:97-139). Past 8192 tokens every layer takes the chunked path
+  (model/attention/sparse.py:284-364, 420): layer 0, without a forecast, the
+  static window; layers 1..11 per-query-block lists from the non-causal
+  routing of the forecast layer L-1 emitted. Every layer's lists bit-exact
+  against the oracle's, sampled attention rows of every layer within the bf16
+  bar, finite logits.
 * Offload at a 32K context (512 blocks of 64, model/attention/async_offload.py:
   170-519): the prefetch selection at lengths 32767 and 32768 in both routings
   (the 257-512-block selection tier), exact block fetches by both transfer
@@ -36,7 +39,7 @@ def case(msg):
 
 
 def test_twelve_layer_forward_at_16k_against_the_oracle(monkeypatch):
-    case("12-layer forward T=16384")
+    case("12-layer forward T=16384 (chunked path)")
     T, bs, k = 16384, 64, 8
     cfg = ModelConfig(n_layer=12, context_length=T, block_size=bs, top_k_blocks=k,
                       attention_backend="hip_sparse", norm_eps=1e-5)
@@ -45,24 +48,18 @@ def test_twelve_layer_forward_at_16k_against_the_oracle(monkeypatch):
     g = torch.Generator().manual_seed(1003)
     ids = torch.randint(0, cfg.vocab_size, (1, T), generator=g).to(DEV)
     prefills = []
-    real_prefill, real_routed = sparda.prefill, sparda.prefill_routed
-
-    def keep(q, kk, v, out, sel=None, n=None, f=None):
-        prefills.append({"q": q.detach().cpu(), "k": kk.detach().cpu(), "v": v.detach().cpu(),
-                         "sel": None if sel is None else sel.cpu().numpy(),
-                         "n": None if n is None else n.cpu().numpy(), "out": out.detach().cpu(),
-                         "f": None if f is None else f.detach().float().cpu().numpy()})
+    real_prefill = sparda.prefill
 
     def prefill_spy(q, kk, v, sel, n_sel, block_size, **kw):
         out = real_prefill(q, kk, v, sel, n_sel, block_size, **kw)
-        keep(q, kk, v, out, sel, n_sel)
+        prefills.append({"q": q.detach().cpu(), "k": kk.detach().cpu(), "v": v.detach().cpu(),
+                         "sel": None if sel is None else sel.cpu().numpy(),
+                         "n": None if n_sel is None else n_sel.cpu().numpy(), "out": out.detach().cpu(),
+                         "causal": kw.get("causal", True)})
         return out
 
-    def routed_spy(q, kk, v, forecast, protos, block_size, top_k, **kw):
-        # the same launch, with the lists written out for the check
-        out, sel, n = real_routed(q, kk, v, forecast, protos, block_size, top_k, want_sel=True, **kw)
-        keep(q, kk, v, out, sel, n, forecast)
-        return out
+    def routed_spy(*a, **kw):
+        raise AssertionError("the per-token routed prefill ran past 8192 tokens")
 
     monkeypatch.setattr(sparda, "prefill", prefill_spy)
     monkeypatch.setattr(sparda, "prefill_routed", routed_spy)
@@ -70,20 +67,19 @@ def test_twelve_layer_forward_at_16k_against_the_oracle(monkeypatch):
         res = model(ids, return_forecasts=True)
     torch.cuda.synchronize()
     assert torch.isfinite(res["logits"]).all()
-    assert len(prefills) == 12 and prefills[0]["sel"] is None  # layer 0: dense causal
-    assert all(p["f"] is not None for p in prefills[1:])
+    assert len(prefills) == 12 and all(p["sel"] is not None and p["causal"] for p in prefills)
     r = np.random.default_rng(16384)
     for L, p in enumerate(prefills):
         q, kk, v = np32(p["q"]), np32(p["k"]), np32(p["v"])
+        tk = None
         if L > 0:
-            # layer L routes with the forecast layer L-1 emitted
-            f = p["f"]
-            assert np.array_equal(f, np32(res["forecasts"][L - 1])), f"layer {L}: forecast hand-off"
-            _, _, sel_o, n_o = O.route(f, O.compress(kk, bs), bs, k, True)
-            assert np.array_equal(p["n"], n_o) and np.array_equal(p["sel"], sel_o), f"layer {L}: selection"
+            # layer L routes with the forecast layer L-1 emitted, every row over all blocks
+            _, tk, _, _ = O.route(np32(res["forecasts"][L - 1]), O.compress(kk, bs), bs, k, False)
+        sel_o, n_o = O.chunked_selection(tk, 1, 4, T, bs, k)
+        assert np.array_equal(p["n"], n_o) and np.array_equal(p["sel"], sel_o), f"layer {L}: selection"
         ts = sorted({int(t) for t in r.integers(0, T, 60)} | {0, 63, 64, T - 1})
         rows = [(0, t) for t in ts]
-        want = O.attention_prefill(q, kk, v, p["sel"], p["n"], bs, True, rows=rows)
+        want = O.attention_prefill(q, kk, v, sel_o, n_o, bs, True, rows=rows)
         got = np32(p["out"])
         assert_close_out(got[0, ts], want[0, ts], torch.bfloat16, what=f"layer {L} attention")
 

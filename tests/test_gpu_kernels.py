@@ -240,9 +240,10 @@ def test_prefill_full_size_sampled_rows():
 
 
 def test_prefill_long_context_16k_sampled_rows_and_selection_invariants():
-    # T = 16384 (256 blocks): the reference switches to its chunked path above
-    # 8192 tokens; this library keeps the per-token rule, checked here against the
-    # oracle on sampled rows, plus the invariants of every selection list
+    # T = 16384 (256 blocks): the per-token rule at a length where the backend
+    # takes the chunked path by default (the kernels serve both; a caller keeps
+    # this rule with use_chunked_gather=False), checked against the oracle on
+    # sampled rows, plus the invariants of every selection list
     case("prefill B=1 T=16384 sampled")
     T, bs, k = 16384, 64, 8
     r = np.random.default_rng(5)
