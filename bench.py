@@ -135,8 +135,9 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
 
     def chunked(ev=None):
         # the reference's path past 8192 tokens (sparse.py:284-364): every
-        # row's non-causal top-k, one list per query block, causal attention
-        # over the lists; ev: 5 events bracketing the four launches
+        # row's non-causal top-k, then one launch that builds each query
+        # block's list and attends over it; ev: 4 events bracketing the three
+        # launches
         if ev is not None:
             ev[0].record()
         protos = sparda.compress(k, BS)
@@ -145,13 +146,10 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         topk = sparda.route(f, protos, BS, TOPK, causal=False)[0]
         if ev is not None:
             ev[2].record()
-        sel, n = sparda.select_chunked(topk, B, HKV, T, BS, TOPK)
+        sparda.prefill_chunked(q, k, v, topk, BS, TOPK, out=out3)
         if ev is not None:
             ev[3].record()
-        sparda.prefill(q, k, v, sel, n, BS, causal=True, out=out3)
-        if ev is not None:
-            ev[4].record()
-        state["csel"], state["cn"] = sel, n
+        state["ctopk"] = topk
 
     def eager(step, n_ev):
         for _ in range(args.warmup):
@@ -213,13 +211,14 @@ def bench_prefill(args, torch, sparda, synth, B=PB, T=PT, seed=1001, BS=BS, TOPK
         ms_two = graphed(two_launch, out2)
         chunk = {}
         if out3 is not None:
-            ms_ch_eager, (_, ms_ch_route, ms_ch_select, ms_ch_attn) = eager(chunked, 5)
+            ms_ch_eager, (_, ms_ch_route, ms_ch_attn) = eager(chunked, 4)
             assert torch.isfinite(out3.float()).all(), "non-finite chunked prefill output"
-            cflop = 4 * D * useful_pairs(state["csel"], state["cn"])
+            csel, cn = sparda.select_chunked(state["ctopk"], B, HKV, T, BS, TOPK)
+            cflop = 4 * D * useful_pairs(csel, cn)
             ms_ch = graphed(chunked, out3)
             chunk = {"chunked": {
                 "ms_per_step": ms_ch, "tok_s": B * T / (ms_ch * 1e-3), "ms_per_step_eager": ms_ch_eager,
-                "route_us": ms_ch_route * 1e3, "select_us": ms_ch_select * 1e3, "attn_us": ms_ch_attn * 1e3,
+                "route_us": ms_ch_route * 1e3, "attn_us": ms_ch_attn * 1e3,
                 "attn_useful_flop": cflop, "attn_tflops": cflop / (ms_ch_attn * 1e-3) / 1e12,
                 "attn_frac": cflop / (ms_ch_attn * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
         # the dense causal step of the same layer (the reference's dense
@@ -1009,8 +1008,7 @@ def main():
     p16 = bench_prefill(args, torch, sparda, synth, B=1, T=MT, seed=1003)
     log(f"prefill 16K: {p16['ms_per_step']:.3f} ms/step, attention {p16['attn_ms']*1e3:.1f} us "
         f"({p16['attn_tflops']:.1f} TFLOP/s useful); chunked path {p16['chunked']['ms_per_step']:.3f} ms/step "
-        f"(route {p16['chunked']['route_us']:.1f} us, lists {p16['chunked']['select_us']:.1f} us, attention "
-        f"{p16['chunked']['attn_us']:.1f} us)")
+        f"(route {p16['chunked']['route_us']:.1f} us, lists + attention {p16['chunked']['attn_us']:.1f} us)")
     log("prefill with the reference's default block configuration (32-key blocks, top-4)")
     p32 = bench_prefill(args, torch, sparda, synth, BS=32, TOPK=4)
     log(f"prefill bs=32 k=4: {p32['ms_per_step']:.3f} ms/step, attention {p32['attn_ms']*1e3:.1f} us")
@@ -1094,9 +1092,9 @@ def main():
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16.items()
                if k not in ("ms_per_step", "tok_s", "chunked")},
             "chunked": {"workload": "the reference's path at this length (the backend's default past 8192 "
-                                    "tokens): compress + every row's non-causal top-k + one list per 64-token "
-                                    "query block (cut to 10 blocks) + causal block-sparse MFMA prefill over the "
-                                    "lists, HIP graph replay",
+                                    "tokens): compress + every row's non-causal top-k + one launch that builds each "
+                                    "64-token query block's list (cut to 10 blocks) and attends causally over it "
+                                    "on the matrix cores, HIP graph replay",
                         **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16["chunked"].items()}},
         },
         "prefill_block32": {

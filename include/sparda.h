@@ -281,6 +281,34 @@ SPARDA_API int sparda_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, 
                                      void* stream);
 
 /*
+ * Chunked-gather prefill: sparda_select_chunked's lists and causal
+ * sparda_prefill over them, in one launch where the shape allows (bf16,
+ * D = 64, block_size 64, Hq/Hkv in 1..4, 16-byte aligned q/k/v rows): each
+ * workgroup builds its 64-token query block's list in LDS and attends every
+ * token of the block over it. Replaces SparseAttention._forward_chunked_gather
+ * after its router call (model/attention/sparse.py:303-364).
+ *   q, k, v, out, scale, dtype: as in sparda_prefill (causal)
+ *   topk: [B,Hkv,T,top_k_width] int32, sparda_route's non-causal top-k; NULL:
+ *         the static window (the reference's chunked path without a forecast)
+ *   sel, n_sel: optional [B,Hkv,T,sel_cap] / [B,Hkv,T], min(NB, top_k+2) <=
+ *         sel_cap <= 34: receive exactly what sparda_select_chunked writes.
+ *         Other shapes run sparda_select_chunked + sparda_prefill as two
+ *         launches through them, and fail without them.
+ * The output equals sparda_prefill over the same lists within rounding (the
+ * one-launch kernel sums in another order), not bit for bit.
+ */
+SPARDA_API int sparda_prefill_chunked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                                      const void* k, const void* v,
+                                      int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                                      int dtype,
+                                      const int32_t* topk, int64_t top_k_width, int64_t top_k,
+                                      int32_t* sel, int32_t* n_sel, int64_t sel_cap,
+                                      int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t block_size, float scale,
+                                      void* out, int64_t out_sb, int64_t out_st,
+                                      void* stream);
+
+/*
  * Block-sparse GQA prefill with an explicit additive mask and, optionally, the
  * attention weights. Replaces the masked-SDPA path of
  * SparseAttention._forward_masked_sdpa with `mask` and return_attn_weights

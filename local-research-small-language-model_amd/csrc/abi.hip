@@ -250,6 +250,41 @@ SPARDA_API int sparda_prefill_routed(const void* q, int64_t q_sb, int64_t q_st, 
                           D, block_size, causal != 0, scale, out, out_sb, out_st, st);
 }
 
+SPARDA_API int sparda_prefill_chunked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
+                                      const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
+                                      const int32_t* topk, int64_t top_k_width, int64_t top_k, int32_t* sel,
+                                      int32_t* n_sel, int64_t sel_cap, int64_t B, int64_t T, int64_t Hq,
+                                      int64_t Hkv, int64_t D, int64_t block_size, float scale, void* out,
+                                      int64_t out_sb, int64_t out_st, void* stream) {
+    SPARDA_REQUIRE(q && k && v && out, SPARDA_ERR_NULL, "prefill_chunked: null q/k/v/out");
+    SPARDA_REQUIRE(!sel == !n_sel, SPARDA_ERR_NULL, "prefill_chunked: sel and n_sel go together");
+    SPARDA_REQUIRE(dtype_ok(dtype), SPARDA_ERR_DTYPE, "prefill_chunked: dtype %d unsupported", dtype);
+    SPARDA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && block_size > 0, SPARDA_ERR_SHAPE,
+                   "prefill_chunked: sizes must be positive");
+    SPARDA_REQUIRE(head_dim_ok(D), SPARDA_ERR_SHAPE, "prefill_chunked: head dim %lld not in {16,32,64,128}",
+                   (long long)D);
+    SPARDA_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= kMaxGroupAbi, SPARDA_ERR_SHAPE,
+                   "prefill_chunked: Hq must be a multiple of Hkv with ratio <= 16");
+    SPARDA_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, SPARDA_ERR_SHAPE, "prefill_chunked: top_k %lld not in [1,%lld]",
+                   (long long)top_k, (long long)kMaxTopK);
+    SPARDA_REQUIRE(!topk || (top_k_width >= 1 && top_k_width <= top_k), SPARDA_ERR_SHAPE,
+                   "prefill_chunked: top-k width %lld not in [1, top_k]", (long long)top_k_width);
+    SPARDA_REQUIRE(T < (1ll << 31) && B <= 65535 && Hkv <= 65535, SPARDA_ERR_SHAPE, "prefill_chunked: too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (block_size == 64 && B * Hkv * cdiv(T, 64) < (1ll << 31) &&
+        prefill_dense_supported(dtype, Hq, Hkv, D, q_sb, q_st, q_sh, kv_sb, kv_st, kv_sh, out_sb, out_st, q, k, v,
+                                out))
+        return launch_prefill_chunked(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, topk, top_k_width, top_k, sel,
+                                      n_sel, sel_cap, B, T, Hq, Hkv, scale, out, out_sb, out_st, st);
+    // other shapes: the lists handed to the prefill through the caller's buffers
+    SPARDA_REQUIRE(sel != nullptr, SPARDA_ERR_SHAPE,
+                   "prefill_chunked: this shape takes two launches and needs sel/n_sel as their hand-off buffers");
+    int rc = launch_chunk_select(topk, top_k_width, B, Hkv, T, block_size, top_k, sel, n_sel, sel_cap, st);
+    if (rc != 0) return rc;
+    return launch_prefill(q, q_sb, q_st, q_sh, k, v, kv_sb, kv_st, kv_sh, dtype, sel, n_sel, sel_cap, B, T, Hq, Hkv,
+                          D, block_size, true, scale, out, out_sb, out_st, st);
+}
+
 SPARDA_API int sparda_prefill_masked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k,
                                      const void* v, int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int dtype,
                                      const int32_t* sel, const int32_t* n_sel, int64_t sel_cap, int64_t B,

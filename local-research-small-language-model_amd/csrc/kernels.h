@@ -47,6 +47,14 @@ int launch_prefill_dense(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh
                          int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t B, int64_t T, int64_t Hq,
                          int64_t Hkv, int causal, float scale, void* out, int64_t out_sb, int64_t out_st,
                          hipStream_t stream);
+// the chunked-gather prefill over 64-key blocks: each query block's list built in
+// the launch from the non-causal top-k (or the static window), causal attention
+// over it (same shape limits as the dense kernel)
+int launch_prefill_chunked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                           int64_t kv_sb, int64_t kv_st, int64_t kv_sh, const int32_t* topk, int64_t ke,
+                           int64_t top_k, int32_t* sel, int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
+                           int64_t Hq, int64_t Hkv, float scale, void* out, int64_t out_sb, int64_t out_st,
+                           hipStream_t stream);
 
 int launch_produce(const void* x, int64_t x_st, const void* w, int64_t M, int64_t C, int64_t Nq, int64_t Nk,
                    int64_t Nf, float eps, const float* cosv, const float* sinv, int64_t T, int64_t pos0,

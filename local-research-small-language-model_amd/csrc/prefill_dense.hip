@@ -25,6 +25,16 @@
 // triangle is not computed); the diagonal block masks the keys past each
 // column's token. No per-token membership logic: every key up to the token
 // (or every key) is attended.
+//
+// The chunked-gather prefill (model/attention/sparse.py:284-364) runs the same
+// kernel with LISTED: one workgroup of 4 wavefronts per query block of 64
+// tokens, which builds the block's list in LDS first (chunk.h: {0, own} U the
+// union of its rows' non-causal top-k, cut to min(NB, k+2)) and walks the
+// listed blocks instead of every block up to the diagonal; all 64 tokens share
+// the list, so every tile is full. The first listed block sets the references
+// (its key 0 is allowed to every token, since listed blocks never lie past
+// the own one).
+#include "chunk.h"
 #include "common.h"
 #include "kernels.h"
 #include "mfma.h"
@@ -35,9 +45,8 @@ namespace {
 
 constexpr int kDBs = 64;                 // keys per KV block
 constexpr int kDD = 64;                  // head dim
-constexpr int kDWaves = 8;               // wavefronts per workgroup
-constexpr int kDThreads = kDWaves * kWave;
-constexpr int kDWin = 16 * kDWaves;      // query tokens per workgroup
+constexpr int kDWaves = 8;               // wavefronts per workgroup (dense)
+constexpr int kLWaves = 4;               // wavefronts per workgroup (listed: one 64-token query block)
 constexpr int kDKRow = kDD + 8;          // K row in LDS, bf16 elements (144 B)
 constexpr int kDVRow = kDD + 16;         // V row in LDS, bf16 elements (160 B)
 constexpr float kDLog2e = 1.4426950408889634f;
@@ -49,15 +58,29 @@ struct DenseSmem {
     int flag;                             // some column's row sum passed kDGuard
 };
 
+// the chunked lists' inputs and outputs (LISTED only)
+struct ChunkArgs {
+    const int32_t* topk;  // [B, Hkv, T, ke] non-causal top-k, or nullptr: the static window
+    int ke, k, cut;       // top-k width, top_k, list length cap min(NB, k + 2)
+    int32_t* sel;         // optional [B, Hkv, T, cap] / [B, Hkv, T]: the lists as sparda_select_chunked writes them
+    int32_t* n_sel;
+    int cap;
+};
+
 }  // namespace
 
-template <int R>
-__global__ void __launch_bounds__(kDThreads, 2)
+template <int R, bool LISTED>
+__global__ void __launch_bounds__((LISTED ? kLWaves : kDWaves) * kWave, 2)
 prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                      const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t kv_sb, int64_t kv_st,
                      int64_t kv_sh, int64_t T, int H, int64_t NBq, int causal, float scale_log2,
-                     uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st) {
+                     uint16_t* __restrict__ out, int64_t out_sb, int64_t out_st, ChunkArgs ch) {
+    constexpr int kNW = LISTED ? kLWaves : kDWaves;
+    constexpr int kThreads = kNW * kWave;
+    constexpr int kWin = 16 * kNW;               // query tokens per workgroup
+    constexpr int kSR = kDBs * 8 / kThreads;     // 16-byte K (and V) chunks each thread stages per block
     __shared__ DenseSmem sm;
+    __shared__ ChunkLds cl;
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
     const int wave = tid / kWave;
@@ -70,18 +93,13 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
     window_order(blockIdx.x, BH, NBq, bg, qw);
     const int b = static_cast<int>(bg / H);
     const int g = static_cast<int>(bg % H);
-    const int64_t t0 = qw * kDWin;
+    const int64_t t0 = qw * kWin;
     const int64_t NB = cdiv(T, kDBs);
-    const int t_valid = static_cast<int>(T - t0 < kDWin ? T - t0 : kDWin);
-    // blocks of the workgroup and of this wavefront (causal: up to the last token's block)
-    const int64_t last_tok = t0 + t_valid - 1;
-    const int nblk = static_cast<int>(causal ? last_tok / kDBs + 1 : NB);
+    const int t_valid = static_cast<int>(T - t0 < kWin ? T - t0 : kWin);
     const int64_t w_first = t0 + 16 * wave;  // this wavefront's first token
     int64_t w_last = w_first + 15;
     w_last = w_last < T - 1 ? w_last : T - 1;
     const bool w_live = w_first < T;
-    const int w_nblk = !w_live ? 0 : static_cast<int>(causal ? w_last / kDBs + 1 : NB);
-
     // Q operands of this wavefront's tiles (column col16 of tile tt; rows past T read row T-1)
     int tok[R];
     bf16x8 qreg[R][2];
@@ -114,22 +132,64 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
     for (int tt = 0; tt < R; ++tt) ref[tt] = -__builtin_inff();
     if (tid == 0) sm.flag = 0;  // ordered before its uses by the staging barrier
 
-    // staging: thread -> 16-byte chunk (row tid / 8, column tid % 8) of K and of V;
-    // rows past T (a ragged last block) read row T-1 (finite values, masked)
+    // staging: thread -> 16-byte chunks (rows tid / 8 + i * kThreads / 8, column
+    // tid % 8) of K and of V; rows past T (a ragged last block) read row T-1
+    // (finite values, masked)
     const uint16_t* kbase = k + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const uint16_t* vbase = v + b * kv_sb + static_cast<int64_t>(g) * kv_sh;
     const int srow = tid / 8, scol = (tid % 8) * 8;
-    const int lds_k = srow * kDKRow + scol, lds_v = srow * kDVRow + scol;
-    auto fetch = [&](int j, uint4& kv_k, uint4& kv_v) __attribute__((always_inline)) {
-        int64_t s = static_cast<int64_t>(j) * kDBs + srow;
-        s = s < T ? s : T - 1;
-        kv_k = *reinterpret_cast<const uint4*>(kbase + s * kv_st + scol);
-        kv_v = *reinterpret_cast<const uint4*>(vbase + s * kv_st + scol);
+    constexpr int kRowStep = kThreads / 8;
+    // the chunks in flight live in one vector register tuple (an array of
+    // uint4 handed between the lambdas would be placed in scratch memory)
+    typedef unsigned int StageV __attribute__((ext_vector_type(4 * kSR)));
+    auto fetch = [&](int j, StageV& kv_k, StageV& kv_v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < kSR; ++i) {
+            int64_t s = static_cast<int64_t>(j) * kDBs + srow + i * kRowStep;
+            s = s < T ? s : T - 1;
+            const uint4 a = *reinterpret_cast<const uint4*>(kbase + s * kv_st + scol);
+            const uint4 c = *reinterpret_cast<const uint4*>(vbase + s * kv_st + scol);
+            kv_k[4 * i] = a.x; kv_k[4 * i + 1] = a.y; kv_k[4 * i + 2] = a.z; kv_k[4 * i + 3] = a.w;
+            kv_v[4 * i] = c.x; kv_v[4 * i + 1] = c.y; kv_v[4 * i + 2] = c.z; kv_v[4 * i + 3] = c.w;
+        }
+    };
+    auto stash = [&](int buf, const StageV& kv_k, const StageV& kv_v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < kSR; ++i) {
+            *reinterpret_cast<uint4*>(&sm.k[buf][(srow + i * kRowStep) * kDKRow + scol]) =
+                uint4{kv_k[4 * i], kv_k[4 * i + 1], kv_k[4 * i + 2], kv_k[4 * i + 3]};
+            *reinterpret_cast<uint4*>(&sm.v[buf][(srow + i * kRowStep) * kDVRow + scol]) =
+                uint4{kv_v[4 * i], kv_v[4 * i + 1], kv_v[4 * i + 2], kv_v[4 * i + 3]};
+        }
     };
 
-    // mode 0: P against the references (block 0 sets them unless `keep`);
-    // mode 1: scores only, the exact column maxima into ref
-    auto compute = [&](int buf, int j, int mode, bool keep) __attribute__((always_inline)) {
+    // blocks of the workgroup and of this wavefront: dense causal, every block up
+    // to the last token's; dense non-causal, every block; listed, the list, built
+    // while the Q rows and block 0 (the first entry of every list) are in flight
+    int nblk, w_nblk;
+    StageV nk0{}, nv0{};
+    if constexpr (LISTED) {
+        fetch(0, nk0, nv0);
+        const int64_t row0 = bg * T + t0;  // (b * Hkv + g) * T + t0
+        chunk_list(cl, ch.topk != nullptr ? ch.topk + row0 * ch.ke : nullptr, t_valid, ch.ke, static_cast<int>(qw),
+                   ch.k, NB, ch.cut);
+        if (ch.sel != nullptr) chunk_write(cl, row0, t_valid, ch.cap, ch.sel, ch.n_sel);
+        nblk = cl.m;
+        w_nblk = w_live ? nblk : 0;
+    } else {
+        const int64_t last_tok = t0 + t_valid - 1;
+        nblk = static_cast<int>(causal ? last_tok / kDBs + 1 : NB);
+        w_nblk = !w_live ? 0 : static_cast<int>(causal ? w_last / kDBs + 1 : NB);
+    }
+    // the u-th block walked
+    auto blk = [&](int u) __attribute__((always_inline)) -> int {
+        if constexpr (LISTED) return cl.lst[u];
+        else return u;
+    };
+
+    // mode 0: P against the references (the first block walked sets them
+    // unless `keep`); mode 1: scores only, the exact column maxima into ref
+    auto compute = [&](int buf, int j, bool first, int mode, bool keep) __attribute__((always_inline)) {
         // K A operands: key 16n + col16, dims 32kk + 8grp .. +7
         bf16x8 ka[4][2];
 #pragma unroll
@@ -172,7 +232,7 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
                     for (int i = 0; i < 4; ++i)
                         if (16 * n + 4 * grp + i > lim) s[n][i] = -__builtin_inff();
             }
-            if (mode == 1 || (j == 0 && !keep)) {  // wave-uniform
+            if (mode == 1 || (first && !keep)) {  // wave-uniform
                 const float cand = pair32_max(pair16_max(max16_nn(s))) * scale_log2;  // block's column max, log2 units
                 ref[tt] = mode == 1 ? fmaxf(ref[tt], cand) : cand;
                 if (mode == 1) continue;
@@ -205,25 +265,24 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
 
     // block u is computed from buffer u & 1 while block u + 1 is in registers;
     // one barrier per block orders its stash before the reads of the next
-    auto walk = [&](int mode, bool keep) __attribute__((always_inline)) {
-        uint4 nk, nv;
-        fetch(0, nk, nv);
-        *reinterpret_cast<uint4*>(&sm.k[0][lds_k]) = nk;
-        *reinterpret_cast<uint4*>(&sm.v[0][lds_v]) = nv;
-        if (nblk > 1) fetch(1, nk, nv);
+    // (nk, nv: block blk(0) already loaded when have0)
+    auto walk = [&](int mode, bool keep, StageV nk, StageV nv, bool have0) __attribute__((always_inline)) {
+        if (!have0) fetch(blk(0), nk, nv);
+        stash(0, nk, nv);
+        if (nblk > 1) fetch(blk(1), nk, nv);
         __syncthreads();
         for (int u = 0; u < nblk; ++u) {
             const int buf = u & 1;
-            if (u < w_nblk) compute(buf, u, mode, keep);  // wave-uniform: blocks past this wavefront's tokens are skipped
+            // wave-uniform: blocks past this wavefront's tokens are skipped
+            if (u < w_nblk) compute(buf, blk(u), u == 0, mode, keep);
             if (u + 1 < nblk) {
-                *reinterpret_cast<uint4*>(&sm.k[buf ^ 1][lds_k]) = nk;
-                *reinterpret_cast<uint4*>(&sm.v[buf ^ 1][lds_v]) = nv;
-                if (u + 2 < nblk) fetch(u + 2, nk, nv);
+                stash(buf ^ 1, nk, nv);
+                if (u + 2 < nblk) fetch(blk(u + 2), nk, nv);
             }
             __syncthreads();
         }
     };
-    walk(0, false);
+    walk(0, false, nk0, nv0, LISTED);
     // a row sum past 2^64 (or not finite): a score more than 64 log2-units above
     // its column's reference somewhere; the row sums sit in lanes 0..15, element 0
     {
@@ -236,9 +295,9 @@ prefill_dense_kernel(const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_st,
     if (sm.flag != 0) {  // workgroup-uniform: every wave walks again
 #pragma unroll
         for (int tt = 0; tt < R; ++tt) ref[tt] = -__builtin_inff();
-        walk(1, true);   // the exact column maxima
+        walk(1, true, nk0, nv0, false);  // the exact column maxima
         clear();
-        walk(0, true);   // against them: every P <= 1
+        walk(0, true, nk0, nv0, false);  // against them: every P <= 1
     }
 
     // ---- epilogue: out[b, t, h*64 + d] = O / l ----
@@ -277,15 +336,15 @@ int launch_prefill_dense(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh
                          int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int64_t B, int64_t T, int64_t Hq,
                          int64_t Hkv, int causal, float scale, void* out, int64_t out_sb, int64_t out_st,
                          hipStream_t stream) {
-    const int64_t NBq = cdiv(T, kDWin);
+    const int64_t NBq = cdiv(T, 16 * kDWaves);
     const int64_t R = Hq / Hkv;
     dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
     const float sl = scale * kDLog2e;
 #define SPARDA_DN(R_)                                                                                      \
-    hipLaunchKernelGGL((prefill_dense_kernel<R_>), grid, dim3(kDThreads), 0, stream,                       \
+    hipLaunchKernelGGL((prefill_dense_kernel<R_, false>), grid, dim3(kDWaves * kWave), 0, stream,          \
                        static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k), \
                        static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, T, static_cast<int>(Hkv), NBq, \
-                       causal, sl, static_cast<uint16_t*>(out), out_sb, out_st)
+                       causal, sl, static_cast<uint16_t*>(out), out_sb, out_st, ChunkArgs{})
     switch (R) {
         case 1: SPARDA_DN(1); break;
         case 2: SPARDA_DN(2); break;
@@ -294,6 +353,39 @@ int launch_prefill_dense(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh
     }
 #undef SPARDA_DN
     return check_hip(hipGetLastError(), "prefill_dense_kernel");
+}
+
+int launch_prefill_chunked(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, const void* v,
+                           int64_t kv_sb, int64_t kv_st, int64_t kv_sh, const int32_t* topk, int64_t ke,
+                           int64_t top_k, int32_t* sel, int32_t* n_sel, int64_t cap, int64_t B, int64_t T,
+                           int64_t Hq, int64_t Hkv, float scale, void* out, int64_t out_sb, int64_t out_st,
+                           hipStream_t stream) {
+    const int64_t NB = cdiv(T, kDBs);
+    if (NB > kChunkMaxNB)
+        return set_error(SPARDA_ERR_SHAPE, "prefill_chunked: more than %d blocks", kChunkMaxNB);
+    const int64_t cut = NB < top_k + 2 ? NB : top_k + 2;
+    if (sel != nullptr && (cap < cut || cap > kMaxSelCap))
+        return set_error(SPARDA_ERR_SHAPE, "prefill_chunked: sel_cap %lld outside [%lld, %d]", (long long)cap,
+                         (long long)cut, kMaxSelCap);
+    const int64_t NBq = NB;  // one workgroup per 64-token query block
+    const int64_t R = Hq / Hkv;
+    dim3 grid(static_cast<unsigned>(B * Hkv * NBq));
+    const float sl = scale * kDLog2e;
+    const ChunkArgs ch{topk, static_cast<int>(ke), static_cast<int>(top_k), static_cast<int>(cut), sel, n_sel,
+                       static_cast<int>(sel != nullptr ? cap : 0)};
+#define SPARDA_CH(R_)                                                                                      \
+    hipLaunchKernelGGL((prefill_dense_kernel<R_, true>), grid, dim3(kLWaves * kWave), 0, stream,           \
+                       static_cast<const uint16_t*>(q), q_sb, q_st, q_sh, static_cast<const uint16_t*>(k), \
+                       static_cast<const uint16_t*>(v), kv_sb, kv_st, kv_sh, T, static_cast<int>(Hkv), NBq, \
+                       1, sl, static_cast<uint16_t*>(out), out_sb, out_st, ch)
+    switch (R) {
+        case 1: SPARDA_CH(1); break;
+        case 2: SPARDA_CH(2); break;
+        case 3: SPARDA_CH(3); break;
+        default: SPARDA_CH(4); break;
+    }
+#undef SPARDA_CH
+    return check_hip(hipGetLastError(), "prefill_dense_kernel (chunked)");
 }
 
 }  // namespace sparda

@@ -7,6 +7,7 @@
 //   top-k     = larger score first, equal scores by lower block index
 #pragma clang fp contract(off)
 
+#include "chunk.h"
 #include "common.h"
 #include "kernels.h"
 #include "select.h"
@@ -267,64 +268,21 @@ int launch_select_fixed(int mode, int64_t B, int64_t Tq, int64_t H, int64_t NB, 
 
 // ---------------------------------------------------------------------------
 // chunked-gather lists (model/attention/sparse.py:303-333): one workgroup per
-// (query block bq, head h, sequence b). The block's set {0, bq} U (the union of
-// its rows' top-k picks, when given and bq > 0; else the static window
-// [bq-k+1, bq]), picks past bq dropped, is a bitmap in LDS; its lowest
-// cut = min(NB, k + 2) entries, ascending, become every row's list (rows of
-// cap entries, -1 padded).
+// (query block bq, head h, sequence b) builds the block's list (chunk.h) and
+// writes it to every row of the block (cap entries, -1 padded).
 // ---------------------------------------------------------------------------
-constexpr int kChunkMaxNB = 4096;
-
 __global__ void __launch_bounds__(256)
 chunk_select_kernel(const int32_t* __restrict__ topk, int ke, int64_t T, int H, int bs, int64_t NB, int k, int cut,
                     int cap, int32_t* __restrict__ sel, int32_t* __restrict__ n_sel) {
-    __shared__ uint32_t bits[kChunkMaxNB / 32];
-    __shared__ int32_t lst[kMaxSelCap];
-    __shared__ int m_lds;
+    __shared__ ChunkLds c;
     const int bq = blockIdx.x;
     const int h = blockIdx.y;
     const int b = blockIdx.z;
-    const int tid = static_cast<int>(threadIdx.x);
-    const int nw = static_cast<int>((NB + 31) / 32);
-    for (int i = tid; i < nw; i += blockDim.x) bits[i] = 0u;
-    __syncthreads();
     const int64_t r0 = static_cast<int64_t>(bq) * bs;
     const int64_t r1 = r0 + bs < T ? r0 + bs : T;
-    const int64_t rowbase = (static_cast<int64_t>(b) * H + h) * T;
-    if (tid == 0) {
-        atomicOr(&bits[0], 1u);
-        atomicOr(&bits[bq / 32], 1u << (bq % 32));
-    }
-    if (topk != nullptr && bq > 0) {
-        const int64_t n = (r1 - r0) * ke;
-        for (int64_t e = tid; e < n; e += blockDim.x) {
-            const int j = topk[(rowbase + r0) * ke + e];
-            if (j >= 0 && j <= bq) atomicOr(&bits[j / 32], 1u << (j % 32));
-        }
-    } else {
-        const int lo = bq - k + 1 > 0 ? bq - k + 1 : 0;
-        for (int j = lo + tid; j <= bq; j += blockDim.x) atomicOr(&bits[j / 32], 1u << (j % 32));
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int m = 0;
-        for (int w = 0; w < nw && m < cut; ++w) {
-            uint32_t x = bits[w];
-            while (x != 0u && m < cut) {
-                lst[m++] = 32 * w + __builtin_ctz(x);
-                x &= x - 1u;
-            }
-        }
-        m_lds = m;
-    }
-    __syncthreads();
-    const int m = m_lds;
-    for (int64_t e = tid; e < (r1 - r0) * cap; e += blockDim.x) {
-        const int64_t t = r0 + e / cap;
-        const int i = static_cast<int>(e % cap);
-        sel[(rowbase + t) * cap + i] = i < m ? lst[i] : -1;
-    }
-    for (int64_t t = r0 + tid; t < r1; t += blockDim.x) n_sel[rowbase + t] = m;
+    const int64_t row0 = (static_cast<int64_t>(b) * H + h) * T + r0;
+    chunk_list(c, topk != nullptr ? topk + row0 * ke : nullptr, r1 - r0, ke, bq, k, NB, cut);
+    chunk_write(c, row0, r1 - r0, cap, sel, n_sel);
 }
 
 int launch_chunk_select(const int32_t* topk, int64_t ke, int64_t B, int64_t H, int64_t T, int64_t bs, int64_t k,

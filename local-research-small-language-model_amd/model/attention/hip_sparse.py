@@ -172,14 +172,11 @@ class HipSparseAttention(BaseAttention):
         static window, cut to min(NB, k+2) (lowest block indices), then the
         causal attention over it. Like the reference's chunked path it takes no
         mask, causality flag or weights."""
-        B, T = xq.shape[:2]
         topk = None
         if self.mode == "forecast" and forecast_vector is not None:
             protos = sparda.compress(xk, self.block_size)
             topk = sparda.route(forecast_vector, protos, self.block_size, self.top_k_blocks, causal=False)[0]
-        sel, n_sel = sparda.select_chunked(topk, B, self.n_kv_head, T, self.block_size, self.top_k_blocks,
-                                           device=xq.device)
-        return self.wo(sparda.prefill(xq, xk, xv, sel, n_sel, self.block_size, causal=True))
+        return self.wo(sparda.prefill_chunked(xq, xk, xv, topk, self.block_size, self.top_k_blocks))
 
     def _prefill(self, xq, xk, xv, forecast_vector, is_causal, mask=None, return_attn_weights=False,
                  use_chunked_gather=None):

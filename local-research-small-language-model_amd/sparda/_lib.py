@@ -69,6 +69,8 @@ SIGNATURES = {
     "sparda_prefill_routed": (_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _int, _i64, _i64,
                                      _i64, _p, _i64, _i64, _f32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _int, _f32, _p, _i64, _i64, _p]),
+    "sparda_prefill_chunked": (_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _i64, _i64, _p, _p,
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p]),
     "sparda_prefill_masked": (_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _int, _p, _p, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _i64, _int, _f32, _p, _int, _i64, _i64, _i64, _i64, _p, _i64,
                                      _i64, _p, _i64, _i64, _i64, _p]),

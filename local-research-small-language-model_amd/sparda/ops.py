@@ -315,6 +315,64 @@ def prefill_routed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, forecast: 
     return (out, sel, n_sel) if want_sel else out
 
 
+def _chunked_one_launch(q, k, v, out, block_size: int) -> bool:
+    """Whether sparda_prefill_chunked takes its one-launch path for these
+    tensors (the library's own test; outside it the call gets the hand-off
+    buffers the two-launch path needs)."""
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if q.dtype != torch.bfloat16 or D != 64 or block_size != 64 or Hq % Hkv or not 1 <= Hq // Hkv <= 4:
+        return False
+    ts = (q, k, v)
+    if any(t.data_ptr() % 16 for t in ts) or out.data_ptr() % 8:
+        return False
+    return all(st % 8 == 0 for t in ts for st in t.stride()[:-1]) and all(st % 4 == 0 for st in out.stride()[:-1])
+
+
+def prefill_chunked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: Optional[torch.Tensor],
+                    block_size: int, top_k: int, scale: Optional[float] = None, want_sel: bool = False,
+                    out: Optional[torch.Tensor] = None):
+    """The chunked-gather prefill (model/attention/sparse.py:303-364) after its
+    router: per query block of block_size tokens the list of
+    ``select_chunked`` (topk [B,Hkv,T,ke] int32 from ``route(...,
+    causal=False)``; None: the static window), then causal attention over it,
+    in one launch where the shape allows. q [B,T,Hq,D], k/v [B,T,Hkv,D].
+    Returns out [B,T,Hq*D], or (out, sel, n_sel) with want_sel (the lists
+    ``select_chunked`` returns)."""
+    dev = require_device(q, k, v, topk)
+    _inference_only(q, k, v)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("sparda: q, k, v must share a dtype")
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    if k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if topk is not None:
+        if topk.dtype != torch.int32 or tuple(topk.shape[:3]) != (B, Hkv, T):
+            raise ValueError("sparda: prefill_chunked takes int32 top-k picks [B,Hkv,T,ke]")
+        topk = topk.contiguous()
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty((B, T, Hq * D), dtype=q.dtype, device=dev)
+    NB = (T + block_size - 1) // block_size
+    cap = min(NB, top_k + 2)
+    sel = n_sel = None
+    if want_sel or not _chunked_one_launch(q, k, v, out, block_size):
+        sel = torch.empty((B, Hkv, T, cap), dtype=torch.int32, device=dev)
+        n_sel = torch.empty((B, Hkv, T), dtype=torch.int32, device=dev)
+    qsb, qst, qsh, _ = q.stride()
+    ksb, kst, ksh, _ = k.stride()
+    osb, ost, _ = out.stride()
+    call("sparda_prefill_chunked", q.data_ptr(), qsb, qst, qsh, k.data_ptr(), v.data_ptr(), ksb, kst, ksh,
+         _dtype_code(q), topk.data_ptr() if topk is not None else None, topk.shape[-1] if topk is not None else 0,
+         top_k, sel.data_ptr() if sel is not None else None, n_sel.data_ptr() if n_sel is not None else None,
+         cap if sel is not None else 0, B, T, Hq, Hkv, D, block_size, float(scale), out.data_ptr(), osb, ost,
+         _stream(dev))
+    return (out, sel, n_sel) if want_sel else out
+
+
 def prefill_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sel: Optional[torch.Tensor],
                    n_sel: Optional[torch.Tensor], block_size: int, causal: bool = True,
                    scale: Optional[float] = None, mask: Optional[torch.Tensor] = None,

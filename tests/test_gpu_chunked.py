@@ -1,7 +1,9 @@
 """GPU parity of the chunked-gather prefill (model/attention/sparse.py:284-364):
 the per-query-block lists (sparda_select_chunked) bit-exact against the
-oracle's, and the whole path (compress, non-causal route, lists, prefill) and
-HipSparseAttention with use_chunked_gather=True against the oracle."""
+oracle's, the one-launch kernel (sparda_prefill_chunked: lists built in the
+launch, attention over them) against the oracle, against sparda_prefill on the
+same lists and against itself (determinism), and HipSparseAttention with
+use_chunked_gather=True against the oracle."""
 
 import numpy as np
 import pytest
@@ -92,11 +94,16 @@ def test_backend_use_chunked_gather(with_forecast):
         topk = None
         if with_forecast:
             topk = sparda.route(f, sparda.compress(xk, 64), 64, 8, causal=False)[0]
-        sel, n = sparda.select_chunked(topk, B, attn.n_kv_head, T, 64, 8, device=DEV)
-        want = attn.wo(sparda.prefill(xq, xk, xv, sel, n, 64, causal=True))
+        o, sel, n = sparda.prefill_chunked(xq, xk, xv, topk, 64, 8, want_sel=True)
+        want = attn.wo(o)
         per_token = attn(x, rot, forecast_vector=f)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+    tk = None if topk is None else topk.cpu().numpy()
+    sel_o, n_o = O.chunked_selection(tk, B, attn.n_kv_head, T, 64, 8)
+    assert np.array_equal(sel.cpu().numpy(), sel_o) and np.array_equal(n.cpu().numpy(), n_o)
+    want_o = O.attention_prefill(np32(xq), np32(xk), np32(xv), sel_o, n_o, 64, True)
+    assert_close_out(np32(o), want_o, torch.bfloat16)
     assert not torch.equal(got, per_token)  # the per-token rule is another selection
 
 
@@ -123,3 +130,62 @@ def test_backend_default_follows_the_length():
         assert not torch.equal(as_chunked, per_token), T
         if chunked:
             assert isinstance(weights_asked, torch.Tensor) and torch.equal(weights_asked, as_chunked)
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,k,spread,forecast", [
+    (2, 1500, 12, 4, 8, None, True), (1, 16384, 12, 4, 8, None, True), (1, 64, 12, 4, 8, None, True),
+    (3, 777, 4, 4, 4, None, True), (1, 2000, 16, 4, 8, None, True), (2, 1000, 8, 4, 4, 16, True),
+    (2, 1500, 12, 4, 8, None, False), (1, 130, 6, 2, 8, None, False)])
+def test_prefill_chunked_one_launch(B, T, Hq, Hkv, k, spread, forecast):
+    # the lists built inside the attention launch equal select_chunked's (and
+    # the oracle's) bit for bit; the output is within the bf16 bar of the
+    # oracle on sampled rows and close to sparda_prefill over the same lists;
+    # two calls give the same bits
+    case(f"prefill_chunked B={B} T={T} Hq={Hq} Hkv={Hkv} k={k} spread={spread} forecast={forecast}")
+    bs, D = 64, 64
+    NB = (T + bs - 1) // bs
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=torch.bfloat16, seed=800 + T + Hq)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    topk = None
+    if forecast:
+        ke = min(k, NB)
+        rng = np.random.default_rng(T + k)
+        tk = rng.integers(0, spread or NB, size=(B, Hkv, T, ke)).astype(np.int32) % NB
+        topk = torch.from_numpy(tk).to(DEV)
+    out, sel, n = sparda.prefill_chunked(d["q"], d["k"], d["v"], topk, bs, k, want_sel=True)
+    out2 = sparda.prefill_chunked(d["q"], d["k"], d["v"], topk, bs, k)
+    sel_l, n_l = sparda.select_chunked(topk, B, Hkv, T, bs, k, device=DEV)
+    lists = sparda.prefill(d["q"], d["k"], d["v"], sel_l, n_l, bs, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "prefill_chunked is not deterministic"
+    assert torch.equal(sel, sel_l) and torch.equal(n, n_l)
+    sel_o, n_o = O.chunked_selection(None if topk is None else topk.cpu().numpy(), B, Hkv, T, bs, k)
+    assert np.array_equal(sel.cpu().numpy(), sel_o) and np.array_equal(n.cpu().numpy(), n_o)
+    r = np.random.default_rng(T)
+    rows = sorted({(int(b), int(t)) for b, t in zip(r.integers(0, B, 96), r.integers(0, T, 96))})
+    rows += [(0, 0), (0, min(T - 1, bs - 1)), (0, min(T - 1, bs)), (B - 1, T - 1)]
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, bs, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(out), want, torch.bfloat16, mask)
+    assert_close_out(np32(out), np32(lists), torch.bfloat16, what="against sparda_prefill on the same lists")
+
+
+def test_prefill_chunked_two_launch_shapes():
+    # shapes outside the one-launch kernel (32-key blocks, fp32) run
+    # select_chunked + prefill through the hand-off buffers: the same bits
+    case("prefill_chunked two-launch shapes")
+    for bs, dtype in ((32, torch.bfloat16), (64, torch.float32)):
+        B, T, Hq, Hkv, D, k = 2, 700, 12, 4, 64, 4
+        NB = (T + bs - 1) // bs
+        x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=dtype, seed=900 + bs)
+        d = {n: t.to(DEV) for n, t in x.items()}
+        tk = np.random.default_rng(bs).integers(0, NB, size=(B, Hkv, T, k)).astype(np.int32)
+        topk = torch.from_numpy(tk).to(DEV)
+        out, sel, n = sparda.prefill_chunked(d["q"], d["k"], d["v"], topk, bs, k, want_sel=True)
+        sel_l, n_l = sparda.select_chunked(topk, B, Hkv, T, bs, k)
+        want = sparda.prefill(d["q"], d["k"], d["v"], sel_l, n_l, bs, causal=True)
+        torch.cuda.synchronize()
+        assert torch.equal(sel, sel_l) and torch.equal(n, n_l)
+        assert torch.equal(out, want), (bs, dtype)

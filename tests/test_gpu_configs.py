@@ -48,26 +48,26 @@ def test_twelve_layer_forward_at_16k_against_the_oracle(monkeypatch):
     g = torch.Generator().manual_seed(1003)
     ids = torch.randint(0, cfg.vocab_size, (1, T), generator=g).to(DEV)
     prefills = []
-    real_prefill = sparda.prefill
+    real_chunked = sparda.prefill_chunked
 
-    def prefill_spy(q, kk, v, sel, n_sel, block_size, **kw):
-        out = real_prefill(q, kk, v, sel, n_sel, block_size, **kw)
+    def chunked_spy(q, kk, v, topk, block_size, top_k, **kw):
+        # the same launch, with the lists it built written out for the check
+        out, sel, n = real_chunked(q, kk, v, topk, block_size, top_k, want_sel=True)
         prefills.append({"q": q.detach().cpu(), "k": kk.detach().cpu(), "v": v.detach().cpu(),
-                         "sel": None if sel is None else sel.cpu().numpy(),
-                         "n": None if n_sel is None else n_sel.cpu().numpy(), "out": out.detach().cpu(),
-                         "causal": kw.get("causal", True)})
+                         "sel": sel.cpu().numpy(), "n": n.cpu().numpy(), "out": out.detach().cpu()})
         return out
 
-    def routed_spy(*a, **kw):
-        raise AssertionError("the per-token routed prefill ran past 8192 tokens")
+    def per_token_spy(*a, **kw):
+        raise AssertionError("a per-token prefill ran past 8192 tokens")
 
-    monkeypatch.setattr(sparda, "prefill", prefill_spy)
-    monkeypatch.setattr(sparda, "prefill_routed", routed_spy)
+    monkeypatch.setattr(sparda, "prefill_chunked", chunked_spy)
+    monkeypatch.setattr(sparda, "prefill_routed", per_token_spy)
+    monkeypatch.setattr(sparda, "prefill", per_token_spy)
     with torch.no_grad():
         res = model(ids, return_forecasts=True)
     torch.cuda.synchronize()
     assert torch.isfinite(res["logits"]).all()
-    assert len(prefills) == 12 and all(p["sel"] is not None and p["causal"] for p in prefills)
+    assert len(prefills) == 12
     r = np.random.default_rng(16384)
     for L, p in enumerate(prefills):
         q, kk, v = np32(p["q"]), np32(p["k"]), np32(p["v"])
