@@ -74,10 +74,12 @@ int launch_compress(const void* k, int dtype, int64_t B, int64_t S, int64_t H, i
 }
 
 // ---------------------------------------------------------------------------
-// router: one lane per query row. A workgroup of kRouteWaves wavefronts takes
-// two sets of 64 consecutive rows of one (b, h): set p and its mirror NS-1-p,
-// so that under the causal mask every workgroup scores about the same number
-// of (row, block) pairs. Within a set the waves split the candidate blocks
+// router: one lane per query row. Under the causal mask a workgroup of
+// kRouteWaves wavefronts takes two sets of 64 consecutive rows of one (b, h):
+// set p and its mirror NS-1-p, so that every workgroup scores about the same
+// number of (row, block) pairs; without it every set has the same work and a
+// workgroup takes one (twice the workgroups, four wavefronts per SIMD instead
+// of two at B=1, T=16384). Within a set the waves split the candidate blocks
 // (wave w scores the blocks j = w mod kRouteWaves), so the block index is
 // uniform across the wavefront: every 16-lane row of the wavefront loads the
 // block's prototype with one coalesced load (lane i of the row holds elements
@@ -103,7 +105,7 @@ route_rows_kernel(const void* __restrict__ f, int64_t fsb, int64_t fst, int64_t 
 
     for (int pass = 0; pass < 2; ++pass) {
         const int64_t set = pass == 0 ? pair : NS - 1 - pair;
-        if (pass == 1 && set == pair) break;  // odd set count: the middle set has no mirror
+        if (pass == 1 && (!causal || set == pair)) break;  // one set without the mask; an odd count's middle set
         const int m = static_cast<int>((2 * pair + pass) % kRouteWaves);
         int32_t picks[KMAX];
         if (!route_set<FDT, DF, KMAX>(f, fsb, fst, fsh, protos, b, h, H, set, Tq, NB, bs, ke, causal, score_pos0,
@@ -137,7 +139,7 @@ static int launch_route_df(const void* f, int64_t fsb, int64_t fst, int64_t fsh,
                            int causal, int64_t score_pos0, int64_t query_pos0, float scale,
                            int32_t* topk, float* scores, int32_t* sel, int32_t* n_sel, int cap,
                            hipStream_t stream) {
-    const int64_t pairs = cdiv(cdiv(Tq, kWave), 2);
+    const int64_t pairs = causal ? cdiv(cdiv(Tq, kWave), 2) : cdiv(Tq, kWave);
     dim3 grid(static_cast<unsigned>(pairs), static_cast<unsigned>(H), static_cast<unsigned>(B));
 #define SPARDA_ROUTE(KM_)                                                                          \
     hipLaunchKernelGGL((route_rows_kernel<FDT, DF, KM_>), grid, dim3(kRouteThreads),               \
