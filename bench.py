@@ -837,9 +837,10 @@ def pmc_workload(args, torch, sparda, synth):
     """Short eager run for hardware-counter passes: at B=4 T=4096, then at B=1
     T=16384, three prefill steps (compress + routed prefill) and one step of
     the three-launch form (compress, router, prefill from its lists); then one
-    dense causal prefill at B=1 T=16384 (no lists); decode steps and a plain
-    device copy of COPY_BYTES (the calibration of FETCH_SIZE / WRITE_SIZE).
-    Counter values are per dispatch, in this order."""
+    dense causal prefill at B=1 T=16384 (no lists) and one step of the chunked
+    path there (compress, non-causal router, prefill_chunked); decode steps and
+    a plain device copy of COPY_BYTES (the calibration of FETCH_SIZE /
+    WRITE_SIZE). Counter values are per dispatch, in this order."""
     x = synth.prefill_inputs(PB, PT, HQ, HKV, D, dtype=torch.bfloat16, seed=1001, device="cuda")
     x16 = synth.prefill_inputs(1, MT, HQ, HKV, D, dtype=torch.bfloat16, seed=1003, device="cuda")
     c = synth.decode_inputs(DB, DS, HQ, HKV, D, dtype=torch.bfloat16, seed=1002, device="cuda")
@@ -855,6 +856,9 @@ def pmc_workload(args, torch, sparda, synth):
             _, _, sel, n_sel = sparda.route(xs["forecast"], protos, BS, TOPK, want_topk=False, want_sel=True)
             sparda.prefill(xs["q"], xs["k"], xs["v"], sel, n_sel, BS)
         sparda.prefill(x16["q"], x16["k"], x16["v"], None, None, BS)
+        protos = sparda.compress(x16["k"], BS)
+        topk = sparda.route(x16["forecast"], protos, BS, TOPK, causal=False)[0]
+        sparda.prefill_chunked(x16["q"], x16["k"], x16["v"], topk, BS, TOPK)
         for _ in range(3):
             sparda.decode(c["q"], c["k_cache"], c["v_cache"], DS, c["forecast"], BS, TOPK, routing="absolute",
                           workspace=ws)
@@ -1095,7 +1099,8 @@ def main():
                                     "tokens): compress + every row's non-causal top-k + one launch that builds each "
                                     "64-token query block's list (cut to 10 blocks) and attends causally over it "
                                     "on the matrix cores, HIP graph replay",
-                        **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16["chunked"].items()}},
+                        **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16["chunked"].items()},
+                        "traffic": traffic.get("prefill_chunked_16k")},
         },
         "prefill_block32": {
             "workload": f"the prefill layer at B={PB}, T={PT} with the reference's default block configuration "
