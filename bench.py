@@ -1059,6 +1059,7 @@ def main():
             f"{cpu_dec.get('value_1_thread')} on 1")
 
     traffic = load_traffic()
+    ch16 = p16["chunked"]
     t_attn = traffic.get("prefill_attention")
     t_dec = traffic.get("decode_step")
     line = {
@@ -1084,23 +1085,27 @@ def main():
         "cpu_baseline": cpu,
         "prefill_detail": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre.items()},
         "prefill_16k": {
-            "workload": f"the same layer at B=1, T={MT} (256 blocks, top-8 + sink + own), the attention shape of "
-                        "one layer of the 12-layer forward; step = compress + routed block-sparse MFMA "
-                        "prefill (the per-token rule), HIP graph replay; the reference's chunked path at "
-                        "this length under chunked",
-            "ms_per_step": round(p16["ms_per_step"], 4),
-            "tok_s": round(p16["tok_s"], 1),
-            "roofline": {"bound": "mfma", "achieved": round(p16["attn_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(p16["attn_tflops"] / PEAK_BF16_TFLOPS, 4),
-                         "traffic": traffic.get("prefill_attention_16k")},
-            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16.items()
-               if k not in ("ms_per_step", "tok_s", "chunked")},
-            "chunked": {"workload": "the reference's path at this length (the backend's default past 8192 "
-                                    "tokens): compress + every row's non-causal top-k + one launch that builds each "
-                                    "64-token query block's list (cut to 10 blocks) and attends causally over it "
-                                    "on the matrix cores, HIP graph replay",
-                        **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16["chunked"].items()},
-                        "traffic": traffic.get("prefill_chunked_16k")},
+            "workload": f"the same layer at B=1, T={MT} (256 blocks, top-8), the attention shape of one layer of "
+                        "the 12-layer forward, on the path the reference and the backend take past 8192 tokens: "
+                        "compress + every row's non-causal top-k + one launch that builds each 64-token query "
+                        "block's list (sink + own + the union of its rows' picks, cut to 10 blocks) and attends "
+                        "causally over it on the matrix cores; HIP graph replay. per_token_rule: the same layer "
+                        "under the per-token rule (compress + routed prefill)",
+            "ms_per_step": round(ch16["ms_per_step"], 4),
+            "tok_s": round(ch16["tok_s"], 1),
+            "roofline": {"bound": "mfma", "achieved": round(ch16["attn_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ch16["attn_tflops"] / PEAK_BF16_TFLOPS, 4),
+                         "traffic": traffic.get("prefill_chunked_16k")},
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in ch16.items()
+               if k not in ("ms_per_step", "tok_s")},
+            "per_token_rule": {
+                "ms_per_step": round(p16["ms_per_step"], 4),
+                "tok_s": round(p16["tok_s"], 1),
+                "roofline": {"bound": "mfma", "achieved": round(p16["attn_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(p16["attn_tflops"] / PEAK_BF16_TFLOPS, 4),
+                             "traffic": traffic.get("prefill_attention_16k")},
+                **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p16.items()
+                   if k not in ("ms_per_step", "tok_s", "chunked")}},
         },
         "prefill_block32": {
             "workload": f"the prefill layer at B={PB}, T={PT} with the reference's default block configuration "
