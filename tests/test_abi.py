@@ -115,6 +115,27 @@ def test_argument_errors_are_reported_before_any_hip_call():
     _expect(-5, "sparda_rows_residual", P + 4, 768, P, 1, 768, 768, P, 768, P, 768, None)  # misaligned a
 
 
+def test_chunked_entry_argument_errors():
+    P = 4096
+    # topk, width, B, H, T, bs, top_k, sel, n_sel, cap, stream
+    _expect(-1, "sparda_select_chunked", P, 8, 1, 4, 1000, 64, 8, None, P, 10, None)      # no sel
+    _expect(-2, "sparda_select_chunked", P, 9, 1, 4, 1000, 64, 8, P, P, 10, None)         # width > top_k
+    _expect(-2, "sparda_select_chunked", P, 8, 1, 4, 1000, 64, 8, P, P, 9, None)          # cap < min(NB, k+2)
+    _expect(-2, "sparda_select_chunked", P, 8, 1, 4, 4097 * 64, 64, 8, P, P, 10, None)    # more than 4096 blocks
+    # q, strides, k, v, kv strides, dtype, topk, width, top_k, sel, n_sel, cap, B, T, Hq, Hkv, D, bs, scale,
+    # out, out strides, stream
+    ch = lambda topk, width, top_k, sel, n_sel, cap, T=1000, bs=64, Hq=12: (
+        P, 768, 768, 64, P, P, 256, 256, 64, 1, topk, width, top_k, sel, n_sel, cap, 1, T, Hq, 4, 64, bs, 0.125,
+        P, 768, 768, None)
+    _expect(-1, "sparda_prefill_chunked", *ch(P, 8, 8, P, None, 10))                    # sel without n_sel
+    _expect(-2, "sparda_prefill_chunked", *ch(P, 8, 33, None, None, 0))                 # top_k > 32
+    _expect(-2, "sparda_prefill_chunked", *ch(P, 9, 8, None, None, 0))                  # width > top_k
+    _expect(-2, "sparda_prefill_chunked", *ch(P, 8, 8, P, P, 9))                        # cap < min(NB, k+2)
+    _expect(-2, "sparda_prefill_chunked", *ch(P, 8, 8, None, None, 0, T=4097 * 64))     # more than 4096 blocks
+    _expect(-2, "sparda_prefill_chunked", *ch(P, 8, 8, None, None, 0, bs=32))           # two launches need the lists
+    _expect(-2, "sparda_prefill_chunked", *ch(P, 8, 8, None, None, 0, Hq=13))           # Hq not a multiple of Hkv
+
+
 def test_decode_workspace_size_formula():
     # the block scores of every (sequence, KV head), rounded up to 256 B
     up = lambda x: (x + 255) // 256 * 256

@@ -189,3 +189,28 @@ def test_prefill_chunked_two_launch_shapes():
         torch.cuda.synchronize()
         assert torch.equal(sel, sel_l) and torch.equal(n, n_l)
         assert torch.equal(out, want), (bs, dtype)
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,k", [(4096 * 64, 3, 1, 8), (5000, 12, 4, 32)])
+def test_prefill_chunked_at_its_limits(T, Hq, Hkv, k):
+    # 4096 blocks (the list bitmap's capacity) and top-32 (lists of 34 blocks)
+    case(f"prefill_chunked limits T={T} Hq={Hq} Hkv={Hkv} k={k}")
+    B, bs, D = 1, 64, 64
+    NB = (T + bs - 1) // bs
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=torch.bfloat16, seed=41 + k)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    tk = np.random.default_rng(k).integers(0, NB, size=(B, Hkv, T, k)).astype(np.int32)
+    topk = torch.from_numpy(tk).to(DEV)
+    out, sel, n = sparda.prefill_chunked(d["q"], d["k"], d["v"], topk, bs, k, want_sel=True)
+    sel_l, n_l = sparda.select_chunked(topk, B, Hkv, T, bs, k)
+    torch.cuda.synchronize()
+    assert torch.equal(sel, sel_l) and torch.equal(n, n_l)
+    sel_o, n_o = O.chunked_selection(tk, B, Hkv, T, bs, k)
+    assert np.array_equal(sel.cpu().numpy(), sel_o) and np.array_equal(n.cpu().numpy(), n_o)
+    r = np.random.default_rng(T)
+    rows = sorted({(0, int(t)) for t in r.integers(0, T, 48)} | {(0, 0), (0, T - 1)})
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, bs, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(out), want, torch.bfloat16, mask)
