@@ -2,9 +2,11 @@
 cases do not pin: the routed prefill (lists bit-exact against the oracle's
 router, sampled rows of the output against the oracle's attention), the
 decode step in both routings (selection bit-exact, output to the bf16 / fp32
-bar) and the dense decode split over workgroups.
+bar), the dense decode split over workgroups, and the chunked-gather prefill
+(the non-causal router, then the lists built inside the attention launch:
+lists bit-exact against the oracle's, sampled rows to the bf16 bar).
 
-Every configuration comes from seeded generators (2026, 2027, 2028) and is
+Every configuration comes from seeded generators (2026, 2027, 2028, 2029) and is
 printed before it runs, so a failure names a reproducible case."""
 
 import numpy as np
@@ -116,3 +118,34 @@ def test_dense_decode_random_lengths(i):
     n = np.full((B, Hkv), NB, np.int32)
     want = O.attention_decode(np32(x["q"]), np32(x["k_cache"]), np32(x["v_cache"]), S, sel, n, bs)
     assert_close_out(np32(out), want, torch.bfloat16)
+
+
+_CHUNKED = _draws(10, 2029)
+
+
+@pytest.mark.parametrize("i", range(len(_CHUNKED)))
+def test_chunked_prefill_random_shapes(i):
+    c = _CHUNKED[i]
+    r = np.random.default_rng(c["seed"])
+    T = int(r.integers(1, 5000))
+    with_forecast = bool(r.integers(0, 4) != 0)
+    B, Hq, Hkv, bs, k = c["B"], c["Hq"], c["Hkv"], c["bs"], c["k"]
+    case(f"chunked prefill B={B} T={T} Hq={Hq} Hkv={Hkv} bs={bs} k={k} forecast={with_forecast} seed={c['seed']}")
+    x = synth.prefill_inputs(B, T, Hq, Hkv, 64, dtype=torch.bfloat16, seed=c["seed"] % 100000)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    topk = tk_o = None
+    if with_forecast:
+        topk = sparda.route(d["forecast"], sparda.compress(d["k"], bs), bs, k, causal=False)[0]
+        _, tk_o, _, _ = O.route(np32(x["forecast"]), O.compress(np32(x["k"]), bs), bs, k, False)
+    got, sel, n = sparda.prefill_chunked(d["q"], d["k"], d["v"], topk, bs, k, want_sel=True)
+    torch.cuda.synchronize()
+    if with_forecast:
+        assert np.array_equal(topk.cpu().numpy(), tk_o)
+    sel_o, n_o = O.chunked_selection(tk_o, B, Hkv, T, bs, k)
+    assert np.array_equal(n.cpu().numpy(), n_o) and np.array_equal(sel.cpu().numpy(), sel_o)
+    rows = sorted({(int(b), int(t)) for b, t in zip(r.integers(0, B, 40), r.integers(0, T, 40))} | {(B - 1, T - 1)})
+    want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, bs, True, rows=rows)
+    mask = np.zeros(want.shape, bool)
+    for b, t in rows:
+        mask[b, t] = True
+    assert_close_out(np32(got), want, torch.bfloat16, mask)
