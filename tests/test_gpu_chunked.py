@@ -214,3 +214,44 @@ def test_prefill_chunked_at_its_limits(T, Hq, Hkv, k):
     for b, t in rows:
         mask[b, t] = True
     assert_close_out(np32(out), want, torch.bfloat16, mask)
+
+
+@pytest.mark.parametrize("T", [1, 2, 63, 65, 129])
+def test_prefill_chunked_tiny_lengths(T):
+    # one or two query blocks, ragged: the lists and the output against the oracle
+    case(f"prefill_chunked tiny T={T}")
+    B, Hq, Hkv, D, bs, k = 2, 12, 4, 64, 64, 8
+    NB = (T + bs - 1) // bs
+    x = synth.prefill_inputs(B, T, Hq, Hkv, D, dtype=torch.bfloat16, seed=70 + T)
+    d = {n: t.to(DEV) for n, t in x.items()}
+    for with_topk in (True, False):
+        tk = np.random.default_rng(T).integers(0, NB, size=(B, Hkv, T, min(k, NB))).astype(np.int32)
+        topk = torch.from_numpy(tk).to(DEV) if with_topk else None
+        out, sel, n = sparda.prefill_chunked(d["q"], d["k"], d["v"], topk, bs, k, want_sel=True)
+        torch.cuda.synchronize()
+        sel_o, n_o = O.chunked_selection(tk if with_topk else None, B, Hkv, T, bs, k)
+        assert np.array_equal(sel.cpu().numpy(), sel_o) and np.array_equal(n.cpu().numpy(), n_o)
+        want = O.attention_prefill(np32(x["q"]), np32(x["k"]), np32(x["v"]), sel_o, n_o, bs, True)
+        assert_close_out(np32(out), want, torch.bfloat16)
+
+
+def test_static_mode_backend_past_8192_takes_the_window():
+    # the static-window backend past 8192 tokens: the chunked path's window
+    # lists (sparse.py:320-328 take the window whenever no forecast routes)
+    case("static mode backend T=8200")
+    from model.transformer import build_attention_backend
+    cfg = ModelConfig(block_size=64, top_k_blocks=8, context_length=8256, attention_backend="static_sparse")
+    attn = build_attention_backend(cfg, 1).to(DEV, torch.bfloat16).eval()
+    rot = RotaryEmbedding(cfg.head_dim, cfg.context_length).to(DEV)
+    g = torch.Generator().manual_seed(14)
+    B, T = 1, 8200
+    x = torch.randn(B, T, cfg.n_embd, generator=g).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        got = attn(x, rot)
+        xq = attn.wq(x).view(B, T, attn.n_head, attn.head_dim)
+        xk = attn.wk(x).view(B, T, attn.n_kv_head, attn.head_dim)
+        xv = attn.wv(x).view(B, T, attn.n_kv_head, attn.head_dim)
+        xq, xk = rot(xq, xk, offset=0)
+        want = attn.wo(sparda.prefill_chunked(xq, xk, xv, None, 64, 8))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
