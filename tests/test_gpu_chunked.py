@@ -255,3 +255,19 @@ def test_static_mode_backend_past_8192_takes_the_window():
         want = attn.wo(sparda.prefill_chunked(xq, xk, xv, None, 64, 8))
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_prefill_chunked_on_strided_views():
+    # q, k and v as slices of one packed [B, T, Hq + 2 Hkv, D] buffer (element
+    # strides, no copies): the same output as on contiguous copies
+    case("prefill_chunked strided views")
+    B, T, Hq, Hkv, D, bs, k = 2, 1000, 12, 4, 64, 64, 8
+    g = torch.Generator().manual_seed(15)
+    packed = torch.randn(B, T, Hq + 2 * Hkv, D, generator=g).to(DEV, torch.bfloat16)
+    q, kk, v = packed[:, :, :Hq], packed[:, :, Hq:Hq + Hkv], packed[:, :, Hq + Hkv:]
+    NB = (T + bs - 1) // bs
+    topk = torch.from_numpy(np.random.default_rng(15).integers(0, NB, size=(B, Hkv, T, k)).astype(np.int32)).to(DEV)
+    got = sparda.prefill_chunked(q, kk, v, topk, bs, k)
+    want = sparda.prefill_chunked(q.contiguous(), kk.contiguous(), v.contiguous(), topk, bs, k)
+    torch.cuda.synchronize()
+    assert not q.is_contiguous() and torch.equal(got, want)
