@@ -953,6 +953,28 @@ def cpu_decode_baseline(args, torch, synth, info):
     return out
 
 
+def cpu_chunked_baseline(args, torch, synth, info):
+    """The reference's chunked-gather prefill (its path past 8192 tokens)
+    restated op for op (oracle/reference_path.py) on the host cores, at the
+    16K leg's shape (B=1, T=16384, one layer): compress, then per 64-token
+    query block the non-causal selector, the mask and its top-k cut, the
+    gather and SDPA. Warm-up 1, runs 3, median (each run is one whole layer)."""
+    from oracle import reference_path as R
+    x = synth.prefill_inputs(1, MT, HQ, HKV, D, dtype=torch.bfloat16, seed=1003)
+    q, k, v = (x[n].transpose(1, 2) for n in ("q", "k", "v"))
+    f = x["forecast"]
+    n = max(_thread_counts(args, torch))
+    torch.set_num_threads(n)
+    with torch.no_grad():
+        med, lo, hi = cpu_timed(lambda: R.chunked_prefill(q, k, v, f, BS, TOPK), warmup=1, runs=3)
+    return {"value": round(MT / med, 1), "unit": "tok/s", "cores": n, "kind": "port",
+            "sample": f"one layer at B=1, T={MT} (bf16) through the reference's chunked-gather path restated "
+                      f"op for op in PyTorch (a loop over the 256 query blocks: selector, mask, top-k cut, gather, "
+                      f"SDPA); warm-up 1, median of 3 runs, {med:.3f} s/run (min {lo:.3f}, max {hi:.3f}); "
+                      f"torch threads={n}",
+            "cpu": info}
+
+
 def cpu_baseline(args, torch, synth, info):
     """Reference prefill path restated op for op (oracle/reference_path.py) on
     the host cores: the full workload (B=4, T=4096) on N threads; on 1 thread
@@ -1047,7 +1069,7 @@ def main():
     tch = bench_teacher(args, torch, sparda, synth)
     log(f"teacher: kernel {tch['us_kernel']:.1f} us ({tch['kernel_tflops']:.0f} TFLOP/s), materialised torch "
         f"{tch['us_materialised_torch']:.1f} us")
-    cpu = cpu_dec = None
+    cpu = cpu_dec = cpu_ch = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         info = cpu_info()
@@ -1057,6 +1079,8 @@ def main():
         cpu_dec = cpu_decode_baseline(args, torch, synth, info)
         log(f"cpu decode: {cpu_dec['value']:.1f} us/step on {cpu_dec['cores']} threads, "
             f"{cpu_dec.get('value_1_thread')} on 1")
+        cpu_ch = cpu_chunked_baseline(args, torch, synth, info)
+        log(f"cpu chunked prefill at T={MT}: {cpu_ch['value']:.1f} tok/s on {cpu_ch['cores']} threads")
 
     traffic = load_traffic()
     ch16 = p16["chunked"]
@@ -1098,6 +1122,7 @@ def main():
                          "traffic": traffic.get("prefill_chunked_16k")},
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in ch16.items()
                if k not in ("ms_per_step", "tok_s")},
+            "cpu_baseline": cpu_ch,
             "per_token_rule": {
                 "ms_per_step": round(p16["ms_per_step"], 4),
                 "tok_s": round(p16["tok_s"], 1),

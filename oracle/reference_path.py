@@ -14,6 +14,10 @@ reference, so its CPU time is the reference's CPU time on the same inputs:
   masked scaled_dot_product_attention       model/attention/sparse.py:226-281
 * decode: full-cache recompression, sink/current scatter, topk compaction,
   physical gather, additive mask, SDPA      model/attention/sparse.py:99-183
+* chunked prefill (past 8192 tokens): per query block, non-causal selector on
+  its rows, mask scatter, future blocks cleared, topk over the 0/1 mask,
+  physical gather, validity + causal mask, SDPA
+                                            model/attention/sparse.py:284-364
 
 ``torch.topk`` leaves the order of tied values unspecified; where that
 matters (the -inf ties of the decode routing) the selection it produced is
@@ -85,6 +89,49 @@ def sparse_prefill(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
     add = torch.repeat_interleave(add, rep, dim=1)
     o = F.scaled_dot_product_attention(xq, k_e, v_e, attn_mask=add)
     return o.transpose(1, 2).reshape(B, T, Hq * D)
+
+
+def chunked_prefill(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor,
+                    forecast: Optional[torch.Tensor], bs: int, top_k: int) -> torch.Tensor:
+    """The chunked-gather prefill, xq [B,Hq,T,D], xk/xv [B,Hkv,T,D], forecast
+    [B,T,Hkv,Df] or None -> [B,T,Hq*D] (before wo). One iteration per query
+    block of bs rows, each with the reference's own tensor operations."""
+    B, Hq, T, D = xq.shape
+    Hkv = xk.shape[1]
+    rep = Hq // Hkv
+    nb = (T + bs - 1) // bs
+    reps = block_means(xk.transpose(1, 2), bs)
+    max_sel = min(nb, top_k + 2)
+    outs = []
+    for b_q in range(nb):
+        s0, s1 = b_q * bs, min(T, (b_q + 1) * bs)
+        mask = torch.zeros((B, Hkv, nb), dtype=torch.bool)
+        mask.scatter_(-1, torch.zeros((B, Hkv, 1), dtype=torch.long), True)
+        mask.scatter_(-1, torch.full((B, Hkv, 1), b_q, dtype=torch.long), True)
+        if forecast is not None and b_q > 0:
+            _, top = select_blocks(forecast[:, s0:s1], reps, bs, top_k, causal=False)
+            mask.scatter_(-1, top.reshape(B, Hkv, -1).clamp(0, nb - 1), True)
+        else:
+            for j in range(max(0, b_q - top_k + 1), b_q + 1):
+                mask.scatter_(-1, torch.full((B, Hkv, 1), j, dtype=torch.long), True)
+        mask[:, :, torch.arange(nb) > b_q] = False
+        val, sel = torch.topk(mask.float(), k=max_sel, dim=-1)
+        pad = nb * bs - T
+        kp = F.pad(xk, (0, 0, 0, pad)).view(B, Hkv, nb, bs, D)
+        vp = F.pad(xv, (0, 0, 0, pad)).view(B, Hkv, nb, bs, D)
+        ix = sel[..., None, None].expand(-1, -1, -1, bs, D)
+        kg = torch.gather(kp, 2, ix).reshape(B, Hkv, max_sel * bs, D)
+        vg = torch.gather(vp, 2, ix).reshape(B, Hkv, max_sel * bs, D)
+        pos = (sel[..., None] * bs + torch.arange(bs)).reshape(B, Hkv, 1, max_sel * bs)
+        ok = (val > 0.5)[..., None].expand(-1, -1, -1, bs).reshape(B, Hkv, 1, max_sel * bs)
+        qpos = torch.arange(s0, s1).view(1, 1, s1 - s0, 1)
+        valid = (pos < T) & (pos <= qpos) & ok
+        add = torch.where(valid, torch.zeros(1, dtype=xq.dtype), torch.full((1,), float("-inf"), dtype=xq.dtype))
+        kg = torch.repeat_interleave(kg, rep, dim=1)
+        vg = torch.repeat_interleave(vg, rep, dim=1)
+        add = torch.repeat_interleave(add, rep, dim=1)
+        outs.append(F.scaled_dot_product_attention(xq[:, :, s0:s1], kg, vg, attn_mask=add))
+    return torch.cat(outs, dim=2).transpose(1, 2).reshape(B, T, Hq * D)
 
 
 def sparse_decode(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor, S: int,

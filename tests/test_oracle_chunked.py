@@ -125,3 +125,37 @@ def test_chunked_attention_equals_the_reference_gather_and_sdpa():
         o = F.scaled_dot_product_attention(xq[:, :, start:end], kg, vg, attn_mask=mask)
         got[:, start:end] = o.transpose(1, 2).reshape(B, end - start, Hq * D).numpy()
     assert np.abs(got - want).max() < 1e-10
+
+
+def test_chunked_restatement_equals_the_oracle_where_the_union_fits():
+    # oracle/reference_path.chunked_prefill (the reference's steps, the CPU
+    # baseline of the chunked leg) against the oracle's lists and attention,
+    # in float64, with picks confined so that no union exceeds the cut (where
+    # torch.topk's choice among equal mask entries would decide)
+    from oracle import reference_path as RP
+    B, T, Hq, Hkv, D, bs, k = 1, 700, 6, 2, 16, 64, 8
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((B, T, Hq, D))
+    kk = rng.standard_normal((B, T, Hkv, D))
+    v = rng.standard_normal((B, T, Hkv, D))
+    f = rng.standard_normal((B, T, Hkv, D))
+    xq, xk, xv = (torch.from_numpy(a).transpose(1, 2) for a in (q, kk, v))
+    NB = (T + bs - 1) // bs
+    # with k + 2 >= NB the cut never binds
+    got = RP.chunked_prefill(xq, xk, xv, torch.from_numpy(f), bs, NB).numpy()
+    _, tk, _, _ = O.route(f, O.compress(kk, bs), bs, NB, False)
+    sel, n = O.chunked_selection(tk, B, Hkv, T, bs, NB)
+    want = O.attention_prefill(q, kk, v, sel, n, bs, True)
+    assert np.abs(got - want).max() < 1e-10
+    # one forecast per query block: every row picks the same k blocks, so the
+    # union ({0, own} and k picks) fits the cut exactly and the selection is real
+    k = 4
+    fb = np.repeat(rng.standard_normal((B, NB, Hkv, D)), bs, axis=1)[:, :T]
+    got = RP.chunked_prefill(xq, xk, xv, torch.from_numpy(fb), bs, k).numpy()
+    _, tk, _, _ = O.route(fb, O.compress(kk, bs), bs, k, False)
+    sel, n = O.chunked_selection(tk, B, Hkv, T, bs, k)
+    assert (n < NB).any()
+    assert np.abs(got - O.attention_prefill(q, kk, v, sel, n, bs, True)).max() < 1e-10
+    got_w = RP.chunked_prefill(xq, xk, xv, None, bs, 3).numpy()
+    sel_w, n_w = O.chunked_selection(None, B, Hkv, T, bs, 3)
+    assert np.abs(got_w - O.attention_prefill(q, kk, v, sel_w, n_w, bs, True)).max() < 1e-10
